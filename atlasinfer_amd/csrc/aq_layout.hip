@@ -1,0 +1,210 @@
+// aq_layout.hip -- outlier index bookkeeping, the reference's compacted code
+// stream, and dequantization.
+//
+// Reference: atlasinfer_core/quant/adaptive_quantizer.py
+//   compacted stream of non-outlier codes     :110,125-126,136 (written)
+//                                             :209-212         (read back)
+//   dequantize_tensor per-block loop          :185-245
+// The reference finds the outliers of each block by comparing against all
+// outlier indices (O(blocks * nnz)) and syncs to the host once per block
+// (:194-195,234).  Here a workgroup owns a 4096-element tile, finds its slice
+// of the ascending index list with two binary searches, stages it in LDS, and
+// every thread walks its 16 elements against it.
+#include "aq_common.h"
+
+namespace {
+
+constexpr int kTile = 4096;  // elements per workgroup (256 threads x 16)
+
+__device__ __forceinline__ int64_t lower_bound_i64(const int64_t* a, int64_t n, int64_t key) {
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    int64_t mid = (lo + hi) >> 1;
+    if (a[mid] < key)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(256) void segment_offsets_kernel(const int64_t* idx, int64_t nnz, int64_t nseg,
+                                                              int64_t seg_len, int32_t* seg_ptr) {
+  const int64_t s = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (s > nseg) return;
+  seg_ptr[s] = (int32_t)lower_bound_i64(idx, nnz, s * seg_len);
+}
+
+__global__ __launch_bounds__(256) void outlier_cols_kernel(const int64_t* idx, int64_t nnz, int64_t K,
+                                                           int32_t* cols) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p < nnz) cols[p] = (int32_t)(idx[p] % K);
+}
+
+// MODE 0: compact (dense -> stream); MODE 1: expand (stream -> dense).
+template <int MODE>
+__global__ __launch_bounds__(256) void reorder_codes_kernel(const uint8_t* src, int64_t padded, const int64_t* idx,
+                                                            int64_t nnz, uint8_t* dst) {
+  __shared__ int64_t lb[2];
+  __shared__ int16_t local[kTile];
+  const int64_t t0 = (int64_t)blockIdx.x * kTile;
+  const int64_t t1 = min(padded, t0 + kTile);
+  if (threadIdx.x < 2) lb[threadIdx.x] = lower_bound_i64(idx, nnz, threadIdx.x ? t1 : t0);
+  __syncthreads();
+  const int64_t lb0 = lb[0];
+  const int cnt = (int)(lb[1] - lb0);
+  for (int i = threadIdx.x; i < cnt; i += 256) local[i] = (int16_t)(idx[lb0 + i] - t0);
+  __syncthreads();
+  const int e0 = threadIdx.x * 16;
+  // outliers of this tile before element e0
+  int lo = 0, hi = cnt;
+  while (lo < hi) {
+    int mid = (lo + hi) >> 1;
+    if (local[mid] < e0)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  int k = lo;
+  for (int e = e0; e < e0 + 16; e++) {
+    const int64_t j = t0 + e;
+    if (j >= t1) break;
+    const bool out = (k < cnt) && (local[k] == e);
+    const int64_t cpos = j - (lb0 + k);  // position in the compacted stream
+    if (MODE == 0) {
+      if (!out) dst[cpos] = src[j];
+    } else {
+      dst[j] = out ? (uint8_t)0 : src[cpos];
+    }
+    k += out;
+  }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* codes, const uint16_t* scales, int64_t numel,
+                                                      int64_t G, uint16_t* out, int vec) {
+  const int64_t j0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 16;
+  if (j0 >= numel) return;
+  uint8_t c[16];
+  const bool full = vec && (j0 + 16 <= numel);
+  if (full) {
+    uint4 u = *reinterpret_cast<const uint4*>(codes + j0);
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 16; k++) c[k] = (uint8_t)(w[k / 4] >> (8 * (k % 4)));
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; k++) c[k] = (j0 + k < numel) ? codes[j0 + k] : 0;
+  }
+  int64_t b = j0 / G;
+  int64_t next = (b + 1) * G;
+  float s = (float)bits_to_h(scales[b]);
+  uint16_t o[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    if (j0 + k == next) {
+      b++;
+      next += G;
+      if (j0 + k < numel) s = (float)bits_to_h(scales[b]);
+    }
+    const float v = FMT == AQ_FMT_INT8 ? (float)(int8_t)c[k] : e4m3_value(c[k]);
+    o[k] = h_to_bits(rn_h(v * s));  // exact product, one rounding
+  }
+  if (full) {
+    uint4* dst = reinterpret_cast<uint4*>(out + j0);
+    uint32_t w[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) w[k] = (uint32_t)o[2 * k] | ((uint32_t)o[2 * k + 1] << 16);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+      if (j0 + k < numel) out[j0 + k] = o[k];
+  }
+}
+
+__global__ __launch_bounds__(256) void scatter_outliers_kernel(const int64_t* idx, const uint16_t* vals, int64_t nnz,
+                                                               int64_t numel, uint16_t* out) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p < nnz && idx[p] < numel) out[idx[p]] = vals[p];
+}
+
+}  // namespace
+
+extern "C" int aq_segment_offsets(const int64_t* flat_idx, int64_t nnz, int64_t nseg, int64_t seg_len,
+                                  int32_t* seg_ptr, void* stream) {
+  AQ_CHECK_ARG(nnz >= 0 && nseg >= 0 && seg_len >= 1, "aq_segment_offsets: bad sizes");
+  AQ_CHECK_ARG(seg_ptr && (nnz == 0 || flat_idx), "aq_segment_offsets: null pointer argument");
+  AQ_CHECK_ARG(nnz < ((int64_t)1 << 31), "aq_segment_offsets: nnz exceeds int32");
+  const int64_t grid = aq::ceil_div(nseg + 1, 256);
+  hipLaunchKernelGGL(segment_offsets_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, flat_idx, nnz,
+                     nseg, seg_len, seg_ptr);
+  AQ_LAUNCH_CHECK("aq_segment_offsets: launch");
+  return AQ_OK;
+}
+
+extern "C" int aq_outlier_cols(const int64_t* flat_idx, int64_t nnz, int64_t K, int32_t* cols, void* stream) {
+  AQ_CHECK_ARG(nnz >= 0 && K >= 1, "aq_outlier_cols: bad sizes");
+  if (nnz == 0) return AQ_OK;
+  AQ_CHECK_ARG(flat_idx && cols, "aq_outlier_cols: null pointer argument");
+  hipLaunchKernelGGL(outlier_cols_kernel, dim3((unsigned)aq::ceil_div(nnz, 256)), dim3(256), 0, (hipStream_t)stream,
+                     flat_idx, nnz, K, cols);
+  AQ_LAUNCH_CHECK("aq_outlier_cols: launch");
+  return AQ_OK;
+}
+
+static int reorder(int mode, const void* src, int64_t padded, const int64_t* idx, int64_t nnz, void* dst,
+                   void* stream, const char* name) {
+  AQ_CHECK_ARG(padded >= 0 && nnz >= 0 && nnz <= padded, "%s: bad sizes", name);
+  if (padded == 0) return AQ_OK;
+  AQ_CHECK_ARG(src && dst && (nnz == 0 || idx), "%s: null pointer argument", name);
+  const int64_t grid = aq::ceil_div(padded, kTile);
+  if (mode == 0)
+    hipLaunchKernelGGL((reorder_codes_kernel<0>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)src, padded, idx, nnz, (uint8_t*)dst);
+  else
+    hipLaunchKernelGGL((reorder_codes_kernel<1>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)src, padded, idx, nnz, (uint8_t*)dst);
+  AQ_LAUNCH_CHECK(name);
+  return AQ_OK;
+}
+
+extern "C" int aq_compact_codes(const void* dense, int64_t padded, const int64_t* flat_idx, int64_t nnz,
+                                void* compact, void* stream) {
+  if (padded == nnz) return AQ_OK;  // every element is an outlier: empty stream
+  return reorder(0, dense, padded, flat_idx, nnz, compact, stream, "aq_compact_codes");
+}
+
+extern "C" int aq_expand_codes(const void* compact, int64_t padded, const int64_t* flat_idx, int64_t nnz,
+                               void* dense, void* stream) {
+  if (padded == nnz) {
+    if (padded == 0) return AQ_OK;
+    return aq::check_hip(hipMemsetAsync(dense, 0, (size_t)padded, (hipStream_t)stream), "aq_expand_codes: memset");
+  }
+  return reorder(1, compact, padded, flat_idx, nnz, dense, stream, "aq_expand_codes");
+}
+
+extern "C" int aq_dequantize(const void* codes, const void* scales, int64_t numel, int64_t G, int fmt,
+                             const int64_t* flat_idx, const void* vals, int64_t nnz, void* out, void* stream) {
+  AQ_CHECK_ARG(numel >= 0 && G >= 1 && nnz >= 0, "aq_dequantize: bad sizes");
+  AQ_CHECK_ARG(fmt == AQ_FMT_INT8 || fmt == AQ_FMT_E4M3, "aq_dequantize: unknown code format %d", fmt);
+  if (numel == 0) return AQ_OK;
+  AQ_CHECK_ARG(codes && scales && out && (nnz == 0 || (flat_idx && vals)), "aq_dequantize: null pointer argument");
+  hipStream_t s = (hipStream_t)stream;
+  const int vec = ((uintptr_t)codes % 16 == 0) && ((uintptr_t)out % 16 == 0);
+  const int64_t grid = aq::ceil_div(numel, 256 * 16);
+  if (fmt == AQ_FMT_INT8)
+    hipLaunchKernelGGL((dequant_kernel<AQ_FMT_INT8>), dim3((unsigned)grid), dim3(256), 0, s, (const uint8_t*)codes,
+                       (const uint16_t*)scales, numel, G, (uint16_t*)out, vec);
+  else
+    hipLaunchKernelGGL((dequant_kernel<AQ_FMT_E4M3>), dim3((unsigned)grid), dim3(256), 0, s, (const uint8_t*)codes,
+                       (const uint16_t*)scales, numel, G, (uint16_t*)out, vec);
+  AQ_LAUNCH_CHECK("aq_dequantize: launch");
+  if (nnz > 0) {
+    hipLaunchKernelGGL(scatter_outliers_kernel, dim3((unsigned)aq::ceil_div(nnz, 256)), dim3(256), 0, s, flat_idx,
+                       (const uint16_t*)vals, nnz, numel, (uint16_t*)out);
+    AQ_LAUNCH_CHECK("aq_dequantize: scatter launch");
+  }
+  return AQ_OK;
+}

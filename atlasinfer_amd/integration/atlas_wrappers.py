@@ -1,0 +1,121 @@
+"""QuantizedLinear: an nn.Linear replacement whose weight stays quantized.
+
+Same interface as the reference class
+(/root/reference/integration/atlas_wrappers.py:21-83; also importable as
+``integration.atlas_wrappers.QuantizedLinear``): constructor
+``(quantized_weights, bias)``, plain attributes ``quantized_weights``,
+``bias`` and ``original_shape``, ``forward(x)`` with F.linear semantics over
+any leading dimensions, the same ``extra_repr``.
+
+The reference's forward dequantizes the whole weight to fp16 (cached) and
+calls F.linear (:56,67).  Here forward is one launch of the fused
+dequant-GEMV / dequant-GEMM (``aq_qlinear``): the codes are decoded in
+registers and never written back as fp16.  Blocks that do not tile the rows
+(block size not a multiple of 32 dividing in_features) take the
+dequantize kernel followed by F.linear on the GPU.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .. import _lib
+from ..quant.adaptive_quantizer import QuantizedTensor, dense_codes, dequantize_tensor, _format_id
+
+
+def qlinear(x: torch.Tensor, qt: QuantizedTensor, bias: Optional[torch.Tensor],
+            codes: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = x W^T + b for W in quantized form, through aq_qlinear.  ``codes``
+    may carry the dense code array (saves the int8 expansion per call)."""
+    dev = x.device
+    K = int(qt.original_shape[-1])
+    N = qt.original_shape.numel() // K
+    x2 = x.reshape(-1, K)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    if M == 0:
+        return y.view(*x.shape[:-1], N)
+    if codes is None:
+        codes = dense_codes(qt, dev)
+    L = _lib.load()
+    ws_bytes = int(L.aq_qlinear_workspace_size(M, N, K))
+    ws = _lib.workspace(dev, ws_bytes, "qlinear")
+    _lib.check(L.aq_qlinear(x2.data_ptr(), M, K, N, codes.data_ptr(), qt.scale_factors.data_ptr(), qt.block_size,
+                            _format_id(qt.code_format), qt.outlier_row_ptr.data_ptr(), _lib.ptr(qt.outlier_cols),
+                            _lib.ptr(qt.fp16_outliers), _lib.ptr(bias), y.data_ptr(), ws.data_ptr(), ws.numel(),
+                            _lib.stream_of(dev)), "aq_qlinear")
+    return y.view(*x.shape[:-1], N)
+
+
+def fused_supported(qt: QuantizedTensor) -> bool:
+    K = int(qt.original_shape[-1]) if len(qt.original_shape) else 0
+    G = qt.block_size
+    return (K > 0 and G >= 32 and G % 32 == 0 and K % G == 0 and qt.outlier_row_ptr is not None)
+
+
+class QuantizedLinear(nn.Module):
+    """A Linear layer that uses a QuantizedTensor for weights."""
+
+    def __init__(self, quantized_weights: QuantizedTensor, bias: Optional[torch.Tensor]):
+        super().__init__()
+        self.quantized_weights = quantized_weights
+        self.bias = bias
+        self.original_shape = getattr(quantized_weights, "original_shape", None)
+        self._codes = None  # dense codes on the compute device (int8 format: expanded once)
+
+    def _weights_on(self, device: torch.device) -> QuantizedTensor:
+        q = self.quantized_weights
+        if not hasattr(q, "fp8_data"):
+            raise TypeError(f"Weight in QuantizedLinear ({id(self)}) is not a valid QuantizedTensor: {type(q)}")
+        if q.fp8_data.device != device:
+            self.quantized_weights = q = q.to(device)
+            self._codes = None
+        if self.bias is not None and self.bias.device != device:
+            self.bias = self.bias.to(device)
+        return q
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        dev = x.device
+        if dev.type != "cuda":
+            raise RuntimeError(f"QuantizedLinear runs on a HIP device; input is on {dev}")
+        q = self._weights_on(dev)
+        if x.dtype != torch.float16:
+            raise RuntimeError(f"expected both mat1 and mat2 to have the same dtype, but got: {x.dtype} != Half")
+        K = int(q.original_shape[-1])
+        if x.shape[-1] != K:
+            raise RuntimeError(f"mat1 and mat2 shapes cannot be multiplied (input last dim {x.shape[-1]} vs "
+                               f"in_features {K})")
+        if not fused_supported(q):
+            return F.linear(x, dequantize_tensor(q, dev), self.bias)
+        if self._codes is None or self._codes.device != dev:
+            self._codes = dense_codes(q, dev)
+        return qlinear(x, q, self.bias, self._codes)
+
+    def _apply(self, fn, recurse=True):
+        # module.to(device) / .cuda() also moves the quantized weight and the
+        # bias (plain attributes, invisible to nn.Module); dtype casts leave
+        # the codes alone.
+        super()._apply(fn, recurse)
+        probe = fn(torch.empty(0, dtype=torch.float16, device=self._current_device()))
+        if probe.device != self._current_device():
+            self._weights_on(probe.device)
+        return self
+
+    def _current_device(self) -> torch.device:
+        q = self.quantized_weights
+        return q.fp8_data.device if hasattr(q, "fp8_data") else torch.device("cpu")
+
+    def extra_repr(self) -> str:
+        q_shape, q_device = None, "N/A"
+        if hasattr(self, "quantized_weights") and self.quantized_weights:
+            q_shape = self.original_shape
+            try:
+                q_device = self.quantized_weights.fp8_data.device
+            except AttributeError:
+                pass
+        return f"quantized_shape={q_shape}, bias={self.bias is not None}, device={q_device}"

@@ -1,0 +1,138 @@
+"""Swap a model's nn.Linear layers for QuantizedLinear.
+
+Mirrors the quantization half of /root/reference/integration/model_modifier.py
+(``MODEL_LAYER_PATTERNS`` :21-50, ``_get_model_patterns`` :52-56,
+``_replace_module`` :58-76, ``find_modules`` :78-92,
+``apply_atlas_quantization_to_model`` :95-143); also importable as
+``integration.model_modifier``.  Differences: the weights are quantized on the
+GPU (bit-identical to a CPU run of the same algorithm) and stay there, and
+this module has no import-time dependency on the KV-cache tier (lmdb).
+"""
+from __future__ import annotations
+
+import gc
+import traceback
+from typing import Dict, List, Optional, Tuple, Type
+
+import torch
+import torch.nn as nn
+
+from .. import _lib
+from ..quant.adaptive_quantizer import quantize_tensor
+from .atlas_wrappers import QuantizedLinear
+
+MODEL_LAYER_PATTERNS = {
+    "opt": {
+        "linear_types": [nn.Linear],
+        "attention_type": ["OPTAttention", "OPTSdpaAttention"],
+        "decoder_layer_type": "OPTDecoderLayer",
+        "decoder_block_path": "model.decoder.layers",
+        "attention_subpath": "self_attn",
+    },
+    "llama": {
+        "linear_types": [nn.Linear],
+        "attention_type": ["LlamaAttention", "LlamaSdpaAttention"],
+        "decoder_layer_type": "LlamaDecoderLayer",
+        "decoder_block_path": "model.layers",
+        "attention_subpath": "self_attn",
+    },
+    "mistral": {
+        "linear_types": [nn.Linear],
+        "attention_type": ["MistralAttention", "MistralSdpaAttention"],
+        "decoder_layer_type": "MistralDecoderLayer",
+        "decoder_block_path": "model.layers",
+        "attention_subpath": "self_attn",
+    },
+    "gemma": {
+        "linear_types": [nn.Linear],
+        "attention_type": ["GemmaAttention", "GemmaSdpaAttention"],
+        "decoder_layer_type": "GemmaDecoderLayer",
+        "decoder_block_path": "model.layers",
+        "attention_subpath": "self_attn",
+    },
+}
+
+
+def _get_model_patterns(model_type: str) -> Optional[Dict]:
+    patterns = MODEL_LAYER_PATTERNS.get(model_type)
+    if patterns is None:
+        print(f"Warning: No layer patterns for '{model_type}'.")
+    return patterns
+
+
+def _replace_module(parent_module: nn.Module, child_name: str, new_module: nn.Module):
+    """setattr the new module in place of the old one."""
+    setattr(parent_module, child_name, new_module)
+
+
+def find_modules(model: nn.Module, target_types: List[Type], target_names: List[str] = [],
+                 exclude_names: List[str] = []) -> List[Tuple[str, nn.Module]]:
+    """Modules matching a type (isinstance) or a class name, skipping any whose
+    qualified name contains an excluded substring (reference :78-92)."""
+    found = []
+    if not isinstance(target_names, list):
+        target_names = [target_names] if target_names else []
+    if not isinstance(target_types, list):
+        target_types = [target_types] if target_types else []
+    if not isinstance(exclude_names, list):
+        exclude_names = [exclude_names] if exclude_names else []
+    for name, module in model.named_modules():
+        if any(ex and ex in name for ex in exclude_names):
+            continue
+        type_match = any(isinstance(module, t) for t in target_types if t is not None)
+        name_match = type(module).__name__ in target_names
+        if type_match or name_match:
+            found.append((name, module))
+    return found
+
+
+def apply_atlas_quantization_to_model(model: nn.Module, model_type: str, quantization_config: Dict,
+                                      excluded_layers: List[str] = ["lm_head", "embed_tokens", "embeddings"],
+                                      *, device: Optional[torch.device] = None):
+    """Quantize every non-excluded nn.Linear of ``model`` in place
+    (reference :95-143).  ``quantization_config`` is splatted into
+    quantize_tensor (block_size, z_threshold, code_format).  Returns
+    (layers_replaced, layers_failed)."""
+    print(f"\n--- Applying Atlas Quantization ({model_type}) ---")
+    patterns = _get_model_patterns(model_type)
+    if patterns is None:
+        print("ERROR: No patterns.")
+        return
+    dev = _lib.compute_device(torch.device(device) if device is not None else None)
+    try:
+        model.to(dtype=torch.float16)
+    except Exception as e:  # same tolerance as the reference's pre-quant move
+        print(f"Warning: Pre-quant cast failed: {e}")
+    target_linear_types = patterns.get("linear_types", [])
+    if not target_linear_types:
+        print("Warning: No linear types.")
+        return
+    linear_modules = find_modules(model, target_types=target_linear_types, exclude_names=excluded_layers)
+    if not linear_modules:
+        print("Warning: No linear layers found.")
+        return
+    print(f"Found {len(linear_modules)} linear layers to quantize...")
+    replaced, failed = 0, 0
+    for name, module in list(linear_modules):
+        parent_name, child_name = name.rsplit(".", 1) if "." in name else ("", name)
+        parent = model.get_submodule(parent_name) if parent_name else model
+        if type(getattr(parent, child_name, None)).__name__ == "QuantizedLinear":
+            continue
+        try:
+            if not hasattr(module, "weight") or module.weight is None:
+                print(f"Warn: No weight {name}. Skip.")
+                failed += 1
+                continue
+            w = module.weight.data.to(dtype=torch.float16, device=dev)
+            b = module.bias.data.to(dtype=torch.float16, device=dev).clone() if getattr(module, "bias", None) is not None else None
+            qt = quantize_tensor(w, **quantization_config)
+            _replace_module(parent, child_name, QuantizedLinear(qt, b))
+            replaced += 1
+            del w, module
+        except Exception as e:
+            print(f"!! FAILED quant layer {name}: {e}")
+            traceback.print_exc()
+            failed += 1
+    gc.collect()
+    print(f"--- Quantization complete. Replaced: {replaced}, Failed/Skipped: {failed} ---")
+    return replaced, failed

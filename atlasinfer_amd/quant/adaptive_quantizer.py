@@ -1,0 +1,287 @@
+"""Adaptive hybrid FP8/FP16 weight quantization on MI355X (gfx950).
+
+Same API as the reference module
+/root/reference/atlasinfer_core/quant/adaptive_quantizer.py (also importable
+under that name, ``atlasinfer_core.quant.adaptive_quantizer``):
+
+* ``QuantizedTensor``          (reference :8-42) -- the six reference fields in
+  order, plus trailing fields with defaults: ``code_format``,
+  ``outlier_row_ptr`` (CSR row pointer, int32 [N+1]) and ``outlier_cols``
+  (int32 [nnz]).
+* ``calculate_zscore_manual``  (reference :44-49)
+* ``quantize_tensor``          (reference :51-148)
+* ``dequantize_tensor``        (reference :156-251)
+* ``clear_dequantized_cache``  (reference :253-263)
+
+Every computation runs in the HIP kernels of libatlasinfer_amd.so; CPU inputs
+are copied to the GPU, processed there and the results copied back to the
+input's device.  Without a HIP device the compute functions raise.
+
+Code formats:
+* ``"int8"`` -- the reference's format, bit for bit: ``fp8_data`` holds the
+  int8 codes of the non-outliers only, in element order.
+* ``"e4m3"`` (default) -- OCP FP8 E4M3 codes computed by the same op
+  sequence with 448 in place of 127; ``fp8_data`` is the dense code array
+  (torch.float8_e4m3fn, one code per element of the zero-padded flat tensor,
+  0 at outliers).
+``block_size=-1`` selects one block per output channel (block = last dim).
+"""
+from __future__ import annotations
+
+import threading
+from typing import NamedTuple, Optional
+
+import numpy as np
+import torch
+
+from .. import _lib
+
+DEFAULT_CODE_FORMAT = "e4m3"
+PER_CHANNEL = -1
+
+
+class QuantizedTensor(NamedTuple):
+    """A tensor quantized into the hybrid FP8/FP16 format (reference :8-18)."""
+    fp8_data: torch.Tensor          # codes (int8 compacted stream, or dense e4m3)
+    fp16_outliers: torch.Tensor     # fp16 outlier values, ascending flat index order
+    outlier_indices: torch.Tensor   # int64 flat indices of the outliers (padded tensor)
+    scale_factors: torch.Tensor     # fp16, one per block
+    original_shape: torch.Size
+    block_size: int
+    code_format: str = "int8"
+    outlier_row_ptr: Optional[torch.Tensor] = None  # int32 [N + 1] over the last dim
+    outlier_cols: Optional[torch.Tensor] = None     # int32 [nnz]
+
+    def to(self, device):
+        """Move every tensor to ``device``; returns self when already there
+        (reference :20-32)."""
+        device = torch.device(device)
+        if self.fp8_data.device == device:
+            return self
+        mv = lambda t: None if t is None else t.to(device)  # noqa: E731
+        return self._replace(
+            fp8_data=mv(self.fp8_data),
+            fp16_outliers=mv(self.fp16_outliers),
+            outlier_indices=mv(self.outlier_indices),
+            scale_factors=mv(self.scale_factors),
+            outlier_row_ptr=mv(self.outlier_row_ptr),
+            outlier_cols=mv(self.outlier_cols),
+        )
+
+    def memory_footprint(self, include_overhead=True) -> int:
+        """Bytes held by the component tensors (+128 when include_overhead,
+        reference :34-42)."""
+        mem = 0
+        for t in (self.fp8_data, self.fp16_outliers, self.outlier_indices, self.scale_factors,
+                  self.outlier_row_ptr, self.outlier_cols):
+            if t is not None:
+                mem += t.element_size() * t.nelement()
+        if include_overhead:
+            mem += 128
+        return mem
+
+
+def _format_id(code_format: str) -> int:
+    try:
+        return _lib.FORMATS[code_format]
+    except KeyError:
+        raise ValueError(f"code_format must be one of {sorted(_lib.FORMATS)}, got {code_format!r}") from None
+
+
+def _threshold_bits(z_threshold: float) -> int:
+    # torch compares an fp16 tensor with a Python float after casting the
+    # scalar to fp16 (double -> float -> half)
+    return int(np.float16(np.float32(z_threshold)).view(np.uint16))
+
+
+def _resolve_block(block_size: int, shape: torch.Size) -> int:
+    if block_size == PER_CHANNEL:
+        return int(shape[-1]) if len(shape) >= 1 and shape[-1] > 0 else 1
+    if not isinstance(block_size, (int, np.integer)) or block_size < 1:
+        raise ValueError(f"block_size must be a positive int or -1 (per output channel), got {block_size!r}")
+    return int(block_size)
+
+
+def calculate_zscore_manual(data: torch.Tensor, eps=1e-6) -> torch.Tensor:
+    """(data - mean) / (std + eps) over all of ``data`` with fp16 tensor
+    semantics (reference :44-49).  fp16 only; at most 65536 elements."""
+    if data.dtype != torch.float16:
+        raise TypeError(f"calculate_zscore_manual: float16 input expected, got {data.dtype}")
+    L = _lib.load()
+    n = data.numel()
+    if n == 0:
+        return torch.empty_like(data)
+    if n > L.aq_max_block_size():
+        raise ValueError(f"calculate_zscore_manual: {n} elements exceed the {L.aq_max_block_size()} limit")
+    dev = _lib.compute_device(data.device)
+    x = data.to(dev).contiguous().view(-1)
+    z = torch.empty_like(x)
+    _lib.check(L.aq_zscore(_lib.ptr(x), n, float(eps), _lib.ptr(z), None, _lib.stream_of(dev)), "aq_zscore")
+    return z.view(data.shape).to(data.device)
+
+
+def _empty(original_shape, block_size, fmt_name, device) -> QuantizedTensor:
+    code_dtype = torch.int8 if fmt_name == "int8" else torch.float8_e4m3fn
+    n = int(original_shape[0]) if len(original_shape) >= 2 else 1
+    return QuantizedTensor(
+        fp8_data=torch.empty((0,), dtype=code_dtype, device=device),
+        fp16_outliers=torch.empty((0,), dtype=torch.float16, device=device),
+        outlier_indices=torch.empty((0,), dtype=torch.long, device=device),
+        scale_factors=torch.empty((0,), dtype=torch.float16, device=device),
+        original_shape=original_shape,
+        block_size=block_size,
+        code_format=fmt_name,
+        outlier_row_ptr=torch.zeros((max(n, 0) + 1 if len(original_shape) >= 2 else 1,), dtype=torch.int32,
+                                    device=device),
+        outlier_cols=torch.empty((0,), dtype=torch.int32, device=device),
+    )
+
+
+def quantize_tensor(
+    fp16_tensor: torch.Tensor,
+    block_size: int = 128,
+    z_threshold: float = 3.0,
+    *,
+    code_format: str = DEFAULT_CODE_FORMAT,
+) -> QuantizedTensor:
+    """Quantize an fp16 tensor into the hybrid format (reference :51-148).
+
+    Per block of ``block_size`` elements of the flattened, zero-padded tensor:
+    elements with |z| > z_threshold are kept as fp16 outliers, the rest are
+    coded against one fp16 scale per block.  Results land on the input's
+    device.
+    """
+    if not isinstance(fp16_tensor, torch.Tensor):
+        raise TypeError(f"Input must be a PyTorch Tensor, got {type(fp16_tensor)}")
+    if fp16_tensor.dtype != torch.float16:
+        print(f"Warning: Input tensor was {fp16_tensor.dtype}, converting to FP16 for quantization.")
+        fp16_tensor = fp16_tensor.to(torch.float16)
+    fmt = _format_id(code_format)
+    input_device = fp16_tensor.device
+    original_shape = fp16_tensor.shape
+    numel = fp16_tensor.numel()
+    G = _resolve_block(block_size, original_shape)
+    if numel == 0:
+        return _empty(original_shape, G, code_format, input_device)
+
+    L = _lib.load()
+    if G > L.aq_max_block_size():
+        raise ValueError(f"block_size {G} exceeds the supported maximum {L.aq_max_block_size()}")
+    dev = _lib.compute_device(input_device)
+    stream = _lib.stream_of(dev)
+    x = fp16_tensor.to(dev).contiguous().view(-1)
+    K = int(original_shape[-1]) if len(original_shape) >= 1 else 1
+    N = numel // K
+    nblocks = (numel + G - 1) // G
+    padded = nblocks * G
+
+    codes = torch.empty(padded, dtype=torch.uint8, device=dev)
+    scales = torch.empty(nblocks, dtype=torch.float16, device=dev)
+    block_off = torch.empty(nblocks + 1, dtype=torch.int32, device=dev)
+    ws_bytes = int(L.aq_quantize_workspace_size(numel, G))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _lib.check(L.aq_quantize(x.data_ptr(), numel, G, _threshold_bits(z_threshold), fmt, codes.data_ptr(),
+                             scales.data_ptr(), block_off.data_ptr(), ws.data_ptr(), ws_bytes, stream),
+               "aq_quantize")
+    nnz = int(block_off[nblocks].item())  # the one host sync: sizes the outlier tensors
+    flat_idx = torch.empty(nnz, dtype=torch.int64, device=dev)
+    vals = torch.empty(nnz, dtype=torch.float16, device=dev)
+    cols = torch.empty(nnz, dtype=torch.int32, device=dev)
+    _lib.check(L.aq_quantize_finish(numel, G, K, block_off.data_ptr(), nnz, ws.data_ptr(), ws_bytes,
+                                    _lib.ptr(flat_idx), _lib.ptr(vals), _lib.ptr(cols), stream),
+               "aq_quantize_finish")
+    row_ptr = torch.empty(N + 1, dtype=torch.int32, device=dev)
+    _lib.check(L.aq_segment_offsets(_lib.ptr(flat_idx), nnz, N, K, row_ptr.data_ptr(), stream),
+               "aq_segment_offsets")
+    if fmt == _lib.FMT_INT8:
+        fp8_data = torch.empty(padded - nnz, dtype=torch.int8, device=dev)
+        _lib.check(L.aq_compact_codes(codes.data_ptr(), padded, _lib.ptr(flat_idx), nnz, _lib.ptr(fp8_data),
+                                      stream), "aq_compact_codes")
+    else:
+        fp8_data = codes.view(torch.float8_e4m3fn)
+    del ws
+    qt = QuantizedTensor(
+        fp8_data=fp8_data,
+        fp16_outliers=vals,
+        outlier_indices=flat_idx,
+        scale_factors=scales,
+        original_shape=original_shape,
+        block_size=G,
+        code_format=code_format,
+        outlier_row_ptr=row_ptr,
+        outlier_cols=cols,
+    )
+    return qt.to(input_device)
+
+
+def dense_codes(qt: QuantizedTensor, device: torch.device) -> torch.Tensor:
+    """One uint8 code per element of the padded tensor, 0 at outliers (the
+    layout the kernels read), on ``device``.  For int8 this expands the
+    reference's compacted stream."""
+    q = qt.to(device)
+    numel = q.original_shape.numel()
+    G = q.block_size
+    padded = (numel + G - 1) // G * G
+    if q.code_format != "int8":
+        return q.fp8_data.view(torch.uint8)
+    L = _lib.load()
+    dense = torch.empty(padded, dtype=torch.uint8, device=device)
+    nnz = q.outlier_indices.numel()
+    _lib.check(L.aq_expand_codes(_lib.ptr(q.fp8_data), padded, _lib.ptr(q.outlier_indices), nnz,
+                                 dense.data_ptr(), _lib.stream_of(device)), "aq_expand_codes")
+    return dense
+
+
+# --- Dequantization cache (reference :153-154): id(QuantizedTensor) -> fp16 tensor
+_dequantized_weights_cache = {}
+_cache_lock = threading.Lock()
+
+
+def dequantize_tensor(quant_data: QuantizedTensor, target_device: torch.device) -> torch.Tensor:
+    """Rebuild the fp16 tensor on ``target_device`` (reference :156-251):
+    fp16(code * scale) for non-outliers, outlier values verbatim.  Memoised by
+    the identity of ``quant_data`` like the reference."""
+    target_device = torch.device(target_device)
+    if target_device.type == "cuda" and target_device.index is None:
+        target_device = torch.device("cuda", torch.cuda.current_device())
+    cache_key = id(quant_data)
+    with _cache_lock:
+        cached = _dequantized_weights_cache.get(cache_key)
+        if cached is not None and cached.device == target_device:
+            return cached
+        elif cached is not None:
+            cached = cached.to(target_device)
+            _dequantized_weights_cache[cache_key] = cached
+            return cached
+
+    numel = quant_data.original_shape.numel()
+    if numel == 0:
+        final = torch.zeros(quant_data.original_shape, dtype=torch.float16, device=target_device)
+    else:
+        L = _lib.load()
+        dev = _lib.compute_device(target_device)
+        q = quant_data.to(dev)
+        fmt = _format_id(q.code_format)
+        codes = dense_codes(q, dev)
+        out = torch.empty(numel, dtype=torch.float16, device=dev)
+        nnz = q.outlier_indices.numel()
+        _lib.check(L.aq_dequantize(codes.data_ptr(), q.scale_factors.data_ptr(), numel, q.block_size, fmt,
+                                   _lib.ptr(q.outlier_indices), _lib.ptr(q.fp16_outliers), nnz, out.data_ptr(),
+                                   _lib.stream_of(dev)), "aq_dequantize")
+        final = out.view(q.original_shape).to(target_device)
+
+    with _cache_lock:
+        _dequantized_weights_cache[cache_key] = final
+    return final
+
+
+def clear_dequantized_cache(quant_data_id=None):
+    """Clear one entry (by id) or the whole cache (reference :253-263)."""
+    global _dequantized_weights_cache
+    with _cache_lock:
+        if quant_data_id is not None and quant_data_id in _dequantized_weights_cache:
+            del _dequantized_weights_cache[quant_data_id]
+        elif quant_data_id is None:
+            _dequantized_weights_cache = {}
+    if torch.cuda.is_available():
+        torch.cuda.empty_cache()

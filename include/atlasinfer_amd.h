@@ -1,0 +1,143 @@
+/*
+ * atlasinfer_amd.h -- C ABI of libatlasinfer_amd.so, the MI355X (gfx950)
+ * implementation of AtlasInfer's adaptive hybrid weight quantization path.
+ *
+ * Conventions
+ *   - extern "C", plain pointers and sizes; no C++ or torch types.
+ *   - Every pointer argument is device memory owned by the caller, unless the
+ *     comment says otherwise.  The library never allocates device memory;
+ *     scratch space comes in through a caller-owned workspace argument whose
+ *     size the matching *_workspace_size() call returns.
+ *   - Every call enqueues work on `stream` (a hipStream_t, passed as void*)
+ *     and returns without synchronising.
+ *   - Return value: AQ_OK (0) or a negative AQ_E* code; aq_last_error()
+ *     returns a thread-local message describing the last failure.
+ *   - fp16 data is passed as IEEE binary16 bit patterns (uint16_t storage).
+ *   - Code formats: AQ_FMT_INT8 is the reference's int8 symmetric code
+ *     (adaptive_quantizer.py:100,119-126); AQ_FMT_E4M3 is OCP FP8 E4M3 (fn).
+ *
+ * Data layout of a quantized weight W[N, K] (row-major, the nn.Linear layout)
+ * with block size G over the flat, zero-padded tensor (padded = ceil(N*K/G)*G):
+ *   codes     uint8  [padded]        one code per element, 0 at outliers
+ *   scales    fp16   [padded / G]    one scale per block
+ *   flat_idx  int64  [nnz]           ascending flat indices of outliers
+ *   vals      fp16   [nnz]           outlier values (verbatim)
+ *   row_ptr   int32  [N + 1]         CSR row pointer over the outliers (< N*K)
+ *   cols      int32  [nnz]           column of each outlier (flat_idx % K)
+ */
+#ifndef ATLASINFER_AMD_H
+#define ATLASINFER_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AQ_ABI_VERSION 1
+
+enum { AQ_FMT_INT8 = 0, AQ_FMT_E4M3 = 1 };
+enum { AQ_OK = 0, AQ_EINVAL = -1, AQ_EHIP = -2, AQ_EUNSUPPORTED = -3, AQ_EWORKSPACE = -4 };
+
+/* ABI version of the loaded library (AQ_ABI_VERSION at build time). */
+int aq_abi_version(void);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* aq_last_error(void);
+
+/* Largest block size aq_quantize accepts (65536). */
+int64_t aq_max_block_size(void);
+
+/*
+ * Quantize, phase 1 of 2.  Replaces the per-block loop of quantize_tensor
+ * (reference: atlasinfer_core/quant/adaptive_quantizer.py:84-133).
+ * For every block of G elements of the zero-padded flat fp16 tensor x[numel]:
+ * z-score statistics, outlier flags (|z| > z_thr), scale, dense codes; the
+ * outliers of each block are staged in the workspace and counted, and the
+ * exclusive prefix sum of the counts is written to block_off.
+ *   x          fp16 [numel]
+ *   z_thr_f16  fp16 bits of the threshold (the reference compares in fp16)
+ *   codes      uint8 [padded]          (out)
+ *   scales     fp16  [padded / G]      (out)
+ *   block_off  int32 [padded / G + 1]  (out) block_off[nblocks] = total nnz
+ *   workspace  >= aq_quantize_workspace_size(numel, G) bytes, kept intact
+ *              until aq_quantize_finish has run.
+ */
+int64_t aq_quantize_workspace_size(int64_t numel, int64_t G);
+int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_thr_f16, int fmt, void* codes,
+                void* scales, int32_t* block_off, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Quantize, phase 2 of 2: write the outlier list in ascending flat order
+ * (the reference's fp16_outliers / outlier_indices, adaptive_quantizer.py:
+ * 109-117,137-138) plus the column of each outlier for row width K.
+ *   nnz        block_off[nblocks] as read back by the caller
+ *   flat_idx   int64 [nnz] (out)     vals fp16 [nnz] (out)
+ *   cols       int32 [nnz] (out, may be NULL)
+ */
+int aq_quantize_finish(int64_t numel, int64_t G, int64_t K, const int32_t* block_off, int64_t nnz,
+                       const void* workspace, int64_t workspace_bytes, int64_t* flat_idx, void* vals,
+                       int32_t* cols, void* stream);
+
+/*
+ * seg_ptr[s] = number of outliers with flat index < s * seg_len, for
+ * s = 0..nseg (CSR row pointer with seg_len = K, block offsets with
+ * seg_len = G).  flat_idx must be ascending.
+ */
+int aq_segment_offsets(const int64_t* flat_idx, int64_t nnz, int64_t nseg, int64_t seg_len,
+                       int32_t* seg_ptr, void* stream);
+
+/* cols[p] = flat_idx[p] % K. */
+int aq_outlier_cols(const int64_t* flat_idx, int64_t nnz, int64_t K, int32_t* cols, void* stream);
+
+/*
+ * Reference layout <-> dense codes.  The reference stores only the codes of
+ * non-outliers, in element order (adaptive_quantizer.py:110,125-126,136;
+ * read back at :209-212).
+ *   aq_compact_codes: dense[padded] -> compact[padded - nnz]
+ *   aq_expand_codes:  compact[padded - nnz] -> dense[padded] (0 at outliers)
+ */
+int aq_compact_codes(const void* dense, int64_t padded, const int64_t* flat_idx, int64_t nnz,
+                     void* compact, void* stream);
+int aq_expand_codes(const void* compact, int64_t padded, const int64_t* flat_idx, int64_t nnz,
+                    void* dense, void* stream);
+
+/*
+ * Dequantize (reference: dequantize_tensor, adaptive_quantizer.py:185-245):
+ * out[j] = fp16(value(codes[j]) * scales[j / G]) for j < numel, then
+ * out[flat_idx[p]] = vals[p] for flat_idx[p] < numel.
+ */
+int aq_dequantize(const void* codes, const void* scales, int64_t numel, int64_t G, int fmt,
+                  const int64_t* flat_idx, const void* vals, int64_t nnz, void* out, void* stream);
+
+/*
+ * calculate_zscore_manual (adaptive_quantizer.py:44-49) of x[n] as one
+ * block: z = fp16(fp16(x - mean) / fp16(std + eps)).  stats (may be NULL)
+ * receives (mean, std, std + eps) as fp16.  n <= aq_max_block_size().
+ */
+int aq_zscore(const void* x, int64_t n, float eps, void* z, void* stats, void* stream);
+
+/*
+ * Quantized linear forward y = x W^T + b with W given by its quantized form
+ * (reference: QuantizedLinear.forward, integration/atlas_wrappers.py:30-74,
+ * which computes F.linear(x, dequantize_tensor(W), b) at :56,67).
+ *   x     fp16 [M, K] row-major      y fp16 [M, N] (out)
+ *   bias  fp16 [N] or NULL
+ *   G must divide K and be a multiple of 32.
+ * M <= 16 runs the dequant-GEMV, larger M the dequant-GEMM; both add the
+ * outliers from the CSR lists in an fp32 epilogue.
+ * workspace: >= aq_qlinear_workspace_size(M, N, K) bytes.  Its first 256 KiB
+ * hold split-K tickets and must be zero before the first call; every call
+ * leaves them at zero again.  Calls that share a workspace must not overlap
+ * (use one workspace per stream).
+ */
+int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K);
+int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const void* codes, const void* scales,
+               int64_t G, int fmt, const int32_t* row_ptr, const int32_t* cols, const void* vals,
+               const void* bias, void* y, void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATLASINFER_AMD_H */

@@ -1,0 +1,80 @@
+"""The C ABI: the library loads, exports every function include/atlasinfer_amd.h
+declares, reports its ABI version, and rejects bad arguments with a status
+code and a message -- all without touching a GPU."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "atlasinfer_amd.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(aq_[a-z0-9_]+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from atlasinfer_amd import _lib
+    return _lib.load()
+
+
+def test_header_declares_the_expected_api():
+    names = declared_functions()
+    for must in ["aq_abi_version", "aq_last_error", "aq_quantize", "aq_quantize_finish", "aq_dequantize",
+                 "aq_qlinear", "aq_zscore", "aq_compact_codes", "aq_expand_codes", "aq_segment_offsets"]:
+        assert must in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    from atlasinfer_amd import _lib
+    so = _lib.LIB_PATH
+    out = subprocess.run(["nm", "-D", "--defined-only", so], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\b(aq_[a-z0-9_]+)\b", out))
+    missing = [n for n in declared_functions() if n not in exported]
+    assert not missing, missing
+    # and the ctypes table covers the header exactly
+    assert sorted(_lib.SIGNATURES) == declared_functions()
+
+
+def test_abi_version(lib):
+    from atlasinfer_amd import _lib
+    assert lib.aq_abi_version() == _lib.ABI_VERSION
+    hdr = open(HEADER).read()
+    assert f"#define AQ_ABI_VERSION {_lib.ABI_VERSION}" in hdr
+
+
+def test_bad_arguments_return_einval_with_message(lib):
+    AQ_EINVAL = -1
+    p = ctypes.c_void_p(16)
+    assert lib.aq_quantize(p, 0, 128, 0x4200, 1, p, p, p, p, 1 << 20, None) == AQ_EINVAL
+    assert b"numel" in lib.aq_last_error()
+    assert lib.aq_quantize(p, 100, 0, 0x4200, 1, p, p, p, p, 1 << 20, None) == AQ_EINVAL
+    assert lib.aq_quantize(p, 100, 1 << 20, 0x4200, 1, p, p, p, p, 1 << 20, None) == AQ_EINVAL
+    assert lib.aq_quantize(p, 100, 64, 0x4200, 7, p, p, p, p, 1 << 20, None) == AQ_EINVAL
+    assert b"format" in lib.aq_last_error()
+    # G must be a multiple of 32 dividing K for the fused linear
+    assert lib.aq_qlinear(p, 1, 4096, 16, p, p, 100, 1, p, p, p, None, p, p, 1 << 20, None) == AQ_EINVAL
+    assert b"block size" in lib.aq_last_error()
+    assert lib.aq_dequantize(p, p, 10, 0, 0, None, None, 0, p, None) == AQ_EINVAL
+    assert lib.aq_zscore(p, 0, 1e-6, p, None, None) == AQ_EINVAL
+
+
+def test_workspace_sizes(lib):
+    assert lib.aq_quantize_workspace_size(4096 * 4096, 4096) >= 4096 * 4096 * 6
+    assert lib.aq_quantize_workspace_size(0, 128) == 0
+    assert lib.aq_qlinear_workspace_size(1, 4096, 4096) > 0
+    assert lib.aq_max_block_size() == 65536
+
+
+def test_workspace_too_small_is_reported(lib):
+    AQ_EWORKSPACE = -4
+    p = ctypes.c_void_p(16)
+    assert lib.aq_quantize(p, 4096, 128, 0x4200, 1, p, p, p, p, 16, None) == AQ_EWORKSPACE
+    assert b"workspace" in lib.aq_last_error()

@@ -1,0 +1,268 @@
+"""GPU parity: the HIP path against the reference's golden vectors and the
+CPU oracle on the same seeded inputs.
+
+Bit-exact: codes, scales, outlier indices/values, dequantized weights,
+z-scores.  Tolerance (north star): layer outputs within
+max|dy| <= 2e-3 * max|x| * max|w| and ||dy||_2 / ||y||_2 <= 1e-3 of
+F.linear(x, dequantize_tensor(W), b) computed in float64.
+"""
+import numpy as np
+import pytest
+import torch
+
+from atlasinfer_core.quant import adaptive_quantizer as AQ
+from conftest import golden_cases
+from integration import atlas_wrappers as AW
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+CASES = golden_cases()
+
+
+def bits(t):
+    if isinstance(t, torch.Tensor):
+        t = t.detach().cpu()
+        return t.view(torch.uint8).numpy() if t.element_size() == 1 else t.view(torch.int16).numpy().view(np.uint16)
+    return t.view(np.uint8) if t.dtype.itemsize == 1 else t.view(np.uint16)
+
+
+def make_weights(rng, shape, sigma=0.02, frac=0.001, t_dof=None):
+    n = int(np.prod(shape))
+    w = rng.standard_t(t_dof, n) * sigma if t_dof else rng.standard_normal(n) * sigma
+    k = int(round(frac * n))
+    pos = rng.permutation(n)[:k]
+    w[pos] = rng.choice([-1.0, 1.0], k) * rng.uniform(8, 20, k) * sigma
+    return w.reshape(shape).astype(np.float16)
+
+
+@pytest.mark.parametrize("name,d", CASES, ids=[c[0] for c in CASES])
+def test_int8_matches_reference_golden(name, d):
+    x = torch.from_numpy(d["x"]).to(DEV)
+    q = AQ.quantize_tensor(x, block_size=int(d["block_size"]), z_threshold=float(d["z_threshold"]),
+                           code_format="int8")
+    assert q.fp8_data.dtype == torch.int8
+    assert np.array_equal(bits(q.fp8_data), bits(d["fp8_data"]))
+    assert np.array_equal(bits(q.scale_factors), bits(d["scale_factors"]))
+    assert np.array_equal(q.outlier_indices.cpu().numpy(), d["outlier_indices"])
+    assert np.array_equal(bits(q.fp16_outliers), bits(d["fp16_outliers"]))
+    AQ.clear_dequantized_cache()
+    deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    assert deq.shape == x.shape
+    assert np.array_equal(bits(deq), bits(d["deq"]))
+
+
+def test_cpu_input_returns_on_cpu_and_matches(oracle):
+    d = dict(CASES)["opt_like_g128"]
+    q = AQ.quantize_tensor(torch.from_numpy(d["x"]), block_size=128, code_format="int8")
+    assert q.fp8_data.device.type == "cpu"
+    assert np.array_equal(bits(q.fp8_data), bits(d["fp8_data"]))
+
+
+def test_zscore_matches_reference_golden():
+    import os
+    from conftest import GOLDEN_DIR
+    with np.load(os.path.join(GOLDEN_DIR, "zscore.npz")) as d:
+        off = 0
+        for n in d["lens"]:
+            x = torch.from_numpy(d["x"][off:off + n]).to(DEV)
+            z = AQ.calculate_zscore_manual(x)
+            assert np.array_equal(bits(z), bits(d["z"][off:off + n])), n
+            off += n
+
+
+SHAPES = [
+    # (rows, cols, block, threshold, format, t_dof, outlier fraction)
+    (64, 256, 128, 3.0, "e4m3", None, 0.001),
+    (48, 512, -1, 3.0, "e4m3", None, 0.001),
+    (33, 1000, 100, 3.0, "e4m3", None, 0.01),     # ragged: G does not divide K
+    (16, 4096, -1, 3.0, "e4m3", 3, 0.01),
+    (8, 14336, -1, 3.0, "int8", None, 0.001),     # per-row block of 14336 (team of 1024)
+    (4, 40000, -1, 3.0, "e4m3", None, 0.001),     # block > 16384: 64 elements per thread
+    (128, 96, 32, 1.0, "int8", None, 0.05),       # many outliers per block
+    (7, 13, 8, 2.0, "e4m3", None, 0.05),          # G < 16, unaligned rows
+    (1, 10, 64, 3.0, "int8", None, 0.0),          # smaller than one block
+    (256, 512, 1, 3.0, "int8", None, 0.0),        # G = 1: std is NaN, no outliers
+]
+
+
+@pytest.mark.parametrize("rows,cols,G,thr,fmt,tdof,frac", SHAPES)
+def test_quantize_matches_oracle(oracle, rows, cols, G, thr, fmt, tdof, frac):
+    rng = np.random.default_rng(rows * 7919 + cols)
+    w = make_weights(rng, (rows, cols), frac=frac, t_dof=tdof)
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=G, z_threshold=thr, code_format=fmt)
+    Gr = cols if G == -1 else G
+    ref = oracle.quantize(w, Gr, thr, oracle.FMT_INT8 if fmt == "int8" else oracle.FMT_E4M3)
+    assert q.block_size == Gr
+    assert np.array_equal(bits(q.scale_factors), bits(ref["scale_factors"]))
+    assert np.array_equal(q.outlier_indices.cpu().numpy(), ref["outlier_indices"])
+    assert np.array_equal(bits(q.fp16_outliers), bits(ref["fp16_outliers"]))
+    assert np.array_equal(bits(q.fp8_data), bits(ref["fp8_data"]))
+    dense = AQ.dense_codes(q, torch.device(DEV))
+    assert np.array_equal(bits(dense), ref["codes"])
+    # CSR view of the same outliers
+    idx = ref["outlier_indices"]
+    inside = idx[idx < rows * cols]
+    rp = q.outlier_row_ptr.cpu().numpy()
+    assert rp[0] == 0 and rp[-1] == inside.size
+    assert np.array_equal(np.diff(rp), np.bincount(inside // cols, minlength=rows))
+    assert np.array_equal(q.outlier_cols.cpu().numpy()[: inside.size], (inside % cols).astype(np.int32))
+    AQ.clear_dequantized_cache()
+    deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    assert np.array_equal(bits(deq), bits(oracle.dequantize(ref)))
+
+
+def test_llama_shape_per_channel_e4m3_full(oracle):
+    """A full 4096 x 4096 projection at the product setting (per-channel e4m3)."""
+    rng = np.random.default_rng(5)
+    w = make_weights(rng, (4096, 4096))
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, code_format="e4m3")
+    ref = oracle.quantize(w, 4096, 3.0, oracle.FMT_E4M3)
+    assert np.array_equal(bits(q.fp8_data), ref["codes"])
+    assert np.array_equal(bits(q.scale_factors), bits(ref["scale_factors"]))
+    assert np.array_equal(q.outlier_indices.cpu().numpy(), ref["outlier_indices"])
+
+
+def test_zscore_matches_oracle(oracle):
+    rng = np.random.default_rng(1)
+    for n in [1, 2, 17, 128, 1000, 4096, 20000, 65536]:
+        x = (rng.standard_normal(n) * 0.5).astype(np.float16)
+        z = AQ.calculate_zscore_manual(torch.from_numpy(x).to(DEV))
+        zr, _ = oracle.zscore(x)
+        assert np.array_equal(bits(z), bits(zr)), n
+
+
+def test_compact_expand_round_trip():
+    rng = np.random.default_rng(9)
+    w = make_weights(rng, (300, 700), frac=0.02)
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=70, code_format="int8")
+    dense = AQ.dense_codes(q, torch.device(DEV))
+    qe = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=70, code_format="e4m3")
+    assert dense.numel() == qe.fp8_data.numel()
+    mask = torch.ones(dense.numel(), dtype=torch.bool, device=DEV)
+    mask[q.outlier_indices] = False
+    assert torch.equal(dense[mask].view(torch.int8), q.fp8_data)
+    assert torch.all(dense[~mask] == 0)
+
+
+def reference_linear(x, w_deq, bias):
+    y = x.double() @ w_deq.double().t()
+    if bias is not None:
+        y = y + bias.double()
+    return y
+
+
+def assert_close(y, yref, x, w):
+    d = (y.double() - yref).abs()
+    bound = 2e-3 * x.abs().max().double() * w.abs().max().double()
+    assert d.max() <= bound, (d.max().item(), bound.item())
+    rel = (y.double() - yref).norm() / yref.norm()
+    assert rel <= 1e-3, rel.item()
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 16, 17, 64, 300])
+@pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128), ("e4m3", 64)])
+def test_qlinear_matches_reference_linear(M, fmt, G):
+    rng = np.random.default_rng(M + 31 * G)
+    N, K = 1024, 2048
+    w = make_weights(rng, (N, K))
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    xs[:, rng.permutation(K)[:4]] *= 30
+    x = torch.from_numpy(xs.astype(np.float16)).to(DEV)
+    b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(DEV)
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=G, code_format=fmt)
+    AQ.clear_dequantized_cache()
+    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    for bias in (None, b):
+        layer = AW.QuantizedLinear(q, bias)
+        y = layer(x)
+        assert y.shape == (M, N) and y.dtype == torch.float16
+        assert_close(y, reference_linear(x, w_deq, bias), x, w_deq)
+
+
+@pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (4096, 14336), (14336, 4096)])
+@pytest.mark.parametrize("M", [1, 16, 512])
+def test_qlinear_llama_shapes(N, K, M):
+    rng = np.random.default_rng(N + K + M)
+    w = make_weights(rng, (N, K))
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, code_format="e4m3")
+    AQ.clear_dequantized_cache()
+    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    y = AW.QuantizedLinear(q, None)(x)
+    assert_close(y, reference_linear(x, w_deq, None), x, w_deq)
+
+
+def test_qlinear_heavy_outliers_and_3d_input():
+    rng = np.random.default_rng(77)
+    w = make_weights(rng, (512, 1024), frac=0.01, t_dof=3)
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=128, code_format="int8")
+    x = torch.from_numpy(rng.standard_normal((2, 3, 1024)).astype(np.float16)).to(DEV)
+    b = torch.from_numpy(rng.standard_normal(512).astype(np.float16)).to(DEV)
+    AQ.clear_dequantized_cache()
+    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    y = AW.QuantizedLinear(q, b)(x)
+    assert y.shape == (2, 3, 512)
+    yref = reference_linear(x.reshape(-1, 1024), w_deq, b).reshape(2, 3, 512)
+    assert_close(y, yref, x, w_deq)
+
+
+def test_qlinear_fallback_for_ragged_blocks():
+    """Block 100 does not tile 1000-wide rows: dequantize kernel + F.linear."""
+    rng = np.random.default_rng(4)
+    w = make_weights(rng, (64, 1000))
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=100, code_format="e4m3")
+    x = torch.from_numpy(rng.standard_normal((5, 1000)).astype(np.float16)).to(DEV)
+    AQ.clear_dequantized_cache()
+    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    assert_close(AW.QuantizedLinear(q, None)(x), reference_linear(x, w_deq, None), x, w_deq)
+
+
+def test_qlinear_repeated_calls_are_deterministic():
+    rng = np.random.default_rng(12)
+    w = make_weights(rng, (1024, 4096))
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1)
+    x = torch.from_numpy(rng.standard_normal((1, 4096)).astype(np.float16)).to(DEV)
+    layer = AW.QuantizedLinear(q, None)
+    y0 = layer(x)
+    for _ in range(5):
+        assert torch.equal(layer(x), y0)
+
+
+def test_module_to_moves_quantized_weights():
+    rng = np.random.default_rng(2)
+    w = make_weights(rng, (64, 128))
+    q = AQ.quantize_tensor(torch.from_numpy(w), block_size=-1)
+    layer = AW.QuantizedLinear(q, torch.zeros(64, dtype=torch.float16))
+    layer.to(DEV)
+    assert layer.quantized_weights.fp8_data.device.type == "cuda"
+    assert layer.bias.device.type == "cuda"
+
+
+def test_model_swap_tiny_opt():
+    transformers = pytest.importorskip("transformers")
+    from integration.model_modifier import apply_atlas_quantization_to_model
+    cfg = transformers.OPTConfig(vocab_size=256, hidden_size=128, num_hidden_layers=2, ffn_dim=512,
+                                 num_attention_heads=4, max_position_embeddings=64, word_embed_proj_dim=128)
+    torch.manual_seed(0)
+    model = transformers.OPTForCausalLM(cfg).half().to(DEV).eval()
+    ids = torch.randint(0, 256, (1, 12), device=DEV)
+    replaced, failed = apply_atlas_quantization_to_model(model, "opt", {"block_size": -1, "z_threshold": 3.0})
+    assert (replaced, failed) == (12, 0)
+    qlin = [m for m in model.modules() if type(m).__name__ == "QuantizedLinear"]
+    assert len(qlin) == 12
+    with torch.no_grad():
+        logits = model(ids).logits
+        # same model with every QuantizedLinear computed as F.linear on the dequantized weight
+        for m in qlin:
+            AQ.clear_dequantized_cache()
+            m._ref_w = AQ.dequantize_tensor(m.quantized_weights, torch.device(DEV)).clone()
+        saved = AW.QuantizedLinear.forward
+        AW.QuantizedLinear.forward = lambda self, x: torch.nn.functional.linear(x, self._ref_w, self.bias)
+        try:
+            ref = model(ids).logits
+        finally:
+            AW.QuantizedLinear.forward = saved
+    rel = (logits.double() - ref.double()).norm() / ref.double().norm()
+    assert rel < 2e-3, rel.item()
+    out = model.generate(ids, max_new_tokens=4, do_sample=False)
+    assert out.shape == (1, 16)

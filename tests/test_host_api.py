@@ -1,0 +1,86 @@
+"""Host-side logic of the reference API mirror that needs no GPU: type checks,
+empty tensors, the QuantizedTensor container, module discovery, and that the
+compute path refuses to run without a HIP device instead of falling back."""
+import pytest
+import torch
+import torch.nn as nn
+
+from atlasinfer_core.quant import adaptive_quantizer as AQ
+from integration import atlas_wrappers as AW
+from integration import model_modifier as MM
+
+
+def test_import_aliases_are_the_implementation():
+    import atlasinfer_amd.quant.adaptive_quantizer as impl
+    import atlasinfer_amd.integration.atlas_wrappers as w
+    import atlasinfer_amd.integration.model_modifier as m
+    assert AQ is impl and AW is w and MM is m
+
+
+def test_non_tensor_input_raises_type_error():
+    with pytest.raises(TypeError):
+        AQ.quantize_tensor([1.0, 2.0])
+
+
+def test_empty_tensor_round_trip_shape():
+    e = torch.empty((0, 10), dtype=torch.float16)
+    for fmt in ["int8", "e4m3"]:
+        q = AQ.quantize_tensor(e, code_format=fmt)
+        assert q.original_shape == e.shape and q.fp8_data.numel() == 0
+        AQ.clear_dequantized_cache()
+        assert AQ.dequantize_tensor(q, torch.device("cpu")).shape == e.shape
+
+
+def test_bad_format_and_block_size():
+    t = torch.ones(4, 4, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        AQ.quantize_tensor(t, code_format="int4")
+    with pytest.raises(ValueError):
+        AQ.quantize_tensor(t, block_size=0)
+
+
+def test_quantized_tensor_fields_and_footprint():
+    q = AQ.QuantizedTensor(torch.zeros(10, dtype=torch.int8), torch.zeros(2, dtype=torch.float16),
+                           torch.zeros(2, dtype=torch.long), torch.zeros(1, dtype=torch.float16),
+                           torch.Size([3, 4]), 64)
+    assert q._fields[:6] == ("fp8_data", "fp16_outliers", "outlier_indices", "scale_factors", "original_shape",
+                             "block_size")
+    assert q.code_format == "int8"  # a tuple built from the six reference fields keeps reference semantics
+    assert q.memory_footprint(include_overhead=False) == 10 + 4 + 16 + 2
+    assert q.memory_footprint() == 32 + 128
+    assert q.to("cpu") is q
+
+
+def test_compute_without_device_raises():
+    if torch.cuda.is_available():
+        pytest.skip("a HIP device is present")
+    from atlasinfer_amd._lib import AQError
+    with pytest.raises(AQError):
+        AQ.quantize_tensor(torch.ones(4, 128, dtype=torch.float16))
+    with pytest.raises(RuntimeError):
+        AW.QuantizedLinear(AQ.quantize_tensor(torch.empty(0, 4, dtype=torch.float16)), None)(
+            torch.ones(1, 4, dtype=torch.float16))
+
+
+class Tiny(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.block = nn.Sequential(nn.Linear(8, 8), nn.ReLU(), nn.Linear(8, 4))
+        self.lm_head = nn.Linear(4, 4)
+        self.embed_tokens = nn.Embedding(3, 8)
+
+
+def test_find_modules_and_exclusions():
+    m = Tiny()
+    names = [n for n, _ in MM.find_modules(m, [nn.Linear], exclude_names=["lm_head", "embed_tokens"])]
+    assert names == ["block.0", "block.2"]
+    names = [n for n, _ in MM.find_modules(m, [], target_names=["Embedding"])]
+    assert names == ["embed_tokens"]
+    assert set(MM.MODEL_LAYER_PATTERNS) == {"opt", "llama", "mistral", "gemma"}
+    assert MM._get_model_patterns("bert") is None
+
+
+def test_extra_repr_format():
+    q = AQ.quantize_tensor(torch.empty(0, 4, dtype=torch.float16))
+    r = AW.QuantizedLinear(q, None).extra_repr()
+    assert r.startswith("quantized_shape=torch.Size([0, 4]), bias=False, device=")

@@ -94,18 +94,10 @@ __device__ __forceinline__ uint8_t e4m3_from_h(f16 v) {
   return (uint8_t)(code | sign);
 }
 
-// Exact value of an E4M3 code as fp16 bits times 2^-8 (the E4M3 exponent
-// field lands in the fp16 exponent field, bias 7 vs 15): the caller folds
-// the 2^8 into the scale.
-__device__ __forceinline__ uint32_t e4m3x2_to_h2bits_scaled(uint32_t two_codes_in_lo16) {
-  // bytes b0 | b1 << 8  ->  fp16 pair (b0 -> low half, b1 -> high half)
-  uint32_t w = (two_codes_in_lo16 & 0xFFu) | ((two_codes_in_lo16 & 0xFF00u) << 8);
-  return ((w & 0x007F007Fu) << 7) | ((w & 0x00800080u) << 8);
-}
-
-__device__ __forceinline__ float e4m3_value(uint8_t c) {
+// Exact fp16 value of an E4M3 code (every E4M3 value is an fp16 value).
+__device__ __forceinline__ f16 e4m3_to_h(uint8_t c) {
   uint32_t hb = ((uint32_t)(c & 0x7Fu) << 7) | ((uint32_t)(c & 0x80u) << 8);
-  return (float)bits_to_h((uint16_t)hb) * 256.0f;
+  return bits_to_h((uint16_t)hb) * (f16)256.0f;  // power-of-two scaling: exact, keeps -0
 }
 
 // -------------------------------------------------------- team reductions

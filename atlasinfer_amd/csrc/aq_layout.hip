@@ -98,17 +98,20 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* codes, cons
   }
   int64_t b = j0 / G;
   int64_t next = (b + 1) * G;
-  float s = (float)bits_to_h(scales[b]);
+  f16 s = bits_to_h(scales[b]);
   uint16_t o[16];
 #pragma unroll
   for (int k = 0; k < 16; k++) {
     if (j0 + k == next) {
       b++;
       next += G;
-      if (j0 + k < numel) s = (float)bits_to_h(scales[b]);
+      if (j0 + k < numel) s = bits_to_h(scales[b]);
     }
-    const float v = FMT == AQ_FMT_INT8 ? (float)(int8_t)c[k] : e4m3_value(c[k]);
-    o[k] = h_to_bits(rn_h(v * s));  // exact product, one rounding
+    // code value and scale are exact fp16 values: one native fp16 multiply
+    // is the single rounding of the exact product (and keeps the sign of 0,
+    // which a widened multiply fused with a +0 addend would not)
+    const f16 v = FMT == AQ_FMT_INT8 ? (f16)(int8_t)c[k] : e4m3_to_h(c[k]);
+    o[k] = h_to_bits(v * s);
   }
   if (full) {
     uint4* dst = reinterpret_cast<uint4*>(out + j0);
@@ -158,7 +161,7 @@ static int reorder(int mode, const void* src, int64_t padded, const int64_t* idx
                    void* stream, const char* name) {
   AQ_CHECK_ARG(padded >= 0 && nnz >= 0 && nnz <= padded, "%s: bad sizes", name);
   if (padded == 0) return AQ_OK;
-  AQ_CHECK_ARG(src && dst && (nnz == 0 || idx), "%s: null pointer argument", name);
+  AQ_CHECK_ARG(dst && (nnz == padded || src) && (nnz == 0 || idx), "%s: null pointer argument", name);
   const int64_t grid = aq::ceil_div(padded, kTile);
   if (mode == 0)
     hipLaunchKernelGGL((reorder_codes_kernel<0>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
@@ -178,10 +181,6 @@ extern "C" int aq_compact_codes(const void* dense, int64_t padded, const int64_t
 
 extern "C" int aq_expand_codes(const void* compact, int64_t padded, const int64_t* flat_idx, int64_t nnz,
                                void* dense, void* stream) {
-  if (padded == nnz) {
-    if (padded == 0) return AQ_OK;
-    return aq::check_hip(hipMemsetAsync(dense, 0, (size_t)padded, (hipStream_t)stream), "aq_expand_codes: memset");
-  }
   return reorder(1, compact, padded, flat_idx, nnz, dense, stream, "aq_expand_codes");
 }
 

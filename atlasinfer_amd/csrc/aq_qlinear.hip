@@ -7,16 +7,24 @@
 // fp16(value(code) * scale) -- bit for bit the weight dequantize_tensor would
 // produce -- and multiplied on the fp16 MFMA units with fp32 accumulation.
 // Outlier positions hold code 0; their fp16 values are added from the CSR
-// lists in the fp32 epilogue, followed by the bias and one rounding to fp16.
+// lists in fp32, then the bias, then one rounding to fp16.
 //
-//  * M <= 16: "skinny" kernel.  One 16x16x32 MFMA per 16 rows x 32 columns of
-//    W; x rows beyond M are zero.  The kernel is HBM-bound (1 byte per weight
-//    against 2*M flops), so K is split across the 4 waves of a workgroup and,
-//    for narrow W, across workgroups; the last workgroup of a column tile to
-//    finish (atomic ticket) sums the partial tiles in a fixed order.
-//  * M > 16: tiled GEMM.  128x128 output tile per workgroup, 64-wide K steps;
-//    x tile (fp16) and code tile (bytes) staged in LDS, codes dequantized to
-//    fp16 MFMA operands in registers.
+//  * M <= 16: dequant-GEMV.  One workgroup of 9 waves per 16 rows of W.
+//    Eight waves stream the rows' codes (16-byte non-temporal loads, four
+//    128-wide K chunks in flight per wave) into 16x16x32 MFMAs with the M
+//    rows of x as the A operand (rows >= M are zero); their partial tiles are
+//    summed through LDS in a fixed order.  The ninth wave meanwhile stages
+//    the rows' CSR outlier lists and the x values they multiply into LDS, so
+//    the epilogue does not wait on memory.  No cross-workgroup reduction:
+//    the grid is N/16 workgroups.
+//  * M > 16: dequant-GEMM.  128x128 output tile per workgroup of 4 waves
+//    (64x64 each), 64-wide K steps; the x tile (fp16) and the code tile
+//    (bytes) go through LDS, the next step's tiles are prefetched into
+//    registers while the current one is multiplied; codes become fp16 MFMA
+//    operands in registers.  Outliers are applied inside the K loop: when
+//    the x tile for columns [k0, k0+64) sits in LDS, each thread adds
+//    x[m, c] * v for the outliers (c, v) of its output columns that fall in
+//    that window (lists staged in LDS once per tile).
 #include <algorithm>
 
 #include "aq_common.h"
@@ -33,20 +41,16 @@ struct QLArgs {
   const uint8_t* codes;
   const uint16_t* scales;
   int G;
-  int kg;  // K / G, scale blocks per row
+  int kg;      // K / G, scale blocks per row
+  int gshift;  // log2(G) when G is a power of two, else -1
   const int32_t* row_ptr;
   const int32_t* cols;
   const uint16_t* vals;
   const uint16_t* bias;
   uint16_t* y;
-  float* part;
-  int32_t* counters;
-  int SK;   // workgroups per column tile (split-K)
-  int cps;  // 128-wide K chunks per split
 };
 
 __device__ __forceinline__ uint32_t perm(uint32_t w, uint32_t sel) { return __builtin_amdgcn_perm(0u, w, sel); }
-
 __device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
 __device__ __forceinline__ uint32_t h2_bits(half2v h) { return __builtin_bit_cast(uint32_t, h); }
 
@@ -55,7 +59,8 @@ template <int FMT>
 __device__ __forceinline__ uint32_t deq_pair(uint32_t w, int hi, half2v s2) {
   const uint32_t p = perm(w, hi ? 0x0C030C02u : 0x0C010C00u);  // [c, 0, c', 0]
   if (FMT == AQ_FMT_E4M3) {
-    // fp16 bits of value * 2^-8; s2 carries s * 2^8
+    // fp16 bits of value * 2^-8 (E4M3 exponent/mantissa land in the fp16
+    // fields); s2 carries s * 2^8
     const uint32_t b = ((p << 7) & 0x3F803F80u) | ((p << 8) & 0x80008000u);
     return h2_bits(as_h2(b) * s2);
   } else {
@@ -83,119 +88,169 @@ __device__ __forceinline__ half2v scale_pair(uint16_t sbits) {
   return (half2v){s, s};
 }
 
-__device__ __forceinline__ float outlier_dot(const QLArgs& a, int m, int n) {
-  float v = 0.0f;
-  const int p1 = a.row_ptr[n + 1];
-  for (int p = a.row_ptr[n]; p < p1; p++)
-    v = __builtin_fmaf((float)bits_to_h(a.x[(size_t)m * a.K + a.cols[p]]), (float)bits_to_h(a.vals[p]), v);
-  return v;
+__device__ __forceinline__ int scale_index(const QLArgs& a, int n, int k) {
+  const int blk = a.gshift >= 0 ? (k >> a.gshift) : (k / a.G);
+  return n * a.kg + blk;
 }
 
-__device__ __forceinline__ void store_out(const QLArgs& a, int m, int n, float v) {
-  v += outlier_dot(a, m, n);
-  if (a.bias) v += (float)bits_to_h(a.bias[n]);
-  a.y[(size_t)m * a.N + n] = h_to_bits(rn_h(v));
-}
+// ------------------------------------------------------------ GEMV (M <= 16)
 
-// ------------------------------------------------------------ skinny (M <= 16)
+constexpr int kGemvStream = 8;  // streaming waves per workgroup; one more wave stages the outliers
+constexpr int kGemvUnroll = 4;  // 128-wide K chunks per wave with loads in flight together
+constexpr int kCsrCap = 2048;   // outlier entries staged per workgroup (16 rows)
+constexpr int kXvCap = 8192;    // staged x values: entries * M <= kXvCap
+constexpr int kStageBatch = 8;  // entries per lane whose loads are issued together
 
-template <int R, int FMT>
-__global__ __launch_bounds__(256) void qlinear_skinny_kernel(QLArgs a) {
-  __shared__ float red[4][R * 256];
-  __shared__ int last_flag;
+template <int FMT>
+__global__ __launch_bounds__(64 * (kGemvStream + 1)) void qlinear_gemv_kernel(QLArgs a) {
+  constexpr int NS = kGemvStream;
+  constexpr int U = kGemvUnroll;
+  __shared__ float red[NS][256];
+  __shared__ int s_rp[17];
+  __shared__ int s_meta[3];  // p0, staged entries, entries with staged x
+  __shared__ int s_col[kCsrCap];
+  __shared__ uint16_t s_val[kCsrCap];
+  __shared__ uint16_t s_xv[kXvCap];
+
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int col = blockIdx.x / a.SK;
-  const int sk = blockIdx.x % a.SK;
-  const int n0 = col * 16 * R;
-  const int nchunks = (a.K + 127) >> 7;
-  const int c_begin = sk * a.cps;
-  const int c_end = min(nchunks, c_begin + a.cps);
-  const int grp = lane >> 4;
-  const int li = lane & 15;
+  const int n0 = blockIdx.x * 16;
+  const int M = a.M, K = a.K, N = a.N;
 
-  float4v acc[R];
+  if (wave == NS) {
+    // Stage the CSR lists of rows n0..n0+15 and the x values they multiply.
+    // Three dependent round trips: row_ptr, then every (col, val), then
+    // every x[m, col]; within each step all loads are issued together.
+    int rp = 0;
+    if (lane <= 16) rp = a.row_ptr[min(n0 + lane, N)];
+    const int p0 = __shfl(rp, 0, 64);
+    const int p1 = __shfl(rp, 16, 64);
+    if (lane <= 16) s_rp[lane] = rp - p0;
+    const int cnt = min(p1 - p0, kCsrCap);
+    const int nx = min(cnt, kXvCap / M);
+    for (int base = 0; base < cnt; base += 64 * kStageBatch) {
+      int col[kStageBatch];
+      uint16_t val[kStageBatch];
 #pragma unroll
-  for (int r = 0; r < R; r++) acc[r] = (float4v){0.f, 0.f, 0.f, 0.f};
-
-  for (int c = c_begin + wave; c < c_end; c += 4) {
-    const int kk = c * 128 + 32 * grp;
-    const bool kv = kk < a.K;
-    uint4 xq[4];
-    if (li < a.M && kv) {
-      const uint4* xp = reinterpret_cast<const uint4*>(a.x + (size_t)li * a.K + kk);
-#pragma unroll
-      for (int j = 0; j < 4; j++) xq[j] = xp[j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; j++) xq[j] = make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      const int n = n0 + 16 * r + li;
-      uint4 q0 = make_uint4(0, 0, 0, 0), q1 = make_uint4(0, 0, 0, 0);
-      uint16_t sb = 0;
-      if (n < a.N && kv) {
-        const uint4* cp = reinterpret_cast<const uint4*>(a.codes + (size_t)n * a.K + kk);
-        q0 = ld_nt16(cp);
-        q1 = ld_nt16(cp + 1);
-        sb = a.scales[(size_t)n * a.kg + kk / a.G];
+      for (int b = 0; b < kStageBatch; b++) {
+        const int e = base + 64 * b + lane;
+        col[b] = 0;
+        val[b] = 0;
+        if (e < cnt) {
+          col[b] = a.cols[p0 + e];
+          val[b] = a.vals[p0 + e];
+        }
       }
-      const half2v s2 = scale_pair<FMT>(sb);
-      const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const half8 wb = deq8<FMT>(qw[2 * j], qw[2 * j + 1], s2);
-        const half8 xa = __builtin_bit_cast(half8, xq[j]);
-        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, wb, acc[r], 0, 0, 0);
+      for (int b = 0; b < kStageBatch; b++) {
+        const int e = base + 64 * b + lane;
+        if (e < cnt) {
+          s_col[e] = col[b];
+          s_val[e] = val[b];
+        }
+      }
+      for (int m = 0; m < M; m++) {
+        uint16_t xv[kStageBatch];
+#pragma unroll
+        for (int b = 0; b < kStageBatch; b++) {
+          const int e = base + 64 * b + lane;
+          xv[b] = (e < nx) ? a.x[(size_t)m * K + col[b]] : (uint16_t)0;
+        }
+#pragma unroll
+        for (int b = 0; b < kStageBatch; b++) {
+          const int e = base + 64 * b + lane;
+          if (e < nx) s_xv[e * M + m] = xv[b];
+        }
       }
     }
+    if (lane == 0) {
+      s_meta[0] = p0;
+      s_meta[1] = cnt;
+      s_meta[2] = nx;
+    }
+  } else {
+    const int grp = lane >> 4;
+    const int li = lane & 15;
+    const int n = n0 + li;
+    const bool nvalid = n < N;
+    const int nchunks = (K + 127) >> 7;
+    const uint8_t* crow = a.codes + (size_t)(nvalid ? n : 0) * K;
+    const uint16_t* xrow = a.x + (size_t)li * K;
+    const bool mvalid = li < M;
+    uint16_t sb_row = 0;
+    if (a.kg == 1 && nvalid) sb_row = a.scales[n];
+    float4v acc = (float4v){0.f, 0.f, 0.f, 0.f};
+    for (int c0 = wave; c0 < nchunks; c0 += U * NS) {
+      uint4 q[U][2];
+      uint4 xq[U][4];
+      uint16_t sb[U];
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int c = c0 + u * NS;
+        const int kk = c * 128 + 32 * grp;
+        const bool kv = (c < nchunks) && (kk < K);
+        q[u][0] = q[u][1] = make_uint4(0, 0, 0, 0);
+        sb[u] = sb_row;
+        if (kv && nvalid) {
+          q[u][0] = ld_nt16(crow + kk);
+          q[u][1] = ld_nt16(crow + kk + 16);
+          if (a.kg != 1) sb[u] = a.scales[scale_index(a, n, kk)];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) xq[u][j] = make_uint4(0, 0, 0, 0);
+        if (kv && mvalid) {
+          const uint4* xp = reinterpret_cast<const uint4*>(xrow + kk);
+#pragma unroll
+          for (int j = 0; j < 4; j++) xq[u][j] = xp[j];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const half2v s2 = scale_pair<FMT>(sb[u]);
+        const uint32_t qw[8] = {q[u][0].x, q[u][0].y, q[u][0].z, q[u][0].w,
+                                q[u][1].x, q[u][1].y, q[u][1].z, q[u][1].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const half8 wb = deq8<FMT>(qw[2 * j], qw[2 * j + 1], s2);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][j]), wb, acc, 0, 0, 0);
+        }
+      }
+    }
+    // C layout: lane l, element i -> m = 4*(l/16) + i, column l % 16
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[wave][lane * 4 + i] = acc[i];
   }
-
-  // reduce the four waves (C layout: lane l, element i -> m = 4*(l/16)+i, n = l%16)
-#pragma unroll
-  for (int r = 0; r < R; r++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) red[wave][r * 256 + lane * 4 + i] = acc[r][i];
   __syncthreads();
 
-  float v[R];
+  if (threadIdx.x < 256) {
+    const int o = threadIdx.x;
+    const int l = o >> 2;
+    const int m = 4 * (l >> 4) + (o & 3);
+    const int nl = l & 15;
+    const int n = n0 + nl;
+    if (m < M && n < N) {
+      float v = 0.0f;
 #pragma unroll
-  for (int q = 0; q < R; q++) {
-    const int o = threadIdx.x + 256 * q;
-    v[q] = (red[0][o] + red[1][o]) + (red[2][o] + red[3][o]);
-  }
-
-  if (a.SK > 1) {
-    float* mine = a.part + ((size_t)col * a.SK + sk) * (R * 256);
-#pragma unroll
-    for (int q = 0; q < R; q++) mine[threadIdx.x + 256 * q] = v[q];
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last_flag = (atomicAdd(&a.counters[col], 1) == a.SK - 1);
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    const float* all = a.part + (size_t)col * a.SK * (R * 256);
-#pragma unroll
-    for (int q = 0; q < R; q++) {
-      const int o = threadIdx.x + 256 * q;
-      float s = 0.0f;
-      for (int k = 0; k < a.SK; k++) s += __builtin_nontemporal_load(all + (size_t)k * (R * 256) + o);
-      v[q] = s;
+      for (int w = 0; w < NS; w++) v += red[w][o];
+      const int p0 = s_meta[0], cnt = s_meta[1], nx = s_meta[2];
+      const int e1 = s_rp[nl + 1];
+      for (int e = s_rp[nl]; e < e1; e++) {
+        float xv, wv;
+        if (e < nx) {
+          xv = (float)bits_to_h(s_xv[e * M + m]);
+          wv = (float)bits_to_h(s_val[e]);
+        } else if (e < cnt) {
+          xv = (float)bits_to_h(a.x[(size_t)m * K + s_col[e]]);
+          wv = (float)bits_to_h(s_val[e]);
+        } else {  // more outliers than the staging holds: straight from memory
+          xv = (float)bits_to_h(a.x[(size_t)m * K + a.cols[p0 + e]]);
+          wv = (float)bits_to_h(a.vals[p0 + e]);
+        }
+        v = __builtin_fmaf(xv, wv, v);
+      }
+      if (a.bias) v += (float)bits_to_h(a.bias[n]);
+      a.y[(size_t)m * N + n] = h_to_bits(rn_h(v));
     }
-    if (threadIdx.x == 0) a.counters[col] = 0;  // every ticket of this tile is in: reset for the next call
-  }
-
-#pragma unroll
-  for (int q = 0; q < R; q++) {
-    const int o = threadIdx.x + 256 * q;
-    const int r = o >> 8;
-    const int l = (o & 255) >> 2;
-    const int i = o & 3;
-    const int m = 4 * (l >> 4) + i;
-    const int n = n0 + 16 * r + (l & 15);
-    if (m < a.M && n < a.N) store_out(a, m, n, v[q]);
   }
 }
 
@@ -204,11 +259,16 @@ __global__ __launch_bounds__(256) void qlinear_skinny_kernel(QLArgs a) {
 constexpr int BM = 128, BN = 128, BK = 64;
 constexpr int APAD = 8;   // halves of padding per LDS row of the x tile
 constexpr int BPAD = 16;  // bytes of padding per LDS row of the code tile
+constexpr int kTileCsrCap = 4096;
 
 template <int FMT>
 __global__ __launch_bounds__(256) void qlinear_gemm_kernel(QLArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t As[BM][BK + APAD];
   __shared__ __attribute__((aligned(16))) uint8_t Bs[BN][BK + BPAD];
+  __shared__ int s_rp[BN + 1];
+  __shared__ int s_col[kTileCsrCap];
+  __shared__ uint16_t s_val[kTileCsrCap];
+
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
@@ -216,6 +276,33 @@ __global__ __launch_bounds__(256) void qlinear_gemm_kernel(QLArgs a) {
   const int li = lane & 15;
   const int bm = blockIdx.y, bn = blockIdx.x;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int M = a.M, K = a.K, N = a.N;
+  const int nbase = bn * BN;
+
+  // outlier lists of this tile's 128 output columns
+  if (t <= BN) s_rp[t] = a.row_ptr[min(nbase + t, N)];
+  __syncthreads();
+  const int p0 = s_rp[0];
+  const int cnt = min(s_rp[BN] - p0, kTileCsrCap);
+  for (int e = t; e < cnt; e += 256) {
+    s_col[e] = a.cols[p0 + e];
+    s_val[e] = a.vals[p0 + e];
+  }
+  int eptr[4], eend[4];
+#pragma unroll
+  for (int ni = 0; ni < 4; ni++) {
+    const int nl = wn + 16 * ni + li;
+    eptr[ni] = s_rp[nl] - p0;
+    eend[ni] = min(s_rp[nl + 1] - p0, cnt);
+  }
+
+  // per-output-channel scales are loaded once
+  half2v srow[4];
+#pragma unroll
+  for (int ni = 0; ni < 4; ni++) {
+    const int gn = nbase + wn + 16 * ni + li;
+    srow[ni] = scale_pair<FMT>((a.kg == 1 && gn < N) ? a.scales[gn] : (uint16_t)0);
+  }
 
   float4v acc[4][4];
 #pragma unroll
@@ -223,40 +310,60 @@ __global__ __launch_bounds__(256) void qlinear_gemm_kernel(QLArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
 
-  for (int k0 = 0; k0 < a.K; k0 += BK) {
+  uint4 ra[4], rb[2];
+  auto load_tiles = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {  // x tile: 128 rows x 8 uint4
       const int idx = t + 256 * i;
       const int row = idx >> 3, c8 = idx & 7;
       const int gm = bm * BM + row, gk = k0 + 8 * c8;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (gm < a.M && gk < a.K) v = *reinterpret_cast<const uint4*>(a.x + (size_t)gm * a.K + gk);
-      *reinterpret_cast<uint4*>(&As[row][8 * c8]) = v;
+      ra[i] = make_uint4(0, 0, 0, 0);
+      if (gm < M && gk < K) ra[i] = *reinterpret_cast<const uint4*>(a.x + (size_t)gm * K + gk);
     }
 #pragma unroll
     for (int i = 0; i < 2; i++) {  // code tile: 128 rows x 4 uint4
       const int idx = t + 256 * i;
       const int row = idx >> 2, c16 = idx & 3;
-      const int gn = bn * BN + row, gk = k0 + 16 * c16;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (gn < a.N && gk < a.K) v = *reinterpret_cast<const uint4*>(a.codes + (size_t)gn * a.K + gk);
-      *reinterpret_cast<uint4*>(&Bs[row][16 * c16]) = v;
+      const int gn = nbase + row, gk = k0 + 16 * c16;
+      rb[i] = make_uint4(0, 0, 0, 0);
+      if (gn < N && gk < K) rb[i] = ld_nt16(a.codes + (size_t)gn * K + gk);
     }
+  };
+  auto store_tiles = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int idx = t + 256 * i;
+      *reinterpret_cast<uint4*>(&As[idx >> 3][8 * (idx & 7)]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int idx = t + 256 * i;
+      *reinterpret_cast<uint4*>(&Bs[idx >> 2][16 * (idx & 3)]) = rb[i];
+    }
+  };
+
+  load_tiles(0);
+  for (int k0 = 0; k0 < K; k0 += BK) {
+    __syncthreads();  // the previous step's LDS reads are done (and the CSR staging, first time)
+    store_tiles();
     __syncthreads();
+    if (k0 + BK < K) load_tiles(k0 + BK);  // in flight while this step computes
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ks++) {
       const int kq = ks * 32 + 8 * grp;
       half8 af[4], bf[4];
 #pragma unroll
       for (int mi = 0; mi < 4; mi++) af[mi] = *reinterpret_cast<const half8*>(&As[wm + 16 * mi + li][kq]);
-      const int gk = k0 + ks * 32;
 #pragma unroll
       for (int ni = 0; ni < 4; ni++) {
         const int nl = wn + 16 * ni + li;
-        const int gn = bn * BN + nl;
         const uint2 cw = *reinterpret_cast<const uint2*>(&Bs[nl][kq]);
-        const uint16_t sb = (gn < a.N && gk < a.K) ? a.scales[(size_t)gn * a.kg + gk / a.G] : (uint16_t)0;
-        bf[ni] = deq8<FMT>(cw.x, cw.y, scale_pair<FMT>(sb));
+        half2v s2 = srow[ni];
+        if (a.kg != 1) {
+          const int gn = nbase + nl, gk = k0 + ks * 32;
+          s2 = scale_pair<FMT>((gn < N && gk < K) ? a.scales[scale_index(a, gn, gk)] : (uint16_t)0);
+        }
+        bf[ni] = deq8<FMT>(cw.x, cw.y, s2);
       }
 #pragma unroll
       for (int mi = 0; mi < 4; mi++)
@@ -264,78 +371,77 @@ __global__ __launch_bounds__(256) void qlinear_gemm_kernel(QLArgs a) {
         for (int ni = 0; ni < 4; ni++)
           acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mi], bf[ni], acc[mi][ni], 0, 0, 0);
     }
-    __syncthreads();
+    // outliers whose column lies in [k0, k0 + BK): x from the LDS tile
+#pragma unroll
+    for (int ni = 0; ni < 4; ni++) {
+      while (eptr[ni] < eend[ni] && s_col[eptr[ni]] < k0 + BK) {
+        const int c = s_col[eptr[ni]] - k0;
+        const float v = (float)bits_to_h(s_val[eptr[ni]]);
+#pragma unroll
+        for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            acc[mi][ni][i] = __builtin_fmaf((float)bits_to_h(As[wm + 16 * mi + 4 * grp + i][c]), v, acc[mi][ni][i]);
+        eptr[ni]++;
+      }
+    }
   }
 
+  const bool overflow = (s_rp[BN] - p0) > kTileCsrCap;
 #pragma unroll
-  for (int mi = 0; mi < 4; mi++)
+  for (int ni = 0; ni < 4; ni++) {
+    const int nl = wn + 16 * ni + li;
+    const int n = nbase + nl;
+    if (n >= N) continue;
+    const float bv = a.bias ? (float)bits_to_h(a.bias[n]) : 0.0f;
 #pragma unroll
-    for (int ni = 0; ni < 4; ni++)
+    for (int mi = 0; mi < 4; mi++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int m = bm * BM + wm + 16 * mi + 4 * grp + i;
-        const int n = bn * BN + wn + 16 * ni + li;
-        if (m < a.M && n < a.N) store_out(a, m, n, acc[mi][ni][i]);
+        if (m >= M) continue;
+        float v = acc[mi][ni][i];
+        if (overflow) {  // entries past the staging capacity: from memory
+          for (int p = max(p0 + cnt, s_rp[nl]); p < s_rp[nl + 1]; p++)
+            v = __builtin_fmaf((float)bits_to_h(a.x[(size_t)m * K + a.cols[p]]), (float)bits_to_h(a.vals[p]), v);
+        }
+        a.y[(size_t)m * N + n] = h_to_bits(rn_h(v + bv));
       }
+  }
 }
 
-constexpr int kSkinnyR = 2;
-// Workspace of the skinny kernel: the split-K tickets first, at a fixed
-// offset, so that every call finds them at zero whatever the previous call's
-// shape was (each call resets the tickets it used); the partial tiles after.
-constexpr int64_t kMaxTickets = 65536;
-constexpr int64_t kTicketBytes = kMaxTickets * 4;
-
-struct SkinnyPlan {
-  int ncol, SK, cps;
-};
-
-SkinnyPlan plan_skinny(int64_t N, int64_t K) {
-  SkinnyPlan p;
-  p.ncol = (int)aq::ceil_div(N, 16 * kSkinnyR);
-  const int nchunks = (int)aq::ceil_div(K, 128);
-  // enough workgroups to cover the 256 CUs several times, each split keeping
-  // at least one 128-wide chunk per wave
-  int sk = (int)aq::ceil_div(1024, p.ncol);
-  sk = std::min(sk, std::max(1, nchunks / 4));
-  sk = std::max(sk, 1);
-  if (p.ncol > kMaxTickets) sk = 1;
-  p.cps = (int)aq::ceil_div(nchunks, sk);
-  p.SK = (int)aq::ceil_div(nchunks, p.cps);
-  return p;
-}
-
-int64_t skinny_ws_bytes(int64_t N, int64_t K) {
-  SkinnyPlan p = plan_skinny(N, K);
-  if (p.SK <= 1) return 256;
-  return kTicketBytes + (int64_t)p.ncol * p.SK * kSkinnyR * 256 * 4;
+int log2_exact(int64_t g) {
+  if (g <= 0 || (g & (g - 1))) return -1;
+  int s = 0;
+  while ((int64_t(1) << s) < g) s++;
+  return s;
 }
 
 }  // namespace
 
 extern "C" int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
-  if (M <= 16) return skinny_ws_bytes(N, K);
-  return 256;
+  (void)M;
+  (void)N;
+  (void)K;
+  return 0;  // the kernels need no memory beyond LDS
 }
 
 extern "C" int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const void* codes, const void* scales,
                           int64_t G, int fmt, const int32_t* row_ptr, const int32_t* cols, const void* vals,
                           const void* bias, void* y, void* workspace, int64_t ws_bytes, void* stream) {
+  (void)workspace;
+  (void)ws_bytes;
   AQ_CHECK_ARG(M >= 0 && K >= 1 && N >= 1, "aq_qlinear: bad sizes M=%lld K=%lld N=%lld", (long long)M,
                (long long)K, (long long)N);
   AQ_CHECK_ARG(G >= 32 && G % 32 == 0 && K % G == 0,
                "aq_qlinear: block size %lld must be a multiple of 32 that divides K=%lld", (long long)G,
                (long long)K);
   AQ_CHECK_ARG(fmt == AQ_FMT_INT8 || fmt == AQ_FMT_E4M3, "aq_qlinear: unknown code format %d", fmt);
-  AQ_CHECK_ARG(M < (1 << 30) && N < (1 << 30) && K < (1 << 30), "aq_qlinear: dimension too large");
+  AQ_CHECK_ARG(M < (1 << 30) && N < (1 << 30) && K < (1 << 30) && (int64_t)N * K < ((int64_t)1 << 40),
+               "aq_qlinear: dimension too large");
   if (M == 0) return AQ_OK;
   AQ_CHECK_ARG(x && codes && scales && row_ptr && y, "aq_qlinear: null pointer argument");
   AQ_CHECK_ARG((uintptr_t)x % 16 == 0 && (uintptr_t)codes % 16 == 0, "aq_qlinear: x and codes must be 16-byte aligned");
-  const int64_t need = aq_qlinear_workspace_size(M, N, K);
-  if (ws_bytes < need)
-    return aq::set_error(AQ_EWORKSPACE, "aq_qlinear: workspace of %lld bytes, %lld needed", (long long)ws_bytes,
-                         (long long)need);
   QLArgs a;
   a.x = (const uint16_t*)x;
   a.M = (int)M;
@@ -345,31 +451,20 @@ extern "C" int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const 
   a.scales = (const uint16_t*)scales;
   a.G = (int)G;
   a.kg = (int)(K / G);
+  a.gshift = log2_exact(G);
   a.row_ptr = row_ptr;
   a.cols = cols;
   a.vals = (const uint16_t*)vals;
   a.bias = (const uint16_t*)bias;
   a.y = (uint16_t*)y;
-  a.part = nullptr;
-  a.counters = nullptr;
-  a.SK = 1;
-  a.cps = 0;
   hipStream_t s = (hipStream_t)stream;
   if (M <= 16) {
-    SkinnyPlan p = plan_skinny(N, K);
-    a.SK = p.SK;
-    a.cps = p.cps;
-    if (p.SK > 1) {
-      AQ_CHECK_ARG(workspace, "aq_qlinear: null workspace");
-      a.counters = (int32_t*)workspace;
-      a.part = (float*)((char*)workspace + kTicketBytes);
-    }
-    const dim3 grid((unsigned)(p.ncol * p.SK));
+    const dim3 grid((unsigned)aq::ceil_div(N, 16));
     if (fmt == AQ_FMT_E4M3)
-      hipLaunchKernelGGL((qlinear_skinny_kernel<kSkinnyR, AQ_FMT_E4M3>), grid, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((qlinear_gemv_kernel<AQ_FMT_E4M3>), grid, dim3(64 * (kGemvStream + 1)), 0, s, a);
     else
-      hipLaunchKernelGGL((qlinear_skinny_kernel<kSkinnyR, AQ_FMT_INT8>), grid, dim3(256), 0, s, a);
-    AQ_LAUNCH_CHECK("aq_qlinear: skinny launch");
+      hipLaunchKernelGGL((qlinear_gemv_kernel<AQ_FMT_INT8>), grid, dim3(64 * (kGemvStream + 1)), 0, s, a);
+    AQ_LAUNCH_CHECK("aq_qlinear: gemv launch");
     return AQ_OK;
   }
   const dim3 grid((unsigned)aq::ceil_div(N, BN), (unsigned)aq::ceil_div(M, BM));

@@ -126,10 +126,8 @@ int aq_zscore(const void* x, int64_t n, float eps, void* z, void* stats, void* s
  *   G must divide K and be a multiple of 32.
  * M <= 16 runs the dequant-GEMV, larger M the dequant-GEMM; both add the
  * outliers from the CSR lists in an fp32 epilogue.
- * workspace: >= aq_qlinear_workspace_size(M, N, K) bytes.  Its first 256 KiB
- * hold split-K tickets and must be zero before the first call; every call
- * leaves them at zero again.  Calls that share a workspace must not overlap
- * (use one workspace per stream).
+ * workspace: >= aq_qlinear_workspace_size(M, N, K) bytes (currently 0: the
+ * kernels keep their partial sums in LDS; NULL is accepted).
  */
 int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K);
 int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const void* codes, const void* scales,

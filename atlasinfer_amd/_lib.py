@@ -22,6 +22,10 @@ ABI_VERSION = 1
 FMT_INT8 = 0
 FMT_E4M3 = 1
 FORMATS = {"int8": FMT_INT8, "e4m3": FMT_E4M3}
+LAYOUT_FLAT = 0
+LAYOUT_TILED = 1
+LAYOUTS = {"flat": LAYOUT_FLAT, "tiled": LAYOUT_TILED}
+MAX_GROUP = 4
 
 # every function the header declares: name -> (restype, argtypes)
 _P = ctypes.c_void_p
@@ -32,18 +36,29 @@ SIGNATURES = {
     "aq_last_error": (ctypes.c_char_p, []),
     "aq_max_block_size": (_I64, []),
     "aq_quantize_workspace_size": (_I64, [_I64, _I64]),
-    "aq_quantize": (ctypes.c_int, [_P, _I64, _I64, ctypes.c_uint16, ctypes.c_int, _P, _P, _I32P, _P, _I64, _P]),
+    "aq_quantize": (ctypes.c_int, [_P, _I64, _I64, ctypes.c_uint16, ctypes.c_int, _I64, ctypes.c_int, _P, _P, _I32P,
+                                   _P, _I64, _P]),
     "aq_quantize_finish": (ctypes.c_int, [_I64, _I64, _I64, _I32P, _I64, _P, _I64, _P, _P, _I32P, _P]),
     "aq_segment_offsets": (ctypes.c_int, [_P, _I64, _I64, _I64, _I32P, _P]),
     "aq_outlier_cols": (ctypes.c_int, [_P, _I64, _I64, _I32P, _P]),
     "aq_compact_codes": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P]),
     "aq_expand_codes": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P]),
-    "aq_dequantize": (ctypes.c_int, [_P, _P, _I64, _I64, ctypes.c_int, _P, _P, _I64, _P, _P]),
+    "aq_tile_codes": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
+    "aq_untile_codes": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
+    "aq_dequantize": (ctypes.c_int, [_P, _P, _I64, _I64, ctypes.c_int, _I64, ctypes.c_int, _P, _P, _I64, _P, _P]),
     "aq_zscore": (ctypes.c_int, [_P, _I64, ctypes.c_float, _P, _P, _P]),
     "aq_qlinear_workspace_size": (_I64, [_I64, _I64, _I64]),
     "aq_qlinear": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, _I64, ctypes.c_int, _I32P, _I32P, _P, _P, _P, _P,
                                   _I64, _P]),
+    "aq_qlinear_grouped": (ctypes.c_int, [_P, _I64, _I64, ctypes.c_int, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                          _P]),
 }
+
+
+def ptr_array(values, ctype=ctypes.c_void_p):
+    """A host array of pointers / ints for the grouped entry points."""
+    return (ctype * len(values))(*values)
+
 
 _lib = None
 _lock = threading.Lock()
@@ -100,17 +115,3 @@ def compute_device(preferred: torch.device | None = None) -> torch.device:
     if not torch.cuda.is_available():
         raise AQError("atlasinfer_amd needs a HIP (MI355X) device; none is visible")
     return torch.device("cuda", torch.cuda.current_device())
-
-
-_ws_cache: dict = {}
-
-
-def workspace(device: torch.device, nbytes: int, kind: str) -> torch.Tensor:
-    """A zero-initialised byte buffer per (device, kind), grown on demand.
-    The kernels that keep counters in it leave them at zero when they end."""
-    key = (device.index, kind)
-    buf = _ws_cache.get(key)
-    if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
-        _ws_cache[key] = buf
-    return buf

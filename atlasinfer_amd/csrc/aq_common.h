@@ -42,6 +42,19 @@ __device__ __forceinline__ uint4 ld_nt16(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// ------------------------------------------------------------ tiled codes
+// Code layout read by the quantized-linear kernels: W[N, K] (N % 16 == 0,
+// K % 128 == 0) is cut into tiles of 16 rows x 128 columns, 2 KiB each,
+// stored tile-row by tile-row.  Inside a tile, byte h*1024 + (g*16 + r)*16 + e
+// holds column 64*h + 16*g + e of tile row r: a wave that loads 16 bytes per
+// lane at tile + lane*16 (and + 1024) receives, in lane g*16 + r, exactly the
+// 16x16x32 MFMA B-operand pieces of row r, and each load instruction reads
+// 1 KiB of contiguous memory.
+__host__ __device__ __forceinline__ int64_t tiled_offset(int64_t n, int64_t k, int64_t nchunks) {
+  return ((((n >> 4) * nchunks + (k >> 7)) << 11) | (((k >> 6) & 1) << 10) | (((k >> 4) & 3) << 8) |
+          ((n & 15) << 4) | (k & 15));
+}
+
 // ------------------------------------------------------------- fp16 helpers
 
 __device__ __forceinline__ f16 bits_to_h(uint16_t b) { return __builtin_bit_cast(f16, b); }

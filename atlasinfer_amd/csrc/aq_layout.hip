@@ -80,14 +80,33 @@ __global__ __launch_bounds__(256) void reorder_codes_kernel(const uint8_t* src, 
   }
 }
 
+// Flat <-> tiled: one thread moves one 16-byte piece (16 consecutive codes of
+// a row occupy 16 consecutive bytes in both layouts).
+template <int TO_TILED>
+__global__ __launch_bounds__(256) void retile_kernel(const uint8_t* src, int64_t N, int64_t K, uint8_t* dst) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p * 16 >= N * K) return;
+  const int64_t j = p * 16;
+  const int64_t t = tiled_offset(j / K, j % K, K / 128);
+  if (TO_TILED)
+    *reinterpret_cast<uint4*>(dst + t) = *reinterpret_cast<const uint4*>(src + j);
+  else
+    *reinterpret_cast<uint4*>(dst + j) = *reinterpret_cast<const uint4*>(src + t);
+}
+
 template <int FMT>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* codes, const uint16_t* scales, int64_t numel,
-                                                      int64_t G, uint16_t* out, int vec) {
+                                                      int64_t G, uint16_t* out, int vec, int tiled, int64_t K) {
   const int64_t j0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 16;
   if (j0 >= numel) return;
   uint8_t c[16];
   const bool full = vec && (j0 + 16 <= numel);
-  if (full) {
+  if (tiled) {  // numel is a multiple of 16 K here
+    uint4 u = *reinterpret_cast<const uint4*>(codes + tiled_offset(j0 / K, j0 % K, K / 128));
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 16; k++) c[k] = (uint8_t)(w[k / 4] >> (8 * (k % 4)));
+  } else if (full) {
     uint4 u = *reinterpret_cast<const uint4*>(codes + j0);
     uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -184,21 +203,52 @@ extern "C" int aq_expand_codes(const void* compact, int64_t padded, const int64_
   return reorder(1, compact, padded, flat_idx, nnz, dense, stream, "aq_expand_codes");
 }
 
-extern "C" int aq_dequantize(const void* codes, const void* scales, int64_t numel, int64_t G, int fmt,
-                             const int64_t* flat_idx, const void* vals, int64_t nnz, void* out, void* stream) {
+static int retile(int to_tiled, const void* src, int64_t N, int64_t K, void* dst, void* stream, const char* name) {
+  AQ_CHECK_ARG(N >= 0 && K >= 128 && N % 16 == 0 && K % 128 == 0,
+               "%s: needs N %% 16 == 0 and K %% 128 == 0 (N=%lld, K=%lld)", name, (long long)N, (long long)K);
+  if (N == 0) return AQ_OK;
+  AQ_CHECK_ARG(src && dst && (uintptr_t)src % 16 == 0 && (uintptr_t)dst % 16 == 0,
+               "%s: null or unaligned pointer", name);
+  const int64_t grid = aq::ceil_div(N * K / 16, 256);
+  if (to_tiled)
+    hipLaunchKernelGGL((retile_kernel<1>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)src, N, K, (uint8_t*)dst);
+  else
+    hipLaunchKernelGGL((retile_kernel<0>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)src, N, K, (uint8_t*)dst);
+  AQ_LAUNCH_CHECK(name);
+  return AQ_OK;
+}
+
+extern "C" int aq_tile_codes(const void* flat, int64_t N, int64_t K, void* tiled, void* stream) {
+  return retile(1, flat, N, K, tiled, stream, "aq_tile_codes");
+}
+
+extern "C" int aq_untile_codes(const void* tiled, int64_t N, int64_t K, void* flat, void* stream) {
+  return retile(0, tiled, N, K, flat, stream, "aq_untile_codes");
+}
+
+extern "C" int aq_dequantize(const void* codes, const void* scales, int64_t numel, int64_t G, int fmt, int64_t K,
+                             int layout, const int64_t* flat_idx, const void* vals, int64_t nnz, void* out,
+                             void* stream) {
   AQ_CHECK_ARG(numel >= 0 && G >= 1 && nnz >= 0, "aq_dequantize: bad sizes");
   AQ_CHECK_ARG(fmt == AQ_FMT_INT8 || fmt == AQ_FMT_E4M3, "aq_dequantize: unknown code format %d", fmt);
+  AQ_CHECK_ARG(layout == AQ_LAYOUT_FLAT || layout == AQ_LAYOUT_TILED, "aq_dequantize: unknown layout %d", layout);
   if (numel == 0) return AQ_OK;
   AQ_CHECK_ARG(codes && scales && out && (nnz == 0 || (flat_idx && vals)), "aq_dequantize: null pointer argument");
+  const int tiled = layout == AQ_LAYOUT_TILED;
+  if (tiled)
+    AQ_CHECK_ARG(K >= 128 && K % 128 == 0 && numel % (16 * K) == 0 && (uintptr_t)codes % 16 == 0,
+                 "aq_dequantize: tiled codes need K %% 128 == 0 and rows %% 16 == 0");
   hipStream_t s = (hipStream_t)stream;
   const int vec = ((uintptr_t)codes % 16 == 0) && ((uintptr_t)out % 16 == 0);
   const int64_t grid = aq::ceil_div(numel, 256 * 16);
   if (fmt == AQ_FMT_INT8)
     hipLaunchKernelGGL((dequant_kernel<AQ_FMT_INT8>), dim3((unsigned)grid), dim3(256), 0, s, (const uint8_t*)codes,
-                       (const uint16_t*)scales, numel, G, (uint16_t*)out, vec);
+                       (const uint16_t*)scales, numel, G, (uint16_t*)out, vec, tiled, K);
   else
     hipLaunchKernelGGL((dequant_kernel<AQ_FMT_E4M3>), dim3((unsigned)grid), dim3(256), 0, s, (const uint8_t*)codes,
-                       (const uint16_t*)scales, numel, G, (uint16_t*)out, vec);
+                       (const uint16_t*)scales, numel, G, (uint16_t*)out, vec, tiled, K);
   AQ_LAUNCH_CHECK("aq_dequantize: launch");
   if (nnz > 0) {
     hipLaunchKernelGGL(scatter_outliers_kernel, dim3((unsigned)aq::ceil_div(nnz, 256)), dim3(256), 0, s, flat_idx,

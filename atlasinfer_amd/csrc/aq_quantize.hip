@@ -38,6 +38,9 @@ struct QuantArgs {
   uint16_t thr_bits;
   int fmt;
   int vec;  // G % 16 == 0 and x 16-byte aligned: 16-byte loads/stores
+  int tiled;        // codes in the tiled layout (rows of K, K % 128 == 0, N % 16 == 0)
+  int64_t K;        // row length for the tiled layout
+  int64_t nchunks;  // K / 128
   uint8_t* codes;
   uint16_t* scales;
   int32_t* block_cnt;  // block_off, holds counts until the scan
@@ -228,7 +231,6 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
   }
   if (gvalid) {
     if (a.vec && i0 + E <= G) {
-      uint4* dst = reinterpret_cast<uint4*>(a.codes + base + i0);
 #pragma unroll
       for (int v = 0; v < E / 16; v++) {
         uint32_t w[4];
@@ -236,12 +238,19 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
         for (int k = 0; k < 4; k++)
           w[k] = (uint32_t)c[v * 16 + 4 * k] | ((uint32_t)c[v * 16 + 4 * k + 1] << 8) |
                  ((uint32_t)c[v * 16 + 4 * k + 2] << 16) | ((uint32_t)c[v * 16 + 4 * k + 3] << 24);
-        dst[v] = make_uint4(w[0], w[1], w[2], w[3]);
+        // 16 consecutive elements of one row land in 16 consecutive bytes of
+        // either layout
+        const int64_t j = base + i0 + 16 * v;
+        const int64_t off = a.tiled ? tiled_offset(j / a.K, j % a.K, a.nchunks) : j;
+        *reinterpret_cast<uint4*>(a.codes + off) = make_uint4(w[0], w[1], w[2], w[3]);
       }
     } else {
 #pragma unroll
       for (int e = 0; e < E; e++)
-        if (i0 + e < G) a.codes[base + i0 + e] = c[e];
+        if (i0 + e < G) {
+          const int64_t j = base + i0 + e;
+          a.codes[a.tiled ? tiled_offset(j / a.K, j % a.K, a.nchunks) : j] = c[e];
+        }
     }
   }
 
@@ -429,13 +438,20 @@ extern "C" int64_t aq_quantize_workspace_size(int64_t numel, int64_t G) {
   return workspace_bytes(nblocks * G, nblocks);
 }
 
-extern "C" int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_thr_f16, int fmt, void* codes,
-                           void* scales, int32_t* block_off, void* workspace, int64_t ws_bytes, void* stream) {
+extern "C" int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_thr_f16, int fmt, int64_t K,
+                           int layout, void* codes, void* scales, int32_t* block_off, void* workspace, int64_t ws_bytes,
+                           void* stream) {
   AQ_CHECK_ARG(numel > 0, "aq_quantize: numel must be > 0 (got %lld)", (long long)numel);
   AQ_CHECK_ARG(G >= 1 && G <= kMaxG, "aq_quantize: block size %lld outside [1, %lld]", (long long)G,
                (long long)kMaxG);
   AQ_CHECK_ARG(fmt == AQ_FMT_INT8 || fmt == AQ_FMT_E4M3, "aq_quantize: unknown code format %d", fmt);
   AQ_CHECK_ARG(x && codes && scales && block_off && workspace, "aq_quantize: null pointer argument");
+  AQ_CHECK_ARG(layout == AQ_LAYOUT_FLAT || layout == AQ_LAYOUT_TILED, "aq_quantize: unknown layout %d", layout);
+  if (layout == AQ_LAYOUT_TILED)
+    AQ_CHECK_ARG(K >= 128 && K % 128 == 0 && numel % (16 * K) == 0 && G % 16 == 0 && K % G == 0,
+                 "aq_quantize: the tiled layout needs K %% 128 == 0, rows %% 16 == 0 and a block dividing K "
+                 "(K=%lld, numel=%lld, G=%lld)",
+                 (long long)K, (long long)numel, (long long)G);
   const int64_t nblocks = aq::ceil_div(numel, G);
   const int64_t padded = nblocks * G;
   if (padded >= (int64_t)1 << 31)
@@ -453,6 +469,9 @@ extern "C" int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_t
   a.thr_bits = z_thr_f16;
   a.fmt = fmt;
   a.vec = (G % 16 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)codes % 16 == 0);
+  a.tiled = layout == AQ_LAYOUT_TILED;
+  a.K = K;
+  a.nchunks = K / 128;
   a.codes = (uint8_t*)codes;
   a.scales = (uint16_t*)scales;
   a.block_cnt = block_off;

@@ -10,12 +10,14 @@ any leading dimensions, the same ``extra_repr``.
 The reference's forward dequantizes the whole weight to fp16 (cached) and
 calls F.linear (:56,67).  Here forward is one launch of the fused
 dequant-GEMV / dequant-GEMM (``aq_qlinear``): the codes are decoded in
-registers and never written back as fp16.  Blocks that do not tile the rows
-(block size not a multiple of 32 dividing in_features) take the
-dequantize kernel followed by F.linear on the GPU.
+registers and never written back as fp16.  Weights that do not tile
+(out_features % 16, in_features % 128, or a block size that is not a
+multiple of 32 dividing in_features) take the dequantize kernel followed by
+F.linear on the GPU.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
@@ -23,13 +25,53 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .. import _lib
-from ..quant.adaptive_quantizer import QuantizedTensor, dense_codes, dequantize_tensor, _format_id
+from ..quant.adaptive_quantizer import (QuantizedTensor, _format_id, _rows_cols, dequantize_tensor, kernel_codes,
+                                        tiled_eligible)
+
+
+def fused_supported(qt: QuantizedTensor) -> bool:
+    """The fused kernels need 16-row x 128-column tiles and blocks of a
+    multiple of 32 that divide the row."""
+    return qt.outlier_row_ptr is not None and tiled_eligible(qt.original_shape, qt.block_size)
+
+
+def qlinear_grouped(x: torch.Tensor, qts, biases=None, codes=None):
+    """[x W_i^T + b_i for each quantized W_i] in one launch; all W_i share
+    in_features (aq_qlinear_grouped).  ``codes`` may carry the tiled code
+    arrays (saves re-tiling int8 weights per call)."""
+    dev = x.device
+    L = _lib.load()
+    n = len(qts)
+    if not 1 <= n <= _lib.MAX_GROUP:
+        raise ValueError(f"1..{_lib.MAX_GROUP} weights per grouped call, got {n}")
+    K = int(qts[0].original_shape[-1])
+    fmt = qts[0].code_format
+    for q in qts:
+        if int(q.original_shape[-1]) != K or q.code_format != fmt or not fused_supported(q):
+            raise ValueError("grouped weights must share in_features and code format and tile")
+    biases = list(biases) if biases is not None else [None] * n
+    codes = list(codes) if codes is not None else [kernel_codes(q, dev) for q in qts]
+    x2 = x.reshape(-1, K)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    Ns = [_rows_cols(q.original_shape)[0] for q in qts]
+    ys = [torch.empty((M, N), dtype=torch.float16, device=dev) for N in Ns]
+    if M > 0:
+        arr = _lib.ptr_array
+        _lib.check(L.aq_qlinear_grouped(
+            x2.data_ptr(), M, K, _format_id(fmt), n, arr(Ns, ctypes.c_int64), arr([c.data_ptr() for c in codes]),
+            arr([q.scale_factors.data_ptr() for q in qts]), arr([q.block_size for q in qts], ctypes.c_int64),
+            arr([q.outlier_row_ptr.data_ptr() for q in qts]), arr([_lib.ptr(q.outlier_cols) for q in qts]),
+            arr([_lib.ptr(q.fp16_outliers) for q in qts]), arr([_lib.ptr(b) for b in biases]),
+            arr([y.data_ptr() for y in ys]), _lib.stream_of(dev)), "aq_qlinear_grouped")
+    return [y.view(*x.shape[:-1], N) for y, N in zip(ys, Ns)]
 
 
 def qlinear(x: torch.Tensor, qt: QuantizedTensor, bias: Optional[torch.Tensor],
             codes: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y = x W^T + b for W in quantized form, through aq_qlinear.  ``codes``
-    may carry the dense code array (saves the int8 expansion per call)."""
+    may carry the tiled code array."""
     dev = x.device
     K = int(qt.original_shape[-1])
     N = qt.original_shape.numel() // K
@@ -41,21 +83,13 @@ def qlinear(x: torch.Tensor, qt: QuantizedTensor, bias: Optional[torch.Tensor],
     if M == 0:
         return y.view(*x.shape[:-1], N)
     if codes is None:
-        codes = dense_codes(qt, dev)
+        codes = kernel_codes(qt, dev)
     L = _lib.load()
-    ws_bytes = int(L.aq_qlinear_workspace_size(M, N, K))
-    ws = _lib.workspace(dev, ws_bytes, "qlinear")
     _lib.check(L.aq_qlinear(x2.data_ptr(), M, K, N, codes.data_ptr(), qt.scale_factors.data_ptr(), qt.block_size,
                             _format_id(qt.code_format), qt.outlier_row_ptr.data_ptr(), _lib.ptr(qt.outlier_cols),
-                            _lib.ptr(qt.fp16_outliers), _lib.ptr(bias), y.data_ptr(), ws.data_ptr(), ws.numel(),
+                            _lib.ptr(qt.fp16_outliers), _lib.ptr(bias), y.data_ptr(), None, 0,
                             _lib.stream_of(dev)), "aq_qlinear")
     return y.view(*x.shape[:-1], N)
-
-
-def fused_supported(qt: QuantizedTensor) -> bool:
-    K = int(qt.original_shape[-1]) if len(qt.original_shape) else 0
-    G = qt.block_size
-    return (K > 0 and G >= 32 and G % 32 == 0 and K % G == 0 and qt.outlier_row_ptr is not None)
 
 
 class QuantizedLinear(nn.Module):
@@ -66,7 +100,7 @@ class QuantizedLinear(nn.Module):
         self.quantized_weights = quantized_weights
         self.bias = bias
         self.original_shape = getattr(quantized_weights, "original_shape", None)
-        self._codes = None  # dense codes on the compute device (int8 format: expanded once)
+        self._codes = None  # tiled codes on the compute device (int8: expanded and tiled once)
 
     def _weights_on(self, device: torch.device) -> QuantizedTensor:
         q = self.quantized_weights
@@ -93,7 +127,7 @@ class QuantizedLinear(nn.Module):
         if not fused_supported(q):
             return F.linear(x, dequantize_tensor(q, dev), self.bias)
         if self._codes is None or self._codes.device != dev:
-            self._codes = dense_codes(q, dev)
+            self._codes = kernel_codes(q, dev)
         return qlinear(x, q, self.bias, self._codes)
 
     def _apply(self, fn, recurse=True):

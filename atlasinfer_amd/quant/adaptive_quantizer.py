@@ -6,8 +6,8 @@ under that name, ``atlasinfer_core.quant.adaptive_quantizer``):
 
 * ``QuantizedTensor``          (reference :8-42) -- the six reference fields in
   order, plus trailing fields with defaults: ``code_format``,
-  ``outlier_row_ptr`` (CSR row pointer, int32 [N+1]) and ``outlier_cols``
-  (int32 [nnz]).
+  ``outlier_row_ptr`` (CSR row pointer, int32 [N+1]), ``outlier_cols``
+  (int32 [nnz]) and ``code_layout``.
 * ``calculate_zscore_manual``  (reference :44-49)
 * ``quantize_tensor``          (reference :51-148)
 * ``dequantize_tensor``        (reference :156-251)
@@ -22,8 +22,11 @@ Code formats:
   int8 codes of the non-outliers only, in element order.
 * ``"e4m3"`` (default) -- OCP FP8 E4M3 codes computed by the same op
   sequence with 448 in place of 127; ``fp8_data`` is the dense code array
-  (torch.float8_e4m3fn, one code per element of the zero-padded flat tensor,
-  0 at outliers).
+  (torch.float8_e4m3fn, one code per element, 0 at outliers).  For weights
+  whose rows tile (2-D view [N, K] with N % 16 == 0, K % 128 == 0, blocks of
+  a multiple of 32 dividing K) the codes are stored in the tiled layout the
+  quantized-linear kernels read (``code_layout == "tiled"``: 16 x 128 tiles,
+  see include/atlasinfer_amd.h); ``dense_codes()`` returns element order.
 ``block_size=-1`` selects one block per output channel (block = last dim).
 """
 from __future__ import annotations
@@ -51,6 +54,7 @@ class QuantizedTensor(NamedTuple):
     code_format: str = "int8"
     outlier_row_ptr: Optional[torch.Tensor] = None  # int32 [N + 1] over the last dim
     outlier_cols: Optional[torch.Tensor] = None     # int32 [nnz]
+    code_layout: str = "flat"                       # "flat" (element order) or "tiled"
 
     def to(self, device):
         """Move every tensor to ``device``; returns self when already there
@@ -120,6 +124,24 @@ def calculate_zscore_manual(data: torch.Tensor, eps=1e-6) -> torch.Tensor:
     return z.view(data.shape).to(data.device)
 
 
+def _rows_cols(shape) -> tuple:
+    K = int(shape[-1]) if len(shape) >= 1 else 1
+    numel = 1
+    for d in shape:
+        numel *= int(d)
+    return (numel // K if K else 0), K
+
+
+def tiled_eligible(shape, block_size: int) -> bool:
+    """Whether codes of a weight of this shape can use the tiled layout (and
+    the fused quantized-linear kernels)."""
+    if len(shape) < 2:
+        return False
+    N, K = _rows_cols(shape)
+    G = block_size
+    return N > 0 and N % 16 == 0 and K >= 128 and K % 128 == 0 and G >= 32 and G % 32 == 0 and K % G == 0
+
+
 def _empty(original_shape, block_size, fmt_name, device) -> QuantizedTensor:
     code_dtype = torch.int8 if fmt_name == "int8" else torch.float8_e4m3fn
     n = int(original_shape[0]) if len(original_shape) >= 2 else 1
@@ -170,19 +192,21 @@ def quantize_tensor(
     dev = _lib.compute_device(input_device)
     stream = _lib.stream_of(dev)
     x = fp16_tensor.to(dev).contiguous().view(-1)
-    K = int(original_shape[-1]) if len(original_shape) >= 1 else 1
-    N = numel // K
+    N, K = _rows_cols(original_shape)
     nblocks = (numel + G - 1) // G
     padded = nblocks * G
+    # e4m3 codes go straight into the layout the fused kernels read; int8
+    # codes stay in element order for the reference's compacted stream
+    layout = "tiled" if (fmt == _lib.FMT_E4M3 and tiled_eligible(original_shape, G)) else "flat"
 
     codes = torch.empty(padded, dtype=torch.uint8, device=dev)
     scales = torch.empty(nblocks, dtype=torch.float16, device=dev)
     block_off = torch.empty(nblocks + 1, dtype=torch.int32, device=dev)
     ws_bytes = int(L.aq_quantize_workspace_size(numel, G))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    _lib.check(L.aq_quantize(x.data_ptr(), numel, G, _threshold_bits(z_threshold), fmt, codes.data_ptr(),
-                             scales.data_ptr(), block_off.data_ptr(), ws.data_ptr(), ws_bytes, stream),
-               "aq_quantize")
+    _lib.check(L.aq_quantize(x.data_ptr(), numel, G, _threshold_bits(z_threshold), fmt, K, _lib.LAYOUTS[layout],
+                             codes.data_ptr(), scales.data_ptr(), block_off.data_ptr(), ws.data_ptr(), ws_bytes,
+                             stream), "aq_quantize")
     nnz = int(block_off[nblocks].item())  # the one host sync: sizes the outlier tensors
     flat_idx = torch.empty(nnz, dtype=torch.int64, device=dev)
     vals = torch.empty(nnz, dtype=torch.float16, device=dev)
@@ -210,15 +234,14 @@ def quantize_tensor(
         code_format=code_format,
         outlier_row_ptr=row_ptr,
         outlier_cols=cols,
+        code_layout=layout,
     )
     return qt.to(input_device)
 
 
-def dense_codes(qt: QuantizedTensor, device: torch.device) -> torch.Tensor:
-    """One uint8 code per element of the padded tensor, 0 at outliers (the
-    layout the kernels read), on ``device``.  For int8 this expands the
-    reference's compacted stream."""
-    q = qt.to(device)
+def _stored_codes(q: QuantizedTensor, device: torch.device) -> torch.Tensor:
+    """The dense codes as stored (flat or tiled), expanding the int8
+    compacted stream."""
     numel = q.original_shape.numel()
     G = q.block_size
     padded = (numel + G - 1) // G * G
@@ -230,6 +253,36 @@ def dense_codes(qt: QuantizedTensor, device: torch.device) -> torch.Tensor:
     _lib.check(L.aq_expand_codes(_lib.ptr(q.fp8_data), padded, _lib.ptr(q.outlier_indices), nnz,
                                  dense.data_ptr(), _lib.stream_of(device)), "aq_expand_codes")
     return dense
+
+
+def dense_codes(qt: QuantizedTensor, device: torch.device) -> torch.Tensor:
+    """One uint8 code per element of the padded tensor in element order, 0 at
+    outliers, on ``device`` (expands the int8 stream, untiles tiled codes)."""
+    q = qt.to(device)
+    codes = _stored_codes(q, device)
+    if q.code_layout != "tiled":
+        return codes
+    L = _lib.load()
+    N, K = _rows_cols(q.original_shape)
+    flat = torch.empty_like(codes)
+    _lib.check(L.aq_untile_codes(codes.data_ptr(), N, K, flat.data_ptr(), _lib.stream_of(device)), "aq_untile_codes")
+    return flat
+
+
+def kernel_codes(qt: QuantizedTensor, device: torch.device) -> torch.Tensor:
+    """Codes in the tiled layout the quantized-linear kernels read (a view of
+    fp8_data when it is stored tiled, else a tiled copy)."""
+    q = qt.to(device)
+    if not tiled_eligible(q.original_shape, q.block_size):
+        raise ValueError(f"shape {tuple(q.original_shape)} with block {q.block_size} does not tile")
+    codes = _stored_codes(q, device)
+    if q.code_layout == "tiled":
+        return codes
+    L = _lib.load()
+    N, K = _rows_cols(q.original_shape)
+    tiled = torch.empty_like(codes)
+    _lib.check(L.aq_tile_codes(codes.data_ptr(), N, K, tiled.data_ptr(), _lib.stream_of(device)), "aq_tile_codes")
+    return tiled
 
 
 # --- Dequantization cache (reference :153-154): id(QuantizedTensor) -> fp16 tensor
@@ -262,12 +315,14 @@ def dequantize_tensor(quant_data: QuantizedTensor, target_device: torch.device) 
         dev = _lib.compute_device(target_device)
         q = quant_data.to(dev)
         fmt = _format_id(q.code_format)
-        codes = dense_codes(q, dev)
+        codes = _stored_codes(q, dev)
+        _, K = _rows_cols(q.original_shape)
         out = torch.empty(numel, dtype=torch.float16, device=dev)
         nnz = q.outlier_indices.numel()
-        _lib.check(L.aq_dequantize(codes.data_ptr(), q.scale_factors.data_ptr(), numel, q.block_size, fmt,
-                                   _lib.ptr(q.outlier_indices), _lib.ptr(q.fp16_outliers), nnz, out.data_ptr(),
-                                   _lib.stream_of(dev)), "aq_dequantize")
+        _lib.check(L.aq_dequantize(codes.data_ptr(), q.scale_factors.data_ptr(), numel, q.block_size, fmt, K,
+                                   _lib.LAYOUTS[q.code_layout], _lib.ptr(q.outlier_indices),
+                                   _lib.ptr(q.fp16_outliers), nnz, out.data_ptr(), _lib.stream_of(dev)),
+                   "aq_dequantize")
         final = out.view(q.original_shape).to(target_device)
 
     with _cache_lock:

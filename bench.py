@@ -9,7 +9,8 @@ fp16 outliers (W ~ N(0, 0.02), 0.1% entries +-U(8,20)*0.02; x ~ N(0,1) with
 rotated so the 256 MB MALL cannot hold them.
 
 One step = the M=1 dequant-GEMV over the seven linears of one layer, replayed
-as a HIP graph (the decode-time shape).  ``value`` = algorithmic bytes per
+as a HIP graph in the decode-time launch pattern (q/k/v in one grouped launch,
+o, gate/up in one grouped launch, down).  ``value`` = algorithmic bytes per
 step / time per step.  The same JSON line carries the M=2048 dequant-GEMM
 throughput, the quantize-kernel throughput, hipBLASLt fp16 F.linear on the
 dequantized weights for comparison, the roofline of the GEMV and the
@@ -109,7 +110,7 @@ def main():
         sys.exit(2)
 
     from atlasinfer_amd import _lib
-    from atlasinfer_amd.integration.atlas_wrappers import qlinear
+    from atlasinfer_amd.integration.atlas_wrappers import qlinear, qlinear_grouped
     from atlasinfer_amd.quant import adaptive_quantizer as AQ
 
     dev = torch.device("cuda:0")
@@ -139,41 +140,57 @@ def main():
         layers.append(layer)
         log(f"layer {li} quantized")
 
-    # ---- M=1 dequant-GEMV: one HIP graph per layer (7 launches)
+    # ---- M=1 dequant-GEMV, one HIP graph per layer.  The decode-time launch
+    # pattern: q/k/v share x (one grouped launch), o, gate/up share x (one
+    # grouped launch), down -- 4 launches; the 7-launch form is timed too.
     xs = {K: gen_x(1, K, gen, dev) for K in {K for _, _, K in LLAMA_LINEARS}}
-    for layer in layers:  # eager warm-up sizes the shared workspace before capture
-        for name, N, K in LLAMA_LINEARS:
-            qlinear(xs[K], layer[name], None)
-    torch.cuda.synchronize()
-    graphs, outs = [], []
-    for layer in layers:
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            outs.append([qlinear(xs[K], layer[name], None) for name, N, K in LLAMA_LINEARS])
-        graphs.append(g)
+
+    def layer_launches(layer, grouped):
+        if not grouped:
+            return [qlinear(xs[K], layer[name], None) for name, N, K in LLAMA_LINEARS]
+        ys = qlinear_grouped(xs[4096], [layer["q_proj"], layer["k_proj"], layer["v_proj"]])
+        ys.append(qlinear(xs[4096], layer["o_proj"], None))
+        ys += qlinear_grouped(xs[4096], [layer["gate_proj"], layer["up_proj"]])
+        ys.append(qlinear(xs[14336], layer["down_proj"], None))
+        return ys
+
     step_bytes = [sum(gemv_bytes(layer[name], 1) for name, _, _ in LLAMA_LINEARS) for layer in layers]
-    for i in range(args.warmup):
-        graphs[i % N_LAYERS].replay()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev[0].record(stream)
-    for i in range(args.steps):
-        graphs[i % N_LAYERS].replay()
-        ev[i + 1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    step_ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]
-    gpu_s = sum(step_ms) / 1e3
+
+    def time_graphs(grouped, steps, warmup):
+        for layer in layers:
+            layer_launches(layer, grouped)
+        torch.cuda.synchronize()
+        graphs = []
+        for layer in layers:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                layer_launches(layer, grouped)
+            graphs.append(g)
+        for i in range(warmup):
+            graphs[i % N_LAYERS].replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream(dev)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev[0].record(stream)
+        for i in range(steps):
+            graphs[i % N_LAYERS].replay()
+            ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        gpu_s = sum(ev[i].elapsed_time(ev[i + 1]) for i in range(steps)) / 1e3
+        return wall, gpu_s
+
+    wall, gpu_s = time_graphs(True, args.steps, args.warmup)
+    wall7, gpu7 = time_graphs(False, max(args.steps // 2, 1), args.warmup)
     total_bytes = sum(step_bytes[i % N_LAYERS] for i in range(args.steps))
     value = total_bytes / wall / 1e9
-    launches = args.steps * len(LLAMA_LINEARS)
-    avg_launch_s = gpu_s / launches
-    bytes_per_launch = total_bytes / launches
-    achieved = bytes_per_launch / avg_launch_s / 1e9
-    log(f"M=1 GEMV: {value:.1f} GB/s wall, {achieved:.1f} GB/s by events, step {1e3 * wall / args.steps:.1f} us")
+    launches = args.steps * 4
+    achieved = (total_bytes / launches) / (gpu_s / launches) / 1e9
+    sep_bytes = sum(step_bytes[i % N_LAYERS] for i in range(max(args.steps // 2, 1)))
+    log(f"M=1 GEMV (4 launches/layer): {value:.1f} GB/s wall, {achieved:.1f} GB/s by events, "
+        f"step {1e6 * wall / args.steps:.1f} us; 7 launches/layer: {sep_bytes / gpu7 / 1e9:.1f} GB/s")
 
     # ---- hipBLASLt fp16 F.linear on the dequantized layer-0 weights, M=1
     def time_eager(fn, iters):
@@ -243,6 +260,7 @@ def main():
         "dtype": "e4m3 codes x fp16 activations, fp32 accumulate",
         "data": "synthetic (seeded N(0,0.02) weights + 0.1% U(8,20)sigma outliers; x N(0,1), 4 channels x30)",
         "config": {"workload": "llama3-8b-linears-m1-gemv", "layers_rotated": N_LAYERS, "M": 1,
+                   "launches_per_layer": "qkv grouped, o, gate+up grouped, down",
                    "block": "per-output-channel", "code_format": "e4m3", "z_threshold": 3.0},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
@@ -253,6 +271,8 @@ def main():
             "hipblaslt_fp16_m2048_tflops": round(blas_tflops, 1),
             "hipblaslt_fp16_m1_us_per_layer": round(blas_m1_s * 1e6, 1),
             "gemv_m1_us_per_layer_events": round(1e6 * gpu_s / args.steps, 2),
+            "gemv_m1_7launch_GBps": round(sep_bytes / gpu7 / 1e9, 1),
+            "gemv_m1_7launch_us_per_layer": round(1e6 * gpu7 / max(args.steps // 2, 1), 2),
             "quantize_GBps": round(q_bytes / q_time / 1e9, 1),
             "quantize_note": "whole quantize_tensor call incl. host sync and outlier gather, per-channel e4m3",
             "sweep": sweep or None,

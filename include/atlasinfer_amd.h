@@ -18,12 +18,20 @@
  *
  * Data layout of a quantized weight W[N, K] (row-major, the nn.Linear layout)
  * with block size G over the flat, zero-padded tensor (padded = ceil(N*K/G)*G):
- *   codes     uint8  [padded]        one code per element, 0 at outliers
+ *   codes     uint8  [padded]        one code per element, 0 at outliers, in
+ *                                    the flat (element) order or tiled (below)
  *   scales    fp16   [padded / G]    one scale per block
  *   flat_idx  int64  [nnz]           ascending flat indices of outliers
  *   vals      fp16   [nnz]           outlier values (verbatim)
  *   row_ptr   int32  [N + 1]         CSR row pointer over the outliers (< N*K)
  *   cols      int32  [nnz]           column of each outlier (flat_idx % K)
+ *
+ * Tiled code layout (AQ_LAYOUT_TILED; needs N % 16 == 0, K % 128 == 0): W is
+ * cut into tiles of 16 rows x 128 columns, 2 KiB each, tile (rb, c) at byte
+ * (rb * K/128 + c) * 2048.  Inside a tile, byte h*1024 + (g*16 + r)*16 + e
+ * holds the code of row 16*rb + r, column 128*c + 64*h + 16*g + e.  This is
+ * the order in which a wave of 64 lanes feeds 16x16x32 MFMAs, so the
+ * quantized-linear kernels read it with fully contiguous 1 KiB loads.
  */
 #ifndef ATLASINFER_AMD_H
 #define ATLASINFER_AMD_H
@@ -37,6 +45,7 @@ extern "C" {
 #define AQ_ABI_VERSION 1
 
 enum { AQ_FMT_INT8 = 0, AQ_FMT_E4M3 = 1 };
+enum { AQ_LAYOUT_FLAT = 0, AQ_LAYOUT_TILED = 1 };
 enum { AQ_OK = 0, AQ_EINVAL = -1, AQ_EHIP = -2, AQ_EUNSUPPORTED = -3, AQ_EWORKSPACE = -4 };
 
 /* ABI version of the loaded library (AQ_ABI_VERSION at build time). */
@@ -52,11 +61,13 @@ int64_t aq_max_block_size(void);
  * Quantize, phase 1 of 2.  Replaces the per-block loop of quantize_tensor
  * (reference: atlasinfer_core/quant/adaptive_quantizer.py:84-133).
  * For every block of G elements of the zero-padded flat fp16 tensor x[numel]:
- * z-score statistics, outlier flags (|z| > z_thr), scale, dense codes; the
- * outliers of each block are staged in the workspace and counted, and the
- * exclusive prefix sum of the counts is written to block_off.
+ * z-score statistics, outlier flags (|z| > z_thr), scale, codes; the outliers
+ * of each block are staged in the workspace and counted, and the exclusive
+ * prefix sum of the counts is written to block_off.
  *   x          fp16 [numel]
  *   z_thr_f16  fp16 bits of the threshold (the reference compares in fp16)
+ *   K, layout  row length and code layout (AQ_LAYOUT_TILED needs K % 128 == 0,
+ *              numel % (16 K) == 0, G % 16 == 0 and K % G == 0)
  *   codes      uint8 [padded]          (out)
  *   scales     fp16  [padded / G]      (out)
  *   block_off  int32 [padded / G + 1]  (out) block_off[nblocks] = total nnz
@@ -64,8 +75,9 @@ int64_t aq_max_block_size(void);
  *              until aq_quantize_finish has run.
  */
 int64_t aq_quantize_workspace_size(int64_t numel, int64_t G);
-int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_thr_f16, int fmt, void* codes,
-                void* scales, int32_t* block_off, void* workspace, int64_t workspace_bytes, void* stream);
+int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_thr_f16, int fmt, int64_t K, int layout,
+                void* codes, void* scales, int32_t* block_off, void* workspace, int64_t workspace_bytes,
+                void* stream);
 
 /*
  * Quantize, phase 2 of 2: write the outlier list in ascending flat order
@@ -91,8 +103,8 @@ int aq_segment_offsets(const int64_t* flat_idx, int64_t nnz, int64_t nseg, int64
 int aq_outlier_cols(const int64_t* flat_idx, int64_t nnz, int64_t K, int32_t* cols, void* stream);
 
 /*
- * Reference layout <-> dense codes.  The reference stores only the codes of
- * non-outliers, in element order (adaptive_quantizer.py:110,125-126,136;
+ * Reference layout <-> dense flat codes.  The reference stores only the codes
+ * of non-outliers, in element order (adaptive_quantizer.py:110,125-126,136;
  * read back at :209-212).
  *   aq_compact_codes: dense[padded] -> compact[padded - nnz]
  *   aq_expand_codes:  compact[padded - nnz] -> dense[padded] (0 at outliers)
@@ -102,12 +114,17 @@ int aq_compact_codes(const void* dense, int64_t padded, const int64_t* flat_idx,
 int aq_expand_codes(const void* compact, int64_t padded, const int64_t* flat_idx, int64_t nnz,
                     void* dense, void* stream);
 
+/* Flat <-> tiled code layout of a [N, K] code matrix (N % 16 == 0, K % 128 == 0). */
+int aq_tile_codes(const void* flat, int64_t N, int64_t K, void* tiled, void* stream);
+int aq_untile_codes(const void* tiled, int64_t N, int64_t K, void* flat, void* stream);
+
 /*
  * Dequantize (reference: dequantize_tensor, adaptive_quantizer.py:185-245):
  * out[j] = fp16(value(codes[j]) * scales[j / G]) for j < numel, then
- * out[flat_idx[p]] = vals[p] for flat_idx[p] < numel.
+ * out[flat_idx[p]] = vals[p] for flat_idx[p] < numel.  codes in `layout`
+ * (tiled codes: rows of K).
  */
-int aq_dequantize(const void* codes, const void* scales, int64_t numel, int64_t G, int fmt,
+int aq_dequantize(const void* codes, const void* scales, int64_t numel, int64_t G, int fmt, int64_t K, int layout,
                   const int64_t* flat_idx, const void* vals, int64_t nnz, void* out, void* stream);
 
 /*
@@ -121,11 +138,12 @@ int aq_zscore(const void* x, int64_t n, float eps, void* z, void* stats, void* s
  * Quantized linear forward y = x W^T + b with W given by its quantized form
  * (reference: QuantizedLinear.forward, integration/atlas_wrappers.py:30-74,
  * which computes F.linear(x, dequantize_tensor(W), b) at :56,67).
- *   x     fp16 [M, K] row-major      y fp16 [M, N] (out)
- *   bias  fp16 [N] or NULL
- *   G must divide K and be a multiple of 32.
+ *   x       fp16 [M, K] row-major, 16-byte aligned    y fp16 [M, N] (out)
+ *   codes   tiled layout; N % 16 == 0, K % 128 == 0
+ *   G       a multiple of 32 that divides K
+ *   bias    fp16 [N] or NULL
  * M <= 16 runs the dequant-GEMV, larger M the dequant-GEMM; both add the
- * outliers from the CSR lists in an fp32 epilogue.
+ * outliers from the CSR lists in fp32 before the single rounding to fp16.
  * workspace: >= aq_qlinear_workspace_size(M, N, K) bytes (currently 0: the
  * kernels keep their partial sums in LDS; NULL is accepted).
  */
@@ -133,6 +151,19 @@ int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K);
 int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const void* codes, const void* scales,
                int64_t G, int fmt, const int32_t* row_ptr, const int32_t* cols, const void* vals,
                const void* bias, void* y, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Several quantized linears that read the same x (e.g. the q/k/v projections
+ * of an attention block, or gate/up of an MLP) in one launch: for i < count,
+ * ys[i] = x W_i^T + b_i, W_i given by codes[i], scales[i], Gs[i], row_ptrs[i],
+ * cols[i], vals[i], biases[i] (entries may be NULL), Ns[i] rows.  All W_i
+ * share K and fmt.  count <= 4.  The arrays themselves are host memory.
+ * Same per-matrix requirements as aq_qlinear.
+ */
+int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, int64_t count, const int64_t* Ns,
+                       const void* const* codes, const void* const* scales, const int64_t* Gs,
+                       const int32_t* const* row_ptrs, const int32_t* const* cols, const void* const* vals,
+                       const void* const* biases, void* const* ys, void* stream);
 
 #ifdef __cplusplus
 }

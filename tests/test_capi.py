@@ -53,17 +53,23 @@ def test_abi_version(lib):
 def test_bad_arguments_return_einval_with_message(lib):
     AQ_EINVAL = -1
     p = ctypes.c_void_p(16)
-    assert lib.aq_quantize(p, 0, 128, 0x4200, 1, p, p, p, p, 1 << 20, None) == AQ_EINVAL
+    assert lib.aq_quantize(p, 0, 128, 0x4200, 1, 128, 0, p, p, p, p, 1 << 20, None) == AQ_EINVAL
     assert b"numel" in lib.aq_last_error()
-    assert lib.aq_quantize(p, 100, 0, 0x4200, 1, p, p, p, p, 1 << 20, None) == AQ_EINVAL
-    assert lib.aq_quantize(p, 100, 1 << 20, 0x4200, 1, p, p, p, p, 1 << 20, None) == AQ_EINVAL
-    assert lib.aq_quantize(p, 100, 64, 0x4200, 7, p, p, p, p, 1 << 20, None) == AQ_EINVAL
+    assert lib.aq_quantize(p, 100, 0, 0x4200, 1, 100, 0, p, p, p, p, 1 << 20, None) == AQ_EINVAL
+    assert lib.aq_quantize(p, 100, 1 << 20, 0x4200, 1, 100, 0, p, p, p, p, 1 << 20, None) == AQ_EINVAL
+    assert lib.aq_quantize(p, 100, 64, 0x4200, 7, 100, 0, p, p, p, p, 1 << 20, None) == AQ_EINVAL
     assert b"format" in lib.aq_last_error()
+    # the tiled layout needs whole 16 x 128 tiles
+    assert lib.aq_quantize(p, 100 * 128, 128, 0x4200, 1, 128, 1, p, p, p, p, 1 << 30, None) == AQ_EINVAL
+    assert b"tiled" in lib.aq_last_error()
     # G must be a multiple of 32 dividing K for the fused linear
     assert lib.aq_qlinear(p, 1, 4096, 16, p, p, 100, 1, p, p, p, None, p, p, 1 << 20, None) == AQ_EINVAL
     assert b"block size" in lib.aq_last_error()
-    assert lib.aq_dequantize(p, p, 10, 0, 0, None, None, 0, p, None) == AQ_EINVAL
+    assert lib.aq_qlinear(p, 1, 4000, 16, p, p, 100, 1, p, p, p, None, p, p, 1 << 20, None) == AQ_EINVAL
+    assert b"multiple of 128" in lib.aq_last_error()
+    assert lib.aq_dequantize(p, p, 10, 0, 0, 10, 0, None, None, 0, p, None) == AQ_EINVAL
     assert lib.aq_zscore(p, 0, 1e-6, p, None, None) == AQ_EINVAL
+    assert lib.aq_tile_codes(p, 20, 128, p, None) == AQ_EINVAL
 
 
 def test_workspace_sizes(lib):
@@ -76,5 +82,5 @@ def test_workspace_sizes(lib):
 def test_workspace_too_small_is_reported(lib):
     AQ_EWORKSPACE = -4
     p = ctypes.c_void_p(16)
-    assert lib.aq_quantize(p, 4096, 128, 0x4200, 1, p, p, p, p, 16, None) == AQ_EWORKSPACE
+    assert lib.aq_quantize(p, 4096, 128, 0x4200, 1, 128, 0, p, p, p, p, 16, None) == AQ_EWORKSPACE
     assert b"workspace" in lib.aq_last_error()

@@ -26,6 +26,14 @@ def bits(t):
     return t.view(np.uint8) if t.dtype.itemsize == 1 else t.view(np.uint16)
 
 
+def tile_np(flat_codes, N, K):
+    """The tiled code layout restated with numpy reshapes: element (n, k) with
+    n = 16 rb + r, k = 128 c + 64 h + 16 g + e goes to tile (rb, c), byte
+    h*1024 + g*256 + r*16 + e."""
+    a = np.asarray(flat_codes, np.uint8).reshape(N // 16, 16, K // 128, 2, 4, 16)  # rb r c h g e
+    return np.ascontiguousarray(a.transpose(0, 2, 3, 4, 1, 5)).reshape(-1)
+
+
 def make_weights(rng, shape, sigma=0.02, frac=0.001, t_dof=None):
     n = int(np.prod(shape))
     w = rng.standard_t(t_dof, n) * sigma if t_dof else rng.standard_normal(n) * sigma
@@ -98,9 +106,12 @@ def test_quantize_matches_oracle(oracle, rows, cols, G, thr, fmt, tdof, frac):
     assert np.array_equal(bits(q.fp16_outliers), bits(ref["fp16_outliers"]))
     if fmt == "int8":  # the reference's compacted stream
         assert np.array_equal(bits(q.fp8_data), bits(ref["fp8_data"]))
-    else:  # dense E4M3 codes
+    else:  # dense E4M3 codes, tiled where the shape allows
         assert q.fp8_data.dtype == torch.float8_e4m3fn
-        assert np.array_equal(bits(q.fp8_data), ref["codes"])
+        tiled = AQ.tiled_eligible(q.original_shape, Gr)
+        assert q.code_layout == ("tiled" if tiled else "flat")
+        expect = tile_np(ref["codes"], rows, cols) if tiled else ref["codes"]
+        assert np.array_equal(bits(q.fp8_data), expect)
     dense = AQ.dense_codes(q, torch.device(DEV))
     assert np.array_equal(bits(dense), ref["codes"])
     # CSR view of the same outliers
@@ -121,7 +132,8 @@ def test_llama_shape_per_channel_e4m3_full(oracle):
     w = make_weights(rng, (4096, 4096))
     q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, code_format="e4m3")
     ref = oracle.quantize(w, 4096, 3.0, oracle.FMT_E4M3)
-    assert np.array_equal(bits(q.fp8_data), ref["codes"])
+    assert q.code_layout == "tiled"
+    assert np.array_equal(bits(q.fp8_data), tile_np(ref["codes"], 4096, 4096))
     assert np.array_equal(bits(q.scale_factors), bits(ref["scale_factors"]))
     assert np.array_equal(q.outlier_indices.cpu().numpy(), ref["outlier_indices"])
 
@@ -307,3 +319,47 @@ def test_signed_zeros_survive(oracle):
     z = AQ.calculate_zscore_manual(torch.from_numpy(x).to(DEV))
     zr, _ = oracle.zscore(x)
     assert np.array_equal(bits(z), bits(zr))
+
+
+def test_tile_untile_round_trip():
+    from atlasinfer_amd import _lib
+    L = _lib.load()
+    rng = np.random.default_rng(21)
+    N, K = 48, 384
+    flat = torch.from_numpy(rng.integers(0, 256, N * K).astype(np.uint8)).to(DEV)
+    tiled = torch.empty_like(flat)
+    back = torch.empty_like(flat)
+    st = _lib.stream_of(torch.device(DEV))
+    _lib.check(L.aq_tile_codes(flat.data_ptr(), N, K, tiled.data_ptr(), st), "tile")
+    _lib.check(L.aq_untile_codes(tiled.data_ptr(), N, K, back.data_ptr(), st), "untile")
+    assert np.array_equal(tiled.cpu().numpy(), tile_np(flat.cpu().numpy(), N, K))
+    assert torch.equal(back, flat)
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 40])
+def test_grouped_launch_matches_single_calls(M):
+    rng = np.random.default_rng(M)
+    K = 1024
+    qts = [AQ.quantize_tensor(torch.from_numpy(make_weights(rng, (N, K))).to(DEV), block_size=-1)
+           for N in (512, 128, 128)]
+    bias = [None, torch.from_numpy(rng.standard_normal(128).astype(np.float16)).to(DEV), None]
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)
+    ys = AW.qlinear_grouped(x, qts, bias)
+    for q, b, y in zip(qts, bias, ys):
+        AQ.clear_dequantized_cache()
+        w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+        assert_close(y, reference_linear(x, w_deq, b), x, w_deq)
+        assert torch.allclose(y, AW.QuantizedLinear(q, b)(x), rtol=2e-3, atol=1e-3)
+
+
+def test_int8_weights_run_through_tiled_kernels():
+    """int8 (reference format) weights are expanded and tiled once for the
+    fused kernels; the result matches F.linear on the dequantized weight."""
+    rng = np.random.default_rng(8)
+    w = make_weights(rng, (256, 512))
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=128, code_format="int8")
+    assert q.code_layout == "flat"
+    x = torch.from_numpy(rng.standard_normal((3, 512)).astype(np.float16)).to(DEV)
+    AQ.clear_dequantized_cache()
+    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    assert_close(AW.QuantizedLinear(q, None)(x), reference_linear(x, w_deq, None), x, w_deq)

@@ -95,6 +95,73 @@ def cpu_baseline(layer_w_cpu, budget_s=12.0):
     return passes, dt, torch.get_num_threads()
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qlinear_gemv_gateup_llama3_8b_m1_traffic.txt")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed
+    FETCH_SIZE/WRITE_SIZE counter summary (line ``traffic_bytes_per_launch:``),
+    or None when there is none."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def time_dominant(layers, x, qlinear_grouped, steps, warmup):
+    """Average duration of the dominant kernel (the gate+up grouped GEMV):
+    one HIP graph holds its launches for every rotated layer back to back;
+    HIP events on the launch stream bracket each replay.  Returns (algorithmic
+    bytes per launch, seconds per launch)."""
+    pairs = [[layer["gate_proj"], layer["up_proj"]] for layer in layers]
+    for p in pairs:
+        qlinear_grouped(x, p)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for p in pairs:
+            qlinear_grouped(x, p)
+    reps = max(steps // len(pairs), 1)
+    for _ in range(max(warmup // len(pairs), 1)):
+        g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    ev[0].record(stream)
+    for i in range(reps):
+        g.replay()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    secs = sum(ev[i].elapsed_time(ev[i + 1]) for i in range(reps)) / 1e3
+    nbytes = sum(gemv_bytes(q, 1) for p in pairs for q in p) // len(pairs)
+    return nbytes, secs / (reps * len(pairs))
+
+
+def kernel_only(args, dev, gen, qlinear_grouped, AQ):
+    """Counter-run workload: the dominant kernel over 4 rotated layers plus a
+    plain 512 MiB device copy whose FETCH_SIZE/WRITE_SIZE calibrate the
+    counters (expected 524288 KiB each way)."""
+    layers = []
+    for _ in range(N_LAYERS):
+        layers.append({name: AQ.quantize_tensor(gen_weight(N, K, gen, dev), block_size=-1, code_format="e4m3")
+                       for name, N, K in LLAMA_LINEARS if name in ("gate_proj", "up_proj")})
+    x = gen_x(1, 4096, gen, dev)
+    nbytes, secs = time_dominant(layers, x, qlinear_grouped, args.steps, args.warmup)
+    src = torch.empty(512 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"kernel_only": True, "algorithmic_bytes_per_launch": nbytes, "us_per_launch":
+                      round(1e6 * secs, 3), "GBps": round(nbytes / secs / 1e9, 1), "copy_bytes": src.numel()}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -103,6 +170,9 @@ def main():
     ap.add_argument("--sweep", action="store_true", help="also time M in {4,16,64,512} per shape")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only the dominant kernel (gate+up grouped GEMV, 4 rotated layers) and a 512 MiB "
+                         "calibration copy, for counter runs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the quantized-linear path is single-GPU here; "
@@ -117,6 +187,10 @@ def main():
     torch.cuda.set_device(dev)
     gen = torch.Generator(device=dev).manual_seed(2024)
     log = lambda *a: print(*a, file=sys.stderr, flush=True)  # noqa: E731
+
+    if args.kernel_only:
+        kernel_only(args, dev, gen, qlinear_grouped, AQ)
+        return
 
     # ---- weights: 4 layers x 7 linears, quantized on the GPU (also timed)
     layers = []
@@ -183,14 +257,15 @@ def main():
         return wall, gpu_s
 
     wall, gpu_s = time_graphs(True, args.steps, args.warmup)
+    dom_bytes, dom_s = time_dominant(layers, xs[4096], qlinear_grouped, args.steps, args.warmup)
     wall7, gpu7 = time_graphs(False, max(args.steps // 2, 1), args.warmup)
     total_bytes = sum(step_bytes[i % N_LAYERS] for i in range(args.steps))
     value = total_bytes / wall / 1e9
-    launches = args.steps * 4
-    achieved = (total_bytes / launches) / (gpu_s / launches) / 1e9
+    achieved = dom_bytes / dom_s / 1e9
     sep_bytes = sum(step_bytes[i % N_LAYERS] for i in range(max(args.steps // 2, 1)))
     log(f"M=1 GEMV (4 launches/layer): {value:.1f} GB/s wall, {achieved:.1f} GB/s by events, "
-        f"step {1e6 * wall / args.steps:.1f} us; 7 launches/layer: {sep_bytes / gpu7 / 1e9:.1f} GB/s")
+        f"step {1e6 * wall / args.steps:.1f} us; 7 launches/layer: {sep_bytes / gpu7 / 1e9:.1f} GB/s; "
+        f"gate+up kernel {1e6 * dom_s:.2f} us/launch, {achieved:.1f} GB/s")
 
     # ---- hipBLASLt fp16 F.linear on the dequantized layer-0 weights, M=1
     def time_eager(fn, iters):
@@ -263,7 +338,9 @@ def main():
                    "launches_per_layer": "qkv grouped, o, gate+up grouped, down",
                    "block": "per-output-channel", "code_format": "e4m3", "z_threshold": 3.0},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "kernel": "qlinear_gemv_kernel<4,E4M3,per-channel>: gate+up grouped, 2x[14336,4096], M=1",
+                     "algorithmic_bytes_per_launch": dom_bytes, "us_per_launch": round(1e6 * dom_s, 3)},
         "cpu_baseline": cpu,
         "extra": {
             "gemm_m2048_tflops": round(gemm_tflops, 1),
@@ -271,6 +348,7 @@ def main():
             "hipblaslt_fp16_m2048_tflops": round(blas_tflops, 1),
             "hipblaslt_fp16_m1_us_per_layer": round(blas_m1_s * 1e6, 1),
             "gemv_m1_us_per_layer_events": round(1e6 * gpu_s / args.steps, 2),
+            "gemv_m1_layer_GBps_events": round(total_bytes / gpu_s / 1e9, 1),
             "gemv_m1_7launch_GBps": round(sep_bytes / gpu7 / 1e9, 1),
             "gemv_m1_7launch_us_per_layer": round(1e6 * gpu7 / max(args.steps // 2, 1), 2),
             "quantize_GBps": round(q_bytes / q_time / 1e9, 1),

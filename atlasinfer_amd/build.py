@@ -36,9 +36,15 @@ FLAGS = [
 ]
 
 
+# per-file additions: the quantized-linear kernels keep MFMA accumulators in
+# ordinary VGPRs (the accumulator-register form made the compiler shuffle
+# accumulators between register files inside the K loop)
+FILE_FLAGS = {"aq_qlinear.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")

@@ -152,6 +152,48 @@ __global__ __launch_bounds__(256) void scatter_outliers_kernel(const int64_t* id
   if (p < nnz && idx[p] < numel) out[idx[p]] = vals[p];
 }
 
+__device__ __forceinline__ int lower_bound_i32(const int32_t* a, int lo, int hi, int key) {
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a[mid] < key)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+// One thread per block of 16 rows x 64 columns (tile row rb, chunk c).
+// Entries are ordered by block, then row, then column, so a block starts
+// after every outlier of the rows above it plus, in each of its own rows,
+// the outliers left of column 64c.
+__global__ __launch_bounds__(256) void outlier_tiles_kernel(const int32_t* row_ptr, const int32_t* cols,
+                                                            const uint16_t* vals, int nrb, int nch,
+                                                            int32_t* tile_ptr, uint32_t* tile_ent) {
+  const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t nblk = (int64_t)nrb * nch;
+  if (b > nblk) return;
+  if (b == nblk) {
+    tile_ptr[b] = row_ptr[nrb * 16];
+    return;
+  }
+  const int rb = (int)(b / nch), c = (int)(b % nch);
+  int lo[16], hi[16];
+  int pos = row_ptr[rb * 16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int p0 = row_ptr[rb * 16 + r], p1 = row_ptr[rb * 16 + r + 1];
+    lo[r] = lower_bound_i32(cols, p0, p1, c * 64);
+    hi[r] = lower_bound_i32(cols, lo[r], p1, c * 64 + 64);
+    pos += lo[r] - p0;
+  }
+  tile_ptr[b] = pos;
+#pragma unroll
+  for (int r = 0; r < 16; r++)
+    for (int p = lo[r]; p < hi[r]; p++)
+      tile_ent[pos++] = ((uint32_t)vals[p] << 16) | ((uint32_t)r << 6) | (uint32_t)(cols[p] - c * 64);
+}
+
 }  // namespace
 
 extern "C" int aq_segment_offsets(const int64_t* flat_idx, int64_t nnz, int64_t nseg, int64_t seg_len,
@@ -255,5 +297,20 @@ extern "C" int aq_dequantize(const void* codes, const void* scales, int64_t nume
                        (const uint16_t*)vals, nnz, numel, (uint16_t*)out);
     AQ_LAUNCH_CHECK("aq_dequantize: scatter launch");
   }
+  return AQ_OK;
+}
+
+extern "C" int aq_outlier_tiles(const int32_t* row_ptr, const int32_t* cols, const void* vals, int64_t N, int64_t K,
+                                int32_t* tile_ptr, uint32_t* tile_ent, void* stream) {
+  AQ_CHECK_ARG(N >= 16 && N % 16 == 0 && K >= 64 && K % 64 == 0 && N < (1 << 30) && K < (1 << 30) &&
+                   (N / 16) * (K / 64) < ((int64_t)1 << 31),
+               "aq_outlier_tiles: N must be a multiple of 16 and K of 64 (N=%lld K=%lld)", (long long)N,
+               (long long)K);
+  AQ_CHECK_ARG(row_ptr && tile_ptr, "aq_outlier_tiles: null pointer argument");
+  const int64_t nblk = (N / 16) * (K / 64);
+  hipLaunchKernelGGL(outlier_tiles_kernel, dim3((unsigned)aq::ceil_div(nblk + 1, 256)), dim3(256), 0,
+                     (hipStream_t)stream, row_ptr, cols, (const uint16_t*)vals, (int)(N / 16), (int)(K / 64),
+                     tile_ptr, tile_ent);
+  AQ_LAUNCH_CHECK("aq_outlier_tiles: launch");
   return AQ_OK;
 }

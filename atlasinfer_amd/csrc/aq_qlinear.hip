@@ -43,6 +43,8 @@ struct QLMat {
   const int32_t* row_ptr;
   const int32_t* cols;
   const uint16_t* vals;
+  const int32_t* tptr;    // outliers per 16 x 64 block (GEMM only)
+  const uint32_t* tent;
   const uint16_t* bias;
   uint16_t* y;
   int N;
@@ -348,186 +350,268 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
 }
 
 // ------------------------------------------------------------ GEMM (M > 16)
+//
+// Workgroup tile BM x 128 (BM = 32 * MI), 4 waves in a 2 x 2 layout, each
+// wave 16*MI rows x 64 columns of 16x16 MFMA tiles; two workgroups share a
+// CU.  K advances in chunks of 64.  Per chunk, every thread
+//   * loads MI 16-byte pieces of x (one lane of MI A fragments: 16 rows x 8
+//     k, in exactly the lane order the MFMA reads), and two 16-byte pieces of
+//     codes (lane order of the tiled layout: one row, 16 consecutive k);
+//   * writes the x pieces to the LDS A buffer, decodes its 32 codes to fp16
+//     weights and writes them to the LDS B buffer in B-fragment order, and
+//     then writes the fp16 value of every outlier that falls in its two
+//     pieces over the zero its code decoded to.  The outliers of a 16-row x
+//     64-column block come as one short list (tile_ptr / tile_ent); a wave
+//     holds up to 64 entries of each of its two blocks, one per lane, and
+//     every lane writes its own with one store (after the wave's bulk
+//     writes of the same block, in program order).
+// The B buffer thus holds exactly the dequantized weight (dequantize_tensor's
+// values, outliers included), and the MFMAs need no correction pass.  Global
+// loads run ahead through two register sets: a chunk's block pointers and
+// bulk data three chunks ahead, its outlier entries two ahead (issued before
+// the next bulk loads, so waiting for them never waits for those); LDS is
+// double buffered with one barrier per chunk.
 
-constexpr int BM = 128, BN = 128, BK = 128;
-constexpr int APAD = 8;  // halves of padding per LDS row of the x tile
-constexpr int kTileCsrCap = 4096;
+constexpr int kGemmBN = 128, kGemmBK = 64;
 
-// x tile of step c into registers: 128 rows x 128 columns, 8 x 16 bytes per
-// thread; rows past M are clamped to row M-1 (their outputs are not stored).
-__device__ __forceinline__ void gemm_load_x(u32x4 (&ra)[8], const uint16_t* x, int mbase, int m_last, int K, int c,
-                                            int t) {
+template <int MI>
+struct GemmRegs {
+  u32x4 a[MI];      // x pieces
+  u32x4 q[2];       // code pieces
+  uint32_t s;        // their scales, piece 0 in the low half (block-wise scales only)
+  int e0[2], e1[2];  // outlier entries of the wave's two blocks: [e0, e1)
+  uint32_t ent[2];  // entry e0 + lane of each block
+};
+
+// Loop-invariant part of the global loads: buffer descriptors over this
+// workgroup's x rows and code rows, and each piece's 32-bit byte offset in
+// them; a chunk only adds a scalar offset.
+template <int MI>
+struct GemmSrc {
+  __amdgpu_buffer_rsrc_t xr, cr;
+  __amdgpu_buffer_rsrc_t tr, er, sr;  // block pointers, entries, scales
+  int xo[MI];  // x pieces
+  int co[2];   // code pieces
+  int to[2];   // block pointer of chunk 0 of each code row, in bytes
+  int so[2];   // scale row of each code piece, in bytes
+};
+
+constexpr int kBufferDword3 = 0x00020000;  // raw (untyped) buffer access on gfx9
+
+template <int MI>
+__device__ __forceinline__ void gemm_src_init(GemmSrc<MI>& S, const QLMat& W, const uint16_t* x, int K, int m_first,
+                                              int m_last, int nbase, int nch128, int t) {
+  const int l = t & 63;
+  const int rows = min(m_last - m_first + 1, 32 * MI);  // this workgroup's x rows
+  S.xr = __builtin_amdgcn_make_buffer_rsrc((void*)(x + (size_t)m_first * K), (short)0, rows * K * 2, kBufferDword3);
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const int idx = t + 256 * i;
-    const int gm = min(mbase + (idx >> 4), m_last);
-    ra[i] = *reinterpret_cast<const u32x4*>(x + (size_t)gm * K + c * BK + 8 * (idx & 15));
+  for (int i = 0; i < MI; i++) {
+    const int f = (t >> 6) + 4 * i;  // A fragment: 16-row group f >> 1, k-step f & 1
+    const int row = min(16 * (f >> 1) + (l & 15), rows - 1);
+    S.xo[i] = (row * K + 32 * (f & 1) + 8 * (l >> 4)) * 2;
+  }
+  const int rb0 = nbase / 16, rb_last = W.N / 16 - 1;
+  const int nrb = min(rb_last - rb0 + 1, kGemmBN / 16);  // this workgroup's tile rows
+  S.cr = __builtin_amdgcn_make_buffer_rsrc((void*)(W.codes + ((size_t)rb0 * nch128 << 11)), (short)0,
+                                           nrb * nch128 * 2048, kBufferDword3);
+  const int nch64 = nch128 * 2;
+  S.tr = __builtin_amdgcn_make_buffer_rsrc((void*)(W.tptr + (size_t)rb0 * nch64), (short)0,
+                                           (nrb * nch64 + 1) * 4, kBufferDword3);
+  S.er = __builtin_amdgcn_make_buffer_rsrc((void*)W.tent, (short)0, 0x7fffffff, kBufferDword3);
+  S.sr = __builtin_amdgcn_make_buffer_rsrc((void*)(W.scales + (size_t)rb0 * 16 * W.kg), (short)0,
+                                           nrb * 16 * W.kg * 2, kBufferDword3);
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    // tile rows past N clamp to the last one and feed only outputs that are never stored
+    const int rb = min(rb0 + (t >> 6) + 4 * i, rb_last) - rb0;
+    S.co[i] = rb * nch128 * 2048 + l * 16;
+    S.to[i] = rb * nch64 * 4;
+    S.so[i] = (rb * 16 + (l & 15)) * W.kg * 2;
   }
 }
 
-__device__ __forceinline__ void gemm_store_x(uint16_t (&As)[BM][BK + APAD], const u32x4 (&ra)[8], int t) {
+// Block pointers and bulk loads (x, codes, scales) of chunk c into one
+// register set.  Everything in the K loop goes through buffer loads: the
+// barrier's release fence waits for outstanding global-pointer loads, which
+// would drain the prefetches every chunk.
+template <int MI, int PC>
+__device__ __forceinline__ void gemm_load(GemmRegs<MI>& R, const GemmSrc<MI>& S, const QLMat& W, int c, int t) {
+  const int l = t & 63;
+  const int k0 = c * kGemmBK;
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const int idx = t + 256 * i;
-    *reinterpret_cast<u32x4*>(&As[idx >> 4][8 * (idx & 15)]) = ra[i];
+  for (int i = 0; i < 2; i++) {
+    R.e0[i] = __builtin_amdgcn_raw_buffer_load_b32(S.tr, S.to[i], c * 4, 0);
+    R.e1[i] = __builtin_amdgcn_raw_buffer_load_b32(S.tr, S.to[i], c * 4 + 4, 0);
   }
-}
-
-// The wave's four code tiles of step c (already in MFMA operand order) and,
-// for block-wise scales, the two scales each lane's pieces use.
-template <int PC>
-__device__ __forceinline__ void gemm_load_codes(u32x4 (&q)[4][2], uint16_t (&sg)[4][2], const QLMat& W,
-                                                const int (&rbi)[4], int nchunks, int c, int lane, int li, int grp) {
+  __builtin_amdgcn_sched_barrier(0);  // block pointers ahead of the bulk loads, as with the entries
 #pragma unroll
-  for (int ni = 0; ni < 4; ni++) {
-    const uint8_t* tp = W.codes + (((size_t)rbi[ni] * nchunks + c) << 11) + lane * 16;
-    q[ni][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tp));
-    q[ni][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tp + 1024));
+  for (int i = 0; i < MI; i++) R.a[i] = __builtin_amdgcn_raw_buffer_load_b128(S.xr, S.xo[i], k0 * 2, 0);
+  const int cs = ((c >> 1) << 11) + ((c & 1) << 10);
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    R.q[i] = __builtin_amdgcn_raw_buffer_load_b128(S.cr, S.co[i], cs, 0);
     if (!PC) {
-      const int n = rbi[ni] * 16 + li;
-      sg[ni][0] = W.scales[scale_index(W, n, c * BK + 16 * grp)];
-      sg[ni][1] = W.scales[scale_index(W, n, c * BK + 64 + 16 * grp)];
-    } else {
-      sg[ni][0] = sg[ni][1] = 0;
+      // the block differs per lane: the offset goes in the vector operand
+      const int kb = W.gshift >= 0 ? ((k0 + 16 * (l >> 4)) >> W.gshift) : (k0 + 16 * (l >> 4)) / W.G;
+      const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so[i] + kb * 2, 0, 0);
+      R.s = i == 0 ? sv : (R.s | (sv << 16));
     }
   }
 }
 
-template <int FMT, int PC>
-__global__ __launch_bounds__(256) void qlinear_gemm_kernel(QLArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[BM][BK + APAD];
-  __shared__ int s_rp[BN + 1];
-  __shared__ int s_col[kTileCsrCap];
-  __shared__ uint16_t s_val[kTileCsrCap];
+// Outlier entries of the chunk whose block pointers R holds: lane j takes
+// entry e0 + j (clamped into the list; the list has 8 slots of padding, so
+// an empty block at the very end still reads inside it).
+template <int MI>
+__device__ __forceinline__ void gemm_load_ent(GemmRegs<MI>& R, const GemmSrc<MI>& S, int t) {
+  const int l = t & 63;
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+    R.ent[i] = __builtin_amdgcn_raw_buffer_load_b32(S.er, max(R.e0[i], min(R.e0[i] + l, R.e1[i] - 1)) * 4, 0, 0);
+  // keep these ahead of the next bulk loads: loads complete in issue order,
+  // so the stage that reads the entries then waits only for them
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Register set -> LDS: x pieces to the A buffer, decoded weights to the B
+// buffer, then the outliers of this thread's pieces over them.
+template <int MI, int FMT, int PC, int DENSE>
+__device__ __forceinline__ void gemm_stage(const GemmRegs<MI>& R, const GemmSrc<MI>& S, uint16_t* As, uint16_t* Bs,
+                                           const half2v (&srow)[2], int t) {
+  const int l = t & 63;
+  const int g = l >> 4, r = l & 15;
+#pragma unroll
+  for (int i = 0; i < MI; i++) {
+    const int f = (t >> 6) + 4 * i;
+    *reinterpret_cast<u32x4*>(As + f * 512 + l * 8) = R.a[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int rb = (t >> 6) + 4 * i;
+    const half2v s2 = PC ? srow[i] : scale2((uint16_t)(R.s >> (16 * i)));
+    const half8 w0 = deq8<FMT>(R.q[i].x, R.q[i].y, s2);
+    const half8 w1 = deq8<FMT>(R.q[i].z, R.q[i].w, s2);
+    uint16_t* frag = Bs + (rb * 2 + (g >> 1)) * 512;
+    *reinterpret_cast<half8*>(frag + (r + 32 * (g & 1)) * 8) = w0;
+    *reinterpret_cast<half8*>(frag + (r + 32 * (g & 1) + 16) * 8) = w1;
+  }
+  // Outliers: lane j writes entry e0 + j of each block.  The block's codes
+  // were written by this same wave just above, and LDS executes a wave's
+  // instructions in order, so each value lands over its decoded zero.
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int rb = (t >> 6) + 4 * i;
+    const int cnt = R.e1[i] - R.e0[i];
+    if (l < cnt) {
+      const uint32_t v = R.ent[i];
+      const int k = v & 63, er = (v >> 6) & 15;
+      Bs[(rb * 2 + (k >> 5)) * 512 + (er + 16 * ((k >> 3) & 3)) * 8 + (k & 7)] = (uint16_t)(v >> 16);
+    }
+    // blocks more than 1/16 outliers (DENSE launches only): the rest from
+    // memory, 64 per round.  Kept out of the common kernel: loads in a
+    // data-dependent loop make every later wait in the chunk a full drain.
+    if (DENSE) {
+      const int e0 = __builtin_amdgcn_readfirstlane(R.e0[i]);
+      const int n = __builtin_amdgcn_readfirstlane(cnt);
+      for (int j = 64 + l; j - l < n; j += 64) {
+        if (j < n) {
+          const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(S.er, (e0 + j) * 4, 0, 0);
+          const int k = v & 63, er = (v >> 6) & 15;
+          Bs[(rb * 2 + (k >> 5)) * 512 + (er + 16 * ((k >> 3) & 3)) * 8 + (k & 7)] = (uint16_t)(v >> 16);
+        }
+      }
+    }
+  }
+}
+
+template <int MI>
+__device__ __forceinline__ void gemm_mma(float4v (&acc)[MI][4], const uint16_t* As, const uint16_t* Bs, int wmf,
+                                         int wnf, int lane) {
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    half8 af[MI], bf[4];
+#pragma unroll
+    for (int mi = 0; mi < MI; mi++) af[mi] = *reinterpret_cast<const half8*>(As + ((wmf + mi) * 2 + j) * 512 + lane * 8);
+#pragma unroll
+    for (int ni = 0; ni < 4; ni++) bf[ni] = *reinterpret_cast<const half8*>(Bs + ((wnf + ni) * 2 + j) * 512 + lane * 8);
+#pragma unroll
+    for (int mi = 0; mi < MI; mi++)
+#pragma unroll
+      for (int ni = 0; ni < 4; ni++)
+        acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mi], bf[ni], acc[mi][ni], 0, 0, 0);
+  }
+}
+
+template <int MI, int FMT, int PC, int DENSE>
+__global__ __launch_bounds__(256, 2) void qlinear_gemm_kernel(QLArgs a) {
+  constexpr int BM = 32 * MI;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kGemmBK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][kGemmBN * kGemmBK];
 
   const QLMat W = pick(a, blockIdx.z);
   const int N = W.N;
-  const int nbase = blockIdx.x * BN;
+  const int nbase = blockIdx.x * kGemmBN;
   if (nbase >= N) return;  // this matrix of the group is narrower than the grid
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
-  const int grp = lane >> 4;
-  const int li = lane & 15;
-  const int mbase = blockIdx.y * BM;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
   const int M = a.M, K = a.K;
-  const int nchunks = K >> 7;
+  const int m_first = blockIdx.y * BM, m_last = M - 1;
+  const int nch = K / kGemmBK;  // even: K is a multiple of 128
+  const int nch128 = K >> 7;
 
-  // outlier lists of this tile's 128 output columns
-  if (t <= BN) s_rp[t] = W.row_ptr[min(nbase + t, N)];
-  __syncthreads();
-  const int p0 = s_rp[0];
-  const int cnt = min(s_rp[BN] - p0, kTileCsrCap);
-  for (int e = t; e < cnt; e += 256) {
-    s_col[e] = W.cols[p0 + e];
-    s_val[e] = W.vals[p0 + e];
-  }
-  int eptr[4], eend[4];
+  GemmSrc<MI> S;
+  gemm_src_init<MI>(S, W, a.x, K, m_first, m_last, nbase, nch128, t);
+  half2v srow[2];  // per-channel scales of this thread's two code rows
 #pragma unroll
-  for (int ni = 0; ni < 4; ni++) {
-    const int nl = wn + 16 * ni + li;
-    eptr[ni] = s_rp[nl] - p0;
-    eend[ni] = min(s_rp[nl + 1] - p0, cnt);
-  }
+  for (int i = 0; i < 2; i++)
+    srow[i] = scale2(PC ? (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so[i], 0, 0) : (uint16_t)0);
+  // prefetches are unconditional (past the last chunk they re-read it): a
+  // conditional load would make the wait before the next use of either
+  // register set drain every load in flight
+  GemmRegs<MI> R0, R1;
+  gemm_load<MI, PC>(R0, S, W, 0, t);
+  gemm_load<MI, PC>(R1, S, W, 1, t);
+  gemm_load_ent<MI>(R0, S, t);
 
-  // This wave's four tile rows (16 output columns each).  Loads are
-  // unconditional so that they all stay in flight: tile rows past N and x
-  // rows past M are clamped to the last valid ones, and only feed outputs
-  // that are never stored.
-  const int rb_last = N / 16 - 1;
-  int rbi[4];
-  half2v srow[4];
+  float4v acc[MI][4];
 #pragma unroll
-  for (int ni = 0; ni < 4; ni++) {
-    rbi[ni] = min((nbase + wn) / 16 + ni, rb_last);
-    srow[ni] = scale2(PC ? W.scales[rbi[ni] * 16 + li] : (uint16_t)0);
-  }
-  const int m_last = M - 1;
-
-  float4v acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < MI; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
 
-  u32x4 ra[8];     // x tile of the next step: 128 rows x 16 x 16 bytes
-  u32x4 qc[4][2];  // codes of this step: [tile row][half]
-  u32x4 qn[4][2];  // codes of the next step
-  uint16_t sc[4][2], sn[4][2];
+  const int wmf = (wave >> 1) * MI;  // first 16-row group of this wave
+  const int wnf = (wave & 1) * 4;    // first 16-column group
 
-  gemm_load_x(ra, a.x, mbase, m_last, K, 0, t);
-  gemm_load_codes<PC>(qc, sc, W, rbi, nchunks, 0, lane, li, grp);
-  for (int c = 0; c < nchunks; c++) {
-    __syncthreads();  // the previous step's LDS reads are done (and the CSR staging, first time)
-    gemm_store_x(As, ra, t);
+  gemm_stage<MI, FMT, PC, DENSE>(R0, S, As[0], Bs[0], srow, t);
+  __syncthreads();
+  gemm_load_ent<MI>(R1, S, t);
+  gemm_load<MI, PC>(R0, S, W, min(2, nch - 1), t);
+  for (int c = 0; c < nch; c += 2) {
+    gemm_mma<MI>(acc, As[0], Bs[0], wmf, wnf, lane);
+    gemm_stage<MI, FMT, PC, DENSE>(R1, S, As[1], Bs[1], srow, t);
     __syncthreads();
-    if (c + 1 < nchunks) {
-      gemm_load_x(ra, a.x, mbase, m_last, K, c + 1, t);
-      gemm_load_codes<PC>(qn, sn, W, rbi, nchunks, c + 1, lane, li, grp);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {  // k-steps of 32 within the 128-wide chunk
-      const int h = j >> 1;
-      const int kq = 64 * h + 16 * grp + 8 * (j & 1);
-      half8 af[4], bf[4];
-#pragma unroll
-      for (int mi = 0; mi < 4; mi++) af[mi] = *reinterpret_cast<const half8*>(&As[wm + 16 * mi + li][kq]);
-#pragma unroll
-      for (int ni = 0; ni < 4; ni++) {
-        const u32x4 q = qc[ni][h];
-        const half2v s2 = PC ? srow[ni] : scale2(sc[ni][h]);
-        bf[ni] = (j & 1) ? deq8<FMT>(q.z, q.w, s2) : deq8<FMT>(q.x, q.y, s2);
-      }
-#pragma unroll
-      for (int mi = 0; mi < 4; mi++)
-#pragma unroll
-        for (int ni = 0; ni < 4; ni++)
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mi], bf[ni], acc[mi][ni], 0, 0, 0);
-    }
-    // outliers whose column lies in this step: x from the LDS tile
-    const int k0 = c * BK;
-#pragma unroll
-    for (int ni = 0; ni < 4; ni++) {
-      while (eptr[ni] < eend[ni] && s_col[eptr[ni]] < k0 + BK) {
-        const int cc = s_col[eptr[ni]] - k0;
-        const float v = (float)bits_to_h(s_val[eptr[ni]]);
-#pragma unroll
-        for (int mi = 0; mi < 4; mi++)
-#pragma unroll
-          for (int i = 0; i < 4; i++)
-            acc[mi][ni][i] = __builtin_fmaf((float)bits_to_h(As[wm + 16 * mi + 4 * grp + i][cc]), v, acc[mi][ni][i]);
-        eptr[ni]++;
-      }
-    }
-#pragma unroll
-    for (int ni = 0; ni < 4; ni++)
-#pragma unroll
-      for (int h = 0; h < 2; h++) {
-        qc[ni][h] = qn[ni][h];
-        sc[ni][h] = sn[ni][h];
-      }
+    gemm_load_ent<MI>(R0, S, t);
+    gemm_load<MI, PC>(R1, S, W, min(c + 3, nch - 1), t);
+    gemm_mma<MI>(acc, As[1], Bs[1], wmf, wnf, lane);
+    if (c + 2 < nch) gemm_stage<MI, FMT, PC, DENSE>(R0, S, As[0], Bs[0], srow, t);
+    __syncthreads();
+    gemm_load_ent<MI>(R1, S, t);
+    gemm_load<MI, PC>(R0, S, W, min(c + 4, nch - 1), t);
   }
 
-  const bool overflow = (s_rp[BN] - p0) > kTileCsrCap;
+  const int grp = lane >> 4, li = lane & 15;
 #pragma unroll
   for (int ni = 0; ni < 4; ni++) {
-    const int nl = wn + 16 * ni + li;
-    const int n = nbase + nl;
+    const int n = nbase + 16 * (wnf + ni) + li;
     if (n >= N) continue;
     const float bv = W.bias ? (float)bits_to_h(W.bias[n]) : 0.0f;
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++)
+    for (int mi = 0; mi < MI; mi++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const int m = mbase + wm + 16 * mi + 4 * grp + i;
-        if (m >= M) continue;
-        float v = acc[mi][ni][i];
-        if (overflow) {  // entries past the staging capacity: from memory
-          for (int p = max(p0 + cnt, s_rp[nl]); p < s_rp[nl + 1]; p++)
-            v = __builtin_fmaf((float)bits_to_h(a.x[(size_t)m * K + W.cols[p]]), (float)bits_to_h(W.vals[p]), v);
-        }
-        W.y[(size_t)m * N + n] = h_to_bits(rn_h(v + bv));
+        const int m = m_first + 16 * (wmf + mi) + 4 * grp + i;
+        if (m < M) W.y[(size_t)m * N + n] = h_to_bits(rn_h(acc[mi][ni][i] + bv));
       }
   }
 }
@@ -554,6 +638,26 @@ hipError_t launch_gemv(const QLArgs& a, int fmt, bool per_channel, int blocks, h
                             : launch_gemv<NS, AQ_FMT_INT8>(a, per_channel, blocks, s);
 }
 
+template <int MI, int FMT, int DENSE>
+hipError_t launch_gemm(const QLArgs& a, bool per_channel, int64_t maxN, hipStream_t s) {
+  const dim3 grid((unsigned)aq::ceil_div(maxN, kGemmBN), (unsigned)aq::ceil_div(a.M, 32 * MI),
+                  (unsigned)a.count);
+  if (per_channel)
+    hipLaunchKernelGGL((qlinear_gemm_kernel<MI, FMT, 1, DENSE>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((qlinear_gemm_kernel<MI, FMT, 0, DENSE>), grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int MI>
+hipError_t launch_gemm(const QLArgs& a, int fmt, bool per_channel, bool dense, int64_t maxN, hipStream_t s) {
+  if (dense)
+    return fmt == AQ_FMT_E4M3 ? launch_gemm<MI, AQ_FMT_E4M3, 1>(a, per_channel, maxN, s)
+                              : launch_gemm<MI, AQ_FMT_INT8, 1>(a, per_channel, maxN, s);
+  return fmt == AQ_FMT_E4M3 ? launch_gemm<MI, AQ_FMT_E4M3, 0>(a, per_channel, maxN, s)
+                            : launch_gemm<MI, AQ_FMT_INT8, 0>(a, per_channel, maxN, s);
+}
+
 }  // namespace
 
 extern "C" int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K) {
@@ -566,8 +670,9 @@ extern "C" int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K) {
 extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, int64_t count, const int64_t* Ns,
                                   const void* const* codes, const void* const* scales, const int64_t* Gs,
                                   const int32_t* const* row_ptrs, const int32_t* const* cols,
-                                  const void* const* vals, const void* const* biases, void* const* ys,
-                                  void* stream) {
+                                  const void* const* vals, const int32_t* const* tile_ptrs,
+                                  const uint32_t* const* tile_ents, const int64_t* tile_maxes,
+                                  const void* const* biases, void* const* ys, void* stream) {
   AQ_CHECK_ARG(count >= 1 && count <= kMaxGroup, "aq_qlinear: 1..%d matrices per call (got %lld)", kMaxGroup,
                (long long)count);
   AQ_CHECK_ARG(M >= 0 && M < (1 << 30) && K >= 128 && K % 128 == 0 && K < (1 << 30),
@@ -592,6 +697,8 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
                    (long long)K);
       AQ_CHECK_ARG(codes[j] && scales[j] && row_ptrs[j] && ys[j] && (uintptr_t)codes[j] % 16 == 0,
                    "aq_qlinear: null or unaligned pointer for matrix %d", i);
+      AQ_CHECK_ARG(M <= 16 || (tile_ptrs && tile_ents && tile_maxes && tile_ptrs[j] && tile_ents[j]),
+                   "aq_qlinear: M > 16 needs the outlier tile lists (aq_outlier_tiles) for matrix %d", i);
       a.first[i] = (int)blocks;
       blocks += N / 16;
       maxN = std::max(maxN, N);
@@ -602,6 +709,8 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
     w.row_ptr = row_ptrs[j];
     w.cols = cols[j];
     w.vals = (const uint16_t*)vals[j];
+    w.tptr = tile_ptrs ? tile_ptrs[j] : nullptr;
+    w.tent = tile_ents ? tile_ents[j] : nullptr;
     w.bias = biases ? (const uint16_t*)biases[j] : nullptr;
     w.y = (uint16_t*)ys[j];
     w.N = (int)N;
@@ -620,28 +729,22 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
                                        : launch_gemv<8>(a, fmt, per_channel, (int)blocks, s);
     return aq::check_hip(e, "aq_qlinear: gemv launch");
   }
-  const dim3 grid((unsigned)aq::ceil_div(maxN, BN), (unsigned)aq::ceil_div(M, BM), (unsigned)count);
-  if (fmt == AQ_FMT_E4M3) {
-    if (per_channel)
-      hipLaunchKernelGGL((qlinear_gemm_kernel<AQ_FMT_E4M3, 1>), grid, dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL((qlinear_gemm_kernel<AQ_FMT_E4M3, 0>), grid, dim3(256), 0, s, a);
-  } else {
-    if (per_channel)
-      hipLaunchKernelGGL((qlinear_gemm_kernel<AQ_FMT_INT8, 1>), grid, dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL((qlinear_gemm_kernel<AQ_FMT_INT8, 0>), grid, dim3(256), 0, s, a);
-  }
-  AQ_LAUNCH_CHECK("aq_qlinear: gemm launch");
-  return AQ_OK;
+  // 32-bit buffer offsets: 128 rows of x (2 bytes each) and 8 tile rows of codes
+  AQ_CHECK_ARG(K <= (1 << 22), "aq_qlinear: K=%lld too large for M > 16 (at most 4194304)", (long long)K);
+  bool dense = false;  // some 16 x 64 block holds more than 64 outliers
+  for (int i = 0; i < count; i++) dense = dense || tile_maxes[i] > 64;
+  const hipError_t e = launch_gemm<4>(a, fmt, per_channel, dense, maxN, s);
+  return aq::check_hip(e, "aq_qlinear: gemm launch");
 }
 
 extern "C" int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const void* codes, const void* scales,
                           int64_t G, int fmt, const int32_t* row_ptr, const int32_t* cols, const void* vals,
-                          const void* bias, void* y, void* workspace, int64_t ws_bytes, void* stream) {
+                          const int32_t* tile_ptr, const uint32_t* tile_ent, int64_t tile_max, const void* bias,
+                          void* y, void* workspace, int64_t ws_bytes, void* stream) {
   (void)workspace;
   (void)ws_bytes;
   const void* b = bias;
   void* yy = y;
-  return aq_qlinear_grouped(x, M, K, fmt, 1, &N, &codes, &scales, &G, &row_ptr, &cols, &vals, &b, &yy, stream);
+  return aq_qlinear_grouped(x, M, K, fmt, 1, &N, &codes, &scales, &G, &row_ptr, &cols, &vals, &tile_ptr, &tile_ent,
+                            &tile_max, &b, &yy, stream);
 }

@@ -26,7 +26,10 @@ import torch.nn.functional as F
 
 from .. import _lib
 from ..quant.adaptive_quantizer import (QuantizedTensor, _format_id, _rows_cols, dequantize_tensor, kernel_codes,
-                                        tiled_eligible)
+                                        outlier_tiles, tiled_eligible)
+
+
+GEMV_MAX_M = 16  # aq_qlinear runs the dequant-GEMV up to this many rows of x
 
 
 def fused_supported(qt: QuantizedTensor) -> bool:
@@ -35,10 +38,12 @@ def fused_supported(qt: QuantizedTensor) -> bool:
     return qt.outlier_row_ptr is not None and tiled_eligible(qt.original_shape, qt.block_size)
 
 
-def qlinear_grouped(x: torch.Tensor, qts, biases=None, codes=None):
+def qlinear_grouped(x: torch.Tensor, qts, biases=None, codes=None, tiles=None):
     """[x W_i^T + b_i for each quantized W_i] in one launch; all W_i share
     in_features (aq_qlinear_grouped).  ``codes`` may carry the tiled code
-    arrays (saves re-tiling int8 weights per call)."""
+    arrays and ``tiles`` the (tile_ptr, tile_ent, tile_max) outlier block
+    lists (saves rebuilding them per call for weights that do not store
+    them)."""
     dev = x.device
     L = _lib.load()
     n = len(qts)
@@ -59,19 +64,25 @@ def qlinear_grouped(x: torch.Tensor, qts, biases=None, codes=None):
     ys = [torch.empty((M, N), dtype=torch.float16, device=dev) for N in Ns]
     if M > 0:
         arr = _lib.ptr_array
+        if M > GEMV_MAX_M:
+            tiles = list(tiles) if tiles is not None else [outlier_tiles(q, dev) for q in qts]
+        else:
+            tiles = [(None, None, 0)] * n
         _lib.check(L.aq_qlinear_grouped(
             x2.data_ptr(), M, K, _format_id(fmt), n, arr(Ns, ctypes.c_int64), arr([c.data_ptr() for c in codes]),
             arr([q.scale_factors.data_ptr() for q in qts]), arr([q.block_size for q in qts], ctypes.c_int64),
             arr([q.outlier_row_ptr.data_ptr() for q in qts]), arr([_lib.ptr(q.outlier_cols) for q in qts]),
-            arr([_lib.ptr(q.fp16_outliers) for q in qts]), arr([_lib.ptr(b) for b in biases]),
+            arr([_lib.ptr(q.fp16_outliers) for q in qts]), arr([_lib.ptr(t[0]) for t in tiles]),
+            arr([_lib.ptr(t[1]) for t in tiles]), arr([t[2] for t in tiles], ctypes.c_int64),
+            arr([_lib.ptr(b) for b in biases]),
             arr([y.data_ptr() for y in ys]), _lib.stream_of(dev)), "aq_qlinear_grouped")
     return [y.view(*x.shape[:-1], N) for y, N in zip(ys, Ns)]
 
 
 def qlinear(x: torch.Tensor, qt: QuantizedTensor, bias: Optional[torch.Tensor],
-            codes: Optional[torch.Tensor] = None) -> torch.Tensor:
+            codes: Optional[torch.Tensor] = None, tiles=None) -> torch.Tensor:
     """y = x W^T + b for W in quantized form, through aq_qlinear.  ``codes``
-    may carry the tiled code array."""
+    may carry the tiled code array and ``tiles`` the outlier block lists."""
     dev = x.device
     K = int(qt.original_shape[-1])
     N = qt.original_shape.numel() // K
@@ -84,11 +95,12 @@ def qlinear(x: torch.Tensor, qt: QuantizedTensor, bias: Optional[torch.Tensor],
         return y.view(*x.shape[:-1], N)
     if codes is None:
         codes = kernel_codes(qt, dev)
+    tp, te, tmax = (tiles if tiles is not None else outlier_tiles(qt, dev)) if M > GEMV_MAX_M else (None, None, 0)
     L = _lib.load()
     _lib.check(L.aq_qlinear(x2.data_ptr(), M, K, N, codes.data_ptr(), qt.scale_factors.data_ptr(), qt.block_size,
                             _format_id(qt.code_format), qt.outlier_row_ptr.data_ptr(), _lib.ptr(qt.outlier_cols),
-                            _lib.ptr(qt.fp16_outliers), _lib.ptr(bias), y.data_ptr(), None, 0,
-                            _lib.stream_of(dev)), "aq_qlinear")
+                            _lib.ptr(qt.fp16_outliers), _lib.ptr(tp), _lib.ptr(te), tmax, _lib.ptr(bias), y.data_ptr(),
+                            None, 0, _lib.stream_of(dev)), "aq_qlinear")
     return y.view(*x.shape[:-1], N)
 
 
@@ -101,6 +113,7 @@ class QuantizedLinear(nn.Module):
         self.bias = bias
         self.original_shape = getattr(quantized_weights, "original_shape", None)
         self._codes = None  # tiled codes on the compute device (int8: expanded and tiled once)
+        self._tiles = None  # outlier block lists on the compute device
 
     def _weights_on(self, device: torch.device) -> QuantizedTensor:
         q = self.quantized_weights
@@ -109,6 +122,7 @@ class QuantizedLinear(nn.Module):
         if q.fp8_data.device != device:
             self.quantized_weights = q = q.to(device)
             self._codes = None
+            self._tiles = None
         if self.bias is not None and self.bias.device != device:
             self.bias = self.bias.to(device)
         return q
@@ -128,7 +142,9 @@ class QuantizedLinear(nn.Module):
             return F.linear(x, dequantize_tensor(q, dev), self.bias)
         if self._codes is None or self._codes.device != dev:
             self._codes = kernel_codes(q, dev)
-        return qlinear(x, q, self.bias, self._codes)
+        if x.numel() > GEMV_MAX_M * x.shape[-1] and (self._tiles is None or self._tiles[0].device != dev):
+            self._tiles = outlier_tiles(q, dev)
+        return qlinear(x, q, self.bias, self._codes, self._tiles)
 
     def _apply(self, fn, recurse=True):
         # module.to(device) / .cuda() also moves the quantized weight and the

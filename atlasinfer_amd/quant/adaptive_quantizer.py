@@ -7,7 +7,9 @@ under that name, ``atlasinfer_core.quant.adaptive_quantizer``):
 * ``QuantizedTensor``          (reference :8-42) -- the six reference fields in
   order, plus trailing fields with defaults: ``code_format``,
   ``outlier_row_ptr`` (CSR row pointer, int32 [N+1]), ``outlier_cols``
-  (int32 [nnz]) and ``code_layout``.
+  (int32 [nnz]), ``code_layout``, and the same outliers listed per block of
+  16 rows x 64 columns for the dequant-GEMM (``outlier_tile_ptr``,
+  ``outlier_tile_ent``, see ``aq_outlier_tiles`` in include/atlasinfer_amd.h).
 * ``calculate_zscore_manual``  (reference :44-49)
 * ``quantize_tensor``          (reference :51-148)
 * ``dequantize_tensor``        (reference :156-251)
@@ -55,6 +57,9 @@ class QuantizedTensor(NamedTuple):
     outlier_row_ptr: Optional[torch.Tensor] = None  # int32 [N + 1] over the last dim
     outlier_cols: Optional[torch.Tensor] = None     # int32 [nnz]
     code_layout: str = "flat"                       # "flat" (element order) or "tiled"
+    outlier_tile_ptr: Optional[torch.Tensor] = None  # int32 [(N/16)*(K/64) + 1]
+    outlier_tile_ent: Optional[torch.Tensor] = None  # int32 [nnz + 8], packed entries
+    outlier_tile_max: int = 0                        # most entries in one block
 
     def to(self, device):
         """Move every tensor to ``device``; returns self when already there
@@ -70,6 +75,8 @@ class QuantizedTensor(NamedTuple):
             scale_factors=mv(self.scale_factors),
             outlier_row_ptr=mv(self.outlier_row_ptr),
             outlier_cols=mv(self.outlier_cols),
+            outlier_tile_ptr=mv(self.outlier_tile_ptr),
+            outlier_tile_ent=mv(self.outlier_tile_ent),
         )
 
     def memory_footprint(self, include_overhead=True) -> int:
@@ -77,7 +84,7 @@ class QuantizedTensor(NamedTuple):
         reference :34-42)."""
         mem = 0
         for t in (self.fp8_data, self.fp16_outliers, self.outlier_indices, self.scale_factors,
-                  self.outlier_row_ptr, self.outlier_cols):
+                  self.outlier_row_ptr, self.outlier_cols, self.outlier_tile_ptr, self.outlier_tile_ent):
             if t is not None:
                 mem += t.element_size() * t.nelement()
         if include_overhead:
@@ -236,6 +243,9 @@ def quantize_tensor(
         outlier_cols=cols,
         code_layout=layout,
     )
+    if layout == "tiled":
+        tp, te, tmax = build_outlier_tiles(qt, dev)
+        qt = qt._replace(outlier_tile_ptr=tp, outlier_tile_ent=te, outlier_tile_max=tmax)
     return qt.to(input_device)
 
 
@@ -283,6 +293,42 @@ def kernel_codes(qt: QuantizedTensor, device: torch.device) -> torch.Tensor:
     tiled = torch.empty_like(codes)
     _lib.check(L.aq_tile_codes(codes.data_ptr(), N, K, tiled.data_ptr(), _lib.stream_of(device)), "aq_tile_codes")
     return tiled
+
+
+def tiles_eligible(shape) -> bool:
+    """Whether the outliers of a weight of this shape can be listed per
+    16 x 64 block (2-D view [N, K] with N % 16 == 0, K % 64 == 0)."""
+    if len(shape) < 2:
+        return False
+    N, K = _rows_cols(shape)
+    return N >= 16 and N % 16 == 0 and K >= 64 and K % 64 == 0
+
+
+def build_outlier_tiles(qt: QuantizedTensor, device: torch.device):
+    """(tile_ptr, tile_ent, tile_max): the outliers of ``qt`` per block of 16
+    rows x 64 columns (aq_outlier_tiles), from its CSR lists, on ``device``,
+    and the largest count in one block (one host sync)."""
+    q = qt.to(device)
+    if not tiles_eligible(q.original_shape) or q.outlier_row_ptr is None:
+        raise ValueError(f"shape {tuple(q.original_shape)} has no 16 x 64 outlier blocks")
+    L = _lib.load()
+    N, K = _rows_cols(q.original_shape)
+    nnz = q.fp16_outliers.numel()
+    tile_ptr = torch.empty((N // 16) * (K // 64) + 1, dtype=torch.int32, device=device)
+    tile_ent = torch.zeros(nnz + 8, dtype=torch.int32, device=device)  # 8 entries of read padding
+    _lib.check(L.aq_outlier_tiles(q.outlier_row_ptr.data_ptr(), _lib.ptr(q.outlier_cols), _lib.ptr(q.fp16_outliers),
+                                  N, K, tile_ptr.data_ptr(), tile_ent.data_ptr(), _lib.stream_of(device)),
+               "aq_outlier_tiles")
+    tile_max = int((tile_ptr[1:] - tile_ptr[:-1]).max().item()) if nnz else 0
+    return tile_ptr, tile_ent, tile_max
+
+
+def outlier_tiles(qt: QuantizedTensor, device: torch.device):
+    """(tile_ptr, tile_ent, tile_max) of ``qt`` on ``device``: the stored
+    block outlier lists, or built from the CSR lists."""
+    if qt.outlier_tile_ptr is not None:
+        return qt.outlier_tile_ptr.to(device), qt.outlier_tile_ent.to(device), qt.outlier_tile_max
+    return build_outlier_tiles(qt, device)
 
 
 # --- Dequantization cache (reference :153-154): id(QuantizedTensor) -> fp16 tensor

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define AQ_ABI_VERSION 1
+#define AQ_ABI_VERSION 2
 
 enum { AQ_FMT_INT8 = 0, AQ_FMT_E4M3 = 1 };
 enum { AQ_LAYOUT_FLAT = 0, AQ_LAYOUT_TILED = 1 };
@@ -103,6 +103,25 @@ int aq_segment_offsets(const int64_t* flat_idx, int64_t nnz, int64_t nseg, int64
 int aq_outlier_cols(const int64_t* flat_idx, int64_t nnz, int64_t K, int32_t* cols, void* stream);
 
 /*
+ * Outlier lists per block of 16 rows x 64 columns, the order in which the
+ * dequant-GEMM consumes them (no counterpart in the reference, whose
+ * dequantize_tensor scans all outlier indices per block,
+ * adaptive_quantizer.py:194-201).  Needs N % 16 == 0, K % 64 == 0.
+ *   tile_ptr int32  [(N/16) * (K/64) + 1]   block (rb, c) = rows 16rb..16rb+15,
+ *                                           columns 64c..64c+63, at index
+ *                                           rb * (K/64) + c; entries
+ *                                           tile_ptr[b] .. tile_ptr[b+1]-1
+ *   tile_ent uint32 [nnz + 8]               (fp16 value << 16) | (row in block
+ *                                           << 6) | column in block, ordered by
+ *                                           block, row, column; the last 8
+ *                                           slots are padding the kernels may
+ *                                           read but never use
+ * from the CSR lists (row_ptr, cols, vals) of the same outliers.
+ */
+int aq_outlier_tiles(const int32_t* row_ptr, const int32_t* cols, const void* vals, int64_t N, int64_t K,
+                     int32_t* tile_ptr, uint32_t* tile_ent, void* stream);
+
+/*
  * Reference layout <-> dense flat codes.  The reference stores only the codes
  * of non-outliers, in element order (adaptive_quantizer.py:110,125-126,136;
  * read back at :209-212).
@@ -142,28 +161,41 @@ int aq_zscore(const void* x, int64_t n, float eps, void* z, void* stats, void* s
  *   codes   tiled layout; N % 16 == 0, K % 128 == 0
  *   G       a multiple of 32 that divides K
  *   bias    fp16 [N] or NULL
- * M <= 16 runs the dequant-GEMV, larger M the dequant-GEMM; both add the
- * outliers from the CSR lists in fp32 before the single rounding to fp16.
+ *   row_ptr, cols, vals   CSR outlier lists (aq_segment_offsets, aq_outlier_cols)
+ *   tile_ptr, tile_ent    the same outliers per 16 x 64 block (aq_outlier_tiles);
+ *                         required when M > 16, ignored (may be NULL) otherwise
+ *   tile_max              the largest entry count of any block (max of
+ *                         tile_ptr[b+1] - tile_ptr[b]); above 64 the GEMM
+ *                         takes a variant that reads the excess from memory
+ * M <= 16 runs the dequant-GEMV, which adds the outliers from the CSR lists in
+ * fp32; larger M the dequant-GEMM, which writes each outlier's fp16 value over
+ * its decoded zero in the weight tile it multiplies.  Either way the result is
+ * x times the dequantized weight accumulated in fp32, plus the bias, rounded
+ * once to fp16.
  * workspace: >= aq_qlinear_workspace_size(M, N, K) bytes (currently 0: the
  * kernels keep their partial sums in LDS; NULL is accepted).
  */
 int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K);
 int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const void* codes, const void* scales,
                int64_t G, int fmt, const int32_t* row_ptr, const int32_t* cols, const void* vals,
-               const void* bias, void* y, void* workspace, int64_t workspace_bytes, void* stream);
+               const int32_t* tile_ptr, const uint32_t* tile_ent, int64_t tile_max, const void* bias, void* y,
+               void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Several quantized linears that read the same x (e.g. the q/k/v projections
  * of an attention block, or gate/up of an MLP) in one launch: for i < count,
  * ys[i] = x W_i^T + b_i, W_i given by codes[i], scales[i], Gs[i], row_ptrs[i],
- * cols[i], vals[i], biases[i] (entries may be NULL), Ns[i] rows.  All W_i
- * share K and fmt.  count <= 4.  The arrays themselves are host memory.
+ * cols[i], vals[i], tile_ptrs[i], tile_ents[i], tile_maxes[i], biases[i]
+ * (entries may be NULL), Ns[i] rows.  All W_i share K and fmt.  count <= 4.
+ * The arrays themselves are host memory; tile_ptrs/tile_ents/tile_maxes may
+ * be NULL when M <= 16.
  * Same per-matrix requirements as aq_qlinear.
  */
 int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, int64_t count, const int64_t* Ns,
                        const void* const* codes, const void* const* scales, const int64_t* Gs,
                        const int32_t* const* row_ptrs, const int32_t* const* cols, const void* const* vals,
-                       const void* const* biases, void* const* ys, void* stream);
+                       const int32_t* const* tile_ptrs, const uint32_t* const* tile_ents,
+                       const int64_t* tile_maxes, const void* const* biases, void* const* ys, void* stream);
 
 #ifdef __cplusplus
 }

@@ -28,7 +28,8 @@ def lib():
 def test_header_declares_the_expected_api():
     names = declared_functions()
     for must in ["aq_abi_version", "aq_last_error", "aq_quantize", "aq_quantize_finish", "aq_dequantize",
-                 "aq_qlinear", "aq_zscore", "aq_compact_codes", "aq_expand_codes", "aq_segment_offsets"]:
+                 "aq_qlinear", "aq_zscore", "aq_compact_codes", "aq_expand_codes", "aq_segment_offsets",
+                 "aq_outlier_tiles"]:
         assert must in names
 
 
@@ -63,10 +64,15 @@ def test_bad_arguments_return_einval_with_message(lib):
     assert lib.aq_quantize(p, 100 * 128, 128, 0x4200, 1, 128, 1, p, p, p, p, 1 << 30, None) == AQ_EINVAL
     assert b"tiled" in lib.aq_last_error()
     # G must be a multiple of 32 dividing K for the fused linear
-    assert lib.aq_qlinear(p, 1, 4096, 16, p, p, 100, 1, p, p, p, None, p, p, 1 << 20, None) == AQ_EINVAL
+    assert lib.aq_qlinear(p, 1, 4096, 16, p, p, 100, 1, p, p, p, None, None, 0, None, p, p, 1 << 20, None) == AQ_EINVAL
     assert b"block size" in lib.aq_last_error()
-    assert lib.aq_qlinear(p, 1, 4000, 16, p, p, 100, 1, p, p, p, None, p, p, 1 << 20, None) == AQ_EINVAL
+    assert lib.aq_qlinear(p, 1, 4000, 16, p, p, 100, 1, p, p, p, None, None, 0, None, p, p, 1 << 20, None) == AQ_EINVAL
     assert b"multiple of 128" in lib.aq_last_error()
+    # the dequant-GEMM (M > 16) needs the outlier block lists
+    assert lib.aq_qlinear(p, 32, 4096, 16, p, p, 4096, 1, p, p, p, None, None, 0, None, p, p, 0, None) == AQ_EINVAL
+    assert b"aq_outlier_tiles" in lib.aq_last_error()
+    assert lib.aq_outlier_tiles(p, p, p, 20, 128, p, p, None) == AQ_EINVAL
+    assert lib.aq_outlier_tiles(p, p, p, 32, 100, p, p, None) == AQ_EINVAL
     assert lib.aq_dequantize(p, p, 10, 0, 0, 10, 0, None, None, 0, p, None) == AQ_EINVAL
     assert lib.aq_zscore(p, 0, 1e-6, p, None, None) == AQ_EINVAL
     assert lib.aq_tile_codes(p, 20, 128, p, None) == AQ_EINVAL

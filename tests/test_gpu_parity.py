@@ -237,6 +237,73 @@ def test_qlinear_heavy_outliers_and_3d_input():
     assert_close(y, yref, x, w_deq)
 
 
+def expected_tiles(q, N, K):
+    """The 16 x 64 block outlier lists restated with numpy from the flat
+    indices: entry (fp16 bits << 16) | (row % 16) << 6 | (col % 64), ordered by
+    block (rb * K/64 + col // 64), then row, then column."""
+    idx = q.outlier_indices.cpu().numpy()
+    vals = bits(q.fp16_outliers).astype(np.uint32)
+    n, c = idx // K, idx % K
+    blk = (n // 16) * (K // 64) + c // 64
+    ent = (vals << 16) | ((n % 16).astype(np.uint32) << 6) | (c % 64).astype(np.uint32)
+    order = np.argsort(blk, kind="stable")  # flat order is already (row, column)
+    ptr = np.searchsorted(blk[order], np.arange((N // 16) * (K // 64) + 1))
+    return ptr.astype(np.int32), ent[order]
+
+
+@pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128)])
+def test_outlier_tiles_match_flat_indices(fmt, G):
+    rng = np.random.default_rng(5 + abs(G))
+    N, K = 96, 512
+    w = make_weights(rng, (N, K), frac=0.02, t_dof=3)
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=G, code_format=fmt)
+    tp, te, tmax = AQ.outlier_tiles(q, torch.device(DEV))
+    ptr, ent = expected_tiles(q, N, K)
+    assert tmax == np.diff(ptr).max()
+    nnz = q.outlier_indices.numel()
+    assert nnz > 100
+    assert np.array_equal(tp.cpu().numpy(), ptr)
+    assert te.numel() == nnz + 8
+    assert np.array_equal(te[:nnz].cpu().numpy().view(np.uint32), ent)
+
+
+@pytest.mark.parametrize("M", [17, 64, 200])
+def test_gemm_crowded_outlier_blocks(M):
+    """Blocks of 16 x 64 holding 0, 1, 9, 17 and 48 outliers: the GEMM reads
+    each block's list in batches of 8."""
+    rng = np.random.default_rng(900 + M)
+    N, K = 256, 1024
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    for (rb, c), per_row in {(0, 0): 3, (1, 5): 1, (3, 15): 2, (7, 2): 1}.items():
+        for r in range(16):
+            cols = rng.permutation(64)[:per_row] + 64 * c
+            w[16 * rb + r, cols] = rng.choice([-1, 1], per_row) * rng.uniform(8, 20, per_row) * 0.02
+    w[16 * 5 + 3, 64 * 9 + 7] = 0.4  # a lone outlier
+    q = AQ.quantize_tensor(torch.from_numpy(w.astype(np.float16)).to(DEV), block_size=-1, code_format="e4m3")
+    tp = q.outlier_tile_ptr.cpu().numpy()
+    counts = np.diff(tp).reshape(N // 16, K // 64)
+    # the N(0, 0.02) background adds a few outliers of its own
+    assert counts[0, 0] >= 48 and counts[3, 15] >= 32 and counts[1, 5] >= 16 and counts[5, 9] >= 1
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)
+    AQ.clear_dequantized_cache()
+    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    assert_close(AW.QuantizedLinear(q, None)(x), reference_linear(x, w_deq, None), x, w_deq)
+
+
+def test_gemm_dense_outliers_long_rows():
+    """Student-t(3) weights with 1% planted outliers (about 2% outliers in
+    all) over 14336-wide rows."""
+    rng = np.random.default_rng(31)
+    N, K, M = 512, 14336, 100
+    w = make_weights(rng, (N, K), frac=0.01, t_dof=3)
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, code_format="e4m3")
+    assert q.outlier_indices.numel() > 0.015 * N * K
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)
+    AQ.clear_dequantized_cache()
+    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    assert_close(AW.QuantizedLinear(q, None)(x), reference_linear(x, w_deq, None), x, w_deq)
+
+
 def test_qlinear_fallback_for_ragged_blocks():
     """Block 100 does not tile 1000-wide rows: dequantize kernel + F.linear."""
     rng = np.random.default_rng(4)

@@ -351,11 +351,12 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
 
 // ------------------------------------------------------------ GEMM (M > 16)
 //
-// Workgroup tile BM x 128 (BM = 32 * MI), 4 waves in a 2 x 2 layout, each
-// wave 16*MI rows x 64 columns of 16x16 MFMA tiles; two workgroups share a
-// CU.  K advances in chunks of 64.  Per chunk, every thread
-//   * loads MI 16-byte pieces of x (one lane of MI A fragments: 16 rows x 8
-//     k, in exactly the lane order the MFMA reads), and two 16-byte pieces of
+// Workgroup tile BM x 128: WAVES waves in a (WAVES/2) x 2 layout of 64 x 64
+// wave tiles (16x16 MFMA tiles); BM = 128 with 4 waves (two workgroups per
+// CU) or 256 with 8 waves (one workgroup per CU, each weight decoded once
+// per 256 rows of x).  K advances in chunks of 64.  Per chunk, every thread
+//   * loads AP 16-byte pieces of x (one lane of AP A fragments: 16 rows x 8
+//     k, in exactly the lane order the MFMA reads), and CP 16-byte pieces of
 //     codes (lane order of the tiled layout: one row, 16 consecutive k);
 //   * writes the x pieces to the LDS A buffer, decodes its 32 codes to fp16
 //     weights and writes them to the LDS B buffer in B-fragment order, and
@@ -374,39 +375,49 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
 
 constexpr int kGemmBN = 128, kGemmBK = 64;
 
-template <int MI>
+// WAVES waves per workgroup in a (WAVES/2) x 2 layout of 64 x 64 wave tiles.
+template <int WAVES>
+struct GemmShape {
+  static constexpr int BM = WAVES / 2 * 64;              // rows of x per workgroup
+  static constexpr int AP = BM * kGemmBK * 2 / 16 / (64 * WAVES);  // x pieces per thread and chunk
+  static constexpr int CP = kGemmBN * kGemmBK / 16 / (64 * WAVES);  // code pieces (= blocks per wave)
+};
+
+template <int WAVES>
 struct GemmRegs {
-  u32x4 a[MI];      // x pieces
-  u32x4 q[2];       // code pieces
-  uint32_t s;        // their scales, piece 0 in the low half (block-wise scales only)
-  int e0[2], e1[2];  // outlier entries of the wave's two blocks: [e0, e1)
-  uint32_t ent[2];  // entry e0 + lane of each block
+  static constexpr int AP = GemmShape<WAVES>::AP, CP = GemmShape<WAVES>::CP;
+  u32x4 a[AP];         // x pieces
+  u32x4 q[CP];         // code pieces
+  uint32_t s;          // their scales, piece 0 in the low half (block-wise scales only)
+  int e0[CP], e1[CP];  // outlier entries of the wave's blocks: [e0, e1)
+  uint32_t ent[CP];    // entry e0 + lane of each block
 };
 
 // Loop-invariant part of the global loads: buffer descriptors over this
 // workgroup's x rows and code rows, and each piece's 32-bit byte offset in
 // them; a chunk only adds a scalar offset.
-template <int MI>
+template <int WAVES>
 struct GemmSrc {
+  static constexpr int AP = GemmShape<WAVES>::AP, CP = GemmShape<WAVES>::CP;
   __amdgpu_buffer_rsrc_t xr, cr;
   __amdgpu_buffer_rsrc_t tr, er, sr;  // block pointers, entries, scales
-  int xo[MI];  // x pieces
-  int co[2];   // code pieces
-  int to[2];   // block pointer of chunk 0 of each code row, in bytes
-  int so[2];   // scale row of each code piece, in bytes
+  int xo[AP];  // x pieces
+  int co[CP];  // code pieces
+  int to[CP];  // block pointer of chunk 0 of each code row, in bytes
+  int so[CP];  // scale row of each code piece, in bytes
 };
 
 constexpr int kBufferDword3 = 0x00020000;  // raw (untyped) buffer access on gfx9
 
-template <int MI>
-__device__ __forceinline__ void gemm_src_init(GemmSrc<MI>& S, const QLMat& W, const uint16_t* x, int K, int m_first,
+template <int WAVES>
+__device__ __forceinline__ void gemm_src_init(GemmSrc<WAVES>& S, const QLMat& W, const uint16_t* x, int K, int m_first,
                                               int m_last, int nbase, int nch128, int t) {
   const int l = t & 63;
-  const int rows = min(m_last - m_first + 1, 32 * MI);  // this workgroup's x rows
+  const int rows = min(m_last - m_first + 1, GemmShape<WAVES>::BM);  // this workgroup's x rows
   S.xr = __builtin_amdgcn_make_buffer_rsrc((void*)(x + (size_t)m_first * K), (short)0, rows * K * 2, kBufferDword3);
 #pragma unroll
-  for (int i = 0; i < MI; i++) {
-    const int f = (t >> 6) + 4 * i;  // A fragment: 16-row group f >> 1, k-step f & 1
+  for (int i = 0; i < S.AP; i++) {
+    const int f = (t >> 6) + WAVES * i;  // A fragment: 16-row group f >> 1, k-step f & 1
     const int row = min(16 * (f >> 1) + (l & 15), rows - 1);
     S.xo[i] = (row * K + 32 * (f & 1) + 8 * (l >> 4)) * 2;
   }
@@ -421,9 +432,9 @@ __device__ __forceinline__ void gemm_src_init(GemmSrc<MI>& S, const QLMat& W, co
   S.sr = __builtin_amdgcn_make_buffer_rsrc((void*)(W.scales + (size_t)rb0 * 16 * W.kg), (short)0,
                                            nrb * 16 * W.kg * 2, kBufferDword3);
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
+  for (int i = 0; i < S.CP; i++) {
     // tile rows past N clamp to the last one and feed only outputs that are never stored
-    const int rb = min(rb0 + (t >> 6) + 4 * i, rb_last) - rb0;
+    const int rb = min(rb0 + (t >> 6) + WAVES * i, rb_last) - rb0;
     S.co[i] = rb * nch128 * 2048 + l * 16;
     S.to[i] = rb * nch64 * 4;
     S.so[i] = (rb * 16 + (l & 15)) * W.kg * 2;
@@ -434,21 +445,23 @@ __device__ __forceinline__ void gemm_src_init(GemmSrc<MI>& S, const QLMat& W, co
 // register set.  Everything in the K loop goes through buffer loads: the
 // barrier's release fence waits for outstanding global-pointer loads, which
 // would drain the prefetches every chunk.
-template <int MI, int PC>
-__device__ __forceinline__ void gemm_load(GemmRegs<MI>& R, const GemmSrc<MI>& S, const QLMat& W, int c, int t) {
+template <int WAVES, int PC>
+__device__ __forceinline__ void gemm_load(GemmRegs<WAVES>& R, const GemmSrc<WAVES>& S, const QLMat& W, int c, int t) {
   const int l = t & 63;
   const int k0 = c * kGemmBK;
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    R.e0[i] = __builtin_amdgcn_raw_buffer_load_b32(S.tr, S.to[i], c * 4, 0);
-    R.e1[i] = __builtin_amdgcn_raw_buffer_load_b32(S.tr, S.to[i], c * 4 + 4, 0);
+  for (int i = 0; i < R.CP; i++) {
+    typedef int int2v __attribute__((ext_vector_type(2)));
+    const int2v p = __builtin_bit_cast(int2v, __builtin_amdgcn_raw_buffer_load_b64(S.tr, S.to[i], c * 4, 0));
+    R.e0[i] = p.x;
+    R.e1[i] = p.y;
   }
   __builtin_amdgcn_sched_barrier(0);  // block pointers ahead of the bulk loads, as with the entries
 #pragma unroll
-  for (int i = 0; i < MI; i++) R.a[i] = __builtin_amdgcn_raw_buffer_load_b128(S.xr, S.xo[i], k0 * 2, 0);
+  for (int i = 0; i < R.AP; i++) R.a[i] = __builtin_amdgcn_raw_buffer_load_b128(S.xr, S.xo[i], k0 * 2, 0);
   const int cs = ((c >> 1) << 11) + ((c & 1) << 10);
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
+  for (int i = 0; i < R.CP; i++) {
     R.q[i] = __builtin_amdgcn_raw_buffer_load_b128(S.cr, S.co[i], cs, 0);
     if (!PC) {
       // the block differs per lane: the offset goes in the vector operand
@@ -460,14 +473,14 @@ __device__ __forceinline__ void gemm_load(GemmRegs<MI>& R, const GemmSrc<MI>& S,
 }
 
 // Outlier entries of the chunk whose block pointers R holds: lane j takes
-// entry e0 + j (clamped into the list; the list has 8 slots of padding, so
-// an empty block at the very end still reads inside it).
-template <int MI>
-__device__ __forceinline__ void gemm_load_ent(GemmRegs<MI>& R, const GemmSrc<MI>& S, int t) {
+// entry e0 + j (the list has 64 slots of padding, so every lane reads
+// inside it; lanes past the block's count ignore what they read).
+template <int WAVES>
+__device__ __forceinline__ void gemm_load_ent(GemmRegs<WAVES>& R, const GemmSrc<WAVES>& S, int t) {
   const int l = t & 63;
 #pragma unroll
-  for (int i = 0; i < 2; i++)
-    R.ent[i] = __builtin_amdgcn_raw_buffer_load_b32(S.er, max(R.e0[i], min(R.e0[i] + l, R.e1[i] - 1)) * 4, 0, 0);
+  for (int i = 0; i < R.CP; i++)
+    R.ent[i] = __builtin_amdgcn_raw_buffer_load_b32(S.er, l * 4, __builtin_amdgcn_readfirstlane(R.e0[i]) * 4, 0);
   // keep these ahead of the next bulk loads: loads complete in issue order,
   // so the stage that reads the entries then waits only for them
   __builtin_amdgcn_sched_barrier(0);
@@ -475,19 +488,19 @@ __device__ __forceinline__ void gemm_load_ent(GemmRegs<MI>& R, const GemmSrc<MI>
 
 // Register set -> LDS: x pieces to the A buffer, decoded weights to the B
 // buffer, then the outliers of this thread's pieces over them.
-template <int MI, int FMT, int PC, int DENSE>
-__device__ __forceinline__ void gemm_stage(const GemmRegs<MI>& R, const GemmSrc<MI>& S, uint16_t* As, uint16_t* Bs,
-                                           const half2v (&srow)[2], int t) {
+template <int WAVES, int FMT, int PC, int DENSE>
+__device__ __forceinline__ void gemm_stage(const GemmRegs<WAVES>& R, const GemmSrc<WAVES>& S, uint16_t* As,
+                                           uint16_t* Bs, const half2v (&srow)[GemmShape<WAVES>::CP], int t) {
   const int l = t & 63;
   const int g = l >> 4, r = l & 15;
 #pragma unroll
-  for (int i = 0; i < MI; i++) {
-    const int f = (t >> 6) + 4 * i;
+  for (int i = 0; i < R.AP; i++) {
+    const int f = (t >> 6) + WAVES * i;
     *reinterpret_cast<u32x4*>(As + f * 512 + l * 8) = R.a[i];
   }
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const int rb = (t >> 6) + 4 * i;
+  for (int i = 0; i < R.CP; i++) {
+    const int rb = (t >> 6) + WAVES * i;
     const half2v s2 = PC ? srow[i] : scale2((uint16_t)(R.s >> (16 * i)));
     const half8 w0 = deq8<FMT>(R.q[i].x, R.q[i].y, s2);
     const half8 w1 = deq8<FMT>(R.q[i].z, R.q[i].w, s2);
@@ -499,14 +512,10 @@ __device__ __forceinline__ void gemm_stage(const GemmRegs<MI>& R, const GemmSrc<
   // were written by this same wave just above, and LDS executes a wave's
   // instructions in order, so each value lands over its decoded zero.
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const int rb = (t >> 6) + 4 * i;
+  for (int i = 0; i < R.CP; i++) {
+    const int rb = (t >> 6) + WAVES * i;
     const int cnt = R.e1[i] - R.e0[i];
-    if (l < cnt) {
-      const uint32_t v = R.ent[i];
-      const int k = v & 63, er = (v >> 6) & 15;
-      Bs[(rb * 2 + (k >> 5)) * 512 + (er + 16 * ((k >> 3) & 3)) * 8 + (k & 7)] = (uint16_t)(v >> 16);
-    }
+    if (l < cnt) Bs[rb * 1024 + (R.ent[i] & 1023)] = (uint16_t)(R.ent[i] >> 16);
     // blocks more than 1/16 outliers (DENSE launches only): the rest from
     // memory, 64 per round.  Kept out of the common kernel: loads in a
     // data-dependent loop make every later wait in the chunk a full drain.
@@ -516,8 +525,7 @@ __device__ __forceinline__ void gemm_stage(const GemmRegs<MI>& R, const GemmSrc<
       for (int j = 64 + l; j - l < n; j += 64) {
         if (j < n) {
           const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(S.er, (e0 + j) * 4, 0, 0);
-          const int k = v & 63, er = (v >> 6) & 15;
-          Bs[(rb * 2 + (k >> 5)) * 512 + (er + 16 * ((k >> 3) & 3)) * 8 + (k & 7)] = (uint16_t)(v >> 16);
+          Bs[rb * 1024 + (v & 1023)] = (uint16_t)(v >> 16);
         }
       }
     }
@@ -542,9 +550,9 @@ __device__ __forceinline__ void gemm_mma(float4v (&acc)[MI][4], const uint16_t* 
   }
 }
 
-template <int MI, int FMT, int PC, int DENSE>
-__global__ __launch_bounds__(256, 2) void qlinear_gemm_kernel(QLArgs a) {
-  constexpr int BM = 32 * MI;
+template <int WAVES, int FMT, int PC, int DENSE>
+__global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void qlinear_gemm_kernel(QLArgs a) {
+  constexpr int BM = GemmShape<WAVES>::BM, CP = GemmShape<WAVES>::CP;
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kGemmBK];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[2][kGemmBN * kGemmBK];
 
@@ -560,44 +568,44 @@ __global__ __launch_bounds__(256, 2) void qlinear_gemm_kernel(QLArgs a) {
   const int nch = K / kGemmBK;  // even: K is a multiple of 128
   const int nch128 = K >> 7;
 
-  GemmSrc<MI> S;
-  gemm_src_init<MI>(S, W, a.x, K, m_first, m_last, nbase, nch128, t);
-  half2v srow[2];  // per-channel scales of this thread's two code rows
+  GemmSrc<WAVES> S;
+  gemm_src_init<WAVES>(S, W, a.x, K, m_first, m_last, nbase, nch128, t);
+  half2v srow[CP];  // per-channel scales of this thread's code rows
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < CP; i++)
     srow[i] = scale2(PC ? (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so[i], 0, 0) : (uint16_t)0);
   // prefetches are unconditional (past the last chunk they re-read it): a
   // conditional load would make the wait before the next use of either
   // register set drain every load in flight
-  GemmRegs<MI> R0, R1;
-  gemm_load<MI, PC>(R0, S, W, 0, t);
-  gemm_load<MI, PC>(R1, S, W, 1, t);
-  gemm_load_ent<MI>(R0, S, t);
+  GemmRegs<WAVES> R0, R1;
+  gemm_load<WAVES, PC>(R0, S, W, 0, t);
+  gemm_load<WAVES, PC>(R1, S, W, 1, t);
+  gemm_load_ent<WAVES>(R0, S, t);
 
-  float4v acc[MI][4];
+  float4v acc[4][4];
 #pragma unroll
-  for (int i = 0; i < MI; i++)
+  for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
 
-  const int wmf = (wave >> 1) * MI;  // first 16-row group of this wave
+  const int wmf = (wave >> 1) * 4;   // first 16-row group of this wave
   const int wnf = (wave & 1) * 4;    // first 16-column group
 
-  gemm_stage<MI, FMT, PC, DENSE>(R0, S, As[0], Bs[0], srow, t);
+  gemm_stage<WAVES, FMT, PC, DENSE>(R0, S, As[0], Bs[0], srow, t);
   __syncthreads();
-  gemm_load_ent<MI>(R1, S, t);
-  gemm_load<MI, PC>(R0, S, W, min(2, nch - 1), t);
+  gemm_load_ent<WAVES>(R1, S, t);
+  gemm_load<WAVES, PC>(R0, S, W, min(2, nch - 1), t);
   for (int c = 0; c < nch; c += 2) {
-    gemm_mma<MI>(acc, As[0], Bs[0], wmf, wnf, lane);
-    gemm_stage<MI, FMT, PC, DENSE>(R1, S, As[1], Bs[1], srow, t);
+    gemm_mma<4>(acc, As[0], Bs[0], wmf, wnf, lane);
+    gemm_stage<WAVES, FMT, PC, DENSE>(R1, S, As[1], Bs[1], srow, t);
     __syncthreads();
-    gemm_load_ent<MI>(R0, S, t);
-    gemm_load<MI, PC>(R1, S, W, min(c + 3, nch - 1), t);
-    gemm_mma<MI>(acc, As[1], Bs[1], wmf, wnf, lane);
-    if (c + 2 < nch) gemm_stage<MI, FMT, PC, DENSE>(R0, S, As[0], Bs[0], srow, t);
+    gemm_load_ent<WAVES>(R0, S, t);
+    gemm_load<WAVES, PC>(R1, S, W, min(c + 3, nch - 1), t);
+    gemm_mma<4>(acc, As[1], Bs[1], wmf, wnf, lane);
+    if (c + 2 < nch) gemm_stage<WAVES, FMT, PC, DENSE>(R0, S, As[0], Bs[0], srow, t);
     __syncthreads();
-    gemm_load_ent<MI>(R1, S, t);
-    gemm_load<MI, PC>(R0, S, W, min(c + 4, nch - 1), t);
+    gemm_load_ent<WAVES>(R1, S, t);
+    gemm_load<WAVES, PC>(R0, S, W, min(c + 4, nch - 1), t);
   }
 
   const int grp = lane >> 4, li = lane & 15;
@@ -607,7 +615,7 @@ __global__ __launch_bounds__(256, 2) void qlinear_gemm_kernel(QLArgs a) {
     if (n >= N) continue;
     const float bv = W.bias ? (float)bits_to_h(W.bias[n]) : 0.0f;
 #pragma unroll
-    for (int mi = 0; mi < MI; mi++)
+    for (int mi = 0; mi < 4; mi++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int m = m_first + 16 * (wmf + mi) + 4 * grp + i;
@@ -638,24 +646,24 @@ hipError_t launch_gemv(const QLArgs& a, int fmt, bool per_channel, int blocks, h
                             : launch_gemv<NS, AQ_FMT_INT8>(a, per_channel, blocks, s);
 }
 
-template <int MI, int FMT, int DENSE>
+template <int WAVES, int FMT, int DENSE>
 hipError_t launch_gemm(const QLArgs& a, bool per_channel, int64_t maxN, hipStream_t s) {
-  const dim3 grid((unsigned)aq::ceil_div(maxN, kGemmBN), (unsigned)aq::ceil_div(a.M, 32 * MI),
+  const dim3 grid((unsigned)aq::ceil_div(maxN, kGemmBN), (unsigned)aq::ceil_div(a.M, GemmShape<WAVES>::BM),
                   (unsigned)a.count);
   if (per_channel)
-    hipLaunchKernelGGL((qlinear_gemm_kernel<MI, FMT, 1, DENSE>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((qlinear_gemm_kernel<WAVES, FMT, 1, DENSE>), grid, dim3(64 * WAVES), 0, s, a);
   else
-    hipLaunchKernelGGL((qlinear_gemm_kernel<MI, FMT, 0, DENSE>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((qlinear_gemm_kernel<WAVES, FMT, 0, DENSE>), grid, dim3(64 * WAVES), 0, s, a);
   return hipGetLastError();
 }
 
-template <int MI>
+template <int WAVES>
 hipError_t launch_gemm(const QLArgs& a, int fmt, bool per_channel, bool dense, int64_t maxN, hipStream_t s) {
   if (dense)
-    return fmt == AQ_FMT_E4M3 ? launch_gemm<MI, AQ_FMT_E4M3, 1>(a, per_channel, maxN, s)
-                              : launch_gemm<MI, AQ_FMT_INT8, 1>(a, per_channel, maxN, s);
-  return fmt == AQ_FMT_E4M3 ? launch_gemm<MI, AQ_FMT_E4M3, 0>(a, per_channel, maxN, s)
-                            : launch_gemm<MI, AQ_FMT_INT8, 0>(a, per_channel, maxN, s);
+    return fmt == AQ_FMT_E4M3 ? launch_gemm<WAVES, AQ_FMT_E4M3, 1>(a, per_channel, maxN, s)
+                              : launch_gemm<WAVES, AQ_FMT_INT8, 1>(a, per_channel, maxN, s);
+  return fmt == AQ_FMT_E4M3 ? launch_gemm<WAVES, AQ_FMT_E4M3, 0>(a, per_channel, maxN, s)
+                            : launch_gemm<WAVES, AQ_FMT_INT8, 0>(a, per_channel, maxN, s);
 }
 
 }  // namespace
@@ -733,7 +741,13 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
   AQ_CHECK_ARG(K <= (1 << 22), "aq_qlinear: K=%lld too large for M > 16 (at most 4194304)", (long long)K);
   bool dense = false;  // some 16 x 64 block holds more than 64 outliers
   for (int i = 0; i < count; i++) dense = dense || tile_maxes[i] > 64;
-  const hipError_t e = launch_gemm<4>(a, fmt, per_channel, dense, maxN, s);
+  // 256-row tiles decode each weight half as often, but only pay off while
+  // they still give every CU a workgroup; smaller grids take 128-row tiles
+  // (two workgroups per CU)
+  int64_t wg256 = 0;
+  for (int i = 0; i < count; i++) wg256 += aq::ceil_div(M, GemmShape<8>::BM) * aq::ceil_div(Ns[i], kGemmBN);
+  const hipError_t e = wg256 >= 256 ? launch_gemm<8>(a, fmt, per_channel, dense, maxN, s)
+                                    : launch_gemm<4>(a, fmt, per_channel, dense, maxN, s);
   return aq::check_hip(e, "aq_qlinear: gemm launch");
 }
 

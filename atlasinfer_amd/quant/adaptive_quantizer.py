@@ -58,7 +58,7 @@ class QuantizedTensor(NamedTuple):
     outlier_cols: Optional[torch.Tensor] = None     # int32 [nnz]
     code_layout: str = "flat"                       # "flat" (element order) or "tiled"
     outlier_tile_ptr: Optional[torch.Tensor] = None  # int32 [(N/16)*(K/64) + 1]
-    outlier_tile_ent: Optional[torch.Tensor] = None  # int32 [nnz + 8], packed entries
+    outlier_tile_ent: Optional[torch.Tensor] = None  # int32 [nnz + 64], packed entries
     outlier_tile_max: int = 0                        # most entries in one block
 
     def to(self, device):
@@ -315,7 +315,7 @@ def build_outlier_tiles(qt: QuantizedTensor, device: torch.device):
     N, K = _rows_cols(q.original_shape)
     nnz = q.fp16_outliers.numel()
     tile_ptr = torch.empty((N // 16) * (K // 64) + 1, dtype=torch.int32, device=device)
-    tile_ent = torch.zeros(nnz + 8, dtype=torch.int32, device=device)  # 8 entries of read padding
+    tile_ent = torch.zeros(nnz + 64, dtype=torch.int32, device=device)  # 64 entries of read padding
     _lib.check(L.aq_outlier_tiles(q.outlier_row_ptr.data_ptr(), _lib.ptr(q.outlier_cols), _lib.ptr(q.fp16_outliers),
                                   N, K, tile_ptr.data_ptr(), tile_ent.data_ptr(), _lib.stream_of(device)),
                "aq_outlier_tiles")

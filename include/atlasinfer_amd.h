@@ -111,11 +111,14 @@ int aq_outlier_cols(const int64_t* flat_idx, int64_t nnz, int64_t K, int32_t* co
  *                                           columns 64c..64c+63, at index
  *                                           rb * (K/64) + c; entries
  *                                           tile_ptr[b] .. tile_ptr[b+1]-1
- *   tile_ent uint32 [nnz + 8]               (fp16 value << 16) | (row in block
- *                                           << 6) | column in block, ordered by
- *                                           block, row, column; the last 8
- *                                           slots are padding the kernels may
- *                                           read but never use
+ *   tile_ent uint32 [nnz + 64]              (fp16 value << 16) | p, where for
+ *                                           row r (0..15) and column k (0..63)
+ *                                           in the block p = (k/32) << 9 |
+ *                                           (k/8 % 4) << 7 | r << 3 | k % 8
+ *                                           (the block's MFMA operand order);
+ *                                           ordered by block, row, column; the
+ *                                           last 64 slots are padding the
+ *                                           kernels may read but never use
  * from the CSR lists (row_ptr, cols, vals) of the same outliers.
  */
 int aq_outlier_tiles(const int32_t* row_ptr, const int32_t* cols, const void* vals, int64_t N, int64_t K,

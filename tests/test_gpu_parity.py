@@ -239,13 +239,15 @@ def test_qlinear_heavy_outliers_and_3d_input():
 
 def expected_tiles(q, N, K):
     """The 16 x 64 block outlier lists restated with numpy from the flat
-    indices: entry (fp16 bits << 16) | (row % 16) << 6 | (col % 64), ordered by
-    block (rb * K/64 + col // 64), then row, then column."""
+    indices: entry (fp16 bits << 16) | p with, for r = row % 16 and
+    k = col % 64, p = (k // 32) << 9 | (k // 8 % 4) << 7 | r << 3 | k % 8,
+    ordered by block (rb * K/64 + col // 64), then row, then column."""
     idx = q.outlier_indices.cpu().numpy()
     vals = bits(q.fp16_outliers).astype(np.uint32)
     n, c = idx // K, idx % K
     blk = (n // 16) * (K // 64) + c // 64
-    ent = (vals << 16) | ((n % 16).astype(np.uint32) << 6) | (c % 64).astype(np.uint32)
+    r, k = (n % 16).astype(np.uint32), (c % 64).astype(np.uint32)
+    ent = (vals << 16) | (k // 32) << 9 | (k // 8 % 4) << 7 | r << 3 | k % 8
     order = np.argsort(blk, kind="stable")  # flat order is already (row, column)
     ptr = np.searchsorted(blk[order], np.arange((N // 16) * (K // 64) + 1))
     return ptr.astype(np.int32), ent[order]
@@ -263,7 +265,7 @@ def test_outlier_tiles_match_flat_indices(fmt, G):
     nnz = q.outlier_indices.numel()
     assert nnz > 100
     assert np.array_equal(tp.cpu().numpy(), ptr)
-    assert te.numel() == nnz + 8
+    assert te.numel() == nnz + 64
     assert np.array_equal(te[:nnz].cpu().numpy().view(np.uint32), ent)
 
 
@@ -288,6 +290,24 @@ def test_gemm_crowded_outlier_blocks(M):
     AQ.clear_dequantized_cache()
     w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
     assert_close(AW.QuantizedLinear(q, None)(x), reference_linear(x, w_deq, None), x, w_deq)
+
+
+@pytest.mark.parametrize("M,N", [(1000, 4096), (2048, 4096), (2100, 4112)])
+def test_gemm_tile_shapes(M, N):
+    """Grids of 256 or more 256 x 128 tiles take the 8-wave kernel (2048 x
+    4096, and 2100 x 4112 with a partial last tile in both directions);
+    smaller ones the 4-wave kernel (1000 x 4096)."""
+    rng = np.random.default_rng(M + N)
+    K = 1024
+    w = make_weights(rng, (N, K))
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, code_format="e4m3")
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    xs[:, rng.permutation(K)[:4]] *= 30
+    x = torch.from_numpy(xs.astype(np.float16)).to(DEV)
+    b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(DEV)
+    AQ.clear_dequantized_cache()
+    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    assert_close(AW.QuantizedLinear(q, b)(x), reference_linear(x, w_deq, b), x, w_deq)
 
 
 def test_gemm_dense_outliers_long_rows():

@@ -11,12 +11,18 @@
 //   V    = sum (x - S/G)^2  (f64, balanced tree)      std  = fp16(f32(sqrt(V/(G-1))))
 //   den  = fp16(std + 1e-6)
 //   flag = |fp16(fp16(x - mean) / den)| > thr   -- evaluated as |fp16(x - mean)| > Th
-//          with Th the largest fp16 whose quotient does not pass (found once
-//          per block by bisection over fp16 bit patterns with the literal
-//          quotient, so both forms agree on every input)
+//          with Th the largest fp16 whose quotient does not pass.  The
+//          literal test is monotone in |x - mean| and turns true within a
+//          few fp16 steps of fp16(thr * den), so the team's lanes evaluate
+//          it on 16 consecutive bit patterns there at once and a ballot
+//          locates the step (bisection over all patterns if it is not in
+//          that window); both forms agree on every input.
 //   amax = max |x| over non-outliers (wave shuffles)
 //   s    = max(fp16(amax / qmax), fp16(1e-6)), 1.0 if all are outliers
 //   code = clamp(rne(fp16(x / s)), +-127)  or  e4m3(clamp(fp16(x / s), +-448))
+//          (the e4m3 rounding by the hardware f32 -> fp8 conversion, which
+//          equals the round-to-nearest-even encoding on every fp16 in
+//          [-448, 448])
 // Outliers are compacted inside the team with a prefix sum (shuffles + LDS)
 // into a per-block staging slot; a scan over the per-block counts and a
 // gather pass then write the ascending outlier list.
@@ -48,6 +54,37 @@ struct QuantArgs {
   uint16_t* stage_val;
 };
 
+// E fp16 elements of one thread, two per 32-bit register (element 2i in
+// the low half); indices are compile-time constants after unrolling, so
+// reading an element costs at most a shift.
+template <int E>
+struct Elems {
+  uint32_t p[E / 2];
+  __device__ __forceinline__ f16 operator[](int e) const {
+    return bits_to_h((uint16_t)((e & 1) ? (p[e >> 1] >> 16) : (p[e >> 1] & 0xFFFFu)));
+  }
+  // Between passes: the compiler may no longer reuse values derived from
+  // the elements in an earlier pass (it would keep E converted copies live
+  // across the whole kernel); re-deriving them is a conversion each.
+  __device__ __forceinline__ void fence() {
+#pragma unroll
+    for (int i = 0; i < E / 2; i++) asm volatile("" : "+v"(p[i]));
+  }
+};
+
+// How much of a block a thread's E elements cover: every element of every
+// block (G is a power of two), all or none of a thread's elements (E
+// divides G), or any prefix.  The first two cases need no per-element
+// bounds tests.
+enum { kAnyLen = 0, kThreadAligned = 1, kFullBlocks = 2 };
+
+template <int MODE>
+__device__ __forceinline__ bool elem_valid(int i0, int e, int64_t G) {
+  if (MODE == kFullBlocks) return true;
+  if (MODE == kThreadAligned) return i0 < G;
+  return i0 + e < G;
+}
+
 // Balanced pairwise tree over 16 leaves.
 __device__ __forceinline__ double tree16(double (&v)[16]) {
 #pragma clang fp contract(off)
@@ -59,8 +96,8 @@ __device__ __forceinline__ double tree16(double (&v)[16]) {
 }
 
 // Balanced tree over the E leaves of one thread, E = 16 * C.
-template <int E>
-__device__ __forceinline__ double thread_tree_sum(const f16 (&xs)[E], int i0, int64_t G, bool sq, double mu) {
+template <int E, int MODE>
+__device__ __forceinline__ double thread_tree_sum(Elems<E>& xs, int i0, int64_t G, bool sq, double mu) {
 #pragma clang fp contract(off)
   constexpr int C = E / 16;
   double part[C];
@@ -69,15 +106,15 @@ __device__ __forceinline__ double thread_tree_sum(const f16 (&xs)[E], int i0, in
     double leaf[16];
 #pragma unroll
     for (int e = 0; e < 16; e++) {
-      const int i = i0 + c * 16 + e;
       double v = (double)(float)xs[c * 16 + e];
       if (sq) {
         double d = v - mu;
         v = d * d;
       }
-      leaf[e] = (i < G) ? v : 0.0;
+      leaf[e] = elem_valid<MODE>(i0, c * 16 + e, G) ? v : 0.0;
     }
     part[c] = tree16(leaf);
+    if (C > 1) xs.fence();  // one group of 16 double leaves live at a time
   }
 #pragma unroll
   for (int w = C; w > 1; w >>= 1)
@@ -92,14 +129,15 @@ struct BlockStats {
 
 // mean / std / std + eps of one block, as calculate_zscore_manual computes
 // them (the torch fp16 tensors mean, std and std + eps).
-template <int TAU, int E>
-__device__ __forceinline__ BlockStats block_stats(const f16 (&xs)[E], int i0, int64_t G, float eps,
+template <int TAU, int E, int MODE = kAnyLen>
+__device__ __forceinline__ BlockStats block_stats(Elems<E>& xs, int i0, int64_t G, float eps,
                                                   double* lds_d) {
 #pragma clang fp contract(off)
-  double s_loc = thread_tree_sum<E>(xs, i0, G, false, 0.0);
+  double s_loc = thread_tree_sum<E, MODE>(xs, i0, G, false, 0.0);
   double S = team_sum_f64<TAU>(s_loc, lds_d);
   double mu = S / (double)G;
-  double v_loc = thread_tree_sum<E>(xs, i0, G, true, mu);
+  xs.fence();
+  double v_loc = thread_tree_sum<E, MODE>(xs, i0, G, true, mu);
   double V = team_sum_f64<TAU>(v_loc, lds_d);
   double var = V / (double)(G - 1);
   BlockStats st;
@@ -133,34 +171,66 @@ __device__ float outlier_cut(f16 den, f16 thr) {
   return (float)bits_to_h((uint16_t)lo);
 }
 
+// Th for a team of TAU threads (the same value in every lane): lane j of the
+// team (j < 16) tests the bit pattern c0 - 8 + j, c0 = bits of fp16(thr * den).
+template <int TAU>
+__device__ float outlier_cut_team(f16 den, f16 thr) {
+  const float fden = (float)den;
+  if (!(fden > 0.0f) || isinf(fden)) return __builtin_nanf("");
+  if (outlier_literal(bits_to_h(0), den, thr)) return -1.0f;        // all are outliers
+  if (!outlier_literal(bits_to_h(0x7C00), den, thr)) return INFINITY;  // none
+  constexpr int W = TAU < 16 ? TAU : 16;
+  constexpr int TL = TAU < 64 ? TAU : 64;  // team lanes within one wave
+  const int lane = threadIdx.x & 63;
+  const int ts = lane & ~(TL - 1);  // the team's first lane in this wave
+  const int j = lane - ts;
+  const float est = (float)thr * fden;
+  const int c0 = est < 65504.0f ? (int)h_to_bits(rn_h(est)) : 0x7BFF;
+  const int cand = c0 - W / 2 + j;
+  // below 0 the test is false (checked at 0 above), past 0x7C00 true (checked at inf)
+  bool p = cand > 0x7C00 || (cand >= 0 && outlier_literal(bits_to_h((uint16_t)cand), den, thr));
+  p = p && j < W;
+  const uint64_t bal = __ballot(p);
+  const uint32_t bits = (uint32_t)(bal >> ts) & ((1u << W) - 1u);
+  if (bits != 0 && !(bits & 1u)) {
+    const int first = c0 - W / 2 + __builtin_ctz(bits);  // smallest pattern that passes
+    return (float)bits_to_h((uint16_t)(first - 1));
+  }
+  return outlier_cut(den, thr);
+}
+
 template <int E>
-__device__ __forceinline__ void load_elems(f16 (&xs)[E], const QuantArgs& a, int64_t base, int i0, bool gvalid) {
+__device__ __forceinline__ void load_elems(Elems<E>& xs, const QuantArgs& a, int64_t base, int i0, bool gvalid) {
   const bool full = gvalid && a.vec && (i0 + E <= a.G) && (base + i0 + E <= a.numel);
   if (full) {
+    // plain loads: each thread reads E / 8 consecutive 16-byte pieces, so a
+    // 128-byte line is touched by several load instructions in a row, and a
+    // non-temporal hint would make each of them fetch it again
     const uint4* src = reinterpret_cast<const uint4*>(a.x + base + i0);
 #pragma unroll
     for (int v = 0; v < E / 8; v++) {
-      uint4 u = ld_nt16(src + v);
-      uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        xs[v * 8 + 2 * k] = bits_to_h((uint16_t)(w[k] & 0xFFFFu));
-        xs[v * 8 + 2 * k + 1] = bits_to_h((uint16_t)(w[k] >> 16));
-      }
+      uint4 u = src[v];
+      xs.p[4 * v] = u.x;
+      xs.p[4 * v + 1] = u.y;
+      xs.p[4 * v + 2] = u.z;
+      xs.p[4 * v + 3] = u.w;
     }
   } else {
 #pragma unroll
-    for (int e = 0; e < E; e++) {
-      const int64_t i = i0 + e;
-      const int64_t j = base + i;
-      uint16_t b = 0;
-      if (gvalid && i < a.G && j < a.numel) b = a.x[j];
-      xs[e] = bits_to_h(b);
+    for (int e = 0; e < E; e += 2) {
+      uint32_t pair = 0;
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int64_t i = i0 + e + h;
+        const int64_t j = base + i;
+        if (gvalid && i < a.G && j < a.numel) pair |= (uint32_t)a.x[j] << (16 * h);
+      }
+      xs.p[e / 2] = pair;
     }
   }
 }
 
-template <int TAU, int E>
+template <int TAU, int E, int MODE>
 __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantArgs a) {
   constexpr int NT = TAU > kWG ? TAU : kWG;
   constexpr int TEAMS = NT / TAU;
@@ -177,30 +247,43 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
   const int64_t base = g * G;
   const int i0 = t * E;
 
-  f16 xs[E];
+  Elems<E> xs;
   load_elems<E>(xs, a, base, i0, gvalid);
 
-  const BlockStats st = block_stats<TAU, E>(xs, i0, G, 1e-6f, lds_d + team * NWT);
+  const BlockStats st = block_stats<TAU, E, MODE>(xs, i0, G, 1e-6f, lds_d + team * NWT);
+  xs.fence();
   const f16 thr = bits_to_h(a.thr_bits);
-  const float cut = outlier_cut(st.den16, thr);
+  const float cut = outlier_cut_team<TAU>(st.den16, thr);
   const bool literal = isnan(cut);
 
-  // outlier flags and the absmax of the rest
+  // outlier flags and the absmax of the rest, 16 elements at a time; the
+  // literal quotient only for blocks whose std + eps is not a positive
+  // finite number (a uniform branch, so the common path has no division)
   uint64_t omask = 0;
   float amax = -1.0f;
 #pragma unroll
-  for (int e = 0; e < E; e++) {
-    if (i0 + e < G) {
-      const f16 d = h_sub(xs[e], st.mean16);
-      const f16 ad = bits_to_h(h_to_bits(d) & 0x7FFFu);
-      const bool o = literal ? outlier_literal(ad, st.den16, thr) : ((float)ad > cut);
-      if (o)
-        omask |= 1ull << e;
-      else
-        amax = fmaxf(amax, fabsf((float)xs[e]));
+  for (int g16 = 0; g16 < E / 16; g16++) {
+#pragma unroll
+    for (int b = 0; b < 16; b++) {
+      const int e = 16 * g16 + b;
+      if (elem_valid<MODE>(i0, e, G)) {
+        const f16 d = h_sub(xs[e], st.mean16);
+        const f16 ad = bits_to_h(h_to_bits(d) & 0x7FFFu);
+        bool o;
+        if (literal)
+          o = outlier_literal(ad, st.den16, thr);
+        else
+          o = (float)ad > cut;
+        if (o)
+          omask |= 1ull << e;
+        else
+          amax = fmaxf(amax, fabsf((float)xs[e]));
+      }
     }
+    if (E > 16) xs.fence();
   }
   amax = team_max_f32<TAU>(amax, lds_f + team * NWT);
+  xs.fence();
 
   const float qmax = a.fmt == AQ_FMT_INT8 ? 127.0f : 448.0f;
   f16 s16 = (f16)1.0f;
@@ -211,46 +294,57 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
   const float s = (float)s16;
   const float r = 1.0f / s;
 
-  // codes
-  uint8_t c[E];
+  // codes, 16 elements at a time (four words in element order)
 #pragma unroll
-  for (int e = 0; e < E; e++) {
-    uint8_t code = 0;
-    if (!((omask >> e) & 1ull) && (i0 + e < G)) {
-      const f16 q = h_div_fast((float)xs[e], s, r);
-      if (a.fmt == AQ_FMT_INT8) {
-        float rr = __builtin_rintf((float)q);
-        rr = fminf(fmaxf(rr, -127.0f), 127.0f);
-        code = (uint8_t)(int8_t)(int)rr;
-      } else {
-        float qc = fminf(fmaxf((float)q, -448.0f), 448.0f);
-        code = e4m3_from_h(rn_h(qc));
-      }
-    }
-    c[e] = code;
-  }
-  if (gvalid) {
-    if (a.vec && i0 + E <= G) {
+  for (int v = 0; v < E / 16; v++) {
+    uint32_t w[4];
+    if (a.fmt == AQ_FMT_INT8) {
 #pragma unroll
-      for (int v = 0; v < E / 16; v++) {
-        uint32_t w[4];
+      for (int k = 0; k < 4; k++) {
+        uint32_t word = 0;
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-          w[k] = (uint32_t)c[v * 16 + 4 * k] | ((uint32_t)c[v * 16 + 4 * k + 1] << 8) |
-                 ((uint32_t)c[v * 16 + 4 * k + 2] << 16) | ((uint32_t)c[v * 16 + 4 * k + 3] << 24);
-        // 16 consecutive elements of one row land in 16 consecutive bytes of
-        // either layout
-        const int64_t j = base + i0 + 16 * v;
-        const int64_t off = a.tiled ? tiled_offset(j / a.K, j % a.K, a.nchunks) : j;
-        *reinterpret_cast<uint4*>(a.codes + off) = make_uint4(w[0], w[1], w[2], w[3]);
+        for (int b = 0; b < 4; b++) {
+          const int e = 16 * v + 4 * k + b;
+          uint32_t code = 0;
+          if (!((omask >> e) & 1ull) && elem_valid<MODE>(i0, e, G)) {
+            float rr = __builtin_rintf((float)h_div_fast((float)xs[e], s, r));
+            rr = fminf(fmaxf(rr, -127.0f), 127.0f);
+            code = (uint8_t)(int8_t)(int)rr;
+          }
+          word |= code << (8 * b);
+        }
+        w[k] = word;
       }
     } else {
+      float qv[16];
 #pragma unroll
-      for (int e = 0; e < E; e++)
-        if (i0 + e < G) {
-          const int64_t j = base + i0 + e;
-          a.codes[a.tiled ? tiled_offset(j / a.K, j % a.K, a.nchunks) : j] = c[e];
-        }
+      for (int b = 0; b < 16; b++) {
+        // outliers and padding get code 0 (+0.0)
+        const int e = 16 * v + b;
+        const float q = (float)h_div_fast((float)xs[e], s, r);
+        qv[b] = (!((omask >> e) & 1ull) && elem_valid<MODE>(i0, e, G)) ? __builtin_amdgcn_fmed3f(q, -448.0f, 448.0f)
+                                                                       : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(qv[4 * k], qv[4 * k + 1], 0, false);
+        w[k] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(qv[4 * k + 2], qv[4 * k + 3], lo, true);
+      }
+    }
+    if (E > 16) xs.fence();
+    if (gvalid) {
+      // 16 consecutive elements of one row land in 16 consecutive bytes of either layout
+      const int64_t j = base + i0 + 16 * v;
+      if (a.vec && i0 + E <= G) {
+        const int64_t off = a.tiled ? tiled_offset(j / a.K, j % a.K, a.nchunks) : j;
+        *reinterpret_cast<uint4*>(a.codes + off) = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+#pragma unroll
+        for (int b = 0; b < 16; b++)
+          if (i0 + 16 * v + b < G)
+            a.codes[a.tiled ? tiled_offset((j + b) / a.K, (j + b) % a.K, a.nchunks) : j + b] =
+                (uint8_t)(w[b / 4] >> (8 * (b % 4)));
+      }
     }
   }
 
@@ -264,8 +358,11 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
     while (m) {
       const int e = __builtin_ctzll(m);
       m &= m - 1;
+      // the value from memory (an L2 hit): indexing the registers with a
+      // run-time e would move them to scratch; padding elements are 0
+      const int64_t j = base + i0 + e;
       a.stage_col[base + k] = i0 + e;
-      a.stage_val[base + k] = h_to_bits(xs[e]);
+      a.stage_val[base + k] = j < a.numel ? a.x[j] : (uint16_t)0;
       k++;
     }
     if (t == 0) {
@@ -346,9 +443,11 @@ __global__ __launch_bounds__(TAU < 64 ? 64 : TAU) void zscore_kernel(const uint1
   const int t = threadIdx.x;
   if (t >= TAU) return;  // only when TAU < 64: the rest of the single wave sits out (no barriers then)
   const int i0 = t * E;
-  f16 xs[E];
+  Elems<E> xs;
 #pragma unroll
-  for (int e = 0; e < E; e++) xs[e] = bits_to_h(i0 + e < n ? x[i0 + e] : (uint16_t)0);
+  for (int e = 0; e < E; e += 2)
+    xs.p[e / 2] = (uint32_t)(i0 + e < n ? x[i0 + e] : (uint16_t)0) |
+                  ((uint32_t)(i0 + e + 1 < n ? x[i0 + e + 1] : (uint16_t)0) << 16);
   const BlockStats st = block_stats<TAU, E>(xs, i0, n, eps, lds_d);
 #pragma unroll
   for (int e = 0; e < E; e++)
@@ -371,30 +470,36 @@ hipError_t launch_quantize_t(const QuantArgs& a, hipStream_t stream) {
   constexpr int NT = TAU > kWG ? TAU : kWG;
   constexpr int TEAMS = NT / TAU;
   const int64_t grid = aq::ceil_div(a.nblocks, TEAMS);
-  hipLaunchKernelGGL((quantize_kernel<TAU, E>), dim3((unsigned)grid), dim3(NT), 0, stream, a);
+  if (a.G == (int64_t)TAU * E)
+    hipLaunchKernelGGL((quantize_kernel<TAU, E, kFullBlocks>), dim3((unsigned)grid), dim3(NT), 0, stream, a);
+  else if (a.G % E == 0)
+    hipLaunchKernelGGL((quantize_kernel<TAU, E, kThreadAligned>), dim3((unsigned)grid), dim3(NT), 0, stream, a);
+  else
+    hipLaunchKernelGGL((quantize_kernel<TAU, E, kAnyLen>), dim3((unsigned)grid), dim3(NT), 0, stream, a);
   return hipGetLastError();
 }
 
+// Team shape per padded block size P: up to 1024 elements, 16 per thread
+// (teams of at most one wave, several per workgroup); 2048, 32 per thread on
+// one wave; from 4096 on, 64 per thread (one wave for 4096, a block of
+// 4096 elements then needs no barrier at all).
 hipError_t launch_quantize(const QuantArgs& a, hipStream_t stream) {
   const int64_t P = next_pow2(a.G);
-  if (P <= 16384) {
-    const int64_t tau = P <= 16 ? 1 : P / 16;
-    switch (tau) {
-      case 1: return launch_quantize_t<1, 16>(a, stream);
-      case 2: return launch_quantize_t<2, 16>(a, stream);
-      case 4: return launch_quantize_t<4, 16>(a, stream);
-      case 8: return launch_quantize_t<8, 16>(a, stream);
-      case 16: return launch_quantize_t<16, 16>(a, stream);
-      case 32: return launch_quantize_t<32, 16>(a, stream);
-      case 64: return launch_quantize_t<64, 16>(a, stream);
-      case 128: return launch_quantize_t<128, 16>(a, stream);
-      case 256: return launch_quantize_t<256, 16>(a, stream);
-      case 512: return launch_quantize_t<512, 16>(a, stream);
-      default: return launch_quantize_t<1024, 16>(a, stream);
-    }
+  switch (P) {
+    case 1: case 2: case 4: case 8: case 16: return launch_quantize_t<1, 16>(a, stream);
+    case 32: return launch_quantize_t<2, 16>(a, stream);
+    case 64: return launch_quantize_t<4, 16>(a, stream);
+    case 128: return launch_quantize_t<8, 16>(a, stream);
+    case 256: return launch_quantize_t<16, 16>(a, stream);
+    case 512: return launch_quantize_t<32, 16>(a, stream);
+    case 1024: return launch_quantize_t<64, 16>(a, stream);
+    case 2048: return launch_quantize_t<64, 32>(a, stream);
+    case 4096: return launch_quantize_t<64, 64>(a, stream);
+    case 8192: return launch_quantize_t<128, 64>(a, stream);
+    case 16384: return launch_quantize_t<256, 64>(a, stream);
+    case 32768: return launch_quantize_t<512, 64>(a, stream);
+    default: return launch_quantize_t<1024, 64>(a, stream);
   }
-  if (P <= 32768) return launch_quantize_t<512, 64>(a, stream);
-  return launch_quantize_t<1024, 64>(a, stream);
 }
 
 template <int TAU, int E>

@@ -408,6 +408,28 @@ def test_signed_zeros_survive(oracle):
     assert np.array_equal(bits(z), bits(zr))
 
 
+def test_e4m3_codes_every_fp16_value(oracle):
+    """Every fp16 value in [-448, 448] quantized with scale 1 (each row holds
+    448, so amax / 448 = 1) and no outliers (threshold 60000): each code is
+    the E4M3 encoding of the value itself, checked against the oracle's
+    round-to-nearest-even encoder for all 48 642 values."""
+    pos = np.arange(0, 0x5F01, dtype=np.uint16)  # +0 .. 448
+    vals = np.concatenate([pos, pos | 0x8000]).view(np.float16)
+    K = 1024
+    rows = -(-vals.size // (K - 1))
+    rows += (-rows) % 16
+    w = np.zeros((rows, K), np.float16)
+    flat = w[:, 1:].reshape(-1)
+    flat[:vals.size] = vals
+    w[:, 1:] = flat.reshape(rows, K - 1)
+    w[:, 0] = 448.0
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, z_threshold=60000.0, code_format="e4m3")
+    assert q.outlier_indices.numel() == 0 and q.code_layout == "tiled"
+    assert np.all(bits(q.scale_factors) == 0x3C00)  # 1.0
+    ref = oracle.quantize(w, K, 60000.0, oracle.FMT_E4M3)
+    assert np.array_equal(bits(AQ.dense_codes(q, torch.device(DEV))), ref["codes"])
+
+
 def test_tile_untile_round_trip():
     from atlasinfer_amd import _lib
     L = _lib.load()

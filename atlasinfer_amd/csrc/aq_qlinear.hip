@@ -12,19 +12,18 @@
 // bias, then one rounding to fp16.
 //
 //  * M <= 16: dequant-GEMV.  One workgroup per 16-row tile row: NS waves
-//    stream its tiles (1 KiB contiguous per load instruction, four 128-wide
+//    stream its tiles (1 KiB contiguous per load instruction, two 128-wide
 //    K chunks in flight per wave) with the M rows of x as the MFMA A operand
 //    (rows >= M are zero), and their partial tiles are summed through LDS in
 //    a fixed order.  Wave 0 then stages the rows' CSR outlier lists and the
-//    x values they multiply into LDS for the epilogue.  NS is 4 for tall
-//    matrices (enough workgroups to fill the GPU) and 8 otherwise.  Several
-//    matrices that read the same x (q/k/v, gate/up) share one launch.
-//  * M > 16: dequant-GEMM.  128x128 output tile per workgroup of 4 waves
-//    (64x64 each), 128-wide K steps.  The x tile goes through LDS; each wave
-//    reads its four code tiles straight from HBM into registers (they are
-//    already in operand order), and the next step's x tile and codes are
-//    loaded while the current step is multiplied.  Outliers are applied
-//    inside the K loop from the LDS x tile, for the columns of the step.
+//    x values they multiply into LDS for the epilogue.  NS (1, 2, 4 or 8)
+//    gives the launch about 1536 waves: one per tile row for a tall group.
+//    Several matrices that read the same x (q/k/v, gate/up) share one
+//    launch.
+//  * M > 16: dequant-GEMM (details at its kernel below): 128 or 256 rows of
+//    x by 128 output columns per workgroup, x and decoded weights staged in
+//    LDS in MFMA operand order, each outlier written over its decoded zero,
+//    loads two 64-wide K chunks ahead.
 #include <algorithm>
 
 #include "aq_common.h"
@@ -107,7 +106,7 @@ __device__ __forceinline__ int scale_index(const QLMat& w, int n, int k) {
 
 // ------------------------------------------------------------ GEMV (M <= 16)
 
-constexpr int kGemvUnroll = 4;  // 128-wide K chunks per wave with loads in flight together
+constexpr int kGemvUnroll = 2;  // 128-wide K chunks per wave with loads in flight together
 // Staging capacity per workgroup (16 rows).  Kept small so that LDS does not
 // limit the workgroups resident per CU; entries beyond it (heavy-tailed
 // weights) are read from memory in the epilogue.
@@ -138,9 +137,8 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   const int nchunks = K >> 7;
 
   // Wave 0 also stages the rows' outliers.  Its row_ptr load goes out first;
-  // the (col, val) loads of up to 64 * kStageBatch entries go out after its
-  // first round of the stream, and for decode the x gather after the second,
-  // so they return while the codes stream in.
+  // the (col, val) loads of up to 64 * kStageBatch entries go out right after
+  // its first round of code loads, so they return while the codes stream in.
   int rp = 0;
   if (wave == 0 && lane <= 16) rp = W.row_ptr[n0 + lane];
   int p0 = 0, cnt = 0;
@@ -206,6 +204,10 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
           xq[u][3] = xp[9];
         }
       }
+      // wave 0's staging loads go out right behind the first code loads: the
+      // row_ptr wait does not wait for the codes (loads retire in order), and
+      // the codes' wait below then does not wait for the staging loads
+      if (wave == 0 && c0 == 0) stage_first_batch();
 #pragma unroll
       for (int u = 1; u < U; u++)
         if (c0 + u * NS >= nchunks)  // wave-uniform
@@ -223,9 +225,6 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][2]), w2, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][3]), w3, acc, 0, 0, 0);
       }
-      // Staging loads go out after this round's waits, so they never hold
-      // up a wait for code loads (the load counter retires in order).
-      if (wave == 0 && c0 == 0) stage_first_batch();
     }
     // C layout: lane l, element i -> m = 4*(l/16) + i, column l % 16
 #pragma unroll
@@ -287,9 +286,10 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   if (M == 1) {
     // decode: 16 threads per row split the row's outliers, then a fixed
     // 16-lane shuffle tree adds them up
-    if (threadIdx.x < 256) {
-      const int nl = threadIdx.x >> 4;
-      const int sub = threadIdx.x & 15;
+    // (256 work items: workgroups of fewer than 4 waves take several rounds)
+    for (int o = threadIdx.x; o < 256; o += 64 * NS) {
+      const int nl = o >> 4;
+      const int sub = o & 15;
       const int p0 = s_meta[0], cnt = s_meta[1], nx = s_meta[2];
       const int e1 = s_rp[nl + 1];
       float v = 0.0f;
@@ -317,34 +317,35 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
         W.y[n0 + nl] = h_to_bits(rn_h(v));
       }
     }
-  } else if (threadIdx.x < 256) {
-    const int o = threadIdx.x;
-    const int l = o >> 2;
-    const int m = 4 * (l >> 4) + (o & 3);
-    const int nl = l & 15;
-    const int n = n0 + nl;
-    if (m < M) {
-      float v = 0.0f;
-#pragma unroll
-      for (int w = 0; w < NS; w++) v += red[w][o];
-      const int p0 = s_meta[0], cnt = s_meta[1], nx = s_meta[2];
-      const int e1 = s_rp[nl + 1];
-      for (int e = s_rp[nl]; e < e1; e++) {
-        float xv, wv;
-        if (e < nx) {
-          xv = (float)bits_to_h(s_xv[e * M + m]);
-          wv = (float)bits_to_h(s_val[e]);
-        } else if (e < cnt) {
-          xv = (float)bits_to_h(a.x[(size_t)m * K + s_col[e]]);
-          wv = (float)bits_to_h(s_val[e]);
-        } else {  // more outliers than the staging holds: straight from memory
-          xv = (float)bits_to_h(a.x[(size_t)m * K + W.cols[p0 + e]]);
-          wv = (float)bits_to_h(W.vals[p0 + e]);
+  } else {
+    for (int o = threadIdx.x; o < 256; o += 64 * NS) {
+      const int l = o >> 2;
+      const int m = 4 * (l >> 4) + (o & 3);
+      const int nl = l & 15;
+      const int n = n0 + nl;
+      if (m < M) {
+        float v = 0.0f;
+  #pragma unroll
+        for (int w = 0; w < NS; w++) v += red[w][o];
+        const int p0 = s_meta[0], cnt = s_meta[1], nx = s_meta[2];
+        const int e1 = s_rp[nl + 1];
+        for (int e = s_rp[nl]; e < e1; e++) {
+          float xv, wv;
+          if (e < nx) {
+            xv = (float)bits_to_h(s_xv[e * M + m]);
+            wv = (float)bits_to_h(s_val[e]);
+          } else if (e < cnt) {
+            xv = (float)bits_to_h(a.x[(size_t)m * K + s_col[e]]);
+            wv = (float)bits_to_h(s_val[e]);
+          } else {  // more outliers than the staging holds: straight from memory
+            xv = (float)bits_to_h(a.x[(size_t)m * K + W.cols[p0 + e]]);
+            wv = (float)bits_to_h(W.vals[p0 + e]);
+          }
+          v = __builtin_fmaf(xv, wv, v);
         }
-        v = __builtin_fmaf(xv, wv, v);
+        if (W.bias) v += (float)bits_to_h(W.bias[n]);
+        W.y[(size_t)m * N + n] = h_to_bits(rn_h(v));
       }
-      if (W.bias) v += (float)bits_to_h(W.bias[n]);
-      W.y[(size_t)m * N + n] = h_to_bits(rn_h(v));
     }
   }
 }
@@ -733,8 +734,13 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
   for (int i = 0; i < count; i++) per_channel = per_channel && a.mat[i].kg == 1;
   if (M <= 16) {
     // tall groups fill the GPU with 4 streaming waves per tile row, short ones need 8
-    const hipError_t e = blocks >= 512 ? launch_gemv<4>(a, fmt, per_channel, (int)blocks, s)
-                                       : launch_gemv<8>(a, fmt, per_channel, (int)blocks, s);
+    // waves per tile row: enough for about 1536 waves in all (1.5 per SIMD),
+    // at most 8; a tall group (gate+up) streams one tile row per wave
+    const int64_t want = (1536 + blocks - 1) / blocks;
+    const hipError_t e = want <= 1 ? launch_gemv<1>(a, fmt, per_channel, (int)blocks, s)
+                       : want <= 2 ? launch_gemv<2>(a, fmt, per_channel, (int)blocks, s)
+                       : want <= 4 ? launch_gemv<4>(a, fmt, per_channel, (int)blocks, s)
+                                   : launch_gemv<8>(a, fmt, per_channel, (int)blocks, s);
     return aq::check_hip(e, "aq_qlinear: gemv launch");
   }
   // 32-bit buffer offsets: 128 rows of x (2 bytes each) and 8 tile rows of codes

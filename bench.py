@@ -8,10 +8,11 @@ fp16 outliers (W ~ N(0, 0.02), 0.1% entries +-U(8,20)*0.02; x ~ N(0,1) with
 4 input channels x30).  Four layers of distinct weights (873 MB of codes) are
 rotated so the 256 MB MALL cannot hold them.
 
-One step = the M=1 dequant-GEMV over the seven linears of one layer, replayed
-as a HIP graph in the decode-time launch pattern (q/k/v in one grouped launch,
-o, gate/up in one grouped launch, down).  ``value`` = algorithmic bytes per
-step / time per step.  The same JSON line carries the M=2048 dequant-GEMM
+One step = the M=1 dequant-GEMV over the seven linears of one layer in the
+decode-time launch pattern (q/k/v in one grouped launch, o, gate/up in one
+grouped launch, down).  The four rotated layers are captured in one HIP graph
+(as a decode step captures all of its layers) and replayed; ``value`` =
+algorithmic bytes per step / wall time per step.  The same JSON line carries the M=2048 dequant-GEMM
 throughput, the quantize-kernel throughput, hipBLASLt fp16 F.linear on the
 dequantized weights for comparison, the roofline of the GEMV and the
 reference's CPU path timed on this host.
@@ -96,6 +97,42 @@ def cpu_baseline(layer_w_cpu, budget_s=12.0):
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qlinear_gemv_gateup_llama3_8b_m1_traffic.txt")
+
+
+def time_quantize_kernel(weights, reps=5):
+    """The quantize kernel alone (aq_quantize: statistics, codes, outlier
+    staging and the scan of outlier counts), per-channel E4M3 into the tiled
+    layout, timed with HIP events on the launch stream over ``reps`` passes
+    of every weight; returns (algorithmic bytes, seconds) of one pass.
+    Bytes: 2 N K read + N K codes + 2 N scales + 6 per outlier staged."""
+    from atlasinfer_amd import _lib
+    from atlasinfer_amd.quant import adaptive_quantizer as AQ
+    L = _lib.load()
+    calls, nbytes = [], 0
+    for w in weights:
+        N, K = w.shape
+        numel = N * K
+        codes = torch.empty(numel, dtype=torch.uint8, device=w.device)
+        scales = torch.empty(N, dtype=torch.float16, device=w.device)
+        off = torch.empty(N + 1, dtype=torch.int32, device=w.device)
+        wsb = int(L.aq_quantize_workspace_size(numel, K))
+        ws = torch.empty(wsb, dtype=torch.uint8, device=w.device)
+        args = (w.data_ptr(), numel, K, AQ._threshold_bits(3.0), _lib.FMT_E4M3, K, _lib.LAYOUT_TILED,
+                codes.data_ptr(), scales.data_ptr(), off.data_ptr(), ws.data_ptr(), wsb)
+        calls.append((args, (codes, scales, off, ws)))
+        _lib.check(L.aq_quantize(*args, _lib.stream_of(w.device)), "aq_quantize")
+        torch.cuda.synchronize()
+        nnz = int(off[N].item())
+        nbytes += 3 * numel + 2 * N + 6 * nnz
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        for args, _keep in calls:
+            L.aq_quantize(*args, stream.cuda_stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return nbytes, e0.elapsed_time(e1) / 1e3 / reps
 
 
 def measured_traffic():
@@ -231,40 +268,51 @@ def main():
     step_bytes = [sum(gemv_bytes(layer[name], 1) for name, _, _ in LLAMA_LINEARS) for layer in layers]
 
     def time_graphs(grouped, steps, warmup):
+        """All rotated layers in one HIP graph, as a captured decode step holds
+        all of its layers (a replay is N_LAYERS steps), plus a graph of the
+        first steps % N_LAYERS layers, so exactly ``steps`` steps are timed.
+        Returns (wall seconds, event seconds, steps timed)."""
         for layer in layers:
             layer_launches(layer, grouped)
         torch.cuda.synchronize()
-        graphs = []
-        for layer in layers:
+
+        def capture(ls):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                layer_launches(layer, grouped)
-            graphs.append(g)
-        for i in range(warmup):
-            graphs[i % N_LAYERS].replay()
+                for layer in ls:
+                    layer_launches(layer, grouped)
+            return g
+
+        g_all = capture(layers)
+        rem = steps % N_LAYERS
+        g_rem = capture(layers[:rem]) if rem else None
+        for _ in range(max(warmup // N_LAYERS, 1)):
+            g_all.replay()
         torch.cuda.synchronize()
+        reps = steps // N_LAYERS
         stream = torch.cuda.current_stream(dev)
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        ev[0].record(stream)
-        for i in range(steps):
-            graphs[i % N_LAYERS].replay()
-            ev[i + 1].record(stream)
+        e0.record(stream)
+        for _ in range(reps):
+            g_all.replay()
+        if g_rem is not None:
+            g_rem.replay()
+        e1.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        gpu_s = sum(ev[i].elapsed_time(ev[i + 1]) for i in range(steps)) / 1e3
-        return wall, gpu_s
+        return wall, e0.elapsed_time(e1) / 1e3, steps
 
-    wall, gpu_s = time_graphs(True, args.steps, args.warmup)
+    wall, gpu_s, nsteps = time_graphs(True, args.steps, args.warmup)
     dom_bytes, dom_s = time_dominant(layers, xs[4096], qlinear_grouped, args.steps, args.warmup)
-    wall7, gpu7 = time_graphs(False, max(args.steps // 2, 1), args.warmup)
-    total_bytes = sum(step_bytes[i % N_LAYERS] for i in range(args.steps))
+    wall7, gpu7, nsteps7 = time_graphs(False, max(args.steps // 2, 1), args.warmup)
+    total_bytes = sum(step_bytes[i % N_LAYERS] for i in range(nsteps))
     value = total_bytes / wall / 1e9
     achieved = dom_bytes / dom_s / 1e9
-    sep_bytes = sum(step_bytes[i % N_LAYERS] for i in range(max(args.steps // 2, 1)))
-    log(f"M=1 GEMV (4 launches/layer): {value:.1f} GB/s wall, {achieved:.1f} GB/s by events, "
-        f"step {1e6 * wall / args.steps:.1f} us; 7 launches/layer: {sep_bytes / gpu7 / 1e9:.1f} GB/s; "
+    sep_bytes = sum(step_bytes[i % N_LAYERS] for i in range(nsteps7))
+    log(f"M=1 GEMV (4 launches/layer): {value:.1f} GB/s wall, {total_bytes / gpu_s / 1e9:.1f} GB/s by events, "
+        f"step {1e6 * wall / nsteps:.1f} us; 7 launches/layer: {sep_bytes / gpu7 / 1e9:.1f} GB/s; "
         f"gate+up kernel {1e6 * dom_s:.2f} us/launch, {achieved:.1f} GB/s")
 
     # ---- hipBLASLt fp16 F.linear on the dequantized layer-0 weights, M=1
@@ -278,6 +326,9 @@ def main():
         e1.record()
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / 1e3 / iters
+
+    qk_bytes, qk_s = time_quantize_kernel([keep_fp16[name] for name, _, _ in LLAMA_LINEARS])
+    log(f"quantize kernel: {qk_bytes / qk_s / 1e9:.1f} GB/s ({1e6 * qk_s:.1f} us per layer)")
 
     blas_m1_s = 0.0
     for name, N, K in LLAMA_LINEARS:
@@ -326,9 +377,9 @@ def main():
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": nsteps,
         "warmup": args.warmup,
-        "ms_per_step": round(1e3 * wall / args.steps, 4),
+        "ms_per_step": round(1e3 * wall / nsteps, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -339,7 +390,7 @@ def main():
                    "block": "per-output-channel", "code_format": "e4m3", "z_threshold": 3.0},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "qlinear_gemv_kernel<4,E4M3,per-channel>: gate+up grouped, 2x[14336,4096], M=1",
+                     "kernel": "qlinear_gemv_kernel (one wave per 16-row tile, E4M3, per-channel): gate+up grouped, 2x[14336,4096], M=1",
                      "algorithmic_bytes_per_launch": dom_bytes, "us_per_launch": round(1e6 * dom_s, 3)},
         "cpu_baseline": cpu,
         "extra": {
@@ -347,12 +398,15 @@ def main():
             "gemm_m2048_frac_fp16_peak": round(gemm_tflops / FP16_PEAK_TFLOPS, 4),
             "hipblaslt_fp16_m2048_tflops": round(blas_tflops, 1),
             "hipblaslt_fp16_m1_us_per_layer": round(blas_m1_s * 1e6, 1),
-            "gemv_m1_us_per_layer_events": round(1e6 * gpu_s / args.steps, 2),
+            "gemv_m1_us_per_layer_events": round(1e6 * gpu_s / nsteps, 2),
             "gemv_m1_layer_GBps_events": round(total_bytes / gpu_s / 1e9, 1),
             "gemv_m1_7launch_GBps": round(sep_bytes / gpu7 / 1e9, 1),
-            "gemv_m1_7launch_us_per_layer": round(1e6 * gpu7 / max(args.steps // 2, 1), 2),
+            "gemv_m1_7launch_us_per_layer": round(1e6 * gpu7 / nsteps7, 2),
+            "quantize_kernel_GBps": round(qk_bytes / qk_s / 1e9, 1),
+            "quantize_kernel_frac_hbm_peak": round(qk_bytes / qk_s / 1e9 / HBM_PEAK_GBS, 4),
+            "quantize_kernel_note": "aq_quantize over the 7 layer-0 weights, per-channel e4m3, events",
             "quantize_GBps": round(q_bytes / q_time / 1e9, 1),
-            "quantize_note": "whole quantize_tensor call incl. host sync and outlier gather, per-channel e4m3",
+            "quantize_note": "whole quantize_tensor call incl. host sync, outlier gather and block lists",
             "sweep": sweep or None,
         },
     }

@@ -199,6 +199,107 @@ def kernel_only(args, dev, gen, qlinear_grouped, AQ):
           flush=True)
 
 
+def plant_outliers(model, gen, sigma=0.02, frac=0.001):
+    """BASELINE weight recipe on a random-init model: every Linear weight
+    gets round(frac * numel) entries replaced by +-U(8, 20) * sigma."""
+    with torch.no_grad():
+        for mod in model.modules():
+            if isinstance(mod, torch.nn.Linear):
+                w = mod.weight.view(-1)
+                k = int(round(frac * w.numel()))
+                pos = torch.randint(0, w.numel(), (k,), generator=gen, device=w.device)
+                sign = torch.where(torch.rand(k, generator=gen, device=w.device) < 0.5, -1.0, 1.0)
+                w[pos] = (sign * (torch.rand(k, generator=gen, device=w.device) * 12 + 8) * sigma).to(w.dtype)
+
+
+def generate_tokps(model, ids, new_tokens):
+    """Greedy HF generate (eager, batch of ids): decode tokens per second per
+    sequence, the prompt's forward pass subtracted."""
+    with torch.no_grad():
+        model(ids)  # warm
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model(ids)
+        torch.cuda.synchronize()
+        t_prefill = time.perf_counter() - t0
+        model.generate(ids, max_new_tokens=4, min_new_tokens=4, do_sample=False, pad_token_id=0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.generate(ids, max_new_tokens=new_tokens, min_new_tokens=new_tokens, do_sample=False, pad_token_id=0)
+        torch.cuda.synchronize()
+        t = time.perf_counter() - t0
+    return new_tokens / max(t - t_prefill, 1e-9), t_prefill
+
+
+def linear_flops(model, tokens):
+    return sum(2 * m.in_features * m.out_features for m in model.modules() if isinstance(m, torch.nn.Linear)) * tokens
+
+
+def bench_models(dev, which, log):
+    """BASELINE configs 1 (OPT-1.3b, every Linear quantized, 32-token prompt,
+    128 greedy tokens, batch 1) and 3 (Mistral-7B, 512-token prompts, 256
+    greedy tokens, batch 1/8/32; prefill TFLOP/s of the linears): random-init
+    weights with planted outliers, fp16 model against the same model with its
+    Linears swapped by apply_atlas_quantization_to_model (per-channel E4M3).
+    HF generate runs eagerly: tok/s there includes the framework's per-token
+    Python work, identical in both columns."""
+    from transformers import MistralConfig, MistralForCausalLM, OPTConfig, OPTForCausalLM
+    from atlasinfer_amd.integration.model_modifier import apply_atlas_quantization_to_model
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(7)
+    qcfg = {"block_size": -1, "z_threshold": 3.0, "code_format": "e4m3"}
+    if "opt" in which:
+        cfg = OPTConfig(num_hidden_layers=24, hidden_size=2048, num_attention_heads=32, ffn_dim=8192,
+                        vocab_size=50272, max_position_embeddings=2048, word_embed_proj_dim=2048)
+        torch.manual_seed(0)
+        with torch.device(dev):
+            model = OPTForCausalLM(cfg).half().eval()
+        plant_outliers(model, gen)
+        ids = torch.randint(0, cfg.vocab_size, (1, 32), generator=gen, device=dev)
+        fp16_tps, _ = generate_tokps(model, ids, 128)
+        t0 = time.perf_counter()
+        rep, fail = apply_atlas_quantization_to_model(model, "opt", qcfg, excluded_layers=[])
+        torch.cuda.synchronize()
+        t_q = time.perf_counter() - t0
+        q_tps, _ = generate_tokps(model, ids, 128)
+        out["opt1.3b"] = {"decode_tok_s": round(q_tps, 1), "fp16_decode_tok_s": round(fp16_tps, 1),
+                          "linears_quantized": rep, "failed": fail, "quantize_s": round(t_q, 2),
+                          "prompt": 32, "new_tokens": 128, "batch": 1}
+        log(f"OPT-1.3b: {out['opt1.3b']}")
+        del model
+        torch.cuda.empty_cache()
+    if "mistral" in which:
+        cfg = MistralConfig(num_hidden_layers=32, hidden_size=4096, num_attention_heads=32, num_key_value_heads=8,
+                            head_dim=128, intermediate_size=14336, vocab_size=32000, rope_theta=1e6,
+                            max_position_embeddings=4096)
+        torch.manual_seed(0)
+        with torch.device(dev):
+            model = MistralForCausalLM(cfg).half().eval()
+        plant_outliers(model, gen)
+        res = {}
+        for phase in ("fp16", "quantized"):
+            if phase == "quantized":
+                t0 = time.perf_counter()
+                rep, fail = apply_atlas_quantization_to_model(model, "mistral", qcfg)
+                torch.cuda.synchronize()
+                res["quantize_s"] = round(time.perf_counter() - t0, 2)
+                res["linears_quantized"] = rep
+                res["failed"] = fail
+            for B in (1, 8, 32):
+                ids = torch.randint(0, cfg.vocab_size, (B, 512), generator=gen, device=dev)
+                tps, t_pre = generate_tokps(model, ids, 256)
+                flops = linear_flops(model, B * 512) if phase == "fp16" else res[f"fp16_b{B}_prefill_flops"]
+                res[f"{phase}_b{B}_decode_tok_s"] = round(tps * B, 1)
+                res[f"{phase}_b{B}_prefill_tflops"] = round(flops / t_pre / 1e12, 1)
+                if phase == "fp16":
+                    res[f"fp16_b{B}_prefill_flops"] = flops
+                log(f"Mistral-7B {phase} batch {B}: {tps * B:.1f} tok/s decode, prefill {flops / t_pre / 1e12:.1f} TFLOP/s")
+        out["mistral7b"] = {k: v for k, v in res.items() if "prefill_flops" not in k}
+        del model
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -207,6 +308,8 @@ def main():
     ap.add_argument("--sweep", action="store_true", help="also time M in {4,16,64,512} per shape")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--models", default="", help="comma list of opt,mistral: also run BASELINE configs 1 / 3 "
+                                                  "(HF generate on random-init models; a few minutes)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant kernel (gate+up grouped GEMV, 4 rotated layers) and a 512 MiB "
                          "calibration copy, for counter runs")
@@ -362,6 +465,12 @@ def main():
                              "TFLOP/s": round(2 * Ms * N * K / s / 1e12, 1)}
             sweep[str(Ms)] = per
 
+    models = None
+    if args.models:
+        import contextlib
+        with contextlib.redirect_stdout(sys.stderr):  # stdout carries only the result line
+            models = bench_models(dev, args.models.split(","), log)
+
     # ---- the reference's CPU path on this host (warm F.linear, M=1)
     cpu = None
     if not args.no_cpu:
@@ -408,6 +517,7 @@ def main():
             "quantize_GBps": round(q_bytes / q_time / 1e9, 1),
             "quantize_note": "whole quantize_tensor call incl. host sync, outlier gather and block lists",
             "sweep": sweep or None,
+            "models": models,
         },
     }
     print(json.dumps(result), flush=True)

@@ -20,7 +20,10 @@
 //    gives the launch about 1536 waves: one per tile row for a tall group.
 //    Several matrices that read the same x (q/k/v, gate/up) share one
 //    launch.
-//  * M > 16: dequant-GEMM (details at its kernel below): 128 or 256 rows of
+//  * 16 < M <= 64: the same streaming, but 8 waves per workgroup share each
+//    chunk of x through LDS (details at its kernel below), since x is then
+//    larger than the codes it multiplies.
+//  * M > 64: dequant-GEMM (details at its kernel below): 128 or 256 rows of
 //    x by 128 output columns per workgroup, x and decoded weights staged in
 //    LDS in MFMA operand order, each outlier written over its decoded zero,
 //    loads two 64-wide K chunks ahead.
@@ -104,8 +107,9 @@ __device__ __forceinline__ int scale_index(const QLMat& w, int n, int k) {
   return n * w.kg + (w.gshift >= 0 ? (k >> w.gshift) : (k / w.G));
 }
 
-// ------------------------------------------------------------ GEMV (M <= 16)
+// ------------------------------------------------------------ GEMV (M <= 64)
 
+constexpr int kGemvMaxM = 64;   // larger M takes the GEMM
 constexpr int kGemvUnroll = 2;  // 128-wide K chunks per wave with loads in flight together
 // Staging capacity per workgroup (16 rows).  Kept small so that LDS does not
 // limit the workgroups resident per CU; entries beyond it (heavy-tailed
@@ -114,10 +118,10 @@ constexpr int kCsrCap = 1024;   // outlier entries
 constexpr int kXvCap = 1024;    // staged x values: entries * M <= kXvCap
 constexpr int kStageBatch = 8;  // entries per lane whose loads are issued together
 
-template <int NS, int FMT, int PC>
+template <int NS, int FMT, int PC, int MG>
 __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   constexpr int U = kGemvUnroll;
-  __shared__ float red[NS][256];
+  __shared__ float red[NS][256 * MG];
   __shared__ int s_rp[17];
   __shared__ int s_meta[3];  // p0, staged entries, entries with staged x
   __shared__ int s_col[kCsrCap];
@@ -172,14 +176,16 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
     const int grp = lane >> 4;
     const int li = lane & 15;
     const int n = n0 + li;
-    const bool mvalid = li < M;
     const uint8_t* tiles = W.codes + ((size_t)rb * nchunks << 11) + lane * 16;
+    // x rows 16 gi + li of each 16-row group gi (rows >= M stay zero)
     const uint16_t* xrow = a.x + (size_t)li * K + 16 * grp;
     const uint16_t sb_row = PC ? W.scales[n] : (uint16_t)0;
-    float4v acc = (float4v){0.f, 0.f, 0.f, 0.f};
+    float4v acc[MG];
+#pragma unroll
+    for (int gi = 0; gi < MG; gi++) acc[gi] = (float4v){0.f, 0.f, 0.f, 0.f};
     for (int c0 = wave; c0 < nchunks; c0 += U * NS) {
       uint4 q[U][2];
-      uint4 xq[U][4];
+      uint4 xq[U][MG][4];
       uint16_t sb[U][2];
 #pragma unroll
       for (int u = 0; u < U; u++) {
@@ -195,13 +201,16 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
           sb[u][1] = W.scales[scale_index(W, n, cc * 128 + 64 + 16 * grp)];
         }
 #pragma unroll
-        for (int j = 0; j < 4; j++) xq[u][j] = make_uint4(0, 0, 0, 0);
-        if (mvalid) {
-          const uint4* xp = reinterpret_cast<const uint4*>(xrow + cc * 128);
-          xq[u][0] = xp[0];
-          xq[u][1] = xp[1];
-          xq[u][2] = xp[8];  // + 64 columns
-          xq[u][3] = xp[9];
+        for (int gi = 0; gi < MG; gi++) {
+#pragma unroll
+          for (int j = 0; j < 4; j++) xq[u][gi][j] = make_uint4(0, 0, 0, 0);
+          if (16 * gi + li < M) {
+            const uint4* xp = reinterpret_cast<const uint4*>(xrow + (size_t)16 * gi * K + cc * 128);
+            xq[u][gi][0] = xp[0];
+            xq[u][gi][1] = xp[1];
+            xq[u][gi][2] = xp[8];  // + 64 columns
+            xq[u][gi][3] = xp[9];
+          }
         }
       }
       // wave 0's staging loads go out right behind the first code loads: the
@@ -212,7 +221,9 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       for (int u = 1; u < U; u++)
         if (c0 + u * NS >= nchunks)  // wave-uniform
 #pragma unroll
-          for (int j = 0; j < 4; j++) xq[u][j] = make_uint4(0, 0, 0, 0);
+          for (int gi = 0; gi < MG; gi++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) xq[u][gi][j] = make_uint4(0, 0, 0, 0);
 #pragma unroll
       for (int u = 0; u < U; u++) {
         const half2v s0 = scale2(sb[u][0]), s1 = scale2(sb[u][1]);
@@ -220,15 +231,20 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
         const half8 w1 = deq8<FMT>(q[u][0].z, q[u][0].w, s0);
         const half8 w2 = deq8<FMT>(q[u][1].x, q[u][1].y, s1);
         const half8 w3 = deq8<FMT>(q[u][1].z, q[u][1].w, s1);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][0]), w0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][1]), w1, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][2]), w2, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][3]), w3, acc, 0, 0, 0);
+#pragma unroll
+        for (int gi = 0; gi < MG; gi++) {
+          acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][gi][0]), w0, acc[gi], 0, 0, 0);
+          acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][gi][1]), w1, acc[gi], 0, 0, 0);
+          acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][gi][2]), w2, acc[gi], 0, 0, 0);
+          acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][gi][3]), w3, acc[gi], 0, 0, 0);
+        }
       }
     }
-    // C layout: lane l, element i -> m = 4*(l/16) + i, column l % 16
+    // C layout: lane l, element i -> m = 16 gi + 4*(l/16) + i, column l % 16
 #pragma unroll
-    for (int i = 0; i < 4; i++) red[wave][lane * 4 + i] = acc[i];
+    for (int gi = 0; gi < MG; gi++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) red[wave][gi * 256 + lane * 4 + i] = acc[gi][i];
   }
 
   if (wave == 0) {
@@ -318,9 +334,9 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       }
     }
   } else {
-    for (int o = threadIdx.x; o < 256; o += 64 * NS) {
-      const int l = o >> 2;
-      const int m = 4 * (l >> 4) + (o & 3);
+    for (int o = threadIdx.x; o < 256 * MG; o += 64 * NS) {
+      const int l = (o & 255) >> 2;
+      const int m = 16 * (o >> 8) + 4 * (l >> 4) + (o & 3);
       const int nl = l & 15;
       const int n = n0 + nl;
       if (m < M) {
@@ -350,7 +366,191 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   }
 }
 
-// ------------------------------------------------------------ GEMM (M > 16)
+// ------------------------------------------- GEMV with x in LDS (16 < M <= 64)
+//
+// With more than 16 rows of x, re-reading x per 16-row tile row would cost
+// far more than the codes (2 M bytes per weight column against 1).  Here a
+// workgroup of 8 waves takes TR = 8 / S tile rows with S waves each; wave
+// (tr, s) streams the codes of tile row tr over the chunks c = S j + s.  For
+// each chunk group j the workgroup stages x[16 MG rows][S chunks] in LDS
+// once, for all TR tile rows, and each wave feeds each decoded fragment to
+// one MFMA per 16-row group of x.  All loads are buffer loads: a workgroup
+// barrier does not wait for them, so the loads of groups j + 1 and j + 2 stay
+// in flight while group j is computed, and the zero that an out-of-range
+// buffer load returns stands in for the rows of x past M, the chunks past K
+// and the tile rows past N (no memory is read for them).  The S partial
+// sums meet in LDS; outliers are added per lane in the epilogue, where a
+// lane owns one output column and 4 MG of its rows.
+
+constexpr int kXWaves = 8;
+constexpr int kXPad = 8;             // halves of padding per LDS row of x
+constexpr uint32_t kOutOfRange = 0x80000000u;  // a buffer offset past every range used here
+constexpr int kBufferDword3 = 0x00020000;      // raw (untyped) buffer access on gfx9
+
+template <int FMT, int PC, int MG, int S>
+__global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) {
+  constexpr int TR = kXWaves / S;
+  constexpr int XR = 16 * MG;              // staged rows of x
+  constexpr int XW = S * 128 + kXPad;      // LDS row pitch (halves)
+  constexpr int XP = XR * S * 16 / (64 * kXWaves);  // 16-byte x pieces per thread and group
+  static_assert(XP >= 1, "x pieces");
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][XR * XW];
+
+  int mi = 0;
+#pragma unroll
+  for (int j = 1; j < kMaxGroup; j++)
+    if (j < a.count && (int)blockIdx.x >= a.first[j]) mi = j;
+  const QLMat W = pick(a, mi);
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int tr = wave % TR, sp = wave / TR;
+  const int M = a.M, K = a.K, N = W.N;
+  const int nchunks = K >> 7;
+  const int nrb = N / 16;
+  const int rb0 = (blockIdx.x - a.first[mi]) * TR;
+  const int rows_here = min(TR, nrb - rb0);  // tile rows of this workgroup inside N
+  const int grp = lane >> 4, li = lane & 15;
+  const int ngroups = (nchunks + S - 1) / S;
+  const int nsteps = (ngroups + 1) & ~1;    // even: the loop body handles two groups
+
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, M * K * 2, kBufferDword3);
+  const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W.codes + ((size_t)rb0 * nchunks << 11)), (short)0, rows_here * nchunks * 2048, kBufferDword3);
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W.scales + (size_t)rb0 * 16 * W.kg), (short)0, rows_here * 16 * W.kg * 2, kBufferDword3);
+  // tile rows past N: every code load of the wave is out of range (zero)
+  const uint32_t code_base = tr < rows_here ? (uint32_t)(tr * nchunks * 2048 + lane * 16) : kOutOfRange;
+  const uint32_t scale_row = (uint32_t)(tr * 16 + li) * W.kg;
+  uint16_t sb_row = 0;
+  if (PC) sb_row = tr < rows_here ? W.scales[(size_t)(rb0 + tr) * 16 + li] : (uint16_t)0;
+
+  struct Slot {
+    u32x4 q0, q1;
+    uint32_t s0, s1;
+    u32x4 x[XP];
+  };
+  auto load = [&](Slot& sl, int j) {
+    const int c = j * S + sp;
+    const uint32_t co = c < nchunks ? code_base + (uint32_t)c * 2048 : kOutOfRange;
+    sl.q0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co, 0, 0));
+    sl.q1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co + 1024, 0, 0));
+    if (!PC) {
+      const uint32_t k = (uint32_t)(c < nchunks ? c : 0) * 128 + 16 * grp;
+      const uint32_t k0 = W.gshift >= 0 ? k >> W.gshift : k / W.G;
+      const uint32_t k1 = W.gshift >= 0 ? (k + 64) >> W.gshift : (k + 64) / W.G;
+      sl.s0 = __builtin_amdgcn_raw_buffer_load_b16(sr, (scale_row + k0) * 2, 0, 0);
+      sl.s1 = __builtin_amdgcn_raw_buffer_load_b16(sr, (scale_row + k1) * 2, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < XP; i++) {
+      const int p = t + 64 * kXWaves * i;
+      const int row = p / (S * 16), col = (p % (S * 16)) * 8 + j * S * 128;
+      // rows past M fall past the end of the range by themselves
+      const uint32_t xo = col < K ? (uint32_t)(row * K + col) * 2 : kOutOfRange;
+      sl.x[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo, 0, 0));
+    }
+  };
+
+  float4v acc[MG];
+#pragma unroll
+  for (int gi = 0; gi < MG; gi++) acc[gi] = (float4v){0.f, 0.f, 0.f, 0.f};
+
+  auto step = [&](Slot& sl, int j, uint16_t* xb) {
+    const half2v s0 = scale2(PC ? sb_row : (uint16_t)sl.s0);
+    const half2v s1 = scale2(PC ? sb_row : (uint16_t)sl.s1);
+    const half8 w0 = deq8<FMT>(sl.q0.x, sl.q0.y, s0);
+    const half8 w1 = deq8<FMT>(sl.q0.z, sl.q0.w, s0);
+    const half8 w2 = deq8<FMT>(sl.q1.x, sl.q1.y, s1);
+    const half8 w3 = deq8<FMT>(sl.q1.z, sl.q1.w, s1);
+#pragma unroll
+    for (int i = 0; i < XP; i++) {
+      const int p = t + 64 * kXWaves * i;
+      *reinterpret_cast<u32x4*>(xb + (p / (S * 16)) * XW + (p % (S * 16)) * 8) = sl.x[i];
+    }
+    __syncthreads();
+    // unconditional: past the last group every offset is out of range, so the
+    // loads read nothing, and the compiler keeps its partial waits
+    __builtin_amdgcn_sched_barrier(0);
+    load(sl, j + 2);
+    __builtin_amdgcn_sched_barrier(0);  // the next group's decode stays below these loads
+    const uint16_t* xw = xb + sp * 128 + 16 * grp;
+#pragma unroll
+    for (int gi = 0; gi < MG; gi++) {
+      // A operand: x row 16 gi + li at columns 16 grp + {0, 8, 64, 72} of this wave's chunk
+      const uint16_t* xp = xw + (16 * gi + li) * XW;
+      acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(xp), w0, acc[gi], 0, 0, 0);
+      acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(xp + 8), w1, acc[gi], 0, 0, 0);
+      acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(xp + 64), w2, acc[gi], 0, 0, 0);
+      acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(xp + 72), w3, acc[gi], 0, 0, 0);
+    }
+  };
+
+  Slot sa, sb;
+  load(sa, 0);
+  load(sb, 1);
+  for (int j = 0; j < nsteps; j += 2) {
+    step(sa, j, xs[0]);
+    step(sb, j + 1, xs[1]);
+  }
+
+  // the S partial sums of each tile row meet in LDS (x is no longer read)
+  float* red = reinterpret_cast<float*>(&xs[0][0]);
+  if (S > 1) {
+    __syncthreads();
+    if (sp > 0)
+#pragma unroll
+      for (int gi = 0; gi < MG; gi++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) red[(((sp - 1) * TR + tr) * MG + gi) * 256 + i * 64 + lane] = acc[gi][i];
+    __syncthreads();
+    if (sp == 0)
+      for (int s2 = 1; s2 < S; s2++)
+#pragma unroll
+        for (int gi = 0; gi < MG; gi++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[gi][i] += red[(((s2 - 1) * TR + tr) * MG + gi) * 256 + i * 64 + lane];
+  }
+  if (sp != 0 || tr >= rows_here) return;  // no barrier follows
+
+  // C layout: lane l, element i -> row m = 16 gi + 4 (l / 16) + i, column n = n0 + l % 16.
+  // Outliers of row n, eight entries at a time: their loads, then all the x
+  // loads they need, then the FMAs.
+  const int n = (rb0 + tr) * 16 + li;
+  const int p_end = W.row_ptr[n + 1];
+  for (int p = W.row_ptr[n]; p < p_end; p += 8) {
+    int col[8];
+    float wv[8];
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+      const int e = min(p + b, p_end - 1);  // loads stay unconditional
+      col[b] = W.cols[e];
+      wv[b] = p + b < p_end ? (float)bits_to_h(W.vals[e]) : 0.0f;
+    }
+#pragma unroll
+    for (int gi = 0; gi < MG; gi++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int m = min(16 * gi + 4 * grp + i, M - 1);
+        float xg[8];
+#pragma unroll
+        for (int b = 0; b < 8; b++) xg[b] = (float)bits_to_h(a.x[(size_t)m * K + col[b]]);
+#pragma unroll
+        for (int b = 0; b < 8; b++) acc[gi][i] = __builtin_fmaf(xg[b], wv[b], acc[gi][i]);
+      }
+  }
+  const float bv = W.bias ? (float)bits_to_h(W.bias[n]) : 0.0f;
+#pragma unroll
+  for (int gi = 0; gi < MG; gi++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int m = 16 * gi + 4 * grp + i;
+      if (m < M) W.y[(size_t)m * N + n] = h_to_bits(rn_h(acc[gi][i] + bv));
+    }
+}
+
+// ------------------------------------------------------------ GEMM (M > 64)
 //
 // Workgroup tile BM x 128: WAVES waves in a (WAVES/2) x 2 layout of 64 x 64
 // wave tiles (16x16 MFMA tiles); BM = 128 with 4 waves (two workgroups per
@@ -408,7 +608,6 @@ struct GemmSrc {
   int so[CP];  // scale row of each code piece, in bytes
 };
 
-constexpr int kBufferDword3 = 0x00020000;  // raw (untyped) buffer access on gfx9
 
 template <int WAVES>
 __device__ __forceinline__ void gemm_src_init(GemmSrc<WAVES>& S, const QLMat& W, const uint16_t* x, int K, int m_first,
@@ -632,19 +831,55 @@ int log2_exact(int64_t g) {
   return s;
 }
 
-template <int NS, int FMT>
+template <int NS, int FMT, int MG>
 hipError_t launch_gemv(const QLArgs& a, bool per_channel, int blocks, hipStream_t s) {
   if (per_channel)
-    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1>), dim3(blocks), dim3(64 * NS), 0, s, a);
+    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, MG>), dim3(blocks), dim3(64 * NS), 0, s, a);
   else
-    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0>), dim3(blocks), dim3(64 * NS), 0, s, a);
+    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, MG>), dim3(blocks), dim3(64 * NS), 0, s, a);
   return hipGetLastError();
 }
 
+template <int NS, int MG>
+hipError_t launch_gemv(const QLArgs& a, int fmt, bool per_channel, int blocks, hipStream_t s) {
+  return fmt == AQ_FMT_E4M3 ? launch_gemv<NS, AQ_FMT_E4M3, MG>(a, per_channel, blocks, s)
+                            : launch_gemv<NS, AQ_FMT_INT8, MG>(a, per_channel, blocks, s);
+}
+
+// M <= 16: one 16-row group of x per MFMA
 template <int NS>
 hipError_t launch_gemv(const QLArgs& a, int fmt, bool per_channel, int blocks, hipStream_t s) {
-  return fmt == AQ_FMT_E4M3 ? launch_gemv<NS, AQ_FMT_E4M3>(a, per_channel, blocks, s)
-                            : launch_gemv<NS, AQ_FMT_INT8>(a, per_channel, blocks, s);
+  return launch_gemv<NS, 1>(a, fmt, per_channel, blocks, s);
+}
+
+template <int FMT, int MG, int S>
+hipError_t launch_gemv_x(const QLArgs& a, bool per_channel, int blocks, hipStream_t s) {
+  if (per_channel)
+    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 1, MG, S>), dim3(blocks), dim3(64 * kXWaves), 0, s, a);
+  else
+    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 0, MG, S>), dim3(blocks), dim3(64 * kXWaves), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int MG, int S>
+hipError_t launch_gemv_x(const QLArgs& a, int fmt, bool per_channel, int blocks, hipStream_t s) {
+  return fmt == AQ_FMT_E4M3 ? launch_gemv_x<AQ_FMT_E4M3, MG, S>(a, per_channel, blocks, s)
+                            : launch_gemv_x<AQ_FMT_INT8, MG, S>(a, per_channel, blocks, s);
+}
+
+// 16 < M <= 64: x row groups of 16 per MFMA (MG = 2 or 4 for M up to 32, 64),
+// S = 2 or 4 waves per tile row; a.first counts workgroups of 8 / S tile rows
+hipError_t launch_gemv_x(QLArgs a, int fmt, bool per_channel, int S, hipStream_t s) {
+  const int TR = kXWaves / S;
+  int wgs = 0;
+  for (int i = 0; i < a.count; i++) {
+    a.first[i] = wgs;
+    wgs += (int)aq::ceil_div(a.mat[i].N / 16, TR);
+  }
+  for (int i = a.count; i <= kMaxGroup; i++) a.first[i] = wgs;
+  if (a.M <= 32)
+    return S == 2 ? launch_gemv_x<2, 2>(a, fmt, per_channel, wgs, s) : launch_gemv_x<2, 4>(a, fmt, per_channel, wgs, s);
+  return S == 2 ? launch_gemv_x<4, 2>(a, fmt, per_channel, wgs, s) : launch_gemv_x<4, 4>(a, fmt, per_channel, wgs, s);
 }
 
 template <int WAVES, int FMT, int DENSE>
@@ -706,8 +941,8 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
                    (long long)K);
       AQ_CHECK_ARG(codes[j] && scales[j] && row_ptrs[j] && ys[j] && (uintptr_t)codes[j] % 16 == 0,
                    "aq_qlinear: null or unaligned pointer for matrix %d", i);
-      AQ_CHECK_ARG(M <= 16 || (tile_ptrs && tile_ents && tile_maxes && tile_ptrs[j] && tile_ents[j]),
-                   "aq_qlinear: M > 16 needs the outlier tile lists (aq_outlier_tiles) for matrix %d", i);
+      AQ_CHECK_ARG(M <= kGemvMaxM || (tile_ptrs && tile_ents && tile_maxes && tile_ptrs[j] && tile_ents[j]),
+                   "aq_qlinear: M > 64 needs the outlier tile lists (aq_outlier_tiles) for matrix %d", i);
       a.first[i] = (int)blocks;
       blocks += N / 16;
       maxN = std::max(maxN, N);
@@ -732,7 +967,15 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
   hipStream_t s = (hipStream_t)stream;
   bool per_channel = true;
   for (int i = 0; i < count; i++) per_channel = per_channel && a.mat[i].kg == 1;
-  if (M <= 16) {
+  if (M > 16 && M <= kGemvMaxM) {
+    // buffer offsets of x and of a workgroup's codes stay below 2^31
+    AQ_CHECK_ARG(K <= (1 << 22), "aq_qlinear: K=%lld too large for 16 < M <= 64 (at most 4194304)", (long long)K);
+    // S = 2 waves per tile row for tall groups, 4 for short ones (measured
+    // on the Llama-3-8B shapes: S = 1 leaves the loads' latency exposed)
+    const int S = blocks >= 768 ? 2 : 4;
+    return aq::check_hip(launch_gemv_x(a, fmt, per_channel, S, s), "aq_qlinear: gemv launch");
+  }
+  if (M <= kGemvMaxM) {
     // tall groups fill the GPU with 4 streaming waves per tile row, short ones need 8
     // waves per tile row: enough for about 1536 waves in all (1.5 per SIMD),
     // at most 8; a tall group (gate+up) streams one tile row per wave
@@ -744,7 +987,7 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
     return aq::check_hip(e, "aq_qlinear: gemv launch");
   }
   // 32-bit buffer offsets: 128 rows of x (2 bytes each) and 8 tile rows of codes
-  AQ_CHECK_ARG(K <= (1 << 22), "aq_qlinear: K=%lld too large for M > 16 (at most 4194304)", (long long)K);
+  AQ_CHECK_ARG(K <= (1 << 22), "aq_qlinear: K=%lld too large for M > 64 (at most 4194304)", (long long)K);
   bool dense = false;  // some 16 x 64 block holds more than 64 outliers
   for (int i = 0; i < count; i++) dense = dense || tile_maxes[i] > 64;
   // 256-row tiles decode each weight half as often, but only pay off while

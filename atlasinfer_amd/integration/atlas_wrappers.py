@@ -29,7 +29,7 @@ from ..quant.adaptive_quantizer import (QuantizedTensor, _format_id, _rows_cols,
                                         outlier_tiles, tiled_eligible)
 
 
-GEMV_MAX_M = 16  # aq_qlinear runs the dequant-GEMV up to this many rows of x
+GEMV_MAX_M = 64  # aq_qlinear runs the dequant-GEMV up to this many rows of x
 
 
 def fused_supported(qt: QuantizedTensor) -> bool:

@@ -305,7 +305,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--sweep", action="store_true", help="also time M in {4,16,64,512} per shape")
+    ap.add_argument("--sweep", action="store_true", help="also time M in {4,16,32,64,512} per shape")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--models", default="", help="comma list of opt,mistral: also run BASELINE configs 1 / 3 "
@@ -455,7 +455,7 @@ def main():
 
     sweep = {}
     if args.sweep:
-        for Ms in (4, 16, 64, 512):
+        for Ms in (4, 16, 32, 64, 512):
             xm = {K: gen_x(Ms, K, gen, dev) for K in {K for _, _, K in LLAMA_LINEARS}}
             per = {}
             for name, N, K in LLAMA_LINEARS:

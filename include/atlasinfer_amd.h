@@ -166,11 +166,11 @@ int aq_zscore(const void* x, int64_t n, float eps, void* z, void* stats, void* s
  *   bias    fp16 [N] or NULL
  *   row_ptr, cols, vals   CSR outlier lists (aq_segment_offsets, aq_outlier_cols)
  *   tile_ptr, tile_ent    the same outliers per 16 x 64 block (aq_outlier_tiles);
- *                         required when M > 16, ignored (may be NULL) otherwise
+ *                         required when M > 64, ignored (may be NULL) otherwise
  *   tile_max              the largest entry count of any block (max of
  *                         tile_ptr[b+1] - tile_ptr[b]); above 64 the GEMM
  *                         takes a variant that reads the excess from memory
- * M <= 16 runs the dequant-GEMV, which adds the outliers from the CSR lists in
+ * M <= 64 runs the dequant-GEMV, which adds the outliers from the CSR lists in
  * fp32; larger M the dequant-GEMM, which writes each outlier's fp16 value over
  * its decoded zero in the weight tile it multiplies.  Either way the result is
  * x times the dequantized weight accumulated in fp32, plus the bias, rounded
@@ -191,7 +191,7 @@ int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const void* codes
  * cols[i], vals[i], tile_ptrs[i], tile_ents[i], tile_maxes[i], biases[i]
  * (entries may be NULL), Ns[i] rows.  All W_i share K and fmt.  count <= 4.
  * The arrays themselves are host memory; tile_ptrs/tile_ents/tile_maxes may
- * be NULL when M <= 16.
+ * be NULL when M <= 64.
  * Same per-matrix requirements as aq_qlinear.
  */
 int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, int64_t count, const int64_t* Ns,

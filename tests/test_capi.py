@@ -68,8 +68,8 @@ def test_bad_arguments_return_einval_with_message(lib):
     assert b"block size" in lib.aq_last_error()
     assert lib.aq_qlinear(p, 1, 4000, 16, p, p, 100, 1, p, p, p, None, None, 0, None, p, p, 1 << 20, None) == AQ_EINVAL
     assert b"multiple of 128" in lib.aq_last_error()
-    # the dequant-GEMM (M > 16) needs the outlier block lists
-    assert lib.aq_qlinear(p, 32, 4096, 16, p, p, 4096, 1, p, p, p, None, None, 0, None, p, p, 0, None) == AQ_EINVAL
+    # the dequant-GEMM (M > 64) needs the outlier block lists
+    assert lib.aq_qlinear(p, 100, 4096, 16, p, p, 4096, 1, p, p, p, None, None, 0, None, p, p, 0, None) == AQ_EINVAL
     assert b"aq_outlier_tiles" in lib.aq_last_error()
     assert lib.aq_outlier_tiles(p, p, p, 20, 128, p, p, None) == AQ_EINVAL
     assert lib.aq_outlier_tiles(p, p, p, 32, 100, p, p, None) == AQ_EINVAL

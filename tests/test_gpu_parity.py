@@ -188,7 +188,7 @@ def assert_close(y, yref, x, w):
     assert worst <= 1.0, worst
 
 
-@pytest.mark.parametrize("M", [1, 2, 4, 16, 17, 64, 300])
+@pytest.mark.parametrize("M", [1, 2, 4, 16, 17, 33, 64, 65, 300])
 @pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128), ("e4m3", 64)])
 def test_qlinear_matches_reference_linear(M, fmt, G):
     rng = np.random.default_rng(M + 31 * abs(G))
@@ -209,7 +209,7 @@ def test_qlinear_matches_reference_linear(M, fmt, G):
 
 
 @pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (4096, 14336), (14336, 4096)])
-@pytest.mark.parametrize("M", [1, 16, 512])
+@pytest.mark.parametrize("M", [1, 16, 40, 64, 512])
 def test_qlinear_llama_shapes(N, K, M):
     rng = np.random.default_rng(N + K + M)
     w = make_weights(rng, (N, K))
@@ -221,6 +221,24 @@ def test_qlinear_llama_shapes(N, K, M):
     w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
     y = AW.QuantizedLinear(q, None)(x)
     assert_close(y, reference_linear(x, w_deq, None), x, w_deq)
+
+
+@pytest.mark.parametrize("N,K", [(1040, 640), (12304, 384)])
+@pytest.mark.parametrize("M", [17, 48, 64])
+@pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128)])
+def test_gemv_shared_x_ragged_shapes(N, K, M, fmt, G):
+    """16 < M <= 64: tile-row counts that leave the last workgroup partly
+    empty, chunk counts that leave the last chunk group partly past K, and
+    both split widths (12304 rows take 2 waves per tile row, 1040 take 4)."""
+    rng = np.random.default_rng(N + K + M + abs(G))
+    w = make_weights(rng, (N, K), frac=0.004)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)
+    b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(DEV)
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=G, code_format=fmt)
+    AQ.clear_dequantized_cache()
+    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    y = AW.QuantizedLinear(q, b)(x)
+    assert_close(y, reference_linear(x, w_deq, b), x, w_deq)
 
 
 def test_qlinear_heavy_outliers_and_3d_input():
@@ -269,7 +287,7 @@ def test_outlier_tiles_match_flat_indices(fmt, G):
     assert np.array_equal(te[:nnz].cpu().numpy().view(np.uint32), ent)
 
 
-@pytest.mark.parametrize("M", [17, 64, 200])
+@pytest.mark.parametrize("M", [17, 65, 200])
 def test_gemm_crowded_outlier_blocks(M):
     """Blocks of 16 x 64 holding 0, 1, 9, 17 and 48 outliers: the GEMM reads
     each block's list in batches of 8."""

@@ -107,6 +107,9 @@ __device__ __forceinline__ int scale_index(const QLMat& w, int n, int k) {
   return n * w.kg + (w.gshift >= 0 ? (k >> w.gshift) : (k / w.G));
 }
 
+constexpr uint32_t kOutOfRange = 0x80000000u;  // a buffer offset past every range used here
+constexpr int kBufferDword3 = 0x00020000;      // raw (untyped) buffer access on gfx9
+
 // ------------------------------------------------------------ GEMV (M <= 64)
 
 constexpr int kGemvMaxM = 64;   // larger M takes the GEMM
@@ -118,15 +121,16 @@ constexpr int kCsrCap = 1024;   // outlier entries
 constexpr int kXvCap = 1024;    // staged x values: entries * M <= kXvCap
 constexpr int kStageBatch = 8;  // entries per lane whose loads are issued together
 
-template <int NS, int FMT, int PC, int MG>
+template <int NS, int FMT, int PC>
 __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   constexpr int U = kGemvUnroll;
-  __shared__ float red[NS][256 * MG];
+  __shared__ float red[NS][256];
   __shared__ int s_rp[17];
   __shared__ int s_meta[3];  // p0, staged entries, entries with staged x
   __shared__ int s_col[kCsrCap];
   __shared__ uint16_t s_val[kCsrCap];
   __shared__ uint16_t s_xv[kXvCap];
+  __shared__ uint16_t s_bias[16];
 
   int mi = 0;
 #pragma unroll
@@ -135,122 +139,140 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   const QLMat W = pick(a, mi);
   const int rb = blockIdx.x - a.first[mi];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: chunk tests stay scalar
   const int n0 = rb * 16;
   const int M = a.M, K = a.K, N = W.N;
   const int nchunks = K >> 7;
+  const int grp = lane >> 4;
+  const int li = lane & 15;
+  const int n = n0 + li;
+
+  // Every load of the stream is a buffer load: rows of x past M, chunks past
+  // K and outlier entries past the row's list lie past the end of their
+  // range and read as zero without touching memory, so no load needs a
+  // condition (which would make the compiler wait for all loads in flight).
+  const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W.codes + ((size_t)rb * nchunks << 11)), (short)0, nchunks * 2048, kBufferDword3);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, M * K * 2, kBufferDword3);
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W.scales + (size_t)n0 * W.kg), (short)0, 16 * W.kg * 2, kBufferDword3);
+  const uint32_t code_lane = lane * 16;
+  const uint32_t x_lane = (uint32_t)(li * K + 16 * grp) * 2;  // x row li, columns 16 grp + ...
+  const uint32_t scale_row = (uint32_t)li * W.kg;
+  const uint16_t sb_row = PC ? W.scales[n] : (uint16_t)0;
 
   // Wave 0 also stages the rows' outliers.  Its row_ptr load goes out first;
   // the (col, val) loads of up to 64 * kStageBatch entries go out right after
-  // its first round of code loads, so they return while the codes stream in.
+  // its first code loads, and the x values of row 0 at those columns (all
+  // that decode needs) right after its first chunks are computed, so all of
+  // them return while the codes stream in.
   int rp = 0;
   if (wave == 0 && lane <= 16) rp = W.row_ptr[n0 + lane];
   int p0 = 0, cnt = 0;
-  int scol[kStageBatch];
-  uint16_t sval[kStageBatch];
-#pragma unroll
-  for (int b = 0; b < kStageBatch; b++) {
-    scol[b] = 0;
-    sval[b] = 0;
-  }
+  uint32_t scol[kStageBatch], sval[kStageBatch], sx0[kStageBatch];
+  uint32_t bias_v = 0;
   auto stage_first_batch = [&]() {
-    p0 = __shfl(rp, 0, 64);
-    cnt = min(__shfl(rp, 16, 64) - p0, kCsrCap);
+    // wave-uniform, so the list descriptors below live in scalar registers
+    p0 = __builtin_amdgcn_readfirstlane(__shfl(rp, 0, 64));
+    cnt = __builtin_amdgcn_readfirstlane(min(__shfl(rp, 16, 64) - p0, kCsrCap));
+    const __amdgpu_buffer_rsrc_t colr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(W.cols + p0), (short)0, cnt * 4, kBufferDword3);
+    const __amdgpu_buffer_rsrc_t valr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(W.vals + p0), (short)0, cnt * 2, kBufferDword3);
 #pragma unroll
     for (int b = 0; b < kStageBatch; b++) {
       const int e = 64 * b + lane;
-      if (e < cnt) {
-        scol[b] = W.cols[p0 + e];
-        sval[b] = W.vals[p0 + e];
-      }
+      scol[b] = __builtin_amdgcn_raw_buffer_load_b32(colr, e * 4, 0, 0);
+      sval[b] = __builtin_amdgcn_raw_buffer_load_b16(valr, e * 2, 0, 0);
+    }
+    // no bias: an empty range, read as zero
+    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(W.bias ? W.bias + n0 : W.vals), (short)0, W.bias ? 32 : 0, kBufferDword3);
+    bias_v = __builtin_amdgcn_raw_buffer_load_b16(br, (lane & 15) * 2, 0, 0);
+  };
+  auto gather_x0 = [&]() {
+#pragma unroll
+    for (int b = 0; b < kStageBatch; b++) {
+      const int e = 64 * b + lane;
+      sx0[b] = __builtin_amdgcn_raw_buffer_load_b16(xr, e < cnt ? scol[b] * 2 : kOutOfRange, 0, 0);
     }
   };
-  if (wave == 0 && nchunks <= wave) stage_first_batch();  // no stream share
 
-  {
-    // The code and scale loads below are unconditional, from addresses that
-    // are always valid, so the compiler keeps all of them in flight (a chunk
-    // past the end of K re-reads chunk c0 with its x zeroed).  x is loaded
-    // only by the lanes of rows m < M (exec-masked): for decode (M = 1) that
-    // is 4 lanes, 256 bytes of x per 2 KiB chunk of codes.
-    const int grp = lane >> 4;
-    const int li = lane & 15;
-    const int n = n0 + li;
-    const uint8_t* tiles = W.codes + ((size_t)rb * nchunks << 11) + lane * 16;
-    // x rows 16 gi + li of each 16-row group gi (rows >= M stay zero)
-    const uint16_t* xrow = a.x + (size_t)li * K + 16 * grp;
-    const uint16_t sb_row = PC ? W.scales[n] : (uint16_t)0;
-    float4v acc[MG];
+  struct Batch {
+    u32x4 q[U][2];
+    u32x4 x[U][4];
+    uint32_t s[U][2];
+  };
+  // Non-temporal code loads pay off when each tile row has one wave (tall
+  // groups such as gate/up), plain ones when several waves share it
+  // (measured on the Llama-3-8B shapes).
+  constexpr int kCodePolicy = NS == 1 ? 2 : 0;  // 2: nt
+  auto load = [&](Batch& B, int c0) {
 #pragma unroll
-    for (int gi = 0; gi < MG; gi++) acc[gi] = (float4v){0.f, 0.f, 0.f, 0.f};
-    for (int c0 = wave; c0 < nchunks; c0 += U * NS) {
-      uint4 q[U][2];
-      uint4 xq[U][MG][4];
-      uint16_t sb[U][2];
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int c = c0 + u * NS;
-        const int cc = c < nchunks ? c : c0;
-        const uint8_t* t = tiles + ((size_t)cc << 11);
-        q[u][0] = ld_nt16(t);
-        q[u][1] = ld_nt16(t + 1024);
-        if (PC) {
-          sb[u][0] = sb[u][1] = sb_row;
-        } else {
-          sb[u][0] = W.scales[scale_index(W, n, cc * 128 + 16 * grp)];
-          sb[u][1] = W.scales[scale_index(W, n, cc * 128 + 64 + 16 * grp)];
-        }
-#pragma unroll
-        for (int gi = 0; gi < MG; gi++) {
-#pragma unroll
-          for (int j = 0; j < 4; j++) xq[u][gi][j] = make_uint4(0, 0, 0, 0);
-          if (16 * gi + li < M) {
-            const uint4* xp = reinterpret_cast<const uint4*>(xrow + (size_t)16 * gi * K + cc * 128);
-            xq[u][gi][0] = xp[0];
-            xq[u][gi][1] = xp[1];
-            xq[u][gi][2] = xp[8];  // + 64 columns
-            xq[u][gi][3] = xp[9];
-          }
-        }
+    for (int u = 0; u < U; u++) {
+      const int c = c0 + u * NS;
+      const bool in = c < nchunks;
+      const uint32_t co = in ? code_lane + (uint32_t)c * 2048 : kOutOfRange;
+      B.q[u][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co, 0, kCodePolicy));
+      B.q[u][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co + 1024, 0, kCodePolicy));
+      if (!PC) {
+        const uint32_t k = (uint32_t)(in ? c : 0) * 128 + 16 * grp;
+        const uint32_t k0 = W.gshift >= 0 ? k >> W.gshift : k / W.G;
+        const uint32_t k1 = W.gshift >= 0 ? (k + 64) >> W.gshift : (k + 64) / W.G;
+        B.s[u][0] = __builtin_amdgcn_raw_buffer_load_b16(sr, (scale_row + k0) * 2, 0, 0);
+        B.s[u][1] = __builtin_amdgcn_raw_buffer_load_b16(sr, (scale_row + k1) * 2, 0, 0);
       }
-      // wave 0's staging loads go out right behind the first code loads: the
-      // row_ptr wait does not wait for the codes (loads retire in order), and
-      // the codes' wait below then does not wait for the staging loads
-      if (wave == 0 && c0 == 0) stage_first_batch();
-#pragma unroll
-      for (int u = 1; u < U; u++)
-        if (c0 + u * NS >= nchunks)  // wave-uniform
-#pragma unroll
-          for (int gi = 0; gi < MG; gi++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) xq[u][gi][j] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        const half2v s0 = scale2(sb[u][0]), s1 = scale2(sb[u][1]);
-        const half8 w0 = deq8<FMT>(q[u][0].x, q[u][0].y, s0);
-        const half8 w1 = deq8<FMT>(q[u][0].z, q[u][0].w, s0);
-        const half8 w2 = deq8<FMT>(q[u][1].x, q[u][1].y, s1);
-        const half8 w3 = deq8<FMT>(q[u][1].z, q[u][1].w, s1);
-#pragma unroll
-        for (int gi = 0; gi < MG; gi++) {
-          acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][gi][0]), w0, acc[gi], 0, 0, 0);
-          acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][gi][1]), w1, acc[gi], 0, 0, 0);
-          acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][gi][2]), w2, acc[gi], 0, 0, 0);
-          acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xq[u][gi][3]), w3, acc[gi], 0, 0, 0);
-        }
-      }
+      const uint32_t xo = in ? x_lane + (uint32_t)c * 256 : kOutOfRange;
+      B.x[u][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo, 0, 0));
+      B.x[u][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + 16, 0, 0));
+      B.x[u][2] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + 128, 0, 0));  // + 64 columns
+      B.x[u][3] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + 144, 0, 0));
     }
-    // C layout: lane l, element i -> m = 16 gi + 4*(l/16) + i, column l % 16
+  };
+  float4v acc = (float4v){0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const Batch& B) {
 #pragma unroll
-    for (int gi = 0; gi < MG; gi++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) red[wave][gi * 256 + lane * 4 + i] = acc[gi][i];
+    for (int u = 0; u < U; u++) {
+      const half2v s0 = scale2(PC ? sb_row : (uint16_t)B.s[u][0]);
+      const half2v s1 = scale2(PC ? sb_row : (uint16_t)B.s[u][1]);
+      const half8 w0 = deq8<FMT>(B.q[u][0].x, B.q[u][0].y, s0);
+      const half8 w1 = deq8<FMT>(B.q[u][0].z, B.q[u][0].w, s0);
+      const half8 w2 = deq8<FMT>(B.q[u][1].x, B.q[u][1].y, s1);
+      const half8 w3 = deq8<FMT>(B.q[u][1].z, B.q[u][1].w, s1);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, B.x[u][0]), w0, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, B.x[u][1]), w1, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, B.x[u][2]), w2, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, B.x[u][3]), w3, acc, 0, 0, 0);
+    }
+  };
+
+  // Two batches of U chunks in flight: the loads of the next batch go out
+  // before the current one is computed.  Past the last chunk the loads are
+  // out of range (no memory traffic) and the products zero.
+  const int step = U * NS;
+  Batch B0, B1;
+  load(B0, wave);
+  if (wave == 0) stage_first_batch();
+  for (int c0 = wave; c0 < nchunks; c0 += 2 * step) {
+    load(B1, c0 + step);
+    __builtin_amdgcn_sched_barrier(0);
+    if (wave == 0 && c0 == 0) gather_x0();
+    compute(B0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(B0, c0 + 2 * step);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(B1);
   }
+  // C layout: lane l, element i -> m = 4 (l / 16) + i, column l % 16
+#pragma unroll
+  for (int i = 0; i < 4; i++) red[wave][lane * 4 + i] = acc[i];
 
   if (wave == 0) {
     // Stage the CSR lists of rows n0..n0+15 and the x values they multiply
-    // (the first batch of (col, val) is already in registers).
+    // (the first batch of (col, val) and row 0's x values are already in
+    // registers).
     if (lane <= 16) s_rp[lane] = rp - p0;
+    if (lane < 16) s_bias[lane] = (uint16_t)bias_v;
     const int nx = min(cnt, kXvCap / M);
     for (int base = 0; base < cnt; base += 64 * kStageBatch) {
       int col[kStageBatch];
@@ -258,8 +280,8 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
 #pragma unroll
       for (int b = 0; b < kStageBatch; b++) {
         const int e = base + 64 * b + lane;
-        col[b] = scol[b];
-        val[b] = sval[b];
+        col[b] = (int)scol[b];
+        val[b] = (uint16_t)sval[b];
         if (base > 0) {
           col[b] = 0;
           val[b] = 0;
@@ -282,7 +304,9 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
 #pragma unroll
         for (int b = 0; b < kStageBatch; b++) {
           const int e = base + 64 * b + lane;
-          xv[b] = (e < nx) ? a.x[(size_t)m * K + col[b]] : (uint16_t)0;
+          xv[b] = (base == 0 && m == 0) ? (uint16_t)sx0[b]
+                  : (e < nx)            ? a.x[(size_t)m * K + col[b]]
+                                        : (uint16_t)0;
         }
 #pragma unroll
         for (int b = 0; b < kStageBatch; b++) {
@@ -328,20 +352,19 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
         float dense = 0.0f;
 #pragma unroll
         for (int w = 0; w < NS; w++) dense += red[w][nl * 4];
-        v = dense + v;
-        if (W.bias) v += (float)bits_to_h(W.bias[n0 + nl]);
+        v = dense + v + (float)bits_to_h(s_bias[nl]);
         W.y[n0 + nl] = h_to_bits(rn_h(v));
       }
     }
   } else {
-    for (int o = threadIdx.x; o < 256 * MG; o += 64 * NS) {
-      const int l = (o & 255) >> 2;
-      const int m = 16 * (o >> 8) + 4 * (l >> 4) + (o & 3);
+    for (int o = threadIdx.x; o < 256; o += 64 * NS) {
+      const int l = o >> 2;
+      const int m = 4 * (l >> 4) + (o & 3);
       const int nl = l & 15;
       const int n = n0 + nl;
       if (m < M) {
         float v = 0.0f;
-  #pragma unroll
+#pragma unroll
         for (int w = 0; w < NS; w++) v += red[w][o];
         const int p0 = s_meta[0], cnt = s_meta[1], nx = s_meta[2];
         const int e1 = s_rp[nl + 1];
@@ -359,7 +382,7 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
           }
           v = __builtin_fmaf(xv, wv, v);
         }
-        if (W.bias) v += (float)bits_to_h(W.bias[n]);
+        v += (float)bits_to_h(s_bias[nl]);
         W.y[(size_t)m * N + n] = h_to_bits(rn_h(v));
       }
     }
@@ -383,9 +406,7 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
 // lane owns one output column and 4 MG of its rows.
 
 constexpr int kXWaves = 8;
-constexpr int kXPad = 8;             // halves of padding per LDS row of x
-constexpr uint32_t kOutOfRange = 0x80000000u;  // a buffer offset past every range used here
-constexpr int kBufferDword3 = 0x00020000;      // raw (untyped) buffer access on gfx9
+constexpr int kXPad = 8;  // halves of padding per LDS row of x
 
 template <int FMT, int PC, int MG, int S>
 __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) {
@@ -403,7 +424,7 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   const QLMat W = pick(a, mi);
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int wave = t >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int tr = wave % TR, sp = wave / TR;
   const int M = a.M, K = a.K, N = W.N;
   const int nchunks = K >> 7;
@@ -831,25 +852,19 @@ int log2_exact(int64_t g) {
   return s;
 }
 
-template <int NS, int FMT, int MG>
+template <int NS, int FMT>
 hipError_t launch_gemv(const QLArgs& a, bool per_channel, int blocks, hipStream_t s) {
   if (per_channel)
-    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, MG>), dim3(blocks), dim3(64 * NS), 0, s, a);
+    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1>), dim3(blocks), dim3(64 * NS), 0, s, a);
   else
-    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, MG>), dim3(blocks), dim3(64 * NS), 0, s, a);
+    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0>), dim3(blocks), dim3(64 * NS), 0, s, a);
   return hipGetLastError();
 }
 
-template <int NS, int MG>
-hipError_t launch_gemv(const QLArgs& a, int fmt, bool per_channel, int blocks, hipStream_t s) {
-  return fmt == AQ_FMT_E4M3 ? launch_gemv<NS, AQ_FMT_E4M3, MG>(a, per_channel, blocks, s)
-                            : launch_gemv<NS, AQ_FMT_INT8, MG>(a, per_channel, blocks, s);
-}
-
-// M <= 16: one 16-row group of x per MFMA
 template <int NS>
 hipError_t launch_gemv(const QLArgs& a, int fmt, bool per_channel, int blocks, hipStream_t s) {
-  return launch_gemv<NS, 1>(a, fmt, per_channel, blocks, s);
+  return fmt == AQ_FMT_E4M3 ? launch_gemv<NS, AQ_FMT_E4M3>(a, per_channel, blocks, s)
+                            : launch_gemv<NS, AQ_FMT_INT8>(a, per_channel, blocks, s);
 }
 
 template <int FMT, int MG, int S>
@@ -919,8 +934,10 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
                                   const void* const* biases, void* const* ys, void* stream) {
   AQ_CHECK_ARG(count >= 1 && count <= kMaxGroup, "aq_qlinear: 1..%d matrices per call (got %lld)", kMaxGroup,
                (long long)count);
-  AQ_CHECK_ARG(M >= 0 && M < (1 << 30) && K >= 128 && K % 128 == 0 && K < (1 << 30),
+  AQ_CHECK_ARG(M >= 0 && M < (1 << 30) && K >= 128 && K % 128 == 0,
                "aq_qlinear: K must be a multiple of 128 (M=%lld K=%lld)", (long long)M, (long long)K);
+  // the kernels address x and a workgroup's codes with 32-bit buffer offsets
+  AQ_CHECK_ARG(K <= (1 << 22), "aq_qlinear: K=%lld too large (at most 4194304)", (long long)K);
   AQ_CHECK_ARG(fmt == AQ_FMT_INT8 || fmt == AQ_FMT_E4M3, "aq_qlinear: unknown code format %d", fmt);
   AQ_CHECK_ARG(x && Ns && codes && scales && Gs && row_ptrs && cols && vals && ys, "aq_qlinear: null pointer argument");
   AQ_CHECK_ARG((uintptr_t)x % 16 == 0, "aq_qlinear: x must be 16-byte aligned");
@@ -968,8 +985,6 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
   bool per_channel = true;
   for (int i = 0; i < count; i++) per_channel = per_channel && a.mat[i].kg == 1;
   if (M > 16 && M <= kGemvMaxM) {
-    // buffer offsets of x and of a workgroup's codes stay below 2^31
-    AQ_CHECK_ARG(K <= (1 << 22), "aq_qlinear: K=%lld too large for 16 < M <= 64 (at most 4194304)", (long long)K);
     // S = 2 waves per tile row for tall groups, 4 for short ones (measured
     // on the Llama-3-8B shapes: S = 1 leaves the loads' latency exposed)
     const int S = blocks >= 768 ? 2 : 4;
@@ -986,8 +1001,6 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
                                    : launch_gemv<8>(a, fmt, per_channel, (int)blocks, s);
     return aq::check_hip(e, "aq_qlinear: gemv launch");
   }
-  // 32-bit buffer offsets: 128 rows of x (2 bytes each) and 8 tile rows of codes
-  AQ_CHECK_ARG(K <= (1 << 22), "aq_qlinear: K=%lld too large for M > 64 (at most 4194304)", (long long)K);
   bool dense = false;  // some 16 x 64 block holds more than 64 outliers
   for (int i = 0; i < count; i++) dense = dense || tile_maxes[i] > 64;
   // 256-row tiles decode each weight half as often, but only pay off while

@@ -161,7 +161,7 @@ int aq_zscore(const void* x, int64_t n, float eps, void* z, void* stats, void* s
  * (reference: QuantizedLinear.forward, integration/atlas_wrappers.py:30-74,
  * which computes F.linear(x, dequantize_tensor(W), b) at :56,67).
  *   x       fp16 [M, K] row-major, 16-byte aligned    y fp16 [M, N] (out)
- *   codes   tiled layout; N % 16 == 0, K % 128 == 0
+ *   codes   tiled layout; N % 16 == 0, K % 128 == 0, K <= 4194304
  *   G       a multiple of 32 that divides K
  *   bias    fp16 [N] or NULL
  *   row_ptr, cols, vals   CSR outlier lists (aq_segment_offsets, aq_outlier_cols)

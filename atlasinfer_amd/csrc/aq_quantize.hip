@@ -32,6 +32,10 @@
 
 namespace {
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+__device__ __forceinline__ uint32_t h2_bits(half2v h) { return __builtin_bit_cast(uint32_t, h); }
+
 constexpr int kWG = 256;            // threads per workgroup for TAU <= 256
 constexpr int kScanChunk = 4096;    // block counts per scan workgroup (256 x 16)
 constexpr int64_t kMaxG = 65536;
@@ -47,6 +51,7 @@ struct QuantArgs {
   int tiled;        // codes in the tiled layout (rows of K, K % 128 == 0, N % 16 == 0)
   int64_t K;        // row length for the tiled layout
   int64_t nchunks;  // K / 128
+  int64_t bpr;      // tiled layout: blocks per row, K / G
   uint8_t* codes;
   uint16_t* scales;
   int32_t* block_cnt;  // block_off, holds counts until the scan
@@ -230,27 +235,14 @@ __device__ __forceinline__ void load_elems(Elems<E>& xs, const QuantArgs& a, int
   }
 }
 
+// The rest of a block after its elements are loaded, for any block length:
+// per-element bounds tests, outlier flags in a 64-bit mask.
 template <int TAU, int E, int MODE>
-__global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantArgs a) {
-  constexpr int NT = TAU > kWG ? TAU : kWG;
-  constexpr int TEAMS = NT / TAU;
-  constexpr int NWT = TAU > 64 ? TAU / 64 : 1;
-  __shared__ double lds_d[TEAMS * NWT];
-  __shared__ float lds_f[TEAMS * NWT];
-  __shared__ int lds_i[TEAMS * NWT];
-
-  const int team = threadIdx.x / TAU;
-  const int t = threadIdx.x % TAU;
-  const int64_t g = (int64_t)blockIdx.x * TEAMS + team;
-  const bool gvalid = g < a.nblocks;
+__device__ __forceinline__ void finish_block_any(const QuantArgs& a, Elems<E>& xs, int64_t g, bool gvalid,
+                                                 int64_t base, int i0, int t, double* lds_d, float* lds_f,
+                                                 int* lds_i) {
   const int64_t G = a.G;
-  const int64_t base = g * G;
-  const int i0 = t * E;
-
-  Elems<E> xs;
-  load_elems<E>(xs, a, base, i0, gvalid);
-
-  const BlockStats st = block_stats<TAU, E, MODE>(xs, i0, G, 1e-6f, lds_d + team * NWT);
+  const BlockStats st = block_stats<TAU, E, MODE>(xs, i0, G, 1e-6f, lds_d);
   xs.fence();
   const f16 thr = bits_to_h(a.thr_bits);
   const float cut = outlier_cut_team<TAU>(st.den16, thr);
@@ -282,7 +274,7 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
     }
     if (E > 16) xs.fence();
   }
-  amax = team_max_f32<TAU>(amax, lds_f + team * NWT);
+  amax = team_max_f32<TAU>(amax, lds_f);
   xs.fence();
 
   const float qmax = a.fmt == AQ_FMT_INT8 ? 127.0f : 448.0f;
@@ -293,6 +285,13 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
   }
   const float s = (float)s16;
   const float r = 1.0f / s;
+
+  // where the thread's elements sit in the [rows, K] matrix (tiled layout)
+  int64_t row = 0, col0 = 0;
+  if (a.tiled) {
+    row = a.bpr == 1 ? g : g / a.bpr;
+    col0 = (g - row * a.bpr) * G + i0;
+  }
 
   // codes, 16 elements at a time (four words in element order)
 #pragma unroll
@@ -336,13 +335,13 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
       // 16 consecutive elements of one row land in 16 consecutive bytes of either layout
       const int64_t j = base + i0 + 16 * v;
       if (a.vec && i0 + E <= G) {
-        const int64_t off = a.tiled ? tiled_offset(j / a.K, j % a.K, a.nchunks) : j;
+        const int64_t off = a.tiled ? tiled_offset(row, col0 + 16 * v, a.nchunks) : j;
         *reinterpret_cast<uint4*>(a.codes + off) = make_uint4(w[0], w[1], w[2], w[3]);
       } else {
 #pragma unroll
         for (int b = 0; b < 16; b++)
           if (i0 + 16 * v + b < G)
-            a.codes[a.tiled ? tiled_offset((j + b) / a.K, (j + b) % a.K, a.nchunks) : j + b] =
+            a.codes[a.tiled ? tiled_offset(row, col0 + 16 * v + b, a.nchunks) : j + b] =
                 (uint8_t)(w[b / 4] >> (8 * (b % 4)));
       }
     }
@@ -351,7 +350,7 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
   // outlier compaction: team prefix sum, then the block's staging slot
   const int cnt = __builtin_popcountll(omask);
   int total;
-  const int pre = team_excl_scan_i32<TAU>(cnt, lds_i + team * NWT, &total);
+  const int pre = team_excl_scan_i32<TAU>(cnt, lds_i, &total);
   if (gvalid) {
     int k = pre;
     uint64_t m = omask;
@@ -370,6 +369,319 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
       a.block_cnt[g] = total;
     }
   }
+}
+
+// mean / std / std + eps as block_stats computes them, with one pass less:
+// S is the same exact-order f64 tree, but the variance comes from
+// Q = sum x^2 (products exact in f32, four f32 chains per thread, f64 across
+// threads) as V = Q - S mu, whose error is below Q 2^-19.  std16 is a
+// monotone function of V (f64 division, sqrt, rounding to f32 and to fp16),
+// so when both ends of V +- Q 2^-16 give the same std16 that is the value
+// the two-pass tree gives.  Otherwise (a near-tie, large |mean| / std, or a
+// non-finite sum) the team runs the two-pass tree.  The decision is the
+// same in every lane of the team (its sums are).
+template <int TAU, int E, int MODE>
+__device__ __forceinline__ BlockStats block_stats_fast(Elems<E>& xs, int i0, int64_t G, float eps, double* lds_d) {
+#pragma clang fp contract(off)
+  const double s_loc = thread_tree_sum<E, MODE>(xs, i0, G, false, 0.0);
+  float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int e = 0; e < E; e++) {
+    const float v = (float)xs[e];  // padding elements are zeros
+    q[e & 3] = __builtin_fmaf(v, v, q[e & 3]);
+  }
+  const double S = team_sum_f64<TAU>(s_loc, lds_d);
+  const double Q = team_sum_f64<TAU>((double)((q[0] + q[1]) + (q[2] + q[3])), lds_d);
+  const double mu = S / (double)G;
+  auto std_of = [&](double V) { return rn_h((float)sqrt(V / (double)(G - 1))); };
+  BlockStats st;
+  st.mean16 = rn_h((float)mu);
+  bool pinned = false;
+  if (G >= 2) {
+    const double V = Q - S * mu;
+    const double err = Q * 0x1p-16;
+    const f16 lo = std_of(fmax(V - err, 0.0));
+    const f16 hi = std_of(V + err);
+    pinned = h_to_bits(lo) == h_to_bits(hi) && !isnan((float)lo);
+    st.std16 = lo;
+  }
+  if (!pinned) {
+    xs.fence();
+    const double v_loc = thread_tree_sum<E, MODE>(xs, i0, G, true, mu);
+    st.std16 = std_of(team_sum_f64<TAU>(v_loc, lds_d));
+  }
+  st.den16 = rn_h((float)st.std16 + eps);
+  return st;
+}
+
+// Packed 16-bit integer operations, written out because the compiler turns
+// the equivalent vector expressions into per-half compares and selects.
+__device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
+  uint32_t d;
+  asm("v_pk_sub_u16 %0, %1, %2 clamp" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+__device__ __forceinline__ uint32_t pk_min_u16(uint32_t a, uint32_t b) {
+  uint32_t d;
+  asm("v_pk_min_u16 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  uint32_t d;
+  asm("v_pk_max_u16 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+
+// fp16(x / s) for both halves of a pair, s > 0, r = fl(1 / s): the f32
+// quotient with one Newton step (the correctly rounded f32 quotient), then
+// fp16.  The fp16 x enters the fused multiply-adds directly; a zero x gives
+// +0 there, so the sign bits are taken from x (for any other x the
+// quotient already carries x's sign).
+__device__ __forceinline__ uint32_t quot2(uint32_t xp, float s, float r) {
+  const half2v x = as_h2(xp);
+  const float q00 = __builtin_fmaf((float)x.x, r, 0.0f), q01 = __builtin_fmaf((float)x.y, r, 0.0f);
+  const float e0 = __builtin_fmaf(q00, s, -(float)x.x), e1 = __builtin_fmaf(q01, s, -(float)x.y);
+  const uint32_t q = h2_bits((half2v){(f16)__builtin_fmaf(-e0, r, q00), (f16)__builtin_fmaf(-e1, r, q01)});
+  return (q & 0x7FFF7FFFu) | (xp & 0x80008000u);
+}
+
+// The rest of a block after its elements are loaded, when a thread's E
+// elements are all inside the block or all padding (E divides G).  Works on
+// element pairs with packed arithmetic: d = x - mean in fp16, then, since
+// non-negative fp16 values order like their bit patterns,
+//   outlier <=> |d| > Th  <=>  sat(bits|d| - bits Th) != 0   (per half).
+// Outliers are replaced by +0 in xs, so the absmax is a packed max over xs
+// and the code pass needs no flags (a +0 gives code 0); their values are
+// read again from memory for the compaction.  Flag bits: word w covers
+// pairs PW w .. PW w + PW - 1, built as acc = 2 acc + m with m holding the
+// pair's low / high outlier bit at bit 0 / 16.
+template <int TAU, int E, int MODE>
+__device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& xs, int64_t g, bool gvalid,
+                                                  int64_t base, int i0, int t, double* lds_d, float* lds_f,
+                                                  int* lds_i) {
+  constexpr int NP = E / 2;              // pairs per thread
+  constexpr int PW = NP < 16 ? NP : 16;  // pairs per flag word
+  constexpr int NWD = NP / PW;
+  const int64_t G = a.G;
+  const bool tvalid = MODE == kFullBlocks || i0 < G;
+
+  const BlockStats st = block_stats_fast<TAU, E, MODE>(xs, i0, G, 1e-6f, lds_d);
+  xs.fence();
+  const f16 thr = bits_to_h(a.thr_bits);
+  const float cut = outlier_cut_team<TAU>(st.den16, thr);
+
+  uint32_t obits[NWD];
+  uint32_t amax2 = 0;  // packed |x| of non-outliers, as bit patterns
+  if (cut >= 0.0f) {
+    // cut is an fp16 value or +inf (none are outliers)
+    const uint32_t th = (uint32_t)h_to_bits((f16)cut) * 0x00010001u;
+    const half2v nm = (half2v){-st.mean16, -st.mean16};
+#pragma unroll
+    for (int w = 0; w < NWD; w++) {
+      uint32_t acc = 0;
+#pragma unroll
+      for (int j = 0; j < PW; j++) {
+        const int i = w * PW + j;
+        const uint32_t ad = h2_bits(as_h2(xs.p[i]) + nm) & 0x7FFF7FFFu;
+        const uint32_t m = pk_min_u16(pk_sub_sat_u16(ad, th), 0x00010001u);
+        xs.p[i] &= ~(m * 0xFFFFu);
+        acc = 2 * acc + m;
+        amax2 = pk_max_u16(amax2, xs.p[i] & 0x7FFF7FFFu);
+      }
+      obits[w] = acc;
+      if (NWD > 1) xs.fence();
+    }
+  } else {
+    // std + eps is not a positive finite number (cut NaN), or even |d| = 0
+    // passes (cut -1): the reference's quotient per element
+#pragma unroll
+    for (int w = 0; w < NWD; w++) {
+      uint32_t acc = 0;
+#pragma unroll
+      for (int j = 0; j < PW; j++) {
+        const int i = w * PW + j;
+        uint32_t m = 0;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const f16 d = h_sub(xs[2 * i + h], st.mean16);
+          if (outlier_literal(bits_to_h(h_to_bits(d) & 0x7FFFu), st.den16, thr)) m |= 1u << (16 * h);
+        }
+        xs.p[i] &= ~(m * 0xFFFFu);
+        acc = 2 * acc + m;
+        amax2 = pk_max_u16(amax2, xs.p[i] & 0x7FFF7FFFu);
+      }
+      obits[w] = acc;
+    }
+  }
+  int nout = 0;
+#pragma unroll
+  for (int w = 0; w < NWD; w++) {
+    if (!tvalid) obits[w] = 0;  // padding threads hold zeros that may pass the test
+    nout += __builtin_popcount(obits[w]);
+  }
+  // the absmax over non-outliers; -1 when the thread has none
+  float amax = tvalid && nout < E ? fmaxf((float)as_h2(amax2).x, (float)as_h2(amax2).y) : -1.0f;
+  amax = team_max_f32<TAU>(amax, lds_f);
+  xs.fence();
+
+  const float qmax = a.fmt == AQ_FMT_INT8 ? 127.0f : 448.0f;
+  f16 s16 = (f16)1.0f;
+  if (amax >= 0.0f) {
+    s16 = rn_h(amax / qmax);
+    if ((float)s16 < 1e-6f) s16 = rn_h(1e-6f);
+  }
+  const float s = (float)s16;
+  const float r = 1.0f / s;
+
+  int64_t row = 0, col0 = 0;  // where the thread's elements sit in the [rows, K] matrix (tiled layout)
+  if (a.tiled) {
+    row = a.bpr == 1 ? g : g / a.bpr;
+    col0 = (g - row * a.bpr) * G + i0;
+  }
+  // codes, 16 elements (8 pairs, four words) at a time
+#pragma unroll
+  for (int v = 0; v < E / 16; v++) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t p0 = xs.p[8 * v + 2 * k], p1 = xs.p[8 * v + 2 * k + 1];
+      if (a.fmt == AQ_FMT_INT8) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+          const f16 xe = xs[16 * v + 4 * k + b];
+          float rr = __builtin_rintf((float)h_div_fast((float)xe, s, r));
+          rr = fminf(fmaxf(rr, -127.0f), 127.0f);
+          word |= (uint32_t)(uint8_t)(int8_t)(int)rr << (8 * b);
+        }
+        w[k] = word;
+      } else {
+        // |x| <= amax and s = fp16(amax / 448) give |x / s| < 448.25, so the
+        // quotient is at most 448.25, which the conversion (round to nearest
+        // even) takes to 448 as the clamp to +-448 would
+        typedef short short2v __attribute__((vector_size(4)));
+        short2v c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16((short2v){0, 0}, as_h2(quot2(p0, s, r)), 1.0f, false);
+        c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(c, as_h2(quot2(p1, s, r)), 1.0f, true);
+        w[k] = __builtin_bit_cast(uint32_t, c);
+      }
+    }
+    if (E > 16) xs.fence();
+    if (gvalid && tvalid) {
+      // 16 consecutive elements of one row land in 16 consecutive bytes of either layout
+      const int64_t j = base + i0 + 16 * v;
+      if (a.vec) {
+        const int64_t off = a.tiled ? tiled_offset(row, col0 + 16 * v, a.nchunks) : j;
+        *reinterpret_cast<uint4*>(a.codes + off) = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+#pragma unroll
+        for (int b = 0; b < 16; b++)
+          a.codes[a.tiled ? tiled_offset(row, col0 + 16 * v + b, a.nchunks) : j + b] =
+              (uint8_t)(w[b / 4] >> (8 * (b % 4)));
+      }
+    }
+  }
+
+  // outlier compaction: team prefix sum, then the block's staging slot in
+  // element order (flag word w: pair PW w + j low / high at bit PW - 1 - j /
+  // 16 + PW - 1 - j, so after a bit reversal L and H below hold them at bit j)
+  int total;
+  const int pre = team_excl_scan_i32<TAU>(nout, lds_i, &total);
+  if (gvalid) {
+    int k = pre;
+#pragma unroll
+    for (int w = 0; w < NWD; w++) {
+      const uint32_t rev = __builtin_bitreverse32(obits[w]);
+      constexpr uint32_t kMask = PW == 32 ? 0xFFFFFFFFu : (1u << PW) - 1u;
+      uint32_t L = (rev >> (32 - PW)) & kMask, H = (rev >> (16 - PW)) & kMask;
+      while (L | H) {
+        const int jl = L ? __builtin_ctz(L) : 32, jh = H ? __builtin_ctz(H) : 32;
+        int e;
+        if (jl <= jh) {
+          e = 2 * (w * PW + jl);
+          L &= L - 1;
+        } else {
+          e = 2 * (w * PW + jh) + 1;
+          H &= H - 1;
+        }
+        // the value from memory (an L2 hit): indexing the registers with a
+        // run-time e would move them to scratch
+        const int64_t jj = base + i0 + e;
+        a.stage_col[base + k] = i0 + e;
+        a.stage_val[base + k] = jj < a.numel ? a.x[jj] : (uint16_t)0;
+        k++;
+      }
+    }
+    if (t == 0) {
+      a.scales[g] = h_to_bits(s16);
+      a.block_cnt[g] = total;
+    }
+  }
+}
+
+template <int TAU, int E, int MODE>
+__global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantArgs a) {
+  constexpr int NT = TAU > kWG ? TAU : kWG;
+  constexpr int TEAMS = NT / TAU;
+  constexpr int NWT = TAU > 64 ? TAU / 64 : 1;
+  __shared__ double lds_d[TEAMS * NWT];
+  __shared__ float lds_f[TEAMS * NWT];
+  __shared__ int lds_i[TEAMS * NWT];
+
+  const int team = threadIdx.x / TAU;
+  const int t = threadIdx.x % TAU;
+  const int64_t g = (int64_t)blockIdx.x * TEAMS + team;
+  const bool gvalid = g < a.nblocks;
+  const int64_t G = a.G;
+  const int64_t base = g * G;
+  const int i0 = t * E;
+
+  // Coalesced loads: a thread's E elements are consecutive, so if each
+  // thread read its own, every load instruction would touch 64 different
+  // 128-byte lines.  Instead the workgroup reads its blocks (TEAMS * G
+  // consecutive elements) with consecutive lanes on consecutive 16-byte
+  // pieces and hands them over through LDS.  The LDS piece index is
+  // swizzled (its low bits XOR the owning thread's low bits) so that the
+  // reads, 8 pieces per thread at a stride of E * 2 bytes, hit distinct
+  // banks.  Used when the workgroup's blocks lie wholly inside x.
+  constexpr int PPT = E / 8;  // 16-byte pieces per thread
+  constexpr bool kStage = MODE != kAnyLen && NT * E * 2 <= 32768;
+  __shared__ uint4 stage[kStage ? NT * PPT : 1];
+  auto swz = [](int P) { return P ^ ((P / PPT) & (PPT - 1)); };
+  Elems<E> xs;
+  bool staged = false;
+  if constexpr (kStage) {
+    const int64_t wg_base = (int64_t)blockIdx.x * TEAMS * G;
+    const int64_t wg_len = TEAMS * G;
+    if (a.vec && (int64_t)(blockIdx.x + 1) * TEAMS <= a.nblocks && wg_base + wg_len <= a.numel) {
+      staged = true;
+      const int npieces = (int)(wg_len >> 3);
+      const uint4* src = reinterpret_cast<const uint4*>(a.x + wg_base);
+#pragma unroll
+      for (int k = 0; k < PPT; k++) {
+        const int P = threadIdx.x + NT * k;
+        if (MODE == kFullBlocks || P < npieces) stage[swz(P)] = src[P];
+      }
+      __syncthreads();
+      const int S0 = (int)((team * G + i0) >> 3);
+#pragma unroll
+      for (int j = 0; j < PPT; j++) {
+        // threads past the end of their block (E divides G < TAU * E) hold padding
+        const uint4 u = i0 < G ? stage[swz(S0 + j)] : make_uint4(0, 0, 0, 0);
+        xs.p[4 * j] = u.x;
+        xs.p[4 * j + 1] = u.y;
+        xs.p[4 * j + 2] = u.z;
+        xs.p[4 * j + 3] = u.w;
+      }
+    }
+  }
+  if (!staged) load_elems<E>(xs, a, base, i0, gvalid);
+
+  if constexpr (MODE == kAnyLen)
+    finish_block_any<TAU, E, MODE>(a, xs, g, gvalid, base, i0, t, lds_d + team * NWT, lds_f + team * NWT,
+                                   lds_i + team * NWT);
+  else
+    finish_block_fast<TAU, E, MODE>(a, xs, g, gvalid, base, i0, t, lds_d + team * NWT, lds_f + team * NWT,
+                                    lds_i + team * NWT);
 }
 
 // ---- exclusive scan of the per-block counts (in place, two passes)
@@ -577,6 +889,7 @@ extern "C" int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_t
   a.tiled = layout == AQ_LAYOUT_TILED;
   a.K = K;
   a.nchunks = K / 128;
+  a.bpr = a.tiled ? K / G : 1;
   a.codes = (uint8_t*)codes;
   a.scales = (uint16_t*)scales;
   a.block_cnt = block_off;

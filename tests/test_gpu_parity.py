@@ -448,6 +448,32 @@ def test_e4m3_codes_every_fp16_value(oracle):
     assert np.array_equal(bits(AQ.dense_codes(q, torch.device(DEV))), ref["codes"])
 
 
+def test_e4m3_quotients_above_448(oracle):
+    """Block maxima whose quotient x / s exceeds 448: with s = fp16(amax /
+    448) rounded down (most of all where s is an fp16 subnormal) amax / s
+    reaches 461.  Every positive fp16 amax with fp16(amax / s) > 448 (an
+    exhaustive search, 4379 values) gets a row holding +amax and -amax;
+    their codes must be the E4M3 encodings of the quotient clamped to
+    +-448 (0x7E, 0xFE), as in the oracle."""
+    vals = np.arange(0x0400, 0x7C00, dtype=np.uint16).view(np.float16)
+    a = vals.astype(np.float32)
+    s = np.maximum((a / np.float32(448)).astype(np.float16), np.float16(1e-6))
+    hit = vals[(a / s.astype(np.float32)).astype(np.float16) > 448]
+    assert hit.size > 4000
+    K = 128
+    rows = hit.size + (-hit.size) % 16
+    w = np.zeros((rows, K), np.float16)
+    w[:hit.size, 0] = hit
+    w[:hit.size, 1] = -hit
+    w[hit.size:, 0] = 1.0
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, z_threshold=60000.0, code_format="e4m3")
+    assert q.outlier_indices.numel() == 0
+    ref = oracle.quantize(w, K, 60000.0, oracle.FMT_E4M3)
+    got = bits(AQ.dense_codes(q, torch.device(DEV))).reshape(rows, K)
+    assert np.array_equal(got, ref["codes"].reshape(rows, K))
+    assert np.all(got[:hit.size, 0] == 0x7E) and np.all(got[:hit.size, 1] == 0xFE)
+
+
 def test_tile_untile_round_trip():
     from atlasinfer_amd import _lib
     L = _lib.load()

@@ -116,14 +116,96 @@ __device__ __forceinline__ f16 e4m3_to_h(uint8_t c) {
 // -------------------------------------------------------- team reductions
 // A team is TAU consecutive threads (TAU a power of two) that own one block.
 // Sums follow a fixed balanced binary tree: leaves in element order, pairs
-// (2i, 2i+1) first.  The xor butterfly realises exactly that tree, and since
-// a + b == b + a bit for bit, every lane ends with the identical value.
+// (2i, 2i+1) first.  Within a wave, level k adds to each lane's value (the
+// sum of its aligned group of 2^(k-1) lanes) the value of some lane of the
+// partner group, so every lane holds the tree node of its 2^k group; since
+// a + b == b + a bit for bit, every lane ends with the identical value.  The
+// partner lane comes from a register-to-register exchange, never through
+// LDS: DPP quad permutations (partners at distance 1 and 2), half-row and
+// row mirrors (the other group of 4 in 8 and of 8 in 16), and the gfx950
+// row swaps (16 lanes, 32 lanes).
+
+// Value of the partner lane at butterfly levels 1-4 (group 2^(L-1) -> 2^L).
+template <int L>
+__device__ __forceinline__ uint32_t xlane_partner_u32(uint32_t v) {
+  if constexpr (L == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  if constexpr (L == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  if constexpr (L == 3) return __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+  return __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false);                       // row_mirror
+}
+
+// Levels 5 and 6: a register swapped with itself by 16-lane rows (rows 0/1
+// and 2/3) or 32-lane halves gives two registers, one holding each group's
+// own value in every lane of the pair of groups and the other the partner
+// group's; combining the two is the tree node, whichever is which.
+template <int L>
+__device__ __forceinline__ void xlane_swap_u32(uint32_t v, uint32_t& a, uint32_t& b) {
+  if constexpr (L == 5) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+  }
+}
+
+template <int L>
+__device__ __forceinline__ double xlane_level_sum_f64(double v) {
+  const uint64_t x = __builtin_bit_cast(uint64_t, v);
+  if constexpr (L <= 4) {
+    const uint64_t p = (uint64_t)xlane_partner_u32<L>((uint32_t)x) |
+                       ((uint64_t)xlane_partner_u32<L>((uint32_t)(x >> 32)) << 32);
+    return v + __builtin_bit_cast(double, p);
+  } else {
+    uint32_t a0, b0, a1, b1;
+    xlane_swap_u32<L>((uint32_t)x, a0, b0);
+    xlane_swap_u32<L>((uint32_t)(x >> 32), a1, b1);
+    return __builtin_bit_cast(double, (uint64_t)a0 | ((uint64_t)a1 << 32)) +
+           __builtin_bit_cast(double, (uint64_t)b0 | ((uint64_t)b1 << 32));
+  }
+}
+
+template <int L>
+__device__ __forceinline__ float xlane_level_max_f32(float v) {
+  const uint32_t x = __builtin_bit_cast(uint32_t, v);
+  if constexpr (L <= 4) {
+    return fmaxf(v, __builtin_bit_cast(float, xlane_partner_u32<L>(x)));
+  } else {
+    uint32_t a, b;
+    xlane_swap_u32<L>(x, a, b);
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+  }
+}
+
+// Sum / max over aligned groups of WL lanes (WL <= 64, a power of two).
+template <int WL>
+__device__ __forceinline__ double wave_group_sum_f64(double v) {
+  if constexpr (WL > 1) v = xlane_level_sum_f64<1>(v);
+  if constexpr (WL > 2) v = xlane_level_sum_f64<2>(v);
+  if constexpr (WL > 4) v = xlane_level_sum_f64<3>(v);
+  if constexpr (WL > 8) v = xlane_level_sum_f64<4>(v);
+  if constexpr (WL > 16) v = xlane_level_sum_f64<5>(v);
+  if constexpr (WL > 32) v = xlane_level_sum_f64<6>(v);
+  return v;
+}
+
+template <int WL>
+__device__ __forceinline__ float wave_group_max_f32(float v) {
+  if constexpr (WL > 1) v = xlane_level_max_f32<1>(v);
+  if constexpr (WL > 2) v = xlane_level_max_f32<2>(v);
+  if constexpr (WL > 4) v = xlane_level_max_f32<3>(v);
+  if constexpr (WL > 8) v = xlane_level_max_f32<4>(v);
+  if constexpr (WL > 16) v = xlane_level_max_f32<5>(v);
+  if constexpr (WL > 32) v = xlane_level_max_f32<6>(v);
+  return v;
+}
 
 template <int TAU>
 __device__ __forceinline__ double team_sum_f64(double v, double* lds_team) {
   constexpr int WL = TAU < 64 ? TAU : 64;
-#pragma unroll
-  for (int m = 1; m < WL; m <<= 1) v = v + __shfl_xor(v, m, 64);
+  v = wave_group_sum_f64<WL>(v);
   if constexpr (TAU > 64) {
     constexpr int NW = TAU / 64;
     const int lane = threadIdx.x & 63;
@@ -146,8 +228,7 @@ __device__ __forceinline__ double team_sum_f64(double v, double* lds_team) {
 template <int TAU>
 __device__ __forceinline__ float team_max_f32(float v, float* lds_team) {
   constexpr int WL = TAU < 64 ? TAU : 64;
-#pragma unroll
-  for (int m = 1; m < WL; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  v = wave_group_max_f32<WL>(v);
   if constexpr (TAU > 64) {
     constexpr int NW = TAU / 64;
     const int lane = threadIdx.x & 63;
@@ -168,12 +249,28 @@ template <int TAU>
 __device__ __forceinline__ int team_excl_scan_i32(int v, int* lds_team, int* total) {
   constexpr int WL = TAU < 64 ? TAU : 64;
   const int lane_in = threadIdx.x & (WL - 1);
+  // inclusive scan: DPP row shifts within rows of 16 lanes (zero from
+  // outside the row), then the gfx9 row broadcasts of lane 15 into rows 1
+  // and 3 and of lane 31 into rows 2 and 3 (other rows receive 0)
   int inc = v;
-#pragma unroll
-  for (int d = 1; d < WL; d <<= 1) {
-    int t = __shfl_up(inc, d, WL);
-    if (lane_in >= d) inc += t;
+  if constexpr (WL > 1) {
+    const int t = __builtin_amdgcn_update_dpp(0, inc, 0x111, 0xF, 0xF, true);  // row_shr:1
+    if (lane_in >= 1) inc += t;
   }
+  if constexpr (WL > 2) {
+    const int t = __builtin_amdgcn_update_dpp(0, inc, 0x112, 0xF, 0xF, true);  // row_shr:2
+    if (lane_in >= 2) inc += t;
+  }
+  if constexpr (WL > 4) {
+    const int t = __builtin_amdgcn_update_dpp(0, inc, 0x114, 0xF, 0xF, true);  // row_shr:4
+    if (lane_in >= 4) inc += t;
+  }
+  if constexpr (WL > 8) {
+    const int t = __builtin_amdgcn_update_dpp(0, inc, 0x118, 0xF, 0xF, true);  // row_shr:8
+    if (lane_in >= 8) inc += t;
+  }
+  if constexpr (WL > 16) inc += __builtin_amdgcn_update_dpp(0, inc, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  if constexpr (WL > 32) inc += __builtin_amdgcn_update_dpp(0, inc, 0x143, 0xC, 0xF, false);  // row_bcast:31
   int wave_total = __shfl(inc, WL - 1, WL);
   int excl = inc - v;
   if constexpr (TAU > 64) {

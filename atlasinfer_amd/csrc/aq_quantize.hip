@@ -421,6 +421,11 @@ __device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
   asm("v_pk_sub_u16 %0, %1, %2 clamp" : "=v"(d) : "v"(a), "v"(b));
   return d;
 }
+__device__ __forceinline__ uint32_t pk_sub_u16(uint32_t a, uint32_t b) {
+  uint32_t d;
+  asm("v_pk_sub_u16 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
 __device__ __forceinline__ uint32_t pk_min_u16(uint32_t a, uint32_t b) {
   uint32_t d;
   asm("v_pk_min_u16 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
@@ -484,7 +489,7 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
         const int i = w * PW + j;
         const uint32_t ad = h2_bits(as_h2(xs.p[i]) + nm) & 0x7FFF7FFFu;
         const uint32_t m = pk_min_u16(pk_sub_sat_u16(ad, th), 0x00010001u);
-        xs.p[i] &= ~(m * 0xFFFFu);
+        xs.p[i] &= ~pk_sub_u16(0u, m);  // 0xFFFF in each outlier half
         acc = 2 * acc + m;
         amax2 = pk_max_u16(amax2, xs.p[i] & 0x7FFF7FFFu);
       }
@@ -560,7 +565,9 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
         // quotient is at most 448.25, which the conversion (round to nearest
         // even) takes to 448 as the clamp to +-448 would
         typedef short short2v __attribute__((vector_size(4)));
-        short2v c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16((short2v){0, 0}, as_h2(quot2(p0, s, r)), 1.0f, false);
+        const uint32_t q0 = quot2(p0, s, r);
+        // both halves of c are written; its initial value is never seen
+        short2v c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(__builtin_bit_cast(short2v, q0), as_h2(q0), 1.0f, false);
         c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(c, as_h2(quot2(p1, s, r)), 1.0f, true);
         w[k] = __builtin_bit_cast(uint32_t, c);
       }

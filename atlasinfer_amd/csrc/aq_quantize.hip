@@ -731,6 +731,29 @@ __global__ __launch_bounds__(256) void scan_apply_kernel(int32_t* off, int64_t n
   if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) off[n] = base_total + total;
 }
 
+// Up to kScanSmall counts (every per-channel weight of a model this size):
+// one workgroup, one launch.
+constexpr int kScanSmall = 1024 * 16;
+__global__ __launch_bounds__(1024) void scan_small_kernel(int32_t* off, int64_t n) {
+  __shared__ int lds[16];
+  const int64_t start = (int64_t)threadIdx.x * 16;
+  int v[16];
+  int s = 0;
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    v[e] = (start + e < n) ? off[start + e] : 0;
+    s += v[e];
+  }
+  int total;
+  int pre = team_excl_scan_i32<1024>(s, lds, &total);
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    if (start + e < n) off[start + e] = pre;
+    pre += v[e];
+  }
+  if (threadIdx.x == 0) off[n] = total;
+}
+
 // ---- gather the staged outliers into the ascending list
 
 template <int TPB>
@@ -904,6 +927,11 @@ extern "C" int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_t
   a.stage_val = w.stage_val;
   hipError_t e = launch_quantize(a, s);
   if (e != hipSuccess) return aq::check_hip(e, "aq_quantize: quantize kernel launch");
+  if (nblocks <= kScanSmall) {
+    hipLaunchKernelGGL(scan_small_kernel, dim3(1), dim3(1024), 0, s, block_off, nblocks);
+    AQ_LAUNCH_CHECK("aq_quantize: scan launch");
+    return AQ_OK;
+  }
   const int64_t nparts = aq::ceil_div(nblocks, kScanChunk);
   hipLaunchKernelGGL(scan_partials_kernel, dim3((unsigned)nparts), dim3(256), 0, s, block_off, nblocks, w.partial);
   AQ_LAUNCH_CHECK("aq_quantize: scan launch");

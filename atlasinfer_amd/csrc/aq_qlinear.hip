@@ -724,14 +724,19 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void qlinear_gemm_k
   const int N = W.N;
   const int M = a.M, K = a.K;
   const int mbands = (M + BM - 1) / BM;
-  const int local = tile - a.first[mi];
+  // split over K (outermost): part ks of the chunks, whose fp32 partial sums
+  // a second kernel adds up
+  const int per_split = ((N + kGemmBN - 1) / kGemmBN) * mbands;
+  const int ks = (tile - a.first[mi]) / per_split;
+  const int local = (tile - a.first[mi]) % per_split;
   const int nbase = (local / mbands) * kGemmBN;
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
   const int m_first = (local % mbands) * BM, m_last = M - 1;
-  const int nch = K / kGemmBK;  // even: K is a multiple of 128
   const int nch128 = K >> 7;
+  const int nch_split = (K / kGemmBK) / a.split;  // even (the host checks)
+  const int c_first = ks * nch_split, c_end = c_first + nch_split;
 
   GemmSrc<WAVES> S;
   gemm_src_init<WAVES>(S, W, a.x, K, m_first, m_last, nbase, nch128, t);
@@ -743,8 +748,8 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void qlinear_gemm_k
   // conditional load would make the wait before the next use of either
   // register set drain every load in flight
   GemmRegs<WAVES> R0, R1;
-  gemm_load<WAVES, PC>(R0, S, W, 0, t);
-  gemm_load<WAVES, PC>(R1, S, W, 1, t);
+  gemm_load<WAVES, PC>(R0, S, W, c_first, t);
+  gemm_load<WAVES, PC>(R1, S, W, c_first + 1, t);
   gemm_load_ent<WAVES>(R0, S, t);
 
   float4v acc[4][4];
@@ -759,21 +764,38 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void qlinear_gemm_k
   gemm_stage<WAVES, FMT, PC, DENSE>(R0, S, As[0], Bs[0], srow, t);
   __syncthreads();
   gemm_load_ent<WAVES>(R1, S, t);
-  gemm_load<WAVES, PC>(R0, S, W, min(2, nch - 1), t);
-  for (int c = 0; c < nch; c += 2) {
+  gemm_load<WAVES, PC>(R0, S, W, min(c_first + 2, c_end - 1), t);
+  for (int c = c_first; c < c_end; c += 2) {
     gemm_mma<4>(acc, As[0], Bs[0], wmf, wnf, lane);
     gemm_stage<WAVES, FMT, PC, DENSE>(R1, S, As[1], Bs[1], srow, t);
     __syncthreads();
     gemm_load_ent<WAVES>(R0, S, t);
-    gemm_load<WAVES, PC>(R1, S, W, min(c + 3, nch - 1), t);
+    gemm_load<WAVES, PC>(R1, S, W, min(c + 3, c_end - 1), t);
     gemm_mma<4>(acc, As[1], Bs[1], wmf, wnf, lane);
-    if (c + 2 < nch) gemm_stage<WAVES, FMT, PC, DENSE>(R0, S, As[0], Bs[0], srow, t);
+    if (c + 2 < c_end) gemm_stage<WAVES, FMT, PC, DENSE>(R0, S, As[0], Bs[0], srow, t);
     __syncthreads();
     gemm_load_ent<WAVES>(R1, S, t);
-    gemm_load<WAVES, PC>(R0, S, W, min(c + 4, nch - 1), t);
+    gemm_load<WAVES, PC>(R0, S, W, min(c + 4, c_end - 1), t);
   }
 
   const int grp = lane >> 4, li = lane & 15;
+  if (a.split > 1) {
+    // partial sums of this part of K, no bias
+    float* part = W.part + (size_t)ks * M * N;
+#pragma unroll
+    for (int ni = 0; ni < 4; ni++) {
+      const int n = nbase + 16 * (wnf + ni) + li;
+      if (n >= N) continue;
+#pragma unroll
+      for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int m = m_first + 16 * (wmf + mi) + 4 * grp + i;
+          if (m < M) part[(size_t)m * N + n] = acc[mi][ni][i];
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int ni = 0; ni < 4; ni++) {
     const int n = nbase + 16 * (wnf + ni) + li;
@@ -787,6 +809,32 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void qlinear_gemm_k
         if (m < M) W.y[(size_t)m * N + n] = h_to_bits(rn_h(acc[mi][ni][i] + bv));
       }
   }
+}
+
+// y = fp16(sum of the split partial sums in order + bias), 4 outputs per
+// thread (N is a multiple of 16).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, int64_t mn, int split, int N,
+                                                            const uint16_t* bias, uint16_t* y) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= mn) return;
+  float4v v = *reinterpret_cast<const float4v*>(part + i);
+  for (int s = 1; s < split; s++) v += *reinterpret_cast<const float4v*>(part + (size_t)s * mn + i);
+  const int n = (int)(i % N);
+  uint16_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) o[j] = h_to_bits(rn_h(v[j] + (bias ? (float)bits_to_h(bias[n + j]) : 0.0f)));
+  *reinterpret_cast<uint2*>(y + i) = make_uint2(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16));
+}
+
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cached[dev];
 }
 
 int log2_exact(int64_t g) {
@@ -849,7 +897,7 @@ hipError_t launch_gemm(QLArgs a, bool per_channel, int64_t maxN, hipStream_t s) 
   int ntiles = 0;
   for (int i = 0; i < a.count; i++) {
     a.first[i] = ntiles;
-    ntiles += (int)aq::ceil_div(a.mat[i].N, kGemmBN) * mbands;
+    ntiles += (int)aq::ceil_div(a.mat[i].N, kGemmBN) * mbands * a.split;
   }
   for (int i = a.count; i <= kMaxGroup; i++) a.first[i] = ntiles;
   const dim3 grid((unsigned)(8 * aq::ceil_div(ntiles, 8)));
@@ -869,21 +917,54 @@ hipError_t launch_gemm(const QLArgs& a, int fmt, bool per_channel, bool dense, i
                             : launch_gemm<WAVES, AQ_FMT_INT8, 0>(a, per_channel, maxN, s);
 }
 
+// GEMM shape choice: 256-row tiles (8 waves, one workgroup per CU) when they
+// still give every CU one, else 128-row tiles (two per CU); a grid that fills
+// at most a quarter of the workgroup slots splits K 2 to 8 ways (up to one
+// full round of workgroups, at least 4 chunks of 64 per part; 16 ways cost
+// more in the reduction than they gained).
+struct GemmPlan {
+  bool wide;
+  int split;
+};
+
+GemmPlan plan_gemm(int64_t M, const int64_t* Ns, int64_t count, int64_t K) {
+  int64_t wg256 = 0, wg128 = 0;
+  for (int i = 0; i < count; i++) {
+    wg256 += aq::ceil_div(M, GemmShape<8>::BM) * aq::ceil_div(Ns[i], kGemmBN);
+    wg128 += aq::ceil_div(M, GemmShape<4>::BM) * aq::ceil_div(Ns[i], kGemmBN);
+  }
+  GemmPlan p{wg256 >= 256, 1};
+  const int64_t tiles = p.wide ? wg256 : wg128;
+  const int64_t slots = (int64_t)cu_count() * (p.wide ? 1 : 2);
+  const int64_t nch = K / kGemmBK;
+  if (4 * tiles <= slots)
+    for (int sp = 8; sp >= 2; sp /= 2)
+      if (tiles * sp <= slots && nch % (2 * sp) == 0 && nch / sp >= 4) {
+        p.split = sp;
+        break;
+      }
+  return p;
+}
+
 }  // namespace
 
 extern "C" int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K) {
-  (void)M;
-  (void)N;
-  (void)K;
-  return 0;  // the kernels need no memory beyond LDS
+  // the GEMM's fp32 partial sums when it would split K for this shape on the
+  // current device (0 for the GEMV and for unsplit grids)
+  if (M <= kGemvMaxM || N <= 0 || K < 128 || K % 128) return 0;
+  const GemmPlan p = plan_gemm(M, &N, 1, K);
+  return p.split > 1 ? p.split * M * N * 4 : 0;
 }
+
+
 
 extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, int64_t count, const int64_t* Ns,
                                   const void* const* codes, const void* const* scales, const int64_t* Gs,
                                   const int32_t* const* row_ptrs, const int32_t* const* cols,
                                   const void* const* vals, const int32_t* const* tile_ptrs,
                                   const uint32_t* const* tile_ents, const int64_t* tile_maxes,
-                                  const void* const* biases, void* const* ys, void* stream) {
+                                  const void* const* biases, void* const* ys, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
   AQ_CHECK_ARG(count >= 1 && count <= kMaxGroup, "aq_qlinear: 1..%d matrices per call (got %lld)", kMaxGroup,
                (long long)count);
   AQ_CHECK_ARG(M >= 0 && M < (1 << 30) && K >= 128 && K % 128 == 0,
@@ -926,12 +1007,14 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
     w.tent = tile_ents ? tile_ents[j] : nullptr;
     w.bias = biases ? (const uint16_t*)biases[j] : nullptr;
     w.y = (uint16_t*)ys[j];
+    w.part = nullptr;
     w.N = (int)N;
     w.G = (int)G;
     w.kg = (int)(K / G);
     w.gshift = log2_exact(G);
   }
   for (int i = (int)count; i <= kMaxGroup; i++) a.first[i] = (int)blocks;
+  a.split = 1;
   if (M == 0) return AQ_OK;
   hipStream_t s = (hipStream_t)stream;
   bool per_channel = true;
@@ -958,21 +1041,40 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
   // 256-row tiles decode each weight half as often, but only pay off while
   // they still give every CU a workgroup; smaller grids take 128-row tiles
   // (two workgroups per CU)
-  int64_t wg256 = 0;
-  for (int i = 0; i < count; i++) wg256 += aq::ceil_div(M, GemmShape<8>::BM) * aq::ceil_div(Ns[i], kGemmBN);
-  const hipError_t e = wg256 >= 256 ? launch_gemm<8>(a, fmt, per_channel, dense, maxN, s)
-                                    : launch_gemm<4>(a, fmt, per_channel, dense, maxN, s);
-  return aq::check_hip(e, "aq_qlinear: gemm launch");
+  // Split K (plan_gemm) as far as the workspace allows: each part's fp32
+  // partial sums go there and splitk_reduce_kernel adds them in a fixed order.
+  int64_t outs = 0;
+  for (int i = 0; i < count; i++) outs += M * Ns[i];
+  const GemmPlan plan = plan_gemm(M, Ns, count, K);
+  const bool wide = plan.wide;
+  a.split = workspace ? plan.split : 1;
+  while (a.split > 1 && workspace_bytes < a.split * outs * 4) a.split /= 2;
+  if (a.split > 1) {
+    AQ_CHECK_ARG((uintptr_t)workspace % 16 == 0, "aq_qlinear: workspace must be 16-byte aligned");
+    float* p = (float*)workspace;
+    for (int i = 0; i < count; i++) {
+      a.mat[i].part = p;
+      p += (size_t)a.split * M * Ns[i];
+    }
+  }
+  hipError_t e = wide ? launch_gemm<8>(a, fmt, per_channel, dense, maxN, s)
+                      : launch_gemm<4>(a, fmt, per_channel, dense, maxN, s);
+  if (e != hipSuccess || a.split == 1) return aq::check_hip(e, "aq_qlinear: gemm launch");
+  for (int i = 0; i < count && e == hipSuccess; i++) {
+    const int64_t mn = M * Ns[i];
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)aq::ceil_div(mn, 1024)), dim3(256), 0, s, a.mat[i].part, mn,
+                       a.split, (int)Ns[i], a.mat[i].bias, a.mat[i].y);
+    e = hipGetLastError();
+  }
+  return aq::check_hip(e, "aq_qlinear: split-K reduce launch");
 }
 
 extern "C" int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const void* codes, const void* scales,
                           int64_t G, int fmt, const int32_t* row_ptr, const int32_t* cols, const void* vals,
                           const int32_t* tile_ptr, const uint32_t* tile_ent, int64_t tile_max, const void* bias,
                           void* y, void* workspace, int64_t ws_bytes, void* stream) {
-  (void)workspace;
-  (void)ws_bytes;
   const void* b = bias;
   void* yy = y;
   return aq_qlinear_grouped(x, M, K, fmt, 1, &N, &codes, &scales, &G, &row_ptr, &cols, &vals, &tile_ptr, &tile_ent,
-                            &tile_max, &b, &yy, stream);
+                            &tile_max, &b, &yy, workspace, ws_bytes, stream);
 }

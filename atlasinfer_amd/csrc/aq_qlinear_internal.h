@@ -24,6 +24,7 @@ struct QLMat {
   const uint32_t* tent;
   const uint16_t* bias;
   uint16_t* y;
+  float* part;  // GEMM split over K: this matrix's fp32 partial sums [split][M][N]
   int N;
   int G;
   int kg;      // K / G, scale blocks per row
@@ -33,6 +34,7 @@ struct QLMat {
 struct QLArgs {
   const uint16_t* x;
   int M, K, count;
+  int split;                 // GEMM: ways the K chunks are split (1: none)
   int first[kMaxGroup + 1];  // GEMV: first workgroup of each matrix
   QLMat mat[kMaxGroup];
 };

@@ -32,6 +32,15 @@ from ..quant.adaptive_quantizer import (QuantizedTensor, _format_id, _rows_cols,
 GEMV_MAX_M = 64  # aq_qlinear runs the dequant-GEMV up to this many rows of x
 
 
+def _workspace(M: int, Ns, K: int, dev: torch.device):
+    """The GEMM's split-K workspace (None for the GEMV) and its size."""
+    if M <= GEMV_MAX_M:
+        return None, 0
+    L = _lib.load()
+    n = sum(int(L.aq_qlinear_workspace_size(M, N, K)) for N in Ns)
+    return torch.empty(n, dtype=torch.uint8, device=dev), n
+
+
 def fused_supported(qt: QuantizedTensor) -> bool:
     """The fused kernels need 16-row x 128-column tiles and blocks of a
     multiple of 32 that divide the row."""
@@ -68,6 +77,7 @@ def qlinear_grouped(x: torch.Tensor, qts, biases=None, codes=None, tiles=None):
             tiles = list(tiles) if tiles is not None else [outlier_tiles(q, dev) for q in qts]
         else:
             tiles = [(None, None, 0)] * n
+        ws, ws_bytes = _workspace(M, Ns, K, dev)
         _lib.check(L.aq_qlinear_grouped(
             x2.data_ptr(), M, K, _format_id(fmt), n, arr(Ns, ctypes.c_int64), arr([c.data_ptr() for c in codes]),
             arr([q.scale_factors.data_ptr() for q in qts]), arr([q.block_size for q in qts], ctypes.c_int64),
@@ -75,7 +85,7 @@ def qlinear_grouped(x: torch.Tensor, qts, biases=None, codes=None, tiles=None):
             arr([_lib.ptr(q.fp16_outliers) for q in qts]), arr([_lib.ptr(t[0]) for t in tiles]),
             arr([_lib.ptr(t[1]) for t in tiles]), arr([t[2] for t in tiles], ctypes.c_int64),
             arr([_lib.ptr(b) for b in biases]),
-            arr([y.data_ptr() for y in ys]), _lib.stream_of(dev)), "aq_qlinear_grouped")
+            arr([y.data_ptr() for y in ys]), _lib.ptr(ws), ws_bytes, _lib.stream_of(dev)), "aq_qlinear_grouped")
     return [y.view(*x.shape[:-1], N) for y, N in zip(ys, Ns)]
 
 
@@ -97,10 +107,11 @@ def qlinear(x: torch.Tensor, qt: QuantizedTensor, bias: Optional[torch.Tensor],
         codes = kernel_codes(qt, dev)
     tp, te, tmax = (tiles if tiles is not None else outlier_tiles(qt, dev)) if M > GEMV_MAX_M else (None, None, 0)
     L = _lib.load()
+    ws, ws_bytes = _workspace(M, [N], K, dev)
     _lib.check(L.aq_qlinear(x2.data_ptr(), M, K, N, codes.data_ptr(), qt.scale_factors.data_ptr(), qt.block_size,
                             _format_id(qt.code_format), qt.outlier_row_ptr.data_ptr(), _lib.ptr(qt.outlier_cols),
                             _lib.ptr(qt.fp16_outliers), _lib.ptr(tp), _lib.ptr(te), tmax, _lib.ptr(bias), y.data_ptr(),
-                            None, 0, _lib.stream_of(dev)), "aq_qlinear")
+                            _lib.ptr(ws), ws_bytes, _lib.stream_of(dev)), "aq_qlinear")
     return y.view(*x.shape[:-1], N)
 
 

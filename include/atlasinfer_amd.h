@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define AQ_ABI_VERSION 2
+#define AQ_ABI_VERSION 3
 
 enum { AQ_FMT_INT8 = 0, AQ_FMT_E4M3 = 1 };
 enum { AQ_LAYOUT_FLAT = 0, AQ_LAYOUT_TILED = 1 };
@@ -175,8 +175,12 @@ int aq_zscore(const void* x, int64_t n, float eps, void* z, void* stats, void* s
  * its decoded zero in the weight tile it multiplies.  Either way the result is
  * x times the dequantized weight accumulated in fp32, plus the bias, rounded
  * once to fp16.
- * workspace: >= aq_qlinear_workspace_size(M, N, K) bytes (currently 0: the
- * kernels keep their partial sums in LDS; NULL is accepted).
+ * workspace: aq_qlinear_workspace_size(M, N, K) bytes, 16-byte aligned, or
+ * NULL.  The GEMM splits K 2 or 4 ways when its grid would leave CUs idle
+ * (k/v projections at M = 2048, most weights at M = 512) and keeps the fp32
+ * partial sums there; a second kernel adds them in a fixed order, so results
+ * are deterministic.  With NULL (or too small a workspace) it runs unsplit.
+ * The GEMV (M <= 64) uses none.
  */
 int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K);
 int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const void* codes, const void* scales,
@@ -191,14 +195,16 @@ int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const void* codes
  * cols[i], vals[i], tile_ptrs[i], tile_ents[i], tile_maxes[i], biases[i]
  * (entries may be NULL), Ns[i] rows.  All W_i share K and fmt.  count <= 4.
  * The arrays themselves are host memory; tile_ptrs/tile_ents/tile_maxes may
- * be NULL when M <= 64.
+ * be NULL when M <= 64.  workspace: the sum over i of
+ * aq_qlinear_workspace_size(M, Ns[i], K) bytes, or NULL (as for aq_qlinear).
  * Same per-matrix requirements as aq_qlinear.
  */
 int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, int64_t count, const int64_t* Ns,
                        const void* const* codes, const void* const* scales, const int64_t* Gs,
                        const int32_t* const* row_ptrs, const int32_t* const* cols, const void* const* vals,
                        const int32_t* const* tile_ptrs, const uint32_t* const* tile_ents,
-                       const int64_t* tile_maxes, const void* const* biases, void* const* ys, void* stream);
+                       const int64_t* tile_maxes, const void* const* biases, void* const* ys, void* workspace,
+                       int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -81,7 +81,10 @@ def test_bad_arguments_return_einval_with_message(lib):
 def test_workspace_sizes(lib):
     assert lib.aq_quantize_workspace_size(4096 * 4096, 4096) >= 4096 * 4096 * 6
     assert lib.aq_quantize_workspace_size(0, 128) == 0
-    assert lib.aq_qlinear_workspace_size(1, 4096, 4096) == 0  # kernels use LDS only
+    assert lib.aq_qlinear_workspace_size(1, 4096, 4096) == 0  # the GEMV needs none
+    assert lib.aq_qlinear_workspace_size(64, 4096, 4096) == 0
+    # the GEMM: fp32 partial sums of up to a 4-way split of K
+    assert lib.aq_qlinear_workspace_size(2048, 1024, 4096) == 4 * 2048 * 1024 * 4
     assert lib.aq_max_block_size() == 65536
 
 

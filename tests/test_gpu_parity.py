@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 import torch
 
+from atlasinfer_amd import _lib
 from atlasinfer_core.quant import adaptive_quantizer as AQ
 from conftest import golden_cases
 from integration import atlas_wrappers as AW
@@ -209,7 +210,7 @@ def test_qlinear_matches_reference_linear(M, fmt, G):
 
 
 @pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (4096, 14336), (14336, 4096)])
-@pytest.mark.parametrize("M", [1, 16, 40, 64, 512])
+@pytest.mark.parametrize("M", [1, 16, 40, 64, 512, 2048])
 def test_qlinear_llama_shapes(N, K, M):
     rng = np.random.default_rng(N + K + M)
     w = make_weights(rng, (N, K))
@@ -239,6 +240,41 @@ def test_gemv_shared_x_ragged_shapes(N, K, M, fmt, G):
     w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
     y = AW.QuantizedLinear(q, b)(x)
     assert_close(y, reference_linear(x, w_deq, b), x, w_deq)
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 1024, 4096), (512, 4096, 4096), (300, 1024, 2048)])
+def test_gemm_split_k_matches_unsplit(M, N, K):
+    """Grids too small for the GPU split K and add fp32 partial sums in a
+    second kernel (workspace given); without a workspace the same call runs
+    unsplit.  Both within the bounds, the split result deterministic."""
+    rng = np.random.default_rng(M + N + K)
+    w = make_weights(rng, (N, K), frac=0.003)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)
+    b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(DEV)
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, code_format="e4m3")
+    AQ.clear_dequantized_cache()
+    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    L = _lib.load()
+    codes = AQ.kernel_codes(q, torch.device(DEV))
+    tp, te, tmax = AQ.outlier_tiles(q, torch.device(DEV))
+    ws_bytes = int(L.aq_qlinear_workspace_size(M, N, K))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+
+    def run(workspace, nbytes):
+        y = torch.empty(M, N, dtype=torch.float16, device=DEV)
+        _lib.check(L.aq_qlinear(x.data_ptr(), M, K, N, codes.data_ptr(), q.scale_factors.data_ptr(), K, 1,
+                                q.outlier_row_ptr.data_ptr(), q.outlier_cols.data_ptr(), q.fp16_outliers.data_ptr(),
+                                tp.data_ptr(), te.data_ptr(), tmax, b.data_ptr(), y.data_ptr(), workspace, nbytes,
+                                _lib.stream_of(torch.device(DEV))), "aq_qlinear")
+        return y
+
+    ref = reference_linear(x, w_deq, b)
+    y_split = run(ws.data_ptr(), ws_bytes)
+    y_split2 = run(ws.data_ptr(), ws_bytes)
+    y_plain = run(None, 0)
+    assert torch.equal(y_split, y_split2)
+    assert_close(y_split, ref, x, w_deq)
+    assert_close(y_plain, ref, x, w_deq)
 
 
 def test_qlinear_heavy_outliers_and_3d_input():

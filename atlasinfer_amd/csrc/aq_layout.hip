@@ -163,13 +163,8 @@ __device__ __forceinline__ int lower_bound_i32(const int32_t* a, int lo, int hi,
   return lo;
 }
 
-// Position of (row r, column k) in a 16 x 64 block, in the order the
-// dequant-GEMM keeps a block in LDS (two 16x32 MFMA B operands of 8-element
-// lane pieces): bit 9 = k / 32, bits 8..7 = (k / 8) % 4, bits 6..3 = r,
-// bits 2..0 = k % 8.  A bijection of the 1024 (r, k) pairs.
-__device__ __forceinline__ uint32_t block_position(int r, int k) {
-  return ((uint32_t)(k >> 5) << 9) | ((uint32_t)((k >> 3) & 3) << 7) | ((uint32_t)r << 3) | (uint32_t)(k & 7);
-}
+// Position of row r (0..15), column k (0..63) in a block's entry: r << 6 | k.
+__device__ __forceinline__ uint32_t block_position(int r, int k) { return ((uint32_t)r << 6) | (uint32_t)k; }
 
 // One thread per block of 16 rows x 64 columns (tile row rb, chunk c).
 // Entries are ordered by block, then row, then column, so a block starts

@@ -499,219 +499,197 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
 
 // ------------------------------------------------------------ GEMM (M > 64)
 //
-// Workgroup tile BM x 128: WAVES waves in a (WAVES/2) x 2 layout of 64 x 64
-// wave tiles (16x16 MFMA tiles); BM = 128 with 4 waves (two workgroups per
-// CU) or 256 with 8 waves (one workgroup per CU, each weight decoded once
-// per 256 rows of x).  K advances in chunks of 64.  Per chunk, every thread
-//   * loads AP 16-byte pieces of x (one lane of AP A fragments: 16 rows x 8
-//     k, in exactly the lane order the MFMA reads), and CP 16-byte pieces of
-//     codes (lane order of the tiled layout: one row, 16 consecutive k);
-//   * writes the x pieces to the LDS A buffer, decodes its 32 codes to fp16
-//     weights and writes them to the LDS B buffer in B-fragment order, and
-//     then writes the fp16 value of every outlier that falls in its two
-//     pieces over the zero its code decoded to.  The outliers of a 16-row x
-//     64-column block come as one short list (tile_ptr / tile_ent); a wave
-//     holds up to 64 entries of each of its two blocks, one per lane, and
-//     every lane writes its own with one store (after the wave's bulk
-//     writes of the same block, in program order).
-// The B buffer thus holds exactly the dequantized weight (dequantize_tensor's
-// values, outliers included), and the MFMAs need no correction pass.  Global
-// loads run ahead through two register sets: a chunk's block pointers and
-// bulk data three chunks ahead, its outlier entries two ahead (issued before
-// the next bulk loads, so waiting for them never waits for those); LDS is
-// double buffered with one barrier per chunk.
+// Workgroup tile BM x 128 (BM = 256 or 128 rows of x by 128 output
+// columns), 8 waves in a 4 x 2 layout of (BM / 4) x 64 wave tiles made of
+// 32x32x16 MFMAs; K advances in chunks of 64.  LDS holds three chunk stages,
+// each an A tile (x, BM rows x 64 fp16) and a B tile (decoded weights, 128
+// rows x 64 fp16).  A tile row is 128 bytes whose eight 16-byte pieces are
+// permuted by the row (tile_off) so that fragment reads and staging writes
+// are free of bank conflicts.
+//
+// In chunk c a wave
+//   * multiplies chunk c, k-step by k-step, with the fragments of the next
+//     k-step read while the current one is on the MFMA unit -- the first
+//     k-step of chunk c + 1 too, which is already complete in LDS;
+//   * stages chunk c + 2 into the stage chunk c - 1 used: its x pieces as
+//     loaded, its 16 codes (one weight row, 16 consecutive k) decoded to
+//     fp16, then the fp16 value of each outlier of its 16 x 64 weight block
+//     over the zero its code decoded to.  Wave w owns block row w, so these
+//     writes follow the bulk writes of the same block in program order;
+//   * issues the global loads of chunk c + 4 (two register sets: loads have
+//     two chunks to land) and the outlier entries of chunk c + 3 (whose
+//     block pointers came with its bulk loads);
+// and the workgroup meets once per chunk at a barrier.  The B tile thus holds
+// exactly dequantize_tensor's weights, outliers included, and the MFMAs need
+// no correction pass.  Every load in the K loop is a buffer load: the
+// barrier's release fence would wait for global-pointer loads.
 
 constexpr int kGemmBN = 128, kGemmBK = 64;
 
-// WAVES waves per workgroup in a (WAVES/2) x 2 layout of 64 x 64 wave tiles.
-template <int WAVES>
-struct GemmShape {
-  static constexpr int BM = WAVES / 2 * 64;              // rows of x per workgroup
-  static constexpr int AP = BM * kGemmBK * 2 / 16 / (64 * WAVES);  // x pieces per thread and chunk
-  static constexpr int CP = kGemmBN * kGemmBK / 16 / (64 * WAVES);  // code pieces (= blocks per wave)
+template <int BM>
+struct GemmCfg {
+  static constexpr int WM = BM / 4;         // wave tile rows
+  static constexpr int MI = WM / 32;        // 32-row MFMA tiles per wave
+  static constexpr int XP = BM / 64;        // 16-byte x pieces per thread and chunk
+  static constexpr int A_BYTES = BM * 128;  // BM rows x 64 fp16
+  static constexpr int B_BYTES = kGemmBN * 128;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
 };
 
-template <int WAVES>
+template <int BM>
 struct GemmRegs {
-  static constexpr int AP = GemmShape<WAVES>::AP, CP = GemmShape<WAVES>::CP;
-  u32x4 a[AP];         // x pieces
-  u32x4 q[CP];         // code pieces
-  uint32_t s;          // their scales, piece 0 in the low half (block-wise scales only)
-  int e0[CP], e1[CP];  // outlier entries of the wave's blocks: [e0, e1)
-  uint32_t ent[CP];    // entry e0 + lane of each block
+  u32x4 a[GemmCfg<BM>::XP];  // x pieces
+  u32x4 q;                   // 16 codes: one weight row, 16 consecutive k
+  uint32_t s;                // their scale (block-wise scales only)
+  int e0, e1;                // outlier entries of the wave's block: [e0, e1)
+  uint32_t ent;              // entry e0 + lane
 };
 
 // Loop-invariant part of the global loads: buffer descriptors over this
-// workgroup's x rows and code rows, and each piece's 32-bit byte offset in
-// them; a chunk only adds a scalar offset.
-template <int WAVES>
+// workgroup's x rows, code rows, block pointers, entries and scales, and
+// each piece's byte offset in chunk 0 (a chunk adds a scalar offset).
+template <int BM>
 struct GemmSrc {
-  static constexpr int AP = GemmShape<WAVES>::AP, CP = GemmShape<WAVES>::CP;
-  __amdgpu_buffer_rsrc_t xr, cr;
-  __amdgpu_buffer_rsrc_t tr, er, sr;  // block pointers, entries, scales
-  int xo[AP];  // x pieces
-  int co[CP];  // code pieces
-  int to[CP];  // block pointer of chunk 0 of each code row, in bytes
-  int so[CP];  // scale row of each code piece, in bytes
+  __amdgpu_buffer_rsrc_t xr, cr, tr, er, sr;
+  int xo[GemmCfg<BM>::XP];
+  int co;  // code piece
+  int to;  // block pointer of chunk 0 of the wave's block row
+  int so;  // scale row
 };
 
-
-template <int WAVES>
-__device__ __forceinline__ void gemm_src_init(GemmSrc<WAVES>& S, const QLMat& W, const uint16_t* x, int K, int m_first,
-                                              int m_last, int nbase, int nch128, int t) {
-  const int l = t & 63;
-  const int rows = min(m_last - m_first + 1, GemmShape<WAVES>::BM);  // this workgroup's x rows
+template <int BM>
+__device__ __forceinline__ void gemm_src_init(GemmSrc<BM>& S, const QLMat& W, const uint16_t* x, int M, int K,
+                                              int m_first, int nbase, int nch128, int t) {
+  const int l = t & 63, w = t >> 6;
+  const int rows = min(M - m_first, BM);  // this workgroup's x rows; the rest clamp to the last
   S.xr = __builtin_amdgcn_make_buffer_rsrc((void*)(x + (size_t)m_first * K), (short)0, rows * K * 2, kBufferDword3);
 #pragma unroll
-  for (int i = 0; i < S.AP; i++) {
-    const int f = (t >> 6) + WAVES * i;  // A fragment: 16-row group f >> 1, k-step f & 1
-    const int row = min(16 * (f >> 1) + (l & 15), rows - 1);
-    S.xo[i] = (row * K + 32 * (f & 1) + 8 * (l >> 4)) * 2;
+  for (int i = 0; i < GemmCfg<BM>::XP; i++) {
+    const int row = min(64 * i + (t >> 3), rows - 1);
+    S.xo[i] = (row * K + 8 * (t & 7)) * 2;
   }
   const int rb0 = nbase / 16, rb_last = W.N / 16 - 1;
-  const int nrb = min(rb_last - rb0 + 1, kGemmBN / 16);  // this workgroup's tile rows
+  const int nrb = min(rb_last - rb0 + 1, kGemmBN / 16);  // this workgroup's block rows
+  const int nch64 = nch128 * 2;
   S.cr = __builtin_amdgcn_make_buffer_rsrc((void*)(W.codes + ((size_t)rb0 * nch128 << 11)), (short)0,
                                            nrb * nch128 * 2048, kBufferDword3);
-  const int nch64 = nch128 * 2;
-  S.tr = __builtin_amdgcn_make_buffer_rsrc((void*)(W.tptr + (size_t)rb0 * nch64), (short)0,
-                                           (nrb * nch64 + 1) * 4, kBufferDword3);
+  S.tr = __builtin_amdgcn_make_buffer_rsrc((void*)(W.tptr + (size_t)rb0 * nch64), (short)0, (nrb * nch64 + 1) * 4,
+                                           kBufferDword3);
+  // entries: e0 + lane stays inside the list and its 64 slots of padding
   S.er = __builtin_amdgcn_make_buffer_rsrc((void*)W.tent, (short)0, 0x7fffffff, kBufferDword3);
   S.sr = __builtin_amdgcn_make_buffer_rsrc((void*)(W.scales + (size_t)rb0 * 16 * W.kg), (short)0,
                                            nrb * 16 * W.kg * 2, kBufferDword3);
-#pragma unroll
-  for (int i = 0; i < S.CP; i++) {
-    // tile rows past N clamp to the last one and feed only outputs that are never stored
-    const int rb = min(rb0 + (t >> 6) + WAVES * i, rb_last) - rb0;
-    S.co[i] = rb * nch128 * 2048 + l * 16;
-    S.to[i] = rb * nch64 * 4;
-    S.so[i] = (rb * 16 + (l & 15)) * W.kg * 2;
-  }
+  // block rows past N clamp to the last one and feed only outputs never stored
+  const int rb = min(rb0 + w, rb_last) - rb0;
+  S.co = rb * nch128 * 2048 + l * 16;
+  S.to = rb * nch64 * 4;
+  S.so = (rb * 16 + (l & 15)) * W.kg * 2;
 }
 
-// Block pointers and bulk loads (x, codes, scales) of chunk c into one
-// register set.  Everything in the K loop goes through buffer loads: the
-// barrier's release fence waits for outstanding global-pointer loads, which
-// would drain the prefetches every chunk.
-template <int WAVES, int PC>
-__device__ __forceinline__ void gemm_load(GemmRegs<WAVES>& R, const GemmSrc<WAVES>& S, const QLMat& W, int c, int t) {
-  const int l = t & 63;
+// Block pointers and bulk loads (x, codes, scale) of chunk c.
+template <int BM, int PC>
+__device__ __forceinline__ void gemm_load(GemmRegs<BM>& R, const GemmSrc<BM>& S, const QLMat& W, int c, int l) {
+  typedef int int2v __attribute__((ext_vector_type(2)));
+  const int2v p = __builtin_bit_cast(int2v, __builtin_amdgcn_raw_buffer_load_b64(S.tr, S.to, c * 4, 0));
+  R.e0 = p.x;
+  R.e1 = p.y;
+  __builtin_amdgcn_sched_barrier(0);  // block pointers ahead of the bulk loads: the entries wait only for them
   const int k0 = c * kGemmBK;
 #pragma unroll
-  for (int i = 0; i < R.CP; i++) {
-    typedef int int2v __attribute__((ext_vector_type(2)));
-    const int2v p = __builtin_bit_cast(int2v, __builtin_amdgcn_raw_buffer_load_b64(S.tr, S.to[i], c * 4, 0));
-    R.e0[i] = p.x;
-    R.e1[i] = p.y;
-  }
-  __builtin_amdgcn_sched_barrier(0);  // block pointers ahead of the bulk loads, as with the entries
-#pragma unroll
-  for (int i = 0; i < R.AP; i++) R.a[i] = __builtin_amdgcn_raw_buffer_load_b128(S.xr, S.xo[i], k0 * 2, 0);
-  const int cs = ((c >> 1) << 11) + ((c & 1) << 10);
-#pragma unroll
-  for (int i = 0; i < R.CP; i++) {
-    R.q[i] = __builtin_amdgcn_raw_buffer_load_b128(S.cr, S.co[i], cs, 0);
-    if (!PC) {
-      // the block differs per lane: the offset goes in the vector operand
-      const int kb = W.gshift >= 0 ? ((k0 + 16 * (l >> 4)) >> W.gshift) : (k0 + 16 * (l >> 4)) / W.G;
-      const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so[i] + kb * 2, 0, 0);
-      R.s = i == 0 ? sv : (R.s | (sv << 16));
-    }
+  for (int i = 0; i < GemmCfg<BM>::XP; i++)
+    R.a[i] = __builtin_amdgcn_raw_buffer_load_b128(S.xr, S.xo[i], k0 * 2, 0);
+  R.q = __builtin_amdgcn_raw_buffer_load_b128(S.cr, S.co, ((c >> 1) << 11) + ((c & 1) << 10), 0);
+  if (!PC) {
+    const int k = k0 + 16 * (l >> 4);
+    const int kb = W.gshift >= 0 ? (k >> W.gshift) : k / W.G;
+    R.s = __builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so + kb * 2, 0, 0);
   }
 }
 
 // Outlier entries of the chunk whose block pointers R holds: lane j takes
-// entry e0 + j (the list has 64 slots of padding, so every lane reads
-// inside it; lanes past the block's count ignore what they read).
-template <int WAVES>
-__device__ __forceinline__ void gemm_load_ent(GemmRegs<WAVES>& R, const GemmSrc<WAVES>& S, int t) {
-  const int l = t & 63;
-#pragma unroll
-  for (int i = 0; i < R.CP; i++)
-    R.ent[i] = __builtin_amdgcn_raw_buffer_load_b32(S.er, l * 4, __builtin_amdgcn_readfirstlane(R.e0[i]) * 4, 0);
-  // keep these ahead of the next bulk loads: loads complete in issue order,
-  // so the stage that reads the entries then waits only for them
+// entry e0 + j (lanes past the block's count ignore what they read).
+template <int BM>
+__device__ __forceinline__ void gemm_load_ent(GemmRegs<BM>& R, const GemmSrc<BM>& S, int l) {
+  // not earlier: the wait for the block pointers would also wait for the
+  // bulk loads issued after them (the empty asm keeps the first use of e0
+  // behind the barrier that precedes this call)
   __builtin_amdgcn_sched_barrier(0);
+  int e0 = R.e0;
+  asm volatile("" : "+v"(e0));
+  R.ent = __builtin_amdgcn_raw_buffer_load_b32(S.er, l * 4, __builtin_amdgcn_readfirstlane(e0) * 4, 0);
+  __builtin_amdgcn_sched_barrier(0);  // ahead of the next bulk loads: loads complete in issue order
 }
 
-// Register set -> LDS: x pieces to the A buffer, decoded weights to the B
-// buffer, then the outliers of this thread's pieces over them.
-template <int WAVES, int FMT, int PC, int DENSE>
-__device__ __forceinline__ void gemm_stage(const GemmRegs<WAVES>& R, const GemmSrc<WAVES>& S, uint16_t* As,
-                                           uint16_t* Bs, const half2v (&srow)[GemmShape<WAVES>::CP], int t) {
-  const int l = t & 63;
-  const int g = l >> 4, r = l & 15;
+// Byte offset of (row, 16-byte piece) in an A or B tile: 128-byte rows,
+// piece p stored at p ^ (row & 7) ^ ((row >> 3) & 1).  Measured on gfx950:
+// 16-byte LDS reads serve 16 lanes per cycle over 64 banks, 16-byte writes
+// 8 lanes over 128 bytes.  Reads of 16 consecutive rows at one piece then
+// fall on 8 distinct pieces among the even rows and 8 among the odd rows,
+// and writes of 8 consecutive rows at one piece (or of one row's 8 pieces)
+// on 8 distinct pieces.
+__device__ __forceinline__ uint32_t tile_off(int row, int piece) {
+  return (uint32_t)(row * 128 + ((piece ^ (row & 7) ^ ((row >> 3) & 1)) << 4));
+}
+
+// x pieces [I0, I1) of R into the A tile.
+template <int BM, int I0, int I1>
+__device__ __forceinline__ void gemm_stage_x(const GemmRegs<BM>& R, uint8_t* As, int t) {
+  const uint32_t o = tile_off(t >> 3, t & 7);  // rows 64 i + t / 8 share the permutation
 #pragma unroll
-  for (int i = 0; i < R.AP; i++) {
-    const int f = (t >> 6) + WAVES * i;
-    *reinterpret_cast<u32x4*>(As + f * 512 + l * 8) = R.a[i];
-  }
-#pragma unroll
-  for (int i = 0; i < R.CP; i++) {
-    const int rb = (t >> 6) + WAVES * i;
-    const half2v s2 = PC ? srow[i] : scale2((uint16_t)(R.s >> (16 * i)));
-    const half8 w0 = deq8<FMT>(R.q[i].x, R.q[i].y, s2);
-    const half8 w1 = deq8<FMT>(R.q[i].z, R.q[i].w, s2);
-    uint16_t* frag = Bs + (rb * 2 + (g >> 1)) * 512;
-    *reinterpret_cast<half8*>(frag + (r + 32 * (g & 1)) * 8) = w0;
-    *reinterpret_cast<half8*>(frag + (r + 32 * (g & 1) + 16) * 8) = w1;
-  }
-  // Outliers: lane j writes entry e0 + j of each block.  The block's codes
-  // were written by this same wave just above, and LDS executes a wave's
-  // instructions in order, so each value lands over its decoded zero.
-#pragma unroll
-  for (int i = 0; i < R.CP; i++) {
-    const int rb = (t >> 6) + WAVES * i;
-    const int cnt = R.e1[i] - R.e0[i];
-    if (l < cnt) Bs[rb * 1024 + (R.ent[i] & 1023)] = (uint16_t)(R.ent[i] >> 16);
-    // blocks more than 1/16 outliers (DENSE launches only): the rest from
-    // memory, 64 per round.  Kept out of the common kernel: loads in a
-    // data-dependent loop make every later wait in the chunk a full drain.
-    if (DENSE) {
-      const int e0 = __builtin_amdgcn_readfirstlane(R.e0[i]);
-      const int n = __builtin_amdgcn_readfirstlane(cnt);
-      for (int j = 64 + l; j - l < n; j += 64) {
-        if (j < n) {
-          const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(S.er, (e0 + j) * 4, 0, 0);
-          Bs[rb * 1024 + (v & 1023)] = (uint16_t)(v >> 16);
-        }
+  for (int i = I0; i < I1; i++) *reinterpret_cast<u32x4*>(As + o + i * 64 * 128) = R.a[i];
+}
+
+// Codes of R decoded into the B tile, then the block's outliers over them.
+template <int BM, int FMT, int PC, int DENSE>
+__device__ __forceinline__ void gemm_stage_w(const GemmRegs<BM>& R, const GemmSrc<BM>& S, uint8_t* Bs, uint8_t* spare,
+                                             half2v srow, int t) {
+  const int l = t & 63, w = t >> 6;
+  const int n = 16 * w + (l & 15), g = l >> 4;
+  const half2v s2 = PC ? srow : scale2((uint16_t)R.s);
+  *reinterpret_cast<half8*>(Bs + tile_off(n, 2 * g)) = deq8<FMT>(R.q.x, R.q.y, s2);
+  *reinterpret_cast<half8*>(Bs + tile_off(n, 2 * g + 1)) = deq8<FMT>(R.q.z, R.q.w, s2);
+  // entry: (fp16 value << 16) | r << 6 | k for row 16 w + r, column k of the chunk
+  auto at = [&](uint32_t e) {
+    const int r = (int)((e >> 6) & 15), k = (int)(e & 63);
+    return tile_off(16 * w + r, k >> 3) + ((k & 7) << 1);
+  };
+  const int cnt = R.e1 - R.e0;
+  // lanes past the block's count write to the spare slot instead (no branch,
+  // so the scheduler may interleave the staging with the MFMAs around it)
+  *reinterpret_cast<uint16_t*>(l < cnt ? Bs + at(R.ent) : spare + 2 * l) = (uint16_t)(R.ent >> 16);
+  // blocks of more than 64 outliers (DENSE launches only): the rest from
+  // memory, 64 per round.  Kept out of the common kernel: loads in a
+  // data-dependent loop make every later wait in the chunk a full drain.
+  if (DENSE) {
+    const int e0 = __builtin_amdgcn_readfirstlane(R.e0);
+    const int ne = __builtin_amdgcn_readfirstlane(cnt);
+    for (int j = 64 + l; j - l < ne; j += 64)
+      if (j < ne) {
+        const uint32_t e = __builtin_amdgcn_raw_buffer_load_b32(S.er, (e0 + j) * 4, 0, 0);
+        *reinterpret_cast<uint16_t*>(Bs + at(e)) = (uint16_t)(e >> 16);
       }
-    }
   }
 }
 
-template <int MI>
-__device__ __forceinline__ void gemm_mma(float4v (&acc)[MI][4], const uint16_t* As, const uint16_t* Bs, int wmf,
-                                         int wnf, int lane) {
-  // let the scheduler interleave the fragment reads with the MFMAs (measured
-  // +4 % at M = 2048, +7 % at M = 512 on the Llama-3-8B shapes)
-  __builtin_amdgcn_iglp_opt(0);
-#pragma unroll
-  for (int j = 0; j < 2; j++) {
-    half8 af[MI], bf[4];
-#pragma unroll
-    for (int mi = 0; mi < MI; mi++) af[mi] = *reinterpret_cast<const half8*>(As + ((wmf + mi) * 2 + j) * 512 + lane * 8);
-#pragma unroll
-    for (int ni = 0; ni < 4; ni++) bf[ni] = *reinterpret_cast<const half8*>(Bs + ((wnf + ni) * 2 + j) * 512 + lane * 8);
-#pragma unroll
-    for (int mi = 0; mi < MI; mi++)
-#pragma unroll
-      for (int ni = 0; ni < 4; ni++)
-        acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mi], bf[ni], acc[mi][ni], 0, 0, 0);
-  }
-}
+template <int BM>
+struct GemmFrags {
+  half8 a[GemmCfg<BM>::MI];
+  half8 b[2];
+};
 
-template <int WAVES, int FMT, int PC, int DENSE>
-__global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void qlinear_gemm_kernel(QLArgs a) {
-  constexpr int BM = GemmShape<WAVES>::BM, CP = GemmShape<WAVES>::CP;
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kGemmBK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][kGemmBN * kGemmBK];
+template <int BM, int FMT, int PC, int DENSE>
+__global__ __launch_bounds__(512, 1) void qlinear_gemm_kernel(QLArgs a) {
+  typedef GemmCfg<BM> C;
+  constexpr int MI = C::MI;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * C::STAGE + 128];  // + the spare slot of gemm_stage_w
+  uint8_t* const spare = lds + 3 * C::STAGE;
 
   // Output tiles of all matrices of the launch in one list (a.first[i]:
-  // first tile of matrix i; within a matrix, tile = n-tile * M-bands +
-  // M-band).  Workgroups go to the 8 XCDs in turn, so workgroup id takes tile
-  // (id % 8) * per + id / 8: each XCD works through its own contiguous run,
-  // all M-bands of a few n-tiles at a time, and their codes and x rows stay
-  // in that XCD's L2.
+  // first tile of matrix i; within a matrix, tile = split part, then n-tile,
+  // then M-band).  Workgroups go to the 8 XCDs in turn, so workgroup id
+  // takes tile (id % 8) * per + id / 8: each XCD works through its own
+  // contiguous run, all M-bands of a few n-tiles at a time, and their codes
+  // and x rows stay in that XCD's L2.
   const int ntiles = a.first[a.count];
   const int per = (ntiles + 7) / 8;
   const int tile = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
@@ -724,89 +702,133 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void qlinear_gemm_k
   const int N = W.N;
   const int M = a.M, K = a.K;
   const int mbands = (M + BM - 1) / BM;
-  // split over K (outermost): part ks of the chunks, whose fp32 partial sums
-  // a second kernel adds up
   const int per_split = ((N + kGemmBN - 1) / kGemmBN) * mbands;
   const int ks = (tile - a.first[mi]) / per_split;
   const int local = (tile - a.first[mi]) % per_split;
   const int nbase = (local / mbands) * kGemmBN;
+  const int m_first = (local % mbands) * BM;
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
-  const int m_first = (local % mbands) * BM, m_last = M - 1;
   const int nch128 = K >> 7;
   const int nch_split = (K / kGemmBK) / a.split;  // even (the host checks)
   const int c_first = ks * nch_split, c_end = c_first + nch_split;
 
-  GemmSrc<WAVES> S;
-  gemm_src_init<WAVES>(S, W, a.x, K, m_first, m_last, nbase, nch128, t);
-  half2v srow[CP];  // per-channel scales of this thread's code rows
-#pragma unroll
-  for (int i = 0; i < CP; i++)
-    srow[i] = scale2(PC ? (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so[i], 0, 0) : (uint16_t)0);
-  // prefetches are unconditional (past the last chunk they re-read it): a
-  // conditional load would make the wait before the next use of either
-  // register set drain every load in flight
-  GemmRegs<WAVES> R0, R1;
-  gemm_load<WAVES, PC>(R0, S, W, c_first, t);
-  gemm_load<WAVES, PC>(R1, S, W, c_first + 1, t);
-  gemm_load_ent<WAVES>(R0, S, t);
+  GemmSrc<BM> S;
+  gemm_src_init<BM>(S, W, a.x, M, K, m_first, nbase, nch128, t);
+  const half2v srow = scale2(PC ? (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so, 0, 0) : (uint16_t)0);
 
-  float4v acc[4][4];
+  // fragment addresses: lane l reads row (l % 32) of a 32-row group, piece
+  // 2 s + l / 32 for k-step s; the permutation depends on the row only
+  // through (l % 32), so one offset per k-step serves every fragment
+  const int wm = wave >> 1, wn = wave & 1;
+  uint32_t foff[4];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int s = 0; s < 4; s++) foff[s] = tile_off(lane & 31, 2 * s + (lane >> 5));
+  const uint32_t a_row0 = (uint32_t)(wm * C::WM) * 128, b_row0 = C::A_BYTES + (uint32_t)(wn * 64) * 128;
+
+  float16v acc[MI][2];
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = (float16v)0.0f;
 
-  const int wmf = (wave >> 1) * 4;   // first 16-row group of this wave
-  const int wnf = (wave & 1) * 4;    // first 16-column group
+  auto read_frags = [&](GemmFrags<BM>& F, uint32_t stage, int s) {
+    const uint8_t* p = lds + stage + foff[s];
+#pragma unroll
+    for (int i = 0; i < MI; i++) F.a[i] = *reinterpret_cast<const half8*>(p + a_row0 + i * 32 * 128);
+#pragma unroll
+    for (int j = 0; j < 2; j++) F.b[j] = *reinterpret_cast<const half8*>(p + b_row0 + j * 32 * 128);
+  };
+  auto mma = [&](const GemmFrags<BM>& F) {
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(F.a[i], F.b[j], acc[i][j], 0, 0, 0);
+  };
 
-  gemm_stage<WAVES, FMT, PC, DENSE>(R0, S, As[0], Bs[0], srow, t);
+  // prologue: chunks c_first, c_first + 1 staged; their successors loading
+  GemmRegs<BM> R0, R1;
+  gemm_load<BM, PC>(R0, S, W, c_first, lane);
+  gemm_load<BM, PC>(R1, S, W, c_first + 1, lane);
+  gemm_load_ent<BM>(R0, S, lane);
+  gemm_load_ent<BM>(R1, S, lane);
+  gemm_stage_x<BM, 0, C::XP>(R0, lds, t);
+  gemm_stage_w<BM, FMT, PC, DENSE>(R0, S, lds + C::A_BYTES, spare, srow, t);
+  gemm_load<BM, PC>(R0, S, W, min(c_first + 2, c_end - 1), lane);
+  gemm_stage_x<BM, 0, C::XP>(R1, lds + C::STAGE, t);
+  gemm_stage_w<BM, FMT, PC, DENSE>(R1, S, lds + C::STAGE + C::A_BYTES, spare, srow, t);
+  gemm_load<BM, PC>(R1, S, W, min(c_first + 3, c_end - 1), lane);
+  gemm_load_ent<BM>(R0, S, lane);
   __syncthreads();
-  gemm_load_ent<WAVES>(R1, S, t);
-  gemm_load<WAVES, PC>(R0, S, W, min(c_first + 2, c_end - 1), t);
+
+  // Fragments are read two k-steps ahead (F[s] holds k-step s of a chunk);
+  // the first two k-steps of chunk c + 1 are read during chunk c, whose
+  // barrier has already made them visible.
+  GemmFrags<BM> F[4];
+  read_frags(F[0], 0, 0);
+  read_frags(F[1], 0, 1);
+  uint32_t cur = 0;  // stage of chunk c, in bytes
+  auto next_stage = [](uint32_t s) { return s == 2 * C::STAGE ? 0u : s + C::STAGE; };
+
+  // chunk c: R holds chunk c + 2 (to stage), Ro chunk c + 3 (entries to
+  // load).  Staging is unconditional: past the last chunk it rewrites a
+  // stage no later k-step reads, with the clamped chunk's data.  The LDS
+  // writes go right after the barrier, behind the reads of k-step 2, while
+  // the MFMAs run on fragments read before the barrier: the reads that wait
+  // behind the writes are needed two k-steps later.
+  auto body = [&](int c, GemmRegs<BM>& R, GemmRegs<BM>& Ro) {
+    const uint32_t nxt = next_stage(cur), stg = next_stage(nxt);
+    read_frags(F[2], cur, 2);
+    mma(F[0]);
+    gemm_load_ent<BM>(Ro, S, lane);
+    gemm_stage_x<BM, 0, C::XP>(R, lds + stg, t);
+    gemm_stage_w<BM, FMT, PC, DENSE>(R, S, lds + stg + C::A_BYTES, spare, srow, t);
+    read_frags(F[3], cur, 3);
+    mma(F[1]);
+    read_frags(F[0], nxt, 0);
+    gemm_load<BM, PC>(R, S, W, min(c + 4, c_end - 1), lane);
+    mma(F[2]);
+    read_frags(F[1], nxt, 1);
+    mma(F[3]);
+    __syncthreads();
+    cur = nxt;
+  };
   for (int c = c_first; c < c_end; c += 2) {
-    gemm_mma<4>(acc, As[0], Bs[0], wmf, wnf, lane);
-    gemm_stage<WAVES, FMT, PC, DENSE>(R1, S, As[1], Bs[1], srow, t);
-    __syncthreads();
-    gemm_load_ent<WAVES>(R0, S, t);
-    gemm_load<WAVES, PC>(R1, S, W, min(c + 3, c_end - 1), t);
-    gemm_mma<4>(acc, As[1], Bs[1], wmf, wnf, lane);
-    if (c + 2 < c_end) gemm_stage<WAVES, FMT, PC, DENSE>(R0, S, As[0], Bs[0], srow, t);
-    __syncthreads();
-    gemm_load_ent<WAVES>(R1, S, t);
-    gemm_load<WAVES, PC>(R0, S, W, min(c + 4, c_end - 1), t);
+    body(c, R0, R1);
+    body(c + 1, R1, R0);
   }
 
-  const int grp = lane >> 4, li = lane & 15;
+  // C layout (32x32): lane l, element e -> row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32
+  const int hi = lane >> 5, lc = lane & 31;
   if (a.split > 1) {
     // partial sums of this part of K, no bias
     float* part = W.part + (size_t)ks * M * N;
 #pragma unroll
-    for (int ni = 0; ni < 4; ni++) {
-      const int n = nbase + 16 * (wnf + ni) + li;
+    for (int j = 0; j < 2; j++) {
+      const int n = nbase + wn * 64 + j * 32 + lc;
       if (n >= N) continue;
 #pragma unroll
-      for (int mi = 0; mi < 4; mi++)
+      for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int m = m_first + 16 * (wmf + mi) + 4 * grp + i;
-          if (m < M) part[(size_t)m * N + n] = acc[mi][ni][i];
+        for (int e = 0; e < 16; e++) {
+          const int m = m_first + wm * C::WM + i * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+          if (m < M) part[(size_t)m * N + n] = acc[i][j][e];
         }
     }
     return;
   }
 #pragma unroll
-  for (int ni = 0; ni < 4; ni++) {
-    const int n = nbase + 16 * (wnf + ni) + li;
+  for (int j = 0; j < 2; j++) {
+    const int n = nbase + wn * 64 + j * 32 + lc;
     if (n >= N) continue;
     const float bv = W.bias ? (float)bits_to_h(W.bias[n]) : 0.0f;
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int m = m_first + 16 * (wmf + mi) + 4 * grp + i;
-        if (m < M) W.y[(size_t)m * N + n] = h_to_bits(rn_h(acc[mi][ni][i] + bv));
+      for (int e = 0; e < 16; e++) {
+        const int m = m_first + wm * C::WM + i * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+        if (m < M) W.y[(size_t)m * N + n] = h_to_bits(rn_h(acc[i][j][e] + bv));
       }
   }
 }
@@ -889,11 +911,10 @@ hipError_t launch_gemv_x(QLArgs a, int fmt, bool per_channel, int S, hipStream_t
   return S == 2 ? launch_gemv_x<4, 2>(a, fmt, per_channel, wgs, s) : launch_gemv_x<4, 4>(a, fmt, per_channel, wgs, s);
 }
 
-template <int WAVES, int FMT, int DENSE>
-hipError_t launch_gemm(QLArgs a, bool per_channel, int64_t maxN, hipStream_t s) {
-  (void)maxN;
+template <int BM, int FMT, int DENSE>
+hipError_t launch_gemm(QLArgs a, bool per_channel, hipStream_t s) {
   // a.first: first output tile of each matrix (see the kernel)
-  const int mbands = (int)aq::ceil_div(a.M, GemmShape<WAVES>::BM);
+  const int mbands = (int)aq::ceil_div(a.M, BM);
   int ntiles = 0;
   for (int i = 0; i < a.count; i++) {
     a.first[i] = ntiles;
@@ -902,26 +923,27 @@ hipError_t launch_gemm(QLArgs a, bool per_channel, int64_t maxN, hipStream_t s) 
   for (int i = a.count; i <= kMaxGroup; i++) a.first[i] = ntiles;
   const dim3 grid((unsigned)(8 * aq::ceil_div(ntiles, 8)));
   if (per_channel)
-    hipLaunchKernelGGL((qlinear_gemm_kernel<WAVES, FMT, 1, DENSE>), grid, dim3(64 * WAVES), 0, s, a);
+    hipLaunchKernelGGL((qlinear_gemm_kernel<BM, FMT, 1, DENSE>), grid, dim3(512), 0, s, a);
   else
-    hipLaunchKernelGGL((qlinear_gemm_kernel<WAVES, FMT, 0, DENSE>), grid, dim3(64 * WAVES), 0, s, a);
+    hipLaunchKernelGGL((qlinear_gemm_kernel<BM, FMT, 0, DENSE>), grid, dim3(512), 0, s, a);
   return hipGetLastError();
 }
 
-template <int WAVES>
-hipError_t launch_gemm(const QLArgs& a, int fmt, bool per_channel, bool dense, int64_t maxN, hipStream_t s) {
+template <int BM>
+hipError_t launch_gemm(const QLArgs& a, int fmt, bool per_channel, bool dense, hipStream_t s) {
   if (dense)
-    return fmt == AQ_FMT_E4M3 ? launch_gemm<WAVES, AQ_FMT_E4M3, 1>(a, per_channel, maxN, s)
-                              : launch_gemm<WAVES, AQ_FMT_INT8, 1>(a, per_channel, maxN, s);
-  return fmt == AQ_FMT_E4M3 ? launch_gemm<WAVES, AQ_FMT_E4M3, 0>(a, per_channel, maxN, s)
-                            : launch_gemm<WAVES, AQ_FMT_INT8, 0>(a, per_channel, maxN, s);
+    return fmt == AQ_FMT_E4M3 ? launch_gemm<BM, AQ_FMT_E4M3, 1>(a, per_channel, s)
+                              : launch_gemm<BM, AQ_FMT_INT8, 1>(a, per_channel, s);
+  return fmt == AQ_FMT_E4M3 ? launch_gemm<BM, AQ_FMT_E4M3, 0>(a, per_channel, s)
+                            : launch_gemm<BM, AQ_FMT_INT8, 0>(a, per_channel, s);
 }
 
-// GEMM shape choice: 256-row tiles (8 waves, one workgroup per CU) when they
-// still give every CU one, else 128-row tiles (two per CU); a grid that fills
-// at most a quarter of the workgroup slots splits K 2 to 8 ways (up to one
-// full round of workgroups, at least 4 chunks of 64 per part; 16 ways cost
-// more in the reduction than they gained).
+// GEMM shape choice.  Both tile heights run one workgroup per CU (their
+// three LDS stages take 144 or 96 KiB); a 128-row tile takes about 3/4 of
+// the time of a 256-row one (measured on gfx950), so 256-row tiles unless
+// the 128-row grid needs less than 4/3 of the rounds.  Then a grid that
+// fills at most half the CUs splits K 2 to 8 ways (up to one full round, at
+// least 4 chunks of 64 per part).
 struct GemmPlan {
   bool wide;
   int split;
@@ -930,14 +952,14 @@ struct GemmPlan {
 GemmPlan plan_gemm(int64_t M, const int64_t* Ns, int64_t count, int64_t K) {
   int64_t wg256 = 0, wg128 = 0;
   for (int i = 0; i < count; i++) {
-    wg256 += aq::ceil_div(M, GemmShape<8>::BM) * aq::ceil_div(Ns[i], kGemmBN);
-    wg128 += aq::ceil_div(M, GemmShape<4>::BM) * aq::ceil_div(Ns[i], kGemmBN);
+    wg256 += aq::ceil_div(M, 256) * aq::ceil_div(Ns[i], kGemmBN);
+    wg128 += aq::ceil_div(M, 128) * aq::ceil_div(Ns[i], kGemmBN);
   }
-  GemmPlan p{wg256 >= 256, 1};
+  const int64_t slots = cu_count();
+  GemmPlan p{4 * aq::ceil_div(wg256, slots) <= 3 * aq::ceil_div(wg128, slots), 1};
   const int64_t tiles = p.wide ? wg256 : wg128;
-  const int64_t slots = (int64_t)cu_count() * (p.wide ? 1 : 2);
   const int64_t nch = K / kGemmBK;
-  if (4 * tiles <= slots)
+  if (2 * tiles <= slots)
     for (int sp = 8; sp >= 2; sp /= 2)
       if (tiles * sp <= slots && nch % (2 * sp) == 0 && nch / sp >= 4) {
         p.split = sp;
@@ -979,7 +1001,7 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
   a.M = (int)M;
   a.K = (int)K;
   a.count = (int)count;
-  int64_t blocks = 0, maxN = 0;
+  int64_t blocks = 0;
   for (int i = 0; i < kMaxGroup; i++) {
     const int j = i < count ? i : 0;
     const int64_t N = Ns[j], G = Gs[j];
@@ -995,7 +1017,6 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
                    "aq_qlinear: M > 64 needs the outlier tile lists (aq_outlier_tiles) for matrix %d", i);
       a.first[i] = (int)blocks;
       blocks += N / 16;
-      maxN = std::max(maxN, N);
     }
     QLMat& w = a.mat[i];
     w.codes = (const uint8_t*)codes[j];
@@ -1057,8 +1078,8 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
       p += (size_t)a.split * M * Ns[i];
     }
   }
-  hipError_t e = wide ? launch_gemm<8>(a, fmt, per_channel, dense, maxN, s)
-                      : launch_gemm<4>(a, fmt, per_channel, dense, maxN, s);
+  hipError_t e = wide ? launch_gemm<256>(a, fmt, per_channel, dense, s)
+                      : launch_gemm<128>(a, fmt, per_channel, dense, s);
   if (e != hipSuccess || a.split == 1) return aq::check_hip(e, "aq_qlinear: gemm launch");
   for (int i = 0; i < count && e == hipSuccess; i++) {
     const int64_t mn = M * Ns[i];

@@ -111,11 +111,9 @@ int aq_outlier_cols(const int64_t* flat_idx, int64_t nnz, int64_t K, int32_t* co
  *                                           columns 64c..64c+63, at index
  *                                           rb * (K/64) + c; entries
  *                                           tile_ptr[b] .. tile_ptr[b+1]-1
- *   tile_ent uint32 [nnz + 64]              (fp16 value << 16) | p, where for
- *                                           row r (0..15) and column k (0..63)
- *                                           in the block p = (k/32) << 9 |
- *                                           (k/8 % 4) << 7 | r << 3 | k % 8
- *                                           (the block's MFMA operand order);
+ *   tile_ent uint32 [nnz + 64]              (fp16 value << 16) | r << 6 | k
+ *                                           for row r (0..15) and column k
+ *                                           (0..63) in the block;
  *                                           ordered by block, row, column; the
  *                                           last 64 slots are padding the
  *                                           kernels may read but never use

@@ -293,15 +293,14 @@ def test_qlinear_heavy_outliers_and_3d_input():
 
 def expected_tiles(q, N, K):
     """The 16 x 64 block outlier lists restated with numpy from the flat
-    indices: entry (fp16 bits << 16) | p with, for r = row % 16 and
-    k = col % 64, p = (k // 32) << 9 | (k // 8 % 4) << 7 | r << 3 | k % 8,
-    ordered by block (rb * K/64 + col // 64), then row, then column."""
+    indices: entry (fp16 bits << 16) | r << 6 | k with r = row % 16 and
+    k = col % 64, ordered by block (rb * K/64 + col // 64), then row, then column."""
     idx = q.outlier_indices.cpu().numpy()
     vals = bits(q.fp16_outliers).astype(np.uint32)
     n, c = idx // K, idx % K
     blk = (n // 16) * (K // 64) + c // 64
     r, k = (n % 16).astype(np.uint32), (c % 64).astype(np.uint32)
-    ent = (vals << 16) | (k // 32) << 9 | (k // 8 % 4) << 7 | r << 3 | k % 8
+    ent = (vals << 16) | r << 6 | k
     order = np.argsort(blk, kind="stable")  # flat order is already (row, column)
     ptr = np.searchsorted(blk[order], np.arange((N // 16) * (K // 64) + 1))
     return ptr.astype(np.int32), ent[order]

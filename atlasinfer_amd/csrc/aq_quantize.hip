@@ -732,26 +732,46 @@ __global__ __launch_bounds__(256) void scan_apply_kernel(int32_t* off, int64_t n
 }
 
 // Up to kScanSmall counts (every per-channel weight of a model this size):
-// one workgroup, one launch.
+// one workgroup, one launch.  The counts go in rounds of 4096, each thread
+// taking 4 consecutive ones with one 16-byte load, so every load and store
+// instruction covers 1 KiB of contiguous memory (per-thread runs of 16 made
+// the single workgroup's loads touch 64 lines each).
 constexpr int kScanSmall = 1024 * 16;
 __global__ __launch_bounds__(1024) void scan_small_kernel(int32_t* off, int64_t n) {
   __shared__ int lds[16];
-  const int64_t start = (int64_t)threadIdx.x * 16;
-  int v[16];
-  int s = 0;
+  int carry = 0;
+  for (int64_t r0 = 0; r0 < n; r0 += 4096) {
+    const int64_t i = r0 + 4 * (int64_t)threadIdx.x;
+    int v[4];
+    const bool whole = i + 4 <= n;
+    if (whole) {
+      const int4 u = *reinterpret_cast<const int4*>(off + i);
+      v[0] = u.x;
+      v[1] = u.y;
+      v[2] = u.z;
+      v[3] = u.w;
+    } else {
 #pragma unroll
-  for (int e = 0; e < 16; e++) {
-    v[e] = (start + e < n) ? off[start + e] : 0;
-    s += v[e];
-  }
-  int total;
-  int pre = team_excl_scan_i32<1024>(s, lds, &total);
+      for (int e = 0; e < 4; e++) v[e] = i + e < n ? off[i + e] : 0;
+    }
+    int total;
+    int pre = team_excl_scan_i32<1024>((v[0] + v[1]) + (v[2] + v[3]), lds, &total) + carry;
+    int o[4];
 #pragma unroll
-  for (int e = 0; e < 16; e++) {
-    if (start + e < n) off[start + e] = pre;
-    pre += v[e];
+    for (int e = 0; e < 4; e++) {
+      o[e] = pre;
+      pre += v[e];
+    }
+    if (whole) {
+      *reinterpret_cast<int4*>(off + i) = make_int4(o[0], o[1], o[2], o[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (i + e < n) off[i + e] = o[e];
+    }
+    carry += total;
   }
-  if (threadIdx.x == 0) off[n] = total;
+  if (threadIdx.x == 0) off[n] = carry;
 }
 
 // ---- gather the staged outliers into the ascending list

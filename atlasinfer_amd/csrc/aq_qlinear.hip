@@ -46,10 +46,14 @@ constexpr int kGemvUnroll = 2;  // 128-wide K chunks per wave with loads in flig
 constexpr int kCsrCap = 1024;   // outlier entries
 constexpr int kXvCap = 1024;    // staged x values: entries * M <= kXvCap
 constexpr int kStageBatch = 8;  // entries per lane whose loads are issued together
+constexpr int kGemvX1MaxK = 16384;  // decode keeps x in LDS up to this row length (32 KiB)
 
-template <int NS, int FMT, int PC>
+template <int NS, int FMT, int PC, int X1>
 __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   constexpr int U = kGemvUnroll;
+  // X1 (M = 1): x is staged in LDS once, K fp16 followed by 64 zero bytes
+  // that the lanes of rows 1..15 of the MFMA A operand read instead
+  extern __shared__ __attribute__((aligned(16))) uint16_t x_lds[];
   __shared__ float red[NS][256];
   __shared__ int s_rp[17];
   __shared__ int s_meta[3];  // p0, staged entries, entries with staged x
@@ -120,7 +124,10 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
 #pragma unroll
     for (int b = 0; b < kStageBatch; b++) {
       const int e = 64 * b + lane;
-      sx0[b] = __builtin_amdgcn_raw_buffer_load_b16(xr, e < cnt ? scol[b] * 2 : kOutOfRange, 0, 0);
+      if (X1)
+        sx0[b] = x_lds[e < cnt ? scol[b] : K];
+      else
+        sx0[b] = __builtin_amdgcn_raw_buffer_load_b16(xr, e < cnt ? scol[b] * 2 : kOutOfRange, 0, 0);
     }
   };
 
@@ -133,7 +140,7 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   // groups such as gate/up), plain ones when several waves share it
   // (measured on the Llama-3-8B shapes).
   constexpr int kCodePolicy = NS == 1 ? 2 : 0;  // 2: nt
-  auto load = [&](Batch& B, int c0) {
+  auto load_q = [&](Batch& B, int c0) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int c = c0 + u * NS;
@@ -148,12 +155,32 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
         B.s[u][0] = __builtin_amdgcn_raw_buffer_load_b16(sr, (scale_row + k0) * 2, 0, 0);
         B.s[u][1] = __builtin_amdgcn_raw_buffer_load_b16(sr, (scale_row + k1) * 2, 0, 0);
       }
-      const uint32_t xo = in ? x_lane + (uint32_t)c * 256 : kOutOfRange;
-      B.x[u][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo, 0, 0));
-      B.x[u][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + 16, 0, 0));
-      B.x[u][2] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + 128, 0, 0));  // + 64 columns
-      B.x[u][3] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + 144, 0, 0));
     }
+  };
+  auto load_x = [&](Batch& B, int c0) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int c = c0 + u * NS;
+      const bool in = c < nchunks;
+      if (X1) {
+        // rows 1..15 and chunks past K read the zeros after x
+        const uint16_t* xp = x_lds + (li == 0 && in ? 128 * c + 16 * grp : K);
+        B.x[u][0] = *reinterpret_cast<const u32x4*>(xp);
+        B.x[u][1] = *reinterpret_cast<const u32x4*>(xp + (li == 0 && in ? 8 : 0));
+        B.x[u][2] = *reinterpret_cast<const u32x4*>(xp + (li == 0 && in ? 64 : 0));  // + 64 columns
+        B.x[u][3] = *reinterpret_cast<const u32x4*>(xp + (li == 0 && in ? 72 : 0));
+      } else {
+        const uint32_t xo = in ? x_lane + (uint32_t)c * 256 : kOutOfRange;
+        B.x[u][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo, 0, 0));
+        B.x[u][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + 16, 0, 0));
+        B.x[u][2] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + 128, 0, 0));  // + 64 columns
+        B.x[u][3] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + 144, 0, 0));
+      }
+    }
+  };
+  auto load = [&](Batch& B, int c0) {
+    load_q(B, c0);
+    load_x(B, c0);
   };
   float4v acc = (float4v){0.f, 0.f, 0.f, 0.f};
   auto compute = [&](const Batch& B) {
@@ -177,17 +204,45 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   // out of range (no memory traffic) and the products zero.
   const int step = U * NS;
   Batch B0, B1;
-  load(B0, wave);
-  if (wave == 0) stage_first_batch();
-  for (int c0 = wave; c0 < nchunks; c0 += 2 * step) {
-    load(B1, c0 + step);
-    __builtin_amdgcn_sched_barrier(0);
-    if (wave == 0 && c0 == 0) gather_x0();
-    compute(B0);
-    __builtin_amdgcn_sched_barrier(0);
-    load(B0, c0 + 2 * step);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(B1);
+  if (X1) {
+    load_q(B0, wave);
+    load_q(B1, wave + step);
+    {
+      // x behind the codes of the first two batches: its wait, which also
+      // waits for them, comes once, before they are needed anyway
+      const __amdgpu_buffer_rsrc_t xr1 = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, K * 2, kBufferDword3);
+      for (int i = threadIdx.x; i < (K >> 3) + 4; i += 64 * NS)
+        *reinterpret_cast<u32x4*>(x_lds + 8 * i) = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr1, i < (K >> 3) ? (uint32_t)i * 16 : kOutOfRange, 0, 0));
+      __syncthreads();
+    }
+    load_x(B0, wave);
+    load_x(B1, wave + step);
+    if (wave == 0) stage_first_batch();
+    for (int c0 = wave; c0 < nchunks; c0 += 2 * step) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (wave == 0 && c0 == 0) gather_x0();
+      compute(B0);
+      __builtin_amdgcn_sched_barrier(0);
+      load(B0, c0 + 2 * step);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(B1);
+      __builtin_amdgcn_sched_barrier(0);
+      load(B1, c0 + 3 * step);
+    }
+  } else {
+    load(B0, wave);
+    if (wave == 0) stage_first_batch();
+    for (int c0 = wave; c0 < nchunks; c0 += 2 * step) {
+      load(B1, c0 + step);
+      __builtin_amdgcn_sched_barrier(0);
+      if (wave == 0 && c0 == 0) gather_x0();
+      compute(B0);
+      __builtin_amdgcn_sched_barrier(0);
+      load(B0, c0 + 2 * step);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(B1);
+    }
   }
   // C layout: lane l, element i -> m = 4 (l / 16) + i, column l % 16
 #pragma unroll
@@ -263,10 +318,11 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
         float xv, wv;
         if (e < cnt) {
           const int col = s_col[e];
-          xv = (float)bits_to_h(e < nx ? s_xv[e] : a.x[col]);
+          xv = (float)bits_to_h(e < nx ? s_xv[e] : X1 ? x_lds[col] : a.x[col]);
           wv = (float)bits_to_h(s_val[e]);
         } else {
-          xv = (float)bits_to_h(a.x[W.cols[p0 + e]]);
+          const int col = W.cols[p0 + e];
+          xv = (float)bits_to_h(X1 ? x_lds[col] : a.x[col]);
           wv = (float)bits_to_h(W.vals[p0 + e]);
         }
         v = __builtin_fmaf(xv, wv, v);
@@ -868,10 +924,20 @@ int log2_exact(int64_t g) {
 
 template <int NS, int FMT>
 hipError_t launch_gemv(const QLArgs& a, bool per_channel, int blocks, hipStream_t s) {
-  if (per_channel)
-    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1>), dim3(blocks), dim3(64 * NS), 0, s, a);
+  // decode (M = 1) with x small enough and at most 4 waves per tile row: x in
+  // LDS (dynamic size).  With 8 waves per tile row (short matrices, 1 to 2
+  // workgroups per CU) the staging latency costs more than the x loads it
+  // saves (measured).
+  const bool x1 = a.M == 1 && a.K <= kGemvX1MaxK && NS <= 4;
+  const size_t lds = x1 ? (size_t)a.K * 2 + 64 : 0;
+  if (per_channel && x1)
+    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 1>), dim3(blocks), dim3(64 * NS), lds, s, a);
+  else if (per_channel)
+    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 0>), dim3(blocks), dim3(64 * NS), 0, s, a);
+  else if (x1)
+    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 1>), dim3(blocks), dim3(64 * NS), lds, s, a);
   else
-    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0>), dim3(blocks), dim3(64 * NS), 0, s, a);
+    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 0>), dim3(blocks), dim3(64 * NS), 0, s, a);
   return hipGetLastError();
 }
 

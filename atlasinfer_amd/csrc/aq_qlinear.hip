@@ -556,73 +556,76 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
 // ------------------------------------------------------------ GEMM (M > 64)
 //
 // Workgroup tile BM x 128 (BM = 256 or 128 rows of x by 128 output
-// columns), 8 waves in a 4 x 2 layout of (BM / 4) x 64 wave tiles made of
-// 32x32x16 MFMAs; K advances in chunks of 64.  LDS holds three chunk stages,
-// each an A tile (x, BM rows x 64 fp16) and a B tile (decoded weights, 128
-// rows x 64 fp16).  A tile row is 128 bytes whose eight 16-byte pieces are
-// permuted by the row (tile_off) so that fragment reads and staging writes
-// are free of bank conflicts.
-//
-// In chunk c a wave
-//   * multiplies chunk c, k-step by k-step, with the fragments of the next
-//     k-step read while the current one is on the MFMA unit -- the first
-//     k-step of chunk c + 1 too, which is already complete in LDS;
-//   * stages chunk c + 2 into the stage chunk c - 1 used: its x pieces as
-//     loaded, its 16 codes (one weight row, 16 consecutive k) decoded to
-//     fp16, then the fp16 value of each outlier of its 16 x 64 weight block
-//     over the zero its code decoded to.  Wave w owns block row w, so these
-//     writes follow the bulk writes of the same block in program order;
-//   * issues the global loads of chunk c + 4 (two register sets: loads have
-//     two chunks to land) and the outlier entries of chunk c + 3 (whose
-//     block pointers came with its bulk loads);
-// and the workgroup meets once per chunk at a barrier.  The B tile thus holds
-// exactly dequantize_tensor's weights, outliers included, and the MFMAs need
-// no correction pass.  Every load in the K loop is a buffer load: the
+// columns), K in chunks of 64, 8 waves in two roles:
+//   * waves 0-3 (consumers, one per SIMD) own a 2 x 2 layout of (BM / 2) x 64
+//     output tiles of 32x32x16 MFMAs.  Per chunk they only read fragments
+//     from LDS and issue MFMAs, fragments two k-steps ahead of their use;
+//   * waves 4-7 (producers) do all global loads, decode the weight codes,
+//     write the x pieces and the decoded weights into LDS, and write each
+//     outlier's fp16 value over the zero its code decoded to (the outliers
+//     of a 16 x 64 weight block come as one short list from aq_outlier_tiles;
+//     producer wave p owns weight block rows 2p and 2p + 1, so these writes
+//     follow its own bulk writes of the same block in program order).
+// LDS holds three chunk stages, each an A tile (x, BM rows x 64 fp16) and a
+// B tile (decoded weights, 128 rows x 64 fp16), rows of 128 bytes whose
+// 16-byte pieces are permuted by the row (tile_off) so that fragment reads
+// and staging writes are free of bank conflicts.  In chunk c the consumers
+// multiply chunk c (and read the first two k-steps of chunk c + 1, already
+// complete) while the producers stage chunk c + 2 into the stage chunk c - 1
+// used, from registers loaded two chunks earlier, and issue the loads of
+// chunk c + 4; the workgroup meets once per chunk at a barrier.  The B tile
+// holds exactly dequantize_tensor's weights, outliers included, so the MFMAs
+// need no correction pass.  Every load in the K loop is a buffer load: the
 // barrier's release fence would wait for global-pointer loads.
 
 constexpr int kGemmBN = 128, kGemmBK = 64;
 
 template <int BM>
 struct GemmCfg {
-  static constexpr int WM = BM / 4;         // wave tile rows
-  static constexpr int MI = WM / 32;        // 32-row MFMA tiles per wave
-  static constexpr int XP = BM / 64;        // 16-byte x pieces per thread and chunk
-  static constexpr int A_BYTES = BM * 128;  // BM rows x 64 fp16
+  static constexpr int WM = BM / 2;            // consumer wave tile rows
+  static constexpr int MI = WM / 32;           // 32-row MFMA tiles per consumer wave
+  static constexpr int XP = BM * 128 / 16 / 256;  // 16-byte x pieces per producer thread and chunk
+  static constexpr int A_BYTES = BM * 128;     // BM rows x 64 fp16
   static constexpr int B_BYTES = kGemmBN * 128;
   static constexpr int STAGE = A_BYTES + B_BYTES;
 };
 
+// A producer thread's share of one chunk: XP x pieces, and for each of its
+// wave's two weight block rows 16 codes (one row, 16 consecutive k), their
+// scale and the block's outlier list.
 template <int BM>
 struct GemmRegs {
-  u32x4 a[GemmCfg<BM>::XP];  // x pieces
-  u32x4 q;                   // 16 codes: one weight row, 16 consecutive k
-  uint32_t s;                // their scale (block-wise scales only)
-  int e0, e1;                // outlier entries of the wave's block: [e0, e1)
-  uint32_t ent;              // entry e0 + lane
+  u32x4 a[GemmCfg<BM>::XP];
+  u32x4 q[2];
+  uint32_t s[2];   // block-wise scales only
+  int e0[2], e1[2];  // outlier entries of each block: [e0, e1)
+  uint32_t ent[2];   // entry e0 + lane of each block
 };
 
-// Loop-invariant part of the global loads: buffer descriptors over this
-// workgroup's x rows, code rows, block pointers, entries and scales, and
-// each piece's byte offset in chunk 0 (a chunk adds a scalar offset).
+// Loop-invariant part of a producer thread's global loads: buffer
+// descriptors over this workgroup's x rows, code rows, block pointers,
+// entries and scales, and each piece's byte offset in chunk 0 (a chunk adds
+// a scalar offset).
 template <int BM>
 struct GemmSrc {
   __amdgpu_buffer_rsrc_t xr, cr, tr, er, sr;
   int xo[GemmCfg<BM>::XP];
-  int co;  // code piece
-  int to;  // block pointer of chunk 0 of the wave's block row
-  int so;  // scale row
+  int co[2];  // code pieces
+  int to[2];  // block pointer of chunk 0 of each block row
+  int so[2];  // scale row of each code piece
 };
 
+// pt: producer thread 0..255
 template <int BM>
 __device__ __forceinline__ void gemm_src_init(GemmSrc<BM>& S, const QLMat& W, const uint16_t* x, int M, int K,
-                                              int m_first, int nbase, int nch128, int t) {
-  const int l = t & 63, w = t >> 6;
+                                              int m_first, int nbase, int nch128, int pt) {
+  const int l = pt & 63, pw = pt >> 6;
   const int rows = min(M - m_first, BM);  // this workgroup's x rows; the rest clamp to the last
   S.xr = __builtin_amdgcn_make_buffer_rsrc((void*)(x + (size_t)m_first * K), (short)0, rows * K * 2, kBufferDword3);
 #pragma unroll
   for (int i = 0; i < GemmCfg<BM>::XP; i++) {
-    const int row = min(64 * i + (t >> 3), rows - 1);
-    S.xo[i] = (row * K + 8 * (t & 7)) * 2;
+    const int row = min(32 * i + (pt >> 3), rows - 1);
+    S.xo[i] = (row * K + 8 * (pt & 7)) * 2;
   }
   const int rb0 = nbase / 16, rb_last = W.N / 16 - 1;
   const int nrb = min(rb_last - rb0 + 1, kGemmBN / 16);  // this workgroup's block rows
@@ -635,44 +638,56 @@ __device__ __forceinline__ void gemm_src_init(GemmSrc<BM>& S, const QLMat& W, co
   S.er = __builtin_amdgcn_make_buffer_rsrc((void*)W.tent, (short)0, 0x7fffffff, kBufferDword3);
   S.sr = __builtin_amdgcn_make_buffer_rsrc((void*)(W.scales + (size_t)rb0 * 16 * W.kg), (short)0,
                                            nrb * 16 * W.kg * 2, kBufferDword3);
-  // block rows past N clamp to the last one and feed only outputs never stored
-  const int rb = min(rb0 + w, rb_last) - rb0;
-  S.co = rb * nch128 * 2048 + l * 16;
-  S.to = rb * nch64 * 4;
-  S.so = (rb * 16 + (l & 15)) * W.kg * 2;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    // block rows past N clamp to the last one and feed only outputs never stored
+    const int rb = min(rb0 + 2 * pw + i, rb_last) - rb0;
+    S.co[i] = rb * nch128 * 2048 + l * 16;
+    S.to[i] = rb * nch64 * 4;
+    S.so[i] = (rb * 16 + (l & 15)) * W.kg * 2;
+  }
 }
 
-// Block pointers and bulk loads (x, codes, scale) of chunk c.
+// Block pointers and bulk loads (x, codes, scales) of chunk c.
 template <int BM, int PC>
 __device__ __forceinline__ void gemm_load(GemmRegs<BM>& R, const GemmSrc<BM>& S, const QLMat& W, int c, int l) {
   typedef int int2v __attribute__((ext_vector_type(2)));
-  const int2v p = __builtin_bit_cast(int2v, __builtin_amdgcn_raw_buffer_load_b64(S.tr, S.to, c * 4, 0));
-  R.e0 = p.x;
-  R.e1 = p.y;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int2v p = __builtin_bit_cast(int2v, __builtin_amdgcn_raw_buffer_load_b64(S.tr, S.to[i], c * 4, 0));
+    R.e0[i] = p.x;
+    R.e1[i] = p.y;
+  }
   __builtin_amdgcn_sched_barrier(0);  // block pointers ahead of the bulk loads: the entries wait only for them
   const int k0 = c * kGemmBK;
 #pragma unroll
   for (int i = 0; i < GemmCfg<BM>::XP; i++)
     R.a[i] = __builtin_amdgcn_raw_buffer_load_b128(S.xr, S.xo[i], k0 * 2, 0);
-  R.q = __builtin_amdgcn_raw_buffer_load_b128(S.cr, S.co, ((c >> 1) << 11) + ((c & 1) << 10), 0);
-  if (!PC) {
-    const int k = k0 + 16 * (l >> 4);
-    const int kb = W.gshift >= 0 ? (k >> W.gshift) : k / W.G;
-    R.s = __builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so + kb * 2, 0, 0);
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    R.q[i] = __builtin_amdgcn_raw_buffer_load_b128(S.cr, S.co[i], ((c >> 1) << 11) + ((c & 1) << 10), 0);
+    if (!PC) {
+      const int k = k0 + 16 * (l >> 4);
+      const int kb = W.gshift >= 0 ? (k >> W.gshift) : k / W.G;
+      R.s[i] = __builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so[i] + kb * 2, 0, 0);
+    }
   }
 }
 
 // Outlier entries of the chunk whose block pointers R holds: lane j takes
-// entry e0 + j (lanes past the block's count ignore what they read).
+// entry e0 + j of each block (lanes past the block's count ignore what they
+// read).  Not earlier than called: the wait for the block pointers would also
+// wait for the bulk loads issued after them (the empty asm keeps the first
+// use of e0 behind the barrier that precedes this call).
 template <int BM>
 __device__ __forceinline__ void gemm_load_ent(GemmRegs<BM>& R, const GemmSrc<BM>& S, int l) {
-  // not earlier: the wait for the block pointers would also wait for the
-  // bulk loads issued after them (the empty asm keeps the first use of e0
-  // behind the barrier that precedes this call)
   __builtin_amdgcn_sched_barrier(0);
-  int e0 = R.e0;
-  asm volatile("" : "+v"(e0));
-  R.ent = __builtin_amdgcn_raw_buffer_load_b32(S.er, l * 4, __builtin_amdgcn_readfirstlane(e0) * 4, 0);
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    int e0 = R.e0[i];
+    asm volatile("" : "+v"(e0));
+    R.ent[i] = __builtin_amdgcn_raw_buffer_load_b32(S.er, l * 4, __builtin_amdgcn_readfirstlane(e0) * 4, 0);
+  }
   __builtin_amdgcn_sched_barrier(0);  // ahead of the next bulk loads: loads complete in issue order
 }
 
@@ -687,43 +702,48 @@ __device__ __forceinline__ uint32_t tile_off(int row, int piece) {
   return (uint32_t)(row * 128 + ((piece ^ (row & 7) ^ ((row >> 3) & 1)) << 4));
 }
 
-// x pieces [I0, I1) of R into the A tile.
-template <int BM, int I0, int I1>
-__device__ __forceinline__ void gemm_stage_x(const GemmRegs<BM>& R, uint8_t* As, int t) {
-  const uint32_t o = tile_off(t >> 3, t & 7);  // rows 64 i + t / 8 share the permutation
-#pragma unroll
-  for (int i = I0; i < I1; i++) *reinterpret_cast<u32x4*>(As + o + i * 64 * 128) = R.a[i];
-}
-
-// Codes of R decoded into the B tile, then the block's outliers over them.
+// R -> one LDS stage: x pieces into the A tile, decoded weights into the B
+// tile, then the outliers over them.  Lanes past a block's count write to the
+// spare slot instead of branching.
 template <int BM, int FMT, int PC, int DENSE>
-__device__ __forceinline__ void gemm_stage_w(const GemmRegs<BM>& R, const GemmSrc<BM>& S, uint8_t* Bs, uint8_t* spare,
-                                             half2v srow, int t) {
-  const int l = t & 63, w = t >> 6;
-  const int n = 16 * w + (l & 15), g = l >> 4;
-  const half2v s2 = PC ? srow : scale2((uint16_t)R.s);
-  *reinterpret_cast<half8*>(Bs + tile_off(n, 2 * g)) = deq8<FMT>(R.q.x, R.q.y, s2);
-  *reinterpret_cast<half8*>(Bs + tile_off(n, 2 * g + 1)) = deq8<FMT>(R.q.z, R.q.w, s2);
-  // entry: (fp16 value << 16) | r << 6 | k for row 16 w + r, column k of the chunk
-  auto at = [&](uint32_t e) {
-    const int r = (int)((e >> 6) & 15), k = (int)(e & 63);
-    return tile_off(16 * w + r, k >> 3) + ((k & 7) << 1);
-  };
-  const int cnt = R.e1 - R.e0;
-  // lanes past the block's count write to the spare slot instead (no branch,
-  // so the scheduler may interleave the staging with the MFMAs around it)
-  *reinterpret_cast<uint16_t*>(l < cnt ? Bs + at(R.ent) : spare + 2 * l) = (uint16_t)(R.ent >> 16);
-  // blocks of more than 64 outliers (DENSE launches only): the rest from
-  // memory, 64 per round.  Kept out of the common kernel: loads in a
-  // data-dependent loop make every later wait in the chunk a full drain.
-  if (DENSE) {
-    const int e0 = __builtin_amdgcn_readfirstlane(R.e0);
-    const int ne = __builtin_amdgcn_readfirstlane(cnt);
-    for (int j = 64 + l; j - l < ne; j += 64)
-      if (j < ne) {
-        const uint32_t e = __builtin_amdgcn_raw_buffer_load_b32(S.er, (e0 + j) * 4, 0, 0);
-        *reinterpret_cast<uint16_t*>(Bs + at(e)) = (uint16_t)(e >> 16);
-      }
+__device__ __forceinline__ void gemm_stage(const GemmRegs<BM>& R, const GemmSrc<BM>& S, uint8_t* stage,
+                                           uint8_t* spare, const half2v (&srow)[2], int pt) {
+  uint8_t* As = stage;
+  uint8_t* Bs = stage + GemmCfg<BM>::A_BYTES;
+  const int l = pt & 63, pw = pt >> 6;
+  const uint32_t xo = tile_off(pt >> 3, pt & 7);  // rows 32 i + pt / 8 share the permutation
+#pragma unroll
+  for (int i = 0; i < GemmCfg<BM>::XP; i++) *reinterpret_cast<u32x4*>(As + xo + i * 32 * 128) = R.a[i];
+  const int g = l >> 4;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int n = 16 * (2 * pw + i) + (l & 15);
+    const half2v s2 = PC ? srow[i] : scale2((uint16_t)R.s[i]);
+    *reinterpret_cast<half8*>(Bs + tile_off(n, 2 * g)) = deq8<FMT>(R.q[i].x, R.q[i].y, s2);
+    *reinterpret_cast<half8*>(Bs + tile_off(n, 2 * g + 1)) = deq8<FMT>(R.q[i].z, R.q[i].w, s2);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    // entry: (fp16 value << 16) | r << 6 | k for row r of the block, column k of the chunk
+    const int rbl = 2 * pw + i;
+    auto at = [&](uint32_t e) {
+      const int r = (int)((e >> 6) & 15), k = (int)(e & 63);
+      return tile_off(16 * rbl + r, k >> 3) + ((k & 7) << 1);
+    };
+    const int cnt = R.e1[i] - R.e0[i];
+    *reinterpret_cast<uint16_t*>(l < cnt ? Bs + at(R.ent[i]) : spare + 2 * l) = (uint16_t)(R.ent[i] >> 16);
+    // blocks of more than 64 outliers (DENSE launches only): the rest from
+    // memory, 64 per round.  Kept out of the common kernel: loads in a
+    // data-dependent loop make every later wait in the chunk a full drain.
+    if (DENSE) {
+      const int e0 = __builtin_amdgcn_readfirstlane(R.e0[i]);
+      const int ne = __builtin_amdgcn_readfirstlane(cnt);
+      for (int j = 64 + l; j - l < ne; j += 64)
+        if (j < ne) {
+          const uint32_t e = __builtin_amdgcn_raw_buffer_load_b32(S.er, (e0 + j) * 4, 0, 0);
+          *reinterpret_cast<uint16_t*>(Bs + at(e)) = (uint16_t)(e >> 16);
+        }
+    }
   }
 }
 
@@ -737,7 +757,7 @@ template <int BM, int FMT, int PC, int DENSE>
 __global__ __launch_bounds__(512, 1) void qlinear_gemm_kernel(QLArgs a) {
   typedef GemmCfg<BM> C;
   constexpr int MI = C::MI;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * C::STAGE + 128];  // + the spare slot of gemm_stage_w
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * C::STAGE + 128];  // + the spare slot of gemm_stage
   uint8_t* const spare = lds + 3 * C::STAGE;
 
   // Output tiles of all matrices of the launch in one list (a.first[i]:
@@ -765,19 +785,57 @@ __global__ __launch_bounds__(512, 1) void qlinear_gemm_kernel(QLArgs a) {
   const int m_first = (local % mbands) * BM;
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int wave = t >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int nch128 = K >> 7;
   const int nch_split = (K / kGemmBK) / a.split;  // even (the host checks)
   const int c_first = ks * nch_split, c_end = c_first + nch_split;
+  auto next_stage = [](uint32_t s) { return s == 2 * C::STAGE ? 0u : s + C::STAGE; };
 
-  GemmSrc<BM> S;
-  gemm_src_init<BM>(S, W, a.x, M, K, m_first, nbase, nch128, t);
-  const half2v srow = scale2(PC ? (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so, 0, 0) : (uint16_t)0);
+  if (wave >= 4) {
+    // ---------------- producers
+    const int pt = t - 256;
+    GemmSrc<BM> S;
+    gemm_src_init<BM>(S, W, a.x, M, K, m_first, nbase, nch128, pt);
+    half2v srow[2];  // per-channel scales of this thread's code rows
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      srow[i] = scale2(PC ? (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so[i], 0, 0) : (uint16_t)0);
+    // prologue: chunks c_first, c_first + 1 staged; their successors loading
+    GemmRegs<BM> R0, R1;
+    gemm_load<BM, PC>(R0, S, W, c_first, lane);
+    gemm_load<BM, PC>(R1, S, W, c_first + 1, lane);
+    gemm_load_ent<BM>(R0, S, lane);
+    gemm_load_ent<BM>(R1, S, lane);
+    gemm_stage<BM, FMT, PC, DENSE>(R0, S, lds, spare, srow, pt);
+    gemm_load<BM, PC>(R0, S, W, min(c_first + 2, c_end - 1), lane);
+    gemm_stage<BM, FMT, PC, DENSE>(R1, S, lds + C::STAGE, spare, srow, pt);
+    gemm_load<BM, PC>(R1, S, W, min(c_first + 3, c_end - 1), lane);
+    gemm_load_ent<BM>(R0, S, lane);
+    __syncthreads();
+    uint32_t cur = 0;  // stage of chunk c, in bytes
+    // chunk c: R holds chunk c + 2 (to stage), Ro chunk c + 3 (entries to
+    // load).  Staging is unconditional: past the last chunk it rewrites a
+    // stage no later k-step reads, with the clamped chunk's data.
+    auto body = [&](int c, GemmRegs<BM>& R, GemmRegs<BM>& Ro) {
+      const uint32_t stg = next_stage(next_stage(cur));
+      gemm_load_ent<BM>(Ro, S, lane);
+      gemm_stage<BM, FMT, PC, DENSE>(R, S, lds + stg, spare, srow, pt);
+      gemm_load<BM, PC>(R, S, W, min(c + 4, c_end - 1), lane);
+      __syncthreads();
+      cur = next_stage(cur);
+    };
+    for (int c = c_first; c < c_end; c += 2) {
+      body(c, R0, R1);
+      body(c + 1, R1, R0);
+    }
+    return;
+  }
 
+  // ---------------- consumers
+  const int wm = wave >> 1, wn = wave & 1;
   // fragment addresses: lane l reads row (l % 32) of a 32-row group, piece
   // 2 s + l / 32 for k-step s; the permutation depends on the row only
   // through (l % 32), so one offset per k-step serves every fragment
-  const int wm = wave >> 1, wn = wave & 1;
   uint32_t foff[4];
 #pragma unroll
   for (int s = 0; s < 4; s++) foff[s] = tile_off(lane & 31, 2 * s + (lane >> 5));
@@ -803,56 +861,41 @@ __global__ __launch_bounds__(512, 1) void qlinear_gemm_kernel(QLArgs a) {
       for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(F.a[i], F.b[j], acc[i][j], 0, 0, 0);
   };
 
-  // prologue: chunks c_first, c_first + 1 staged; their successors loading
-  GemmRegs<BM> R0, R1;
-  gemm_load<BM, PC>(R0, S, W, c_first, lane);
-  gemm_load<BM, PC>(R1, S, W, c_first + 1, lane);
-  gemm_load_ent<BM>(R0, S, lane);
-  gemm_load_ent<BM>(R1, S, lane);
-  gemm_stage_x<BM, 0, C::XP>(R0, lds, t);
-  gemm_stage_w<BM, FMT, PC, DENSE>(R0, S, lds + C::A_BYTES, spare, srow, t);
-  gemm_load<BM, PC>(R0, S, W, min(c_first + 2, c_end - 1), lane);
-  gemm_stage_x<BM, 0, C::XP>(R1, lds + C::STAGE, t);
-  gemm_stage_w<BM, FMT, PC, DENSE>(R1, S, lds + C::STAGE + C::A_BYTES, spare, srow, t);
-  gemm_load<BM, PC>(R1, S, W, min(c_first + 3, c_end - 1), lane);
-  gemm_load_ent<BM>(R0, S, lane);
-  __syncthreads();
-
-  // Fragments are read two k-steps ahead (F[s] holds k-step s of a chunk);
-  // the first two k-steps of chunk c + 1 are read during chunk c, whose
-  // barrier has already made them visible.
+  __syncthreads();  // the producers' prologue
+  // F[s] holds k-step s of a chunk: read two k-steps ahead; the first two
+  // k-steps of chunk c + 1 are read during chunk c, whose last barrier made
+  // them visible
   GemmFrags<BM> F[4];
   read_frags(F[0], 0, 0);
   read_frags(F[1], 0, 1);
-  uint32_t cur = 0;  // stage of chunk c, in bytes
-  auto next_stage = [](uint32_t s) { return s == 2 * C::STAGE ? 0u : s + C::STAGE; };
-
-  // chunk c: R holds chunk c + 2 (to stage), Ro chunk c + 3 (entries to
-  // load).  Staging is unconditional: past the last chunk it rewrites a
-  // stage no later k-step reads, with the clamped chunk's data.  The LDS
-  // writes go right after the barrier, behind the reads of k-step 2, while
-  // the MFMAs run on fragments read before the barrier: the reads that wait
-  // behind the writes are needed two k-steps later.
-  auto body = [&](int c, GemmRegs<BM>& R, GemmRegs<BM>& Ro) {
-    const uint32_t nxt = next_stage(cur), stg = next_stage(nxt);
+  uint32_t cur = 0;
+  // (the scheduling barriers keep each read group two k-steps ahead of its
+  // MFMAs; left alone, the compiler sinks the reads next to their use)
+  for (int c = c_first; c < c_end; c++) {
+    const uint32_t nxt = next_stage(cur);
     read_frags(F[2], cur, 2);
+    __builtin_amdgcn_sched_barrier(0);
     mma(F[0]);
-    gemm_load_ent<BM>(Ro, S, lane);
-    gemm_stage_x<BM, 0, C::XP>(R, lds + stg, t);
-    gemm_stage_w<BM, FMT, PC, DENSE>(R, S, lds + stg + C::A_BYTES, spare, srow, t);
+    __builtin_amdgcn_sched_barrier(0);
     read_frags(F[3], cur, 3);
+    __builtin_amdgcn_sched_barrier(0);
     mma(F[1]);
+    __builtin_amdgcn_sched_barrier(0);
     read_frags(F[0], nxt, 0);
-    gemm_load<BM, PC>(R, S, W, min(c + 4, c_end - 1), lane);
+    __builtin_amdgcn_sched_barrier(0);
     mma(F[2]);
+    __builtin_amdgcn_sched_barrier(0);
     read_frags(F[1], nxt, 1);
+    __builtin_amdgcn_sched_barrier(0);
     mma(F[3]);
-    __syncthreads();
+    // The barrier needs this chunk's reads done (the producers overwrite
+    // its stage next), not the reads of chunk c + 1 just issued: wait for
+    // all but the newest 2 (MI + 2) LDS operations, instead of the full
+    // drain a fenced barrier would do.  The memory clobber keeps every LDS
+    // access on its side of the barrier.
+    static_assert(2 * (MI + 2) <= 15, "lgkmcnt field");
+    asm volatile("s_waitcnt lgkmcnt(%0)\n\ts_barrier" ::"n"(2 * (MI + 2)) : "memory");
     cur = nxt;
-  };
-  for (int c = c_first; c < c_end; c += 2) {
-    body(c, R0, R1);
-    body(c + 1, R1, R0);
   }
 
   // C layout (32x32): lane l, element e -> row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32

@@ -556,11 +556,14 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
 // ------------------------------------------------------------ GEMM (M > 64)
 //
 // Workgroup tile BM x 128 (BM = 256 or 128 rows of x by 128 output
-// columns), K in chunks of 64, 8 waves in two roles:
-//   * waves 0-3 (consumers, one per SIMD) own a 2 x 2 layout of (BM / 2) x 64
+// columns), K in chunks of 64, 12 waves in two roles:
+//   * waves 0-7 (consumers, two per SIMD) own a 4 x 2 layout of (BM / 4) x 64
 //     output tiles of 32x32x16 MFMAs.  Per chunk they only read fragments
-//     from LDS and issue MFMAs, fragments two k-steps ahead of their use;
-//   * waves 4-7 (producers) do all global loads, decode the weight codes,
+//     from LDS and issue MFMAs, fragments two k-steps ahead of their use.
+//     Eight of them: on gfx950 a wave's LDS reads are latency-bound (about
+//     100 B/clk per CU with four reading waves, 195 with eight, measured),
+//     and the fragments of a chunk take 128 KiB;
+//   * waves 8-11 (producers) do all global loads, decode the weight codes,
 //     write the x pieces and the decoded weights into LDS, and write each
 //     outlier's fp16 value over the zero its code decoded to (the outliers
 //     of a 16 x 64 weight block come as one short list from aq_outlier_tiles;
@@ -582,7 +585,7 @@ constexpr int kGemmBN = 128, kGemmBK = 64;
 
 template <int BM>
 struct GemmCfg {
-  static constexpr int WM = BM / 2;            // consumer wave tile rows
+  static constexpr int WM = BM / 4;            // consumer wave tile rows
   static constexpr int MI = WM / 32;           // 32-row MFMA tiles per consumer wave
   static constexpr int XP = BM * 128 / 16 / 256;  // 16-byte x pieces per producer thread and chunk
   static constexpr int A_BYTES = BM * 128;     // BM rows x 64 fp16
@@ -753,8 +756,10 @@ struct GemmFrags {
   half8 b[2];
 };
 
+constexpr int kGemmConsumers = 8, kGemmThreads = 64 * (kGemmConsumers + 4);
+
 template <int BM, int FMT, int PC, int DENSE>
-__global__ __launch_bounds__(512, 1) void qlinear_gemm_kernel(QLArgs a) {
+__global__ __launch_bounds__(kGemmThreads, 1) void qlinear_gemm_kernel(QLArgs a) {
   typedef GemmCfg<BM> C;
   constexpr int MI = C::MI;
   __shared__ __attribute__((aligned(16))) uint8_t lds[3 * C::STAGE + 128];  // + the spare slot of gemm_stage
@@ -791,9 +796,9 @@ __global__ __launch_bounds__(512, 1) void qlinear_gemm_kernel(QLArgs a) {
   const int c_first = ks * nch_split, c_end = c_first + nch_split;
   auto next_stage = [](uint32_t s) { return s == 2 * C::STAGE ? 0u : s + C::STAGE; };
 
-  if (wave >= 4) {
+  if (wave >= kGemmConsumers) {
     // ---------------- producers
-    const int pt = t - 256;
+    const int pt = t - 64 * kGemmConsumers;
     GemmSrc<BM> S;
     gemm_src_init<BM>(S, W, a.x, M, K, m_first, nbase, nch128, pt);
     half2v srow[2];  // per-channel scales of this thread's code rows
@@ -1032,9 +1037,9 @@ hipError_t launch_gemm(QLArgs a, bool per_channel, hipStream_t s) {
   for (int i = a.count; i <= kMaxGroup; i++) a.first[i] = ntiles;
   const dim3 grid((unsigned)(8 * aq::ceil_div(ntiles, 8)));
   if (per_channel)
-    hipLaunchKernelGGL((qlinear_gemm_kernel<BM, FMT, 1, DENSE>), grid, dim3(512), 0, s, a);
+    hipLaunchKernelGGL((qlinear_gemm_kernel<BM, FMT, 1, DENSE>), grid, dim3(kGemmThreads), 0, s, a);
   else
-    hipLaunchKernelGGL((qlinear_gemm_kernel<BM, FMT, 0, DENSE>), grid, dim3(512), 0, s, a);
+    hipLaunchKernelGGL((qlinear_gemm_kernel<BM, FMT, 0, DENSE>), grid, dim3(kGemmThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -937,6 +937,270 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qlinear_gemm_kernel(QLArgs a)
   }
 }
 
+// ------------------------------------------------ GEMM, 256 x 256 tiles
+//
+// For grids with at least one 256 x 256 output tile per CU (the MLP
+// projections of a prefill): half the LDS traffic per flop of the 256 x 128
+// kernel above, which is what bounds it.  8 waves, each computing a 128 x 64
+// tile (2 x 4 layout) and each also staging a share of the next chunk; two
+// LDS stages, one barrier per chunk.  Per chunk c a wave reads the fragments
+// of chunk c one k-step ahead of its MFMAs, stages chunk c + 1 (x pieces,
+// decoded weights, outlier patches) into the other stage, and reloads its
+// registers with chunk c + 2.  With two stages the first fragments of a chunk
+// are read after its barrier; each wave then has 32 MFMAs (1024 cycles of the
+// SIMD's matrix unit per wave pair) to hide them.
+
+struct WideRegs {
+  u32x4 a[4];      // x pieces
+  u32x4 q[2];      // codes of the wave's two block rows
+  uint32_t s[2];   // their scales (block-wise scales only)
+  int e0[2], e1[2];
+  uint32_t ent[2];
+};
+
+struct WideSrc {
+  __amdgpu_buffer_rsrc_t xr, cr, tr, er, sr;
+  int xo[4];
+  int co[2], to[2], so[2];
+};
+
+constexpr int kWideBM = 256, kWideBN = 256;
+constexpr int kWideA = kWideBM * 128, kWideStage = kWideA + kWideBN * 128;
+
+__device__ __forceinline__ void wide_src_init(WideSrc& S, const QLMat& W, const uint16_t* x, int M, int K,
+                                              int m_first, int nbase, int nch128, int t) {
+  const int l = t & 63, w = t >> 6;
+  const int rows = min(M - m_first, kWideBM);
+  S.xr = __builtin_amdgcn_make_buffer_rsrc((void*)(x + (size_t)m_first * K), (short)0, rows * K * 2, kBufferDword3);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int row = min(64 * i + (t >> 3), rows - 1);
+    S.xo[i] = (row * K + 8 * (t & 7)) * 2;
+  }
+  const int rb0 = nbase / 16, rb_last = W.N / 16 - 1;
+  const int nrb = min(rb_last - rb0 + 1, kWideBN / 16);
+  const int nch64 = nch128 * 2;
+  S.cr = __builtin_amdgcn_make_buffer_rsrc((void*)(W.codes + ((size_t)rb0 * nch128 << 11)), (short)0,
+                                           nrb * nch128 * 2048, kBufferDword3);
+  S.tr = __builtin_amdgcn_make_buffer_rsrc((void*)(W.tptr + (size_t)rb0 * nch64), (short)0, (nrb * nch64 + 1) * 4,
+                                           kBufferDword3);
+  S.er = __builtin_amdgcn_make_buffer_rsrc((void*)W.tent, (short)0, 0x7fffffff, kBufferDword3);
+  S.sr = __builtin_amdgcn_make_buffer_rsrc((void*)(W.scales + (size_t)rb0 * 16 * W.kg), (short)0,
+                                           nrb * 16 * W.kg * 2, kBufferDword3);
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int rb = min(rb0 + 2 * w + i, rb_last) - rb0;
+    S.co[i] = rb * nch128 * 2048 + l * 16;
+    S.to[i] = rb * nch64 * 4;
+    S.so[i] = (rb * 16 + (l & 15)) * W.kg * 2;
+  }
+}
+
+template <int PC>
+__device__ __forceinline__ void wide_load(WideRegs& R, const WideSrc& S, const QLMat& W, int c, int l) {
+  typedef int int2v __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int2v p = __builtin_bit_cast(int2v, __builtin_amdgcn_raw_buffer_load_b64(S.tr, S.to[i], c * 4, 0));
+    R.e0[i] = p.x;
+    R.e1[i] = p.y;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int k0 = c * kGemmBK;
+#pragma unroll
+  for (int i = 0; i < 4; i++) R.a[i] = __builtin_amdgcn_raw_buffer_load_b128(S.xr, S.xo[i], k0 * 2, 0);
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    R.q[i] = __builtin_amdgcn_raw_buffer_load_b128(S.cr, S.co[i], ((c >> 1) << 11) + ((c & 1) << 10), 0);
+    if (!PC) {
+      const int k = k0 + 16 * (l >> 4);
+      const int kb = W.gshift >= 0 ? (k >> W.gshift) : k / W.G;
+      R.s[i] = __builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so[i] + kb * 2, 0, 0);
+    }
+  }
+}
+
+__device__ __forceinline__ void wide_load_ent(WideRegs& R, const WideSrc& S, int l) {
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    int e0 = R.e0[i];
+    asm volatile("" : "+v"(e0));
+    R.ent[i] = __builtin_amdgcn_raw_buffer_load_b32(S.er, l * 4, __builtin_amdgcn_readfirstlane(e0) * 4, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int FMT, int PC, int DENSE>
+__device__ __forceinline__ void wide_stage(const WideRegs& R, const WideSrc& S, uint8_t* stage, uint8_t* spare,
+                                           const half2v (&srow)[2], int t) {
+  uint8_t* As = stage;
+  uint8_t* Bs = stage + kWideA;
+  const int l = t & 63, w = t >> 6, g = l >> 4;
+  const uint32_t xo = tile_off(t >> 3, t & 7);  // rows 64 i + t / 8 share the permutation
+#pragma unroll
+  for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4*>(As + xo + i * 64 * 128) = R.a[i];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int n = 16 * (2 * w + i) + (l & 15);
+    const half2v s2 = PC ? srow[i] : scale2((uint16_t)R.s[i]);
+    *reinterpret_cast<half8*>(Bs + tile_off(n, 2 * g)) = deq8<FMT>(R.q[i].x, R.q[i].y, s2);
+    *reinterpret_cast<half8*>(Bs + tile_off(n, 2 * g + 1)) = deq8<FMT>(R.q[i].z, R.q[i].w, s2);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int rbl = 2 * w + i;
+    auto at = [&](uint32_t e) {
+      const int r = (int)((e >> 6) & 15), k = (int)(e & 63);
+      return tile_off(16 * rbl + r, k >> 3) + ((k & 7) << 1);
+    };
+    const int cnt = R.e1[i] - R.e0[i];
+    *reinterpret_cast<uint16_t*>(l < cnt ? Bs + at(R.ent[i]) : spare + 2 * l) = (uint16_t)(R.ent[i] >> 16);
+    if (DENSE) {
+      const int e0 = __builtin_amdgcn_readfirstlane(R.e0[i]);
+      const int ne = __builtin_amdgcn_readfirstlane(cnt);
+      for (int j = 64 + l; j - l < ne; j += 64)
+        if (j < ne) {
+          const uint32_t e = __builtin_amdgcn_raw_buffer_load_b32(S.er, (e0 + j) * 4, 0, 0);
+          *reinterpret_cast<uint16_t*>(Bs + at(e)) = (uint16_t)(e >> 16);
+        }
+    }
+  }
+}
+
+template <int FMT, int PC, int DENSE>
+__global__ __launch_bounds__(512, 1) void qlinear_gemm_wide_kernel(QLArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kWideStage + 128];
+  uint8_t* const spare = lds + 2 * kWideStage;
+
+  // tiles: as in qlinear_gemm_kernel, with 256-column n-tiles
+  const int ntiles = a.first[a.count];
+  const int per = (ntiles + 7) / 8;
+  const int tile = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (tile >= ntiles) return;
+  int mi = 0;
+#pragma unroll
+  for (int j = 1; j < kMaxGroup; j++)
+    if (j < a.count && tile >= a.first[j]) mi = j;
+  const QLMat W = pick(a, mi);
+  const int N = W.N;
+  const int M = a.M, K = a.K;
+  const int mbands = (M + kWideBM - 1) / kWideBM;
+  const int per_split = ((N + kWideBN - 1) / kWideBN) * mbands;
+  const int ks = (tile - a.first[mi]) / per_split;
+  const int local = (tile - a.first[mi]) % per_split;
+  const int nbase = (local / mbands) * kWideBN;
+  const int m_first = (local % mbands) * kWideBM;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int nch128 = K >> 7;
+  const int nch_split = (K / kGemmBK) / a.split;
+  const int c_first = ks * nch_split, c_end = c_first + nch_split;
+
+  WideSrc S;
+  wide_src_init(S, W, a.x, M, K, m_first, nbase, nch128, t);
+  half2v srow[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+    srow[i] = scale2(PC ? (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so[i], 0, 0) : (uint16_t)0);
+
+  const int wm = wave >> 2, wn = wave & 3;
+  uint32_t foff[4];
+#pragma unroll
+  for (int s = 0; s < 4; s++) foff[s] = tile_off(lane & 31, 2 * s + (lane >> 5));
+  const uint32_t a_row0 = (uint32_t)(wm * 128) * 128, b_row0 = kWideA + (uint32_t)(wn * 64) * 128;
+
+  float16v acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = (float16v)0.0f;
+  struct Frags {
+    half8 a[4];
+    half8 b[2];
+  };
+  auto read_frags = [&](Frags& F, uint32_t stage, int s) {
+    const uint8_t* p = lds + stage + foff[s];
+#pragma unroll
+    for (int i = 0; i < 4; i++) F.a[i] = *reinterpret_cast<const half8*>(p + a_row0 + i * 32 * 128);
+#pragma unroll
+    for (int j = 0; j < 2; j++) F.b[j] = *reinterpret_cast<const half8*>(p + b_row0 + j * 32 * 128);
+  };
+  auto mma = [&](const Frags& F) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(F.a[i], F.b[j], acc[i][j], 0, 0, 0);
+  };
+
+  // prologue: chunk c_first staged, chunk c_first + 1 loading
+  WideRegs R;
+  wide_load<PC>(R, S, W, c_first, lane);
+  wide_load_ent(R, S, lane);
+  wide_stage<FMT, PC, DENSE>(R, S, lds, spare, srow, t);
+  wide_load<PC>(R, S, W, min(c_first + 1, c_end - 1), lane);
+  __syncthreads();
+
+  Frags F0, F1;
+  uint32_t cur = 0;
+  for (int c = c_first; c < c_end; c++) {
+    const uint32_t oth = cur ^ kWideStage;
+    wide_load_ent(R, S, lane);  // entries of chunk c + 1
+    read_frags(F0, cur, 0);
+    read_frags(F1, cur, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(F0);
+    __builtin_amdgcn_sched_barrier(0);
+    // chunk c + 1 into the other stage (last read in chunk c - 1, before
+    // the previous barrier); past the last chunk, a harmless rewrite
+    wide_stage<FMT, PC, DENSE>(R, S, lds + oth, spare, srow, t);
+    wide_load<PC>(R, S, W, min(c + 2, c_end - 1), lane);
+    read_frags(F0, cur, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(F1);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(F1, cur, 3);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(F0);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(F1);
+    __syncthreads();
+    cur = oth;
+  }
+
+  const int hi = lane >> 5, lc = lane & 31;
+  if (a.split > 1) {
+    float* part = W.part + (size_t)ks * M * N;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int n = nbase + wn * 64 + j * 32 + lc;
+      if (n >= N) continue;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int m = m_first + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+          if (m < M) part[(size_t)m * N + n] = acc[i][j][e];
+        }
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int n = nbase + wn * 64 + j * 32 + lc;
+    if (n >= N) continue;
+    const float bv = W.bias ? (float)bits_to_h(W.bias[n]) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int m = m_first + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+        if (m < M) W.y[(size_t)m * N + n] = h_to_bits(rn_h(acc[i][j][e] + bv));
+      }
+  }
+}
+
 // y = fp16(sum of the split partial sums in order + bias), 4 outputs per
 // thread (N is a multiple of 16).
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, int64_t mn, int split, int N,
@@ -1052,26 +1316,30 @@ hipError_t launch_gemm(const QLArgs& a, int fmt, bool per_channel, bool dense, h
                             : launch_gemm<BM, AQ_FMT_INT8, 0>(a, per_channel, s);
 }
 
-// GEMM shape choice.  Both tile heights run one workgroup per CU (their
-// three LDS stages take 144 or 96 KiB); a 128-row tile takes about 3/4 of
-// the time of a 256-row one (measured on gfx950), so 256-row tiles unless
-// the 128-row grid needs less than 4/3 of the rounds.  Then a grid that
-// fills at most half the CUs splits K 2 to 8 ways (up to one full round, at
-// least 4 chunks of 64 per part).
+// GEMM shape choice.  256 x 256 tiles (qlinear_gemm_wide_kernel) when they
+// give every CU at least one.  Otherwise 256 x 128 or 128 x 128 tiles: both
+// run one workgroup per CU (their three LDS stages take 144 or 96 KiB), and a
+// 128-row tile takes about 3/4 of the time of a 256-row one (measured on
+// gfx950), so 256-row tiles unless the 128-row grid needs less than 4/3 of
+// the rounds.  Then a grid that fills at most half the CUs splits K 2 to 8
+// ways (up to one full round, at least 4 chunks of 64 per part).
+enum { kTile256x128 = 0, kTile128x128 = 1, kTile256x256 = 2 };
 struct GemmPlan {
-  bool wide;
+  int tile;
   int split;
 };
 
 GemmPlan plan_gemm(int64_t M, const int64_t* Ns, int64_t count, int64_t K) {
-  int64_t wg256 = 0, wg128 = 0;
+  int64_t wgw = 0, wg256 = 0, wg128 = 0;
   for (int i = 0; i < count; i++) {
+    wgw += aq::ceil_div(M, kWideBM) * aq::ceil_div(Ns[i], kWideBN);
     wg256 += aq::ceil_div(M, 256) * aq::ceil_div(Ns[i], kGemmBN);
     wg128 += aq::ceil_div(M, 128) * aq::ceil_div(Ns[i], kGemmBN);
   }
   const int64_t slots = cu_count();
-  GemmPlan p{4 * aq::ceil_div(wg256, slots) <= 3 * aq::ceil_div(wg128, slots), 1};
-  const int64_t tiles = p.wide ? wg256 : wg128;
+  if (wgw >= slots) return GemmPlan{kTile256x256, 1};
+  GemmPlan p{4 * aq::ceil_div(wg256, slots) <= 3 * aq::ceil_div(wg128, slots) ? kTile256x128 : kTile128x128, 1};
+  const int64_t tiles = p.tile == kTile256x128 ? wg256 : wg128;
   const int64_t nch = K / kGemmBK;
   if (2 * tiles <= slots)
     for (int sp = 8; sp >= 2; sp /= 2)
@@ -1080,6 +1348,31 @@ GemmPlan plan_gemm(int64_t M, const int64_t* Ns, int64_t count, int64_t K) {
         break;
       }
   return p;
+}
+
+template <int FMT, int DENSE>
+hipError_t launch_gemm_wide(QLArgs a, bool per_channel, hipStream_t s) {
+  const int mbands = (int)aq::ceil_div(a.M, kWideBM);
+  int ntiles = 0;
+  for (int i = 0; i < a.count; i++) {
+    a.first[i] = ntiles;
+    ntiles += (int)aq::ceil_div(a.mat[i].N, kWideBN) * mbands * a.split;
+  }
+  for (int i = a.count; i <= kMaxGroup; i++) a.first[i] = ntiles;
+  const dim3 grid((unsigned)(8 * aq::ceil_div(ntiles, 8)));
+  if (per_channel)
+    hipLaunchKernelGGL((qlinear_gemm_wide_kernel<FMT, 1, DENSE>), grid, dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL((qlinear_gemm_wide_kernel<FMT, 0, DENSE>), grid, dim3(512), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_wide(const QLArgs& a, int fmt, bool per_channel, bool dense, hipStream_t s) {
+  if (dense)
+    return fmt == AQ_FMT_E4M3 ? launch_gemm_wide<AQ_FMT_E4M3, 1>(a, per_channel, s)
+                              : launch_gemm_wide<AQ_FMT_INT8, 1>(a, per_channel, s);
+  return fmt == AQ_FMT_E4M3 ? launch_gemm_wide<AQ_FMT_E4M3, 0>(a, per_channel, s)
+                            : launch_gemm_wide<AQ_FMT_INT8, 0>(a, per_channel, s);
 }
 
 }  // namespace
@@ -1181,7 +1474,6 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
   int64_t outs = 0;
   for (int i = 0; i < count; i++) outs += M * Ns[i];
   const GemmPlan plan = plan_gemm(M, Ns, count, K);
-  const bool wide = plan.wide;
   a.split = workspace ? plan.split : 1;
   while (a.split > 1 && workspace_bytes < a.split * outs * 4) a.split /= 2;
   if (a.split > 1) {
@@ -1192,8 +1484,9 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
       p += (size_t)a.split * M * Ns[i];
     }
   }
-  hipError_t e = wide ? launch_gemm<256>(a, fmt, per_channel, dense, s)
-                      : launch_gemm<128>(a, fmt, per_channel, dense, s);
+  hipError_t e = plan.tile == kTile256x256   ? launch_gemm_wide(a, fmt, per_channel, dense, s)
+                 : plan.tile == kTile256x128 ? launch_gemm<256>(a, fmt, per_channel, dense, s)
+                                             : launch_gemm<128>(a, fmt, per_channel, dense, s);
   if (e != hipSuccess || a.split == 1) return aq::check_hip(e, "aq_qlinear: gemm launch");
   for (int i = 0; i < count && e == hipSuccess; i++) {
     const int64_t mn = M * Ns[i];

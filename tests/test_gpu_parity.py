@@ -347,13 +347,35 @@ def test_gemm_crowded_outlier_blocks(M):
 
 @pytest.mark.parametrize("M,N", [(1000, 4096), (2048, 4096), (2100, 4112)])
 def test_gemm_tile_shapes(M, N):
-    """Grids of 256 or more 256 x 128 tiles take the 8-wave kernel (2048 x
-    4096, and 2100 x 4112 with a partial last tile in both directions);
-    smaller ones the 4-wave kernel (1000 x 4096)."""
+    """Grids of 256 or more 256 x 128 tiles take 256-row tiles (2048 x 4096,
+    and 2100 x 4112 with a partial last tile in both directions); smaller
+    ones 128-row tiles (1000 x 4096)."""
     rng = np.random.default_rng(M + N)
     K = 1024
     w = make_weights(rng, (N, K))
     q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, code_format="e4m3")
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    xs[:, rng.permutation(K)[:4]] *= 30
+    x = torch.from_numpy(xs.astype(np.float16)).to(DEV)
+    b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(DEV)
+    AQ.clear_dequantized_cache()
+    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    assert_close(AW.QuantizedLinear(q, b)(x), reference_linear(x, w_deq, b), x, w_deq)
+
+
+@pytest.mark.parametrize("fmt,G,M,N,K", [("e4m3", -1, 2000, 8208, 1024), ("int8", 128, 2048, 8192, 512)])
+def test_gemm_wide_tiles(fmt, G, M, N, K):
+    """Grids of 256 or more 256 x 256 tiles take the 256 x 256 kernel: a
+    partial last M-band and n-tile (2000 x 8208), block-wise int8 scales
+    (2048 x 8192), bias, and one 16 x 64 weight block with more than 64
+    outliers (read past the first 64 entries)."""
+    rng = np.random.default_rng(M + N + K)
+    w = make_weights(rng, (N, K)).astype(np.float32)
+    for r in range(16):  # 5 per row of block (0, 0): 80 in one block
+        cols = rng.permutation(64)[:5]
+        w[r, cols] = rng.choice([-1, 1], 5) * rng.uniform(8, 20, 5) * 0.02
+    q = AQ.quantize_tensor(torch.from_numpy(w.astype(np.float16)).to(DEV), block_size=G, code_format=fmt)
+    assert AQ.outlier_tiles(q, torch.device(DEV))[2] > 64
     xs = rng.standard_normal((M, K)).astype(np.float32)
     xs[:, rng.permutation(K)[:4]] *= 30
     x = torch.from_numpy(xs.astype(np.float16)).to(DEV)

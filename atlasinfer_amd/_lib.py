@@ -17,7 +17,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libatlasinfer_amd.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 FMT_INT8 = 0
 FMT_E4M3 = 1

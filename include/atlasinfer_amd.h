@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define AQ_ABI_VERSION 3
+#define AQ_ABI_VERSION 4
 
 enum { AQ_FMT_INT8 = 0, AQ_FMT_E4M3 = 1 };
 enum { AQ_LAYOUT_FLAT = 0, AQ_LAYOUT_TILED = 1 };

@@ -77,6 +77,21 @@ struct Elems {
   }
 };
 
+// The staged copy of a workgroup's blocks in LDS: 16-byte pieces, each
+// thread's E / 8 pieces (P = thread * E / 8 + j) stored at P with its low
+// bits XORed with the thread's, so that a thread's reads, at a stride of
+// E * 2 bytes between threads, hit distinct banks.
+template <int E>
+__device__ __forceinline__ int stage_swz(int P) {
+  constexpr int PPT = E / 8;
+  return P ^ ((P / PPT) & (PPT - 1));
+}
+// uint16 index of the workgroup's element i in the staged copy.
+template <int E>
+__device__ __forceinline__ int staged_index(int i) {
+  return (stage_swz<E>(i >> 3) << 3) | (i & 7);
+}
+
 // How much of a block a thread's E elements cover: every element of every
 // block (G is a power of two), all or none of a thread's elements (E
 // divides G), or any prefix.  The first two cases need no per-element
@@ -463,7 +478,7 @@ __device__ __forceinline__ uint32_t quot2(uint32_t xp, float s, float r) {
 template <int TAU, int E, int MODE>
 __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& xs, int64_t g, bool gvalid,
                                                   int64_t base, int i0, int t, double* lds_d, float* lds_f,
-                                                  int* lds_i) {
+                                                  int* lds_i, const uint16_t* staged, int unit_e0) {
   constexpr int NP = E / 2;              // pairs per thread
   constexpr int PW = NP < 16 ? NP : 16;  // pairs per flag word
   constexpr int NWD = NP / PW;
@@ -610,11 +625,12 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
           e = 2 * (w * PW + jh) + 1;
           H &= H - 1;
         }
-        // the value from memory (an L2 hit): indexing the registers with a
-        // run-time e would move them to scratch
+        // the value from the staged copy in LDS, else from memory (an L2
+        // hit): indexing the registers with a run-time e would move them to
+        // scratch
         const int64_t jj = base + i0 + e;
         a.stage_col[base + k] = i0 + e;
-        a.stage_val[base + k] = jj < a.numel ? a.x[jj] : (uint16_t)0;
+        a.stage_val[base + k] = staged ? staged[staged_index<E>(unit_e0 + e)] : (jj < a.numel ? a.x[jj] : (uint16_t)0);
         k++;
       }
     }
@@ -646,14 +662,12 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
   // thread read its own, every load instruction would touch 64 different
   // 128-byte lines.  Instead the workgroup reads its blocks (TEAMS * G
   // consecutive elements) with consecutive lanes on consecutive 16-byte
-  // pieces and hands them over through LDS.  The LDS piece index is
-  // swizzled (its low bits XOR the owning thread's low bits) so that the
-  // reads, 8 pieces per thread at a stride of E * 2 bytes, hit distinct
-  // banks.  Used when the workgroup's blocks lie wholly inside x.
+  // pieces and hands them over through LDS (stage_swz).  Used when the
+  // workgroup's blocks lie wholly inside x; the staged copy also serves the
+  // outlier values to the compaction.
   constexpr int PPT = E / 8;  // 16-byte pieces per thread
   constexpr bool kStage = MODE != kAnyLen && NT * E * 2 <= 32768;
   __shared__ uint4 stage[kStage ? NT * PPT : 1];
-  auto swz = [](int P) { return P ^ ((P / PPT) & (PPT - 1)); };
   Elems<E> xs;
   bool staged = false;
   if constexpr (kStage) {
@@ -666,14 +680,14 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
 #pragma unroll
       for (int k = 0; k < PPT; k++) {
         const int P = threadIdx.x + NT * k;
-        if (MODE == kFullBlocks || P < npieces) stage[swz(P)] = src[P];
+        if (MODE == kFullBlocks || P < npieces) stage[stage_swz<E>(P)] = src[P];
       }
       __syncthreads();
       const int S0 = (int)((team * G + i0) >> 3);
 #pragma unroll
       for (int j = 0; j < PPT; j++) {
         // threads past the end of their block (E divides G < TAU * E) hold padding
-        const uint4 u = i0 < G ? stage[swz(S0 + j)] : make_uint4(0, 0, 0, 0);
+        const uint4 u = (MODE == kFullBlocks || i0 < G) ? stage[stage_swz<E>(S0 + j)] : make_uint4(0, 0, 0, 0);
         xs.p[4 * j] = u.x;
         xs.p[4 * j + 1] = u.y;
         xs.p[4 * j + 2] = u.z;
@@ -688,7 +702,8 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
                                    lds_i + team * NWT);
   else
     finish_block_fast<TAU, E, MODE>(a, xs, g, gvalid, base, i0, t, lds_d + team * NWT, lds_f + team * NWT,
-                                    lds_i + team * NWT);
+                                    lds_i + team * NWT, staged ? reinterpret_cast<const uint16_t*>(stage) : nullptr,
+                                    (int)(team * G + i0));
 }
 
 // ---- exclusive scan of the per-block counts (in place, two passes)

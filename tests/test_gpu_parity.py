@@ -483,6 +483,38 @@ def test_signed_zeros_survive(oracle):
     assert np.array_equal(bits(z), bits(zr))
 
 
+@pytest.mark.parametrize("G", [128, 4096])
+def test_quantize_block_means_near_fp16_ties(oracle, G):
+    """Blocks whose exact mean sits within a few 2^-24 / G of the midpoint of
+    two fp16 neighbours h1 < h2 ~ 2^-13 (mean = h1 + 2^-24 + d 2^-24 / G,
+    d in -3..3), the rest of each block cancelling pairs +-B with B up to
+    6e4, so fp32 partial sums of the block lose the small terms: every
+    block's mean16, and so its codes and outliers, must be the oracle's."""
+    rng = np.random.default_rng(G)
+    rows, K = 64, 4096
+    nb = rows * K // G
+    w = np.zeros((nb, G), np.float16)
+    h1 = np.float16(2.0 ** -13) + np.float16(2.0 ** -23) * rng.integers(0, 1023, nb).astype(np.float16)
+    d = rng.integers(-3, 4, nb)
+    npair = (G - 4) // 2
+    big = (rng.uniform(1.0, 6e4, (nb, npair)) * rng.choice([1e-4, 1.0], (nb, 1))).astype(np.float16)
+    vals = np.concatenate([h1[:, None] * np.float16(G), np.full((nb, 1), np.float16(2.0 ** -24 * G)),
+                           (d * 2.0 ** -24).astype(np.float16)[:, None], np.zeros((nb, 1), np.float16),
+                           big, -big], axis=1)
+    for i in range(nb):
+        w[i] = vals[i, rng.permutation(G)]
+    w = w.reshape(rows, K)
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=G, z_threshold=3.0, code_format="e4m3")
+    ref = oracle.quantize(w, G, 3.0, oracle.FMT_E4M3)
+    assert np.array_equal(bits(q.scale_factors), bits(ref["scale_factors"]))
+    assert np.array_equal(q.outlier_indices.cpu().numpy(), ref["outlier_indices"])
+    assert np.array_equal(bits(q.fp16_outliers), bits(ref["fp16_outliers"]))
+    assert np.array_equal(bits(AQ.dense_codes(q, torch.device(DEV))), ref["codes"])
+    z = AQ.calculate_zscore_manual(torch.from_numpy(w[0, :G].copy()).to(DEV))
+    zr, _ = oracle.zscore(w[0, :G])
+    assert np.array_equal(bits(z), bits(zr))
+
+
 def test_e4m3_codes_every_fp16_value(oracle):
     """Every fp16 value in [-448, 448] quantized with scale 1 (each row holds
     448, so amax / 448 = 1) and no outliers (threshold 60000): each code is

@@ -61,6 +61,8 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   __shared__ uint16_t s_val[kCsrCap];
   __shared__ uint16_t s_xv[kXvCap];
   __shared__ uint16_t s_bias[16];
+  __shared__ float s_prod[64 * kStageBatch];  // decode: x * value of the first batch of entries
+  __shared__ float s_osum[16];                // decode: outlier sum per row
 
   int mi = 0;
 #pragma unroll
@@ -129,6 +131,34 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       else
         sx0[b] = __builtin_amdgcn_raw_buffer_load_b16(xr, e < cnt ? scol[b] * 2 : kOutOfRange, 0, 0);
     }
+  };
+  // Decode (M = 1), wave 0, early in the stream so that its LDS round trips
+  // overlap the code loads in flight: the products x * value of the first
+  // batch of entries go to LDS, then 4 lanes per row add up the row's
+  // entries (lane j of row r: entries j, j + 4, ... of the row, in order; a
+  // tile with more entries than the first batch reads the rest from
+  // memory) and two DPP levels add the 4 partial sums.
+  auto decode_outliers = [&]() {
+#pragma unroll
+    for (int b = 0; b < kStageBatch; b++) {
+      const int e = 64 * b + lane;
+      if (e < cnt) s_prod[e] = (float)bits_to_h((uint16_t)sx0[b]) * (float)bits_to_h((uint16_t)sval[b]);
+    }
+    __builtin_amdgcn_wave_barrier();  // the wave's LDS writes before its reads
+    const int r = lane >> 2;
+    const int e0 = __shfl(rp, r, 64) - p0, e1 = __shfl(rp, r + 1, 64) - p0;
+    float v = 0.0f;
+    for (int e = e0 + (lane & 3); e < e1; e += 4) {
+      if (e < 64 * kStageBatch && e < cnt) {
+        v += s_prod[e];
+      } else {
+        const int col = W.cols[p0 + e];
+        v += (float)bits_to_h(X1 ? x_lds[col] : a.x[col]) * (float)bits_to_h(W.vals[p0 + e]);
+      }
+    }
+    v += __builtin_bit_cast(float, xlane_partner_u32<1>(__builtin_bit_cast(uint32_t, v)));
+    v += __builtin_bit_cast(float, xlane_partner_u32<2>(__builtin_bit_cast(uint32_t, v)));
+    if ((lane & 3) == 0) s_osum[r] = v;
   };
 
   struct Batch {
@@ -226,6 +256,8 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       load(B0, c0 + 2 * step);
       __builtin_amdgcn_sched_barrier(0);
+      if (M == 1 && wave == 0 && c0 == 0) decode_outliers();
+      __builtin_amdgcn_sched_barrier(0);
       compute(B1);
       __builtin_amdgcn_sched_barrier(0);
       load(B1, c0 + 3 * step);
@@ -241,12 +273,28 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       load(B0, c0 + 2 * step);
       __builtin_amdgcn_sched_barrier(0);
+      if (M == 1 && wave == 0 && c0 == 0) decode_outliers();
+      __builtin_amdgcn_sched_barrier(0);
       compute(B1);
     }
   }
   // C layout: lane l, element i -> m = 4 (l / 16) + i, column l % 16
 #pragma unroll
   for (int i = 0; i < 4; i++) red[wave][lane * 4 + i] = acc[i];
+
+  if (M == 1) {
+    // decode: dense part (C element (m = 0, column nl) sits in lane nl,
+    // slot 0 of each wave) + outlier sum + bias, by wave 0's lanes 0..15
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+      float dense = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NS; w++) dense += red[w][lane * 4];
+      const float v = dense + s_osum[lane] + (float)bits_to_h((uint16_t)bias_v);
+      W.y[n0 + lane] = h_to_bits(rn_h(v));
+    }
+    return;
+  }
 
   if (wave == 0) {
     // Stage the CSR lists of rows n0..n0+15 and the x values they multiply
@@ -304,69 +352,34 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   }
   __syncthreads();
 
-  if (M == 1) {
-    // decode: 16 threads per row split the row's outliers, then a fixed
-    // 16-lane shuffle tree adds them up
-    // (256 work items: workgroups of fewer than 4 waves take several rounds)
-    for (int o = threadIdx.x; o < 256; o += 64 * NS) {
-      const int nl = o >> 4;
-      const int sub = o & 15;
+  // 1 < M <= 16: a thread per (m, column) output, its row's outliers in order
+  for (int o = threadIdx.x; o < 256; o += 64 * NS) {
+    const int l = o >> 2;
+    const int m = 4 * (l >> 4) + (o & 3);
+    const int nl = l & 15;
+    const int n = n0 + nl;
+    if (m < M) {
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NS; w++) v += red[w][o];
       const int p0 = s_meta[0], cnt = s_meta[1], nx = s_meta[2];
       const int e1 = s_rp[nl + 1];
-      float v = 0.0f;
-      for (int e = s_rp[nl] + sub; e < e1; e += 16) {
+      for (int e = s_rp[nl]; e < e1; e++) {
         float xv, wv;
-        if (e < cnt) {
-          const int col = s_col[e];
-          xv = (float)bits_to_h(e < nx ? s_xv[e] : X1 ? x_lds[col] : a.x[col]);
+        if (e < nx) {
+          xv = (float)bits_to_h(s_xv[e * M + m]);
           wv = (float)bits_to_h(s_val[e]);
-        } else {
-          const int col = W.cols[p0 + e];
-          xv = (float)bits_to_h(X1 ? x_lds[col] : a.x[col]);
+        } else if (e < cnt) {
+          xv = (float)bits_to_h(a.x[(size_t)m * K + s_col[e]]);
+          wv = (float)bits_to_h(s_val[e]);
+        } else {  // more outliers than the staging holds: straight from memory
+          xv = (float)bits_to_h(a.x[(size_t)m * K + W.cols[p0 + e]]);
           wv = (float)bits_to_h(W.vals[p0 + e]);
         }
         v = __builtin_fmaf(xv, wv, v);
       }
-#pragma unroll
-      for (int d = 1; d < 16; d <<= 1) v = v + __shfl_xor(v, d, 64);
-      if (sub == 0) {
-        // dense part: C element (m = 0, column nl) sits in lane nl, slot 0
-        float dense = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NS; w++) dense += red[w][nl * 4];
-        v = dense + v + (float)bits_to_h(s_bias[nl]);
-        W.y[n0 + nl] = h_to_bits(rn_h(v));
-      }
-    }
-  } else {
-    for (int o = threadIdx.x; o < 256; o += 64 * NS) {
-      const int l = o >> 2;
-      const int m = 4 * (l >> 4) + (o & 3);
-      const int nl = l & 15;
-      const int n = n0 + nl;
-      if (m < M) {
-        float v = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NS; w++) v += red[w][o];
-        const int p0 = s_meta[0], cnt = s_meta[1], nx = s_meta[2];
-        const int e1 = s_rp[nl + 1];
-        for (int e = s_rp[nl]; e < e1; e++) {
-          float xv, wv;
-          if (e < nx) {
-            xv = (float)bits_to_h(s_xv[e * M + m]);
-            wv = (float)bits_to_h(s_val[e]);
-          } else if (e < cnt) {
-            xv = (float)bits_to_h(a.x[(size_t)m * K + s_col[e]]);
-            wv = (float)bits_to_h(s_val[e]);
-          } else {  // more outliers than the staging holds: straight from memory
-            xv = (float)bits_to_h(a.x[(size_t)m * K + W.cols[p0 + e]]);
-            wv = (float)bits_to_h(W.vals[p0 + e]);
-          }
-          v = __builtin_fmaf(xv, wv, v);
-        }
-        v += (float)bits_to_h(s_bias[nl]);
-        W.y[(size_t)m * N + n] = h_to_bits(rn_h(v));
-      }
+      v += (float)bits_to_h(s_bias[nl]);
+      W.y[(size_t)m * N + n] = h_to_bits(rn_h(v));
     }
   }
 }

@@ -235,15 +235,41 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   const int step = U * NS;
   Batch B0, B1;
   if (X1) {
-    load_q(B0, wave);
-    load_q(B1, wave + step);
     {
-      // x behind the codes of the first two batches: its wait, which also
-      // waits for them, comes once, before they are needed anyway
+      // x in 16-byte pieces (K / 8 of x, then 4 of zeros: pieces past x are
+      // out of range and read as zero), XB pieces per lane at a time.  The
+      // first XB go out ahead of the first two batches of codes, so their
+      // wait (x comes from L2) leaves the codes in flight; longer rows take
+      // further rounds of XB.
+      constexpr int XB = 8;
+      const int nxp = (K >> 3) + 4;
       const __amdgpu_buffer_rsrc_t xr1 = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, K * 2, kBufferDword3);
-      for (int i = threadIdx.x; i < (K >> 3) + 4; i += 64 * NS)
-        *reinterpret_cast<u32x4*>(x_lds + 8 * i) = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr1, i < (K >> 3) ? (uint32_t)i * 16 : kOutOfRange, 0, 0));
+      u32x4 xv[XB];
+      auto x_round = [&](int i0) {
+#pragma unroll
+        for (int j = 0; j < XB; j++) {
+          const int i = i0 + 64 * NS * j;
+          xv[j] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr1, i < (K >> 3) ? (uint32_t)i * 16 : kOutOfRange, 0, 0));
+        }
+      };
+      auto x_store = [&](int i0) {
+#pragma unroll
+        for (int j = 0; j < XB; j++) {
+          const int i = i0 + 64 * NS * j;
+          if (i < nxp) *reinterpret_cast<u32x4*>(x_lds + 8 * i) = xv[j];
+        }
+      };
+      x_round(threadIdx.x);
+      __builtin_amdgcn_sched_barrier(0);  // keep the issue order
+      load_q(B0, wave);
+      load_q(B1, wave + step);
+      __builtin_amdgcn_sched_barrier(0);
+      x_store(threadIdx.x);
+      for (int i0 = threadIdx.x + 64 * NS * XB; i0 < nxp; i0 += 64 * NS * XB) {
+        x_round(i0);
+        x_store(i0);
+      }
       __syncthreads();
     }
     load_x(B0, wave);

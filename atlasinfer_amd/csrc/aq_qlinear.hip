@@ -166,10 +166,12 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
     u32x4 x[U][4];
     uint32_t s[U][2];
   };
-  // Non-temporal code loads pay off when each tile row has one wave (tall
-  // groups such as gate/up), plain ones when several waves share it
-  // (measured on the Llama-3-8B shapes).
-  constexpr int kCodePolicy = NS == 1 ? 2 : 0;  // 2: nt
+  // Codes are read once per call: non-temporal loads.  Launched alone, a
+  // short matrix with several waves per tile row runs a few percent faster
+  // with plain loads, but in a decoder layer's sequence of launches the
+  // non-temporal ones win (the caches keep x and the small data instead;
+  // measured on the Llama-3-8B shapes).
+  constexpr int kCodePolicy = 2;  // nt
   auto load_q = [&](Batch& B, int c0) {
 #pragma unroll
     for (int u = 0; u < U; u++) {

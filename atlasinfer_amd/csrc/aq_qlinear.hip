@@ -20,9 +20,10 @@
 //    gives the launch about 1536 waves: one per tile row for a tall group.
 //    Several matrices that read the same x (q/k/v, gate/up) share one
 //    launch.
-//  * 16 < M <= 64: the same streaming, but 8 waves per workgroup share each
+//  * 8 <= M <= 64: the same streaming, but 8 waves per workgroup share each
 //    chunk of x through LDS (details at its kernel below), since x is then
-//    larger than the codes it multiplies.
+//    comparable to or larger than the codes it multiplies.  (M = 1..7 re-read
+//    x per tile row above; decode stages it in LDS once per workgroup.)
 //  * M > 64: dequant-GEMM (details at its kernel below): 128 or 256 rows of
 //    x by 128 output columns per workgroup, x and decoded weights staged in
 //    LDS in MFMA operand order, each outlier written over its decoded zero,
@@ -39,6 +40,7 @@ using namespace aqk;
 // ------------------------------------------------------------ GEMV (M <= 64)
 
 constexpr int kGemvMaxM = 64;   // larger M takes the GEMM
+constexpr int kGemvXMinM = 8;   // from here on the GEMV shares x through LDS (qlinear_gemv_x_kernel)
 constexpr int kGemvUnroll = 2;  // 128-wide K chunks per wave with loads in flight together
 // Staging capacity per workgroup (16 rows).  Kept small so that LDS does not
 // limit the workgroups resident per CU; entries beyond it (heavy-tailed
@@ -412,10 +414,10 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   }
 }
 
-// ------------------------------------------- GEMV with x in LDS (16 < M <= 64)
+// ------------------------------------------- GEMV with x in LDS (8 <= M <= 64)
 //
-// With more than 16 rows of x, re-reading x per 16-row tile row would cost
-// far more than the codes (2 M bytes per weight column against 1).  Here a
+// With 8 or more rows of x, re-reading x per 16-row tile row would cost as
+// much as the codes or more (2 M bytes per weight column against 1).  Here a
 // workgroup of 8 waves takes TR = 8 / S tile rows with S waves each; wave
 // (tr, s) streams the codes of tile row tr over the chunks c = S j + s.  For
 // each chunk group j the workgroup stages x[16 MG rows][S chunks] in LDS
@@ -478,8 +480,9 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   auto load = [&](Slot& sl, int j) {
     const int c = j * S + sp;
     const uint32_t co = c < nchunks ? code_base + (uint32_t)c * 2048 : kOutOfRange;
-    sl.q0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co, 0, 0));
-    sl.q1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co + 1024, 0, 0));
+    // codes are read once per call: non-temporal
+    sl.q0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co, 0, 2));
+    sl.q1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co + 1024, 0, 2));
     if (!PC) {
       const uint32_t k = (uint32_t)(c < nchunks ? c : 0) * 128 + 16 * grp;
       const uint32_t k0 = W.gshift >= 0 ? k >> W.gshift : k / W.G;
@@ -1315,7 +1318,7 @@ hipError_t launch_gemv_x(const QLArgs& a, int fmt, bool per_channel, int blocks,
                             : launch_gemv_x<AQ_FMT_INT8, MG, S>(a, per_channel, blocks, s);
 }
 
-// 16 < M <= 64: x row groups of 16 per MFMA (MG = 2 or 4 for M up to 32, 64),
+// 8 <= M <= 64: x row groups of 16 per MFMA (MG = 1, 2 or 4 for M up to 16, 32, 64),
 // S = 2 or 4 waves per tile row; a.first counts workgroups of 8 / S tile rows
 hipError_t launch_gemv_x(QLArgs a, int fmt, bool per_channel, int S, hipStream_t s) {
   const int TR = kXWaves / S;
@@ -1325,6 +1328,8 @@ hipError_t launch_gemv_x(QLArgs a, int fmt, bool per_channel, int S, hipStream_t
     wgs += (int)aq::ceil_div(a.mat[i].N / 16, TR);
   }
   for (int i = a.count; i <= kMaxGroup; i++) a.first[i] = wgs;
+  if (a.M <= 16)
+    return S == 2 ? launch_gemv_x<1, 2>(a, fmt, per_channel, wgs, s) : launch_gemv_x<1, 4>(a, fmt, per_channel, wgs, s);
   if (a.M <= 32)
     return S == 2 ? launch_gemv_x<2, 2>(a, fmt, per_channel, wgs, s) : launch_gemv_x<2, 4>(a, fmt, per_channel, wgs, s);
   return S == 2 ? launch_gemv_x<4, 2>(a, fmt, per_channel, wgs, s) : launch_gemv_x<4, 4>(a, fmt, per_channel, wgs, s);
@@ -1488,9 +1493,11 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
   hipStream_t s = (hipStream_t)stream;
   bool per_channel = true;
   for (int i = 0; i < count; i++) per_channel = per_channel && a.mat[i].kg == 1;
-  if (M > 16 && M <= kGemvMaxM) {
+  if (M >= kGemvXMinM && M <= kGemvMaxM) {
     // S = 2 waves per tile row for tall groups, 4 for short ones (measured
-    // on the Llama-3-8B shapes: S = 1 leaves the loads' latency exposed)
+    // on the Llama-3-8B shapes: S = 1 leaves the loads' latency exposed).
+    // Per decoder layer of those shapes it beats re-reading x per tile row
+    // from M = 8 on (M = 16: 90 against 127 us)
     const int S = blocks >= 768 ? 2 : 4;
     return aq::check_hip(launch_gemv_x(a, fmt, per_channel, S, s), "aq_qlinear: gemv launch");
   }

@@ -85,7 +85,7 @@ SHAPES = [
     (48, 512, -1, 3.0, "e4m3", None, 0.001),
     (33, 1000, 100, 3.0, "e4m3", None, 0.01),     # ragged: G does not divide K
     (16, 4096, -1, 3.0, "e4m3", 3, 0.01),
-    (8, 14336, -1, 3.0, "int8", None, 0.001),     # per-row block of 14336 (team of 1024)
+    (8, 14336, -1, 3.0, "int8", None, 0.001),     # per-row block of 14336 (team of 512 x 32)
     (4, 40000, -1, 3.0, "e4m3", None, 0.001),     # block > 16384: 64 elements per thread
     (128, 96, 32, 1.0, "int8", None, 0.05),       # many outliers per block
     (7, 13, 8, 2.0, "e4m3", None, 0.05),          # G < 16, unaligned rows

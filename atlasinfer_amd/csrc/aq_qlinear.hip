@@ -432,6 +432,7 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
 
 constexpr int kXWaves = 8;
 constexpr int kXPad = 8;  // halves of padding per LDS row of x
+constexpr int kXCsrCap = 512;  // outlier entries of a tile row staged in LDS (the rest: epilogue)
 
 template <int FMT, int PC, int MG, int S>
 __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) {
@@ -441,6 +442,7 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   constexpr int XP = XR * S * 16 / (64 * kXWaves);  // 16-byte x pieces per thread and group
   static_assert(XP >= 1, "x pieces");
   __shared__ __attribute__((aligned(16))) uint16_t xs[2][XR * XW];
+  __shared__ uint32_t x_ent[TR][kXCsrCap];  // (value << 16) | column of the tile row's first outliers
 
   int mi = 0;
 #pragma unroll
@@ -534,12 +536,67 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
     }
   };
 
+  // Outliers: wave sp = 0 of each tile row copies the tile row's first
+  // kXCsrCap entries (from the CSR lists, fetched behind the first code
+  // loads) into LDS for itself, and in each chunk group adds, per lane, the
+  // products of its row's entries in the group's columns with the x values
+  // staged there (rows 4 grp + i of each 16-row group).  Entries past the
+  // cap, and all of them when K >= 65536 (the column does not fit 16 bits),
+  // are added in the epilogue.  (Sharing the rows among the S waves of the
+  // tile row measured slower.)
+  int op = 0, oend = 0;  // this lane's row: next staged entry and end of its staged entries
+  int staged_row = 0;    // how many of the row's entries are staged
+  auto stage_outliers = [&]() {
+    const bool fits = sp == 0 && tr < rows_here && K < 65536;
+    const int n0r = (rb0 + tr) * 16;
+    int rpv = 0;
+    if (fits && lane <= 16) rpv = W.row_ptr[n0r + lane];
+    const int p0 = __shfl(rpv, 0, 64);
+    const int cnt = fits ? min(__shfl(rpv, 16, 64) - p0, kXCsrCap) : 0;
+    for (int e0 = 0; e0 < cnt; e0 += 64 * 8) {
+      uint32_t ent[8];
+#pragma unroll
+      for (int b = 0; b < 8; b++) {
+        const int e = min(e0 + 64 * b + lane, cnt - 1);  // loads stay unconditional
+        ent[b] = ((uint32_t)W.vals[p0 + e] << 16) | (uint32_t)W.cols[p0 + e];
+      }
+#pragma unroll
+      for (int b = 0; b < 8; b++)
+        if (e0 + 64 * b + lane < cnt) x_ent[tr][e0 + 64 * b + lane] = ent[b];
+    }
+    op = min(__shfl(rpv, li, 64) - p0, cnt);
+    oend = min(__shfl(rpv, li + 1, 64) - p0, cnt);
+    if (!fits) op = oend = 0;
+    staged_row = oend - op;
+    // the wave's own LDS writes precede its reads in the loop
+    __builtin_amdgcn_wave_barrier();
+  };
+  auto add_outliers = [&](int j, const uint16_t* xb) {
+    const int gstart = j * S * 128, gend = gstart + S * 128;
+    while (op < oend) {
+      const uint32_t ent = x_ent[tr][op];
+      const int col = (int)(ent & 0xFFFFu);
+      if (col >= gend) break;
+      const float wv = (float)bits_to_h((uint16_t)(ent >> 16));
+      const uint16_t* xc = xb + (col - gstart) + 4 * grp * XW;
+#pragma unroll
+      for (int gi = 0; gi < MG; gi++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          acc[gi][i] = __builtin_fmaf((float)bits_to_h(xc[(16 * gi + i) * XW]), wv, acc[gi][i]);
+      op++;
+    }
+  };
+
   Slot sa, sb;
   load(sa, 0);
   load(sb, 1);
+  if (sp == 0) stage_outliers();
   for (int j = 0; j < nsteps; j += 2) {
     step(sa, j, xs[0]);
+    if (sp == 0) add_outliers(j, xs[0]);
     step(sb, j + 1, xs[1]);
+    if (sp == 0) add_outliers(j + 1, xs[1]);
   }
 
   // the S partial sums of each tile row meet in LDS (x is no longer read)
@@ -566,7 +623,8 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   // loads they need, then the FMAs.
   const int n = (rb0 + tr) * 16 + li;
   const int p_end = W.row_ptr[n + 1];
-  for (int p = W.row_ptr[n]; p < p_end; p += 8) {
+  // the row's entries past the staged ones
+  for (int p = W.row_ptr[n] + staged_row; p < p_end; p += 8) {
     int col[8];
     float wv[8];
 #pragma unroll

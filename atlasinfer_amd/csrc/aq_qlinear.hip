@@ -20,9 +20,9 @@
 //    gives the launch about 1536 waves: one per tile row for a tall group.
 //    Several matrices that read the same x (q/k/v, gate/up) share one
 //    launch.
-//  * 8 <= M <= 64: the same streaming, but 8 waves per workgroup share each
+//  * 6 <= M <= 64: the same streaming, but 8 waves per workgroup share each
 //    chunk of x through LDS (details at its kernel below), since x is then
-//    comparable to or larger than the codes it multiplies.  (M = 1..7 re-read
+//    comparable to or larger than the codes it multiplies.  (M = 1..5 re-read
 //    x per tile row above; decode stages it in LDS once per workgroup.)
 //  * M > 64: dequant-GEMM (details at its kernel below): 128 or 256 rows of
 //    x by 128 output columns per workgroup, x and decoded weights staged in
@@ -40,7 +40,7 @@ using namespace aqk;
 // ------------------------------------------------------------ GEMV (M <= 64)
 
 constexpr int kGemvMaxM = 64;   // larger M takes the GEMM
-constexpr int kGemvXMinM = 8;   // from here on the GEMV shares x through LDS (qlinear_gemv_x_kernel)
+constexpr int kGemvXMinM = 6;   // from here on the GEMV shares x through LDS (qlinear_gemv_x_kernel)
 constexpr int kGemvUnroll = 2;  // 128-wide K chunks per wave with loads in flight together
 // Staging capacity per workgroup (16 rows).  Kept small so that LDS does not
 // limit the workgroups resident per CU; entries beyond it (heavy-tailed
@@ -414,10 +414,10 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   }
 }
 
-// ------------------------------------------- GEMV with x in LDS (8 <= M <= 64)
+// ------------------------------------------- GEMV with x in LDS (6 <= M <= 64)
 //
-// With 8 or more rows of x, re-reading x per 16-row tile row would cost as
-// much as the codes or more (2 M bytes per weight column against 1).  Here a
+// With 6 or more rows of x, re-reading x per 16-row tile row costs more
+// than sharing it (2 M bytes per weight column against 1 of codes).  Here a
 // workgroup of 8 waves takes TR = 8 / S tile rows with S waves each; wave
 // (tr, s) streams the codes of tile row tr over the chunks c = S j + s.  For
 // each chunk group j the workgroup stages x[16 MG rows][S chunks] in LDS
@@ -1376,7 +1376,7 @@ hipError_t launch_gemv_x(const QLArgs& a, int fmt, bool per_channel, int blocks,
                             : launch_gemv_x<AQ_FMT_INT8, MG, S>(a, per_channel, blocks, s);
 }
 
-// 8 <= M <= 64: x row groups of 16 per MFMA (MG = 1, 2 or 4 for M up to 16, 32, 64),
+// 6 <= M <= 64: x row groups of 16 per MFMA (MG = 1, 2 or 4 for M up to 16, 32, 64),
 // S = 2 or 4 waves per tile row; a.first counts workgroups of 8 / S tile rows
 hipError_t launch_gemv_x(QLArgs a, int fmt, bool per_channel, int S, hipStream_t s) {
   const int TR = kXWaves / S;
@@ -1555,7 +1555,7 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
     // S = 2 waves per tile row for tall groups, 4 for short ones (measured
     // on the Llama-3-8B shapes: S = 1 leaves the loads' latency exposed).
     // Per decoder layer of those shapes it beats re-reading x per tile row
-    // from M = 8 on (M = 16: 90 against 127 us)
+    // from M = 6 on (M = 6: 76 against 78 us, M = 16: 77 against 127 us)
     const int S = blocks >= 768 ? 2 : 4;
     return aq::check_hip(launch_gemv_x(a, fmt, per_channel, S, s), "aq_qlinear: gemv launch");
   }

@@ -42,29 +42,23 @@ using namespace aqk;
 constexpr int kGemvMaxM = 64;   // larger M takes the GEMM
 constexpr int kGemvXMinM = 6;   // from here on the GEMV shares x through LDS (qlinear_gemv_x_kernel)
 constexpr int kGemvUnroll = 2;  // 128-wide K chunks per wave with loads in flight together
-// Staging capacity per workgroup (16 rows).  Kept small so that LDS does not
-// limit the workgroups resident per CU; entries beyond it (heavy-tailed
-// weights) are read from memory in the epilogue.
-constexpr int kCsrCap = 1024;   // outlier entries
-constexpr int kXvCap = 1024;    // staged x values: entries * M <= kXvCap
-constexpr int kStageBatch = 8;  // entries per lane whose loads are issued together
+constexpr int kGemvDirectMaxM = kGemvXMinM - 1;  // rows of x qlinear_gemv_kernel takes
+// Outlier entries of a 16-row tile held in registers (64 * kStageBatch);
+// entries beyond them (heavy-tailed weights) are read from memory.
+constexpr int kStageBatch = 8;
 constexpr int kGemvX1MaxK = 16384;  // decode keeps x in LDS up to this row length (32 KiB)
 
-template <int NS, int FMT, int PC, int X1>
+// MM: the most rows of x (1 for decode, kGemvDirectMaxM otherwise)
+template <int NS, int FMT, int PC, int X1, int MM>
 __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
+  static_assert(!X1 || MM == 1, "x in LDS is for decode");
   constexpr int U = kGemvUnroll;
   // X1 (M = 1): x is staged in LDS once, K fp16 followed by 64 zero bytes
   // that the lanes of rows 1..15 of the MFMA A operand read instead
   extern __shared__ __attribute__((aligned(16))) uint16_t x_lds[];
   __shared__ float red[NS][256];
-  __shared__ int s_rp[17];
-  __shared__ int s_meta[3];  // p0, staged entries, entries with staged x
-  __shared__ int s_col[kCsrCap];
-  __shared__ uint16_t s_val[kCsrCap];
-  __shared__ uint16_t s_xv[kXvCap];
-  __shared__ uint16_t s_bias[16];
-  __shared__ float s_prod[64 * kStageBatch];  // decode: x * value of the first batch of entries
-  __shared__ float s_osum[16];                // decode: outlier sum per row
+  __shared__ float s_prod[MM][64 * kStageBatch];  // x * value of the tile's first entries
+  __shared__ float s_osum[MM][16];                // outlier sum per (row of x, output column)
 
   int mi = 0;
 #pragma unroll
@@ -95,20 +89,24 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   const uint32_t scale_row = (uint32_t)li * W.kg;
   const uint16_t sb_row = PC ? W.scales[n] : (uint16_t)0;
 
-  // Wave 0 also stages the rows' outliers.  Its row_ptr load goes out first;
-  // the (col, val) loads of up to 64 * kStageBatch entries go out right after
-  // its first code loads, and the x values of row 0 at those columns (all
-  // that decode needs) right after its first chunks are computed, so all of
-  // them return while the codes stream in.
+  // Wave 0 also handles the rows' outliers.  Its row_ptr load goes out
+  // first; the (col, val) loads of up to 64 * kStageBatch entries go out
+  // right after its first code loads, and the x values at those columns
+  // right before its first chunk is computed, so all of them return while
+  // the codes stream in.
   int rp = 0;
   if (wave == 0 && lane <= 16) rp = W.row_ptr[n0 + lane];
+  // every lane: the bias of column n0 + lane % 16 (no bias: an empty range,
+  // read as zero)
+  const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W.bias ? W.bias + n0 : W.vals), (short)0, W.bias ? 32 : 0, kBufferDword3);
+  const uint32_t bias_v = __builtin_amdgcn_raw_buffer_load_b16(br, (lane & 15) * 2, 0, 0);
   int p0 = 0, cnt = 0;
-  uint32_t scol[kStageBatch], sval[kStageBatch], sx0[kStageBatch];
-  uint32_t bias_v = 0;
+  uint32_t scol[kStageBatch], sval[kStageBatch], sx[MM][kStageBatch];
   auto stage_first_batch = [&]() {
     // wave-uniform, so the list descriptors below live in scalar registers
     p0 = __builtin_amdgcn_readfirstlane(__shfl(rp, 0, 64));
-    cnt = __builtin_amdgcn_readfirstlane(min(__shfl(rp, 16, 64) - p0, kCsrCap));
+    cnt = __builtin_amdgcn_readfirstlane(min(__shfl(rp, 16, 64) - p0, 64 * kStageBatch));
     const __amdgpu_buffer_rsrc_t colr =
         __builtin_amdgcn_make_buffer_rsrc((void*)(W.cols + p0), (short)0, cnt * 4, kBufferDword3);
     const __amdgpu_buffer_rsrc_t valr =
@@ -119,48 +117,62 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       scol[b] = __builtin_amdgcn_raw_buffer_load_b32(colr, e * 4, 0, 0);
       sval[b] = __builtin_amdgcn_raw_buffer_load_b16(valr, e * 2, 0, 0);
     }
-    // no bias: an empty range, read as zero
-    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(W.bias ? W.bias + n0 : W.vals), (short)0, W.bias ? 32 : 0, kBufferDword3);
-    bias_v = __builtin_amdgcn_raw_buffer_load_b16(br, (lane & 15) * 2, 0, 0);
   };
-  auto gather_x0 = [&]() {
+  auto gather_x = [&]() {
 #pragma unroll
     for (int b = 0; b < kStageBatch; b++) {
       const int e = 64 * b + lane;
-      if (X1)
-        sx0[b] = x_lds[e < cnt ? scol[b] : K];
-      else
-        sx0[b] = __builtin_amdgcn_raw_buffer_load_b16(xr, e < cnt ? scol[b] * 2 : kOutOfRange, 0, 0);
+      if (X1) {
+        sx[0][b] = x_lds[e < cnt ? scol[b] : K];
+      } else {
+#pragma unroll
+        for (int m = 0; m < MM; m++)  // rows past M: out of range, zero
+          sx[m][b] = __builtin_amdgcn_raw_buffer_load_b16(xr, e < cnt && m < M ? (m * K + scol[b]) * 2 : kOutOfRange,
+                                                          0, 0);
+      }
     }
   };
-  // Decode (M = 1), wave 0, early in the stream so that its LDS round trips
-  // overlap the code loads in flight: the products x * value of the first
-  // batch of entries go to LDS, then 4 lanes per row add up the row's
-  // entries (lane j of row r: entries j, j + 4, ... of the row, in order; a
-  // tile with more entries than the first batch reads the rest from
-  // memory) and two DPP levels add the 4 partial sums.
-  auto decode_outliers = [&]() {
+  // Wave 0, early in the stream so that its LDS round trips overlap the code
+  // loads in flight: the products x * value of the first entries go to LDS,
+  // then 4 lanes per output column r add up the column's entries (lane j:
+  // entries j, j + 4, ... of the row r of W, in order; a tile with more
+  // entries than the registers hold reads the rest from memory) for each
+  // row of x, and two DPP levels add the 4 partial sums.
+  auto outlier_sums = [&]() {
 #pragma unroll
     for (int b = 0; b < kStageBatch; b++) {
       const int e = 64 * b + lane;
-      if (e < cnt) s_prod[e] = (float)bits_to_h((uint16_t)sx0[b]) * (float)bits_to_h((uint16_t)sval[b]);
+      const float wv = (float)bits_to_h((uint16_t)sval[b]);
+#pragma unroll
+      for (int m = 0; m < MM; m++)
+        if (e < cnt && m < M) s_prod[m][e] = (float)bits_to_h((uint16_t)sx[m][b]) * wv;
     }
     __builtin_amdgcn_wave_barrier();  // the wave's LDS writes before its reads
     const int r = lane >> 2;
     const int e0 = __shfl(rp, r, 64) - p0, e1 = __shfl(rp, r + 1, 64) - p0;
-    float v = 0.0f;
+    float v[MM];
+#pragma unroll
+    for (int m = 0; m < MM; m++) v[m] = 0.0f;
     for (int e = e0 + (lane & 3); e < e1; e += 4) {
-      if (e < 64 * kStageBatch && e < cnt) {
-        v += s_prod[e];
+      if (e < cnt) {
+#pragma unroll
+        for (int m = 0; m < MM; m++)
+          if (m < M) v[m] += s_prod[m][e];
       } else {
         const int col = W.cols[p0 + e];
-        v += (float)bits_to_h(X1 ? x_lds[col] : a.x[col]) * (float)bits_to_h(W.vals[p0 + e]);
+        const float wv = (float)bits_to_h(W.vals[p0 + e]);
+#pragma unroll
+        for (int m = 0; m < MM; m++)
+          if (m < M) v[m] += (float)bits_to_h(X1 ? x_lds[col] : a.x[(size_t)m * K + col]) * wv;
       }
     }
-    v += __builtin_bit_cast(float, xlane_partner_u32<1>(__builtin_bit_cast(uint32_t, v)));
-    v += __builtin_bit_cast(float, xlane_partner_u32<2>(__builtin_bit_cast(uint32_t, v)));
-    if ((lane & 3) == 0) s_osum[r] = v;
+#pragma unroll
+    for (int m = 0; m < MM; m++) {
+      float t = v[m];
+      t += __builtin_bit_cast(float, xlane_partner_u32<1>(__builtin_bit_cast(uint32_t, t)));
+      t += __builtin_bit_cast(float, xlane_partner_u32<2>(__builtin_bit_cast(uint32_t, t)));
+      if ((lane & 3) == 0 && m < M) s_osum[m][r] = t;
+    }
   };
 
   struct Batch {
@@ -281,12 +293,12 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
     if (wave == 0) stage_first_batch();
     for (int c0 = wave; c0 < nchunks; c0 += 2 * step) {
       __builtin_amdgcn_sched_barrier(0);
-      if (wave == 0 && c0 == 0) gather_x0();
+      if (wave == 0 && c0 == 0) gather_x();
       compute(B0);
       __builtin_amdgcn_sched_barrier(0);
       load(B0, c0 + 2 * step);
       __builtin_amdgcn_sched_barrier(0);
-      if (M == 1 && wave == 0 && c0 == 0) decode_outliers();
+      if (wave == 0 && c0 == 0) outlier_sums();
       __builtin_amdgcn_sched_barrier(0);
       compute(B1);
       __builtin_amdgcn_sched_barrier(0);
@@ -298,12 +310,12 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
     for (int c0 = wave; c0 < nchunks; c0 += 2 * step) {
       load(B1, c0 + step);
       __builtin_amdgcn_sched_barrier(0);
-      if (wave == 0 && c0 == 0) gather_x0();
+      if (wave == 0 && c0 == 0) gather_x();
       compute(B0);
       __builtin_amdgcn_sched_barrier(0);
       load(B0, c0 + 2 * step);
       __builtin_amdgcn_sched_barrier(0);
-      if (M == 1 && wave == 0 && c0 == 0) decode_outliers();
+      if (wave == 0 && c0 == 0) outlier_sums();
       __builtin_amdgcn_sched_barrier(0);
       compute(B1);
     }
@@ -311,106 +323,27 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   // C layout: lane l, element i -> m = 4 (l / 16) + i, column l % 16
 #pragma unroll
   for (int i = 0; i < 4; i++) red[wave][lane * 4 + i] = acc[i];
-
-  if (M == 1) {
-    // decode: dense part (C element (m = 0, column nl) sits in lane nl,
-    // slot 0 of each wave) + outlier sum + bias, by wave 0's lanes 0..15
-    __syncthreads();
+  __syncthreads();
+  if (MM == 1) {
+    // decode: C element (m = 0, column nl) sits in lane nl, slot 0
     if (wave == 0 && lane < 16) {
       float dense = 0.0f;
 #pragma unroll
       for (int w = 0; w < NS; w++) dense += red[w][lane * 4];
-      const float v = dense + s_osum[lane] + (float)bits_to_h((uint16_t)bias_v);
+      const float v = dense + s_osum[0][lane] + (float)bits_to_h((uint16_t)bias_v);
       W.y[n0 + lane] = h_to_bits(rn_h(v));
     }
     return;
   }
-
-  if (wave == 0) {
-    // Stage the CSR lists of rows n0..n0+15 and the x values they multiply
-    // (the first batch of (col, val) and row 0's x values are already in
-    // registers).
-    if (lane <= 16) s_rp[lane] = rp - p0;
-    if (lane < 16) s_bias[lane] = (uint16_t)bias_v;
-    const int nx = min(cnt, kXvCap / M);
-    for (int base = 0; base < cnt; base += 64 * kStageBatch) {
-      int col[kStageBatch];
-      uint16_t val[kStageBatch];
+  // output (m, column nl): dense part (C element in lane 16 (m / 4) + nl,
+  // slot m % 4 of each wave) + outlier sum + bias (nl = lane % 16)
+  for (int o = threadIdx.x; o < 16 * M; o += 64 * NS) {
+    const int m = o >> 4, nl = o & 15;
+    float dense = 0.0f;
 #pragma unroll
-      for (int b = 0; b < kStageBatch; b++) {
-        const int e = base + 64 * b + lane;
-        col[b] = (int)scol[b];
-        val[b] = (uint16_t)sval[b];
-        if (base > 0) {
-          col[b] = 0;
-          val[b] = 0;
-          if (e < cnt) {
-            col[b] = W.cols[p0 + e];
-            val[b] = W.vals[p0 + e];
-          }
-        }
-      }
-#pragma unroll
-      for (int b = 0; b < kStageBatch; b++) {
-        const int e = base + 64 * b + lane;
-        if (e < cnt) {
-          s_col[e] = col[b];
-          s_val[e] = val[b];
-        }
-      }
-      for (int m = 0; m < M; m++) {
-        uint16_t xv[kStageBatch];
-#pragma unroll
-        for (int b = 0; b < kStageBatch; b++) {
-          const int e = base + 64 * b + lane;
-          xv[b] = (base == 0 && m == 0) ? (uint16_t)sx0[b]
-                  : (e < nx)            ? a.x[(size_t)m * K + col[b]]
-                                        : (uint16_t)0;
-        }
-#pragma unroll
-        for (int b = 0; b < kStageBatch; b++) {
-          const int e = base + 64 * b + lane;
-          if (e < nx) s_xv[e * M + m] = xv[b];
-        }
-      }
-    }
-    if (lane == 0) {
-      s_meta[0] = p0;
-      s_meta[1] = cnt;
-      s_meta[2] = nx;
-    }
-  }
-  __syncthreads();
-
-  // 1 < M <= 16: a thread per (m, column) output, its row's outliers in order
-  for (int o = threadIdx.x; o < 256; o += 64 * NS) {
-    const int l = o >> 2;
-    const int m = 4 * (l >> 4) + (o & 3);
-    const int nl = l & 15;
-    const int n = n0 + nl;
-    if (m < M) {
-      float v = 0.0f;
-#pragma unroll
-      for (int w = 0; w < NS; w++) v += red[w][o];
-      const int p0 = s_meta[0], cnt = s_meta[1], nx = s_meta[2];
-      const int e1 = s_rp[nl + 1];
-      for (int e = s_rp[nl]; e < e1; e++) {
-        float xv, wv;
-        if (e < nx) {
-          xv = (float)bits_to_h(s_xv[e * M + m]);
-          wv = (float)bits_to_h(s_val[e]);
-        } else if (e < cnt) {
-          xv = (float)bits_to_h(a.x[(size_t)m * K + s_col[e]]);
-          wv = (float)bits_to_h(s_val[e]);
-        } else {  // more outliers than the staging holds: straight from memory
-          xv = (float)bits_to_h(a.x[(size_t)m * K + W.cols[p0 + e]]);
-          wv = (float)bits_to_h(W.vals[p0 + e]);
-        }
-        v = __builtin_fmaf(xv, wv, v);
-      }
-      v += (float)bits_to_h(s_bias[nl]);
-      W.y[(size_t)m * N + n] = h_to_bits(rn_h(v));
-    }
+    for (int w = 0; w < NS; w++) dense += red[w][(16 * (m >> 2) + nl) * 4 + (m & 3)];
+    const float v = dense + s_osum[m][nl] + (float)bits_to_h((uint16_t)bias_v);
+    W.y[(size_t)m * N + n0 + nl] = h_to_bits(rn_h(v));
   }
 }
 
@@ -1342,16 +1275,26 @@ hipError_t launch_gemv(const QLArgs& a, bool per_channel, int blocks, hipStream_
   // LDS (dynamic size).  With 8 waves per tile row (short matrices, 1 to 2
   // workgroups per CU) the staging latency costs more than the x loads it
   // saves (measured).
+  // Decode gets instances for one row of x (no registers or loads for more).
   const bool x1 = a.M == 1 && a.K <= kGemvX1MaxK && NS <= 4;
   const size_t lds = x1 ? (size_t)a.K * 2 + 64 : 0;
-  if (per_channel && x1)
-    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 1>), dim3(blocks), dim3(64 * NS), lds, s, a);
-  else if (per_channel)
-    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 0>), dim3(blocks), dim3(64 * NS), 0, s, a);
-  else if (x1)
-    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 1>), dim3(blocks), dim3(64 * NS), lds, s, a);
-  else
-    hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 0>), dim3(blocks), dim3(64 * NS), 0, s, a);
+  constexpr int R = kGemvDirectMaxM;
+  const dim3 g(blocks), b(64 * NS);
+  if (per_channel) {
+    if (x1)
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 1, 1>), g, b, lds, s, a);
+    else if (a.M == 1)
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 0, 1>), g, b, 0, s, a);
+    else
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 0, R>), g, b, 0, s, a);
+  } else {
+    if (x1)
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 1, 1>), g, b, lds, s, a);
+    else if (a.M == 1)
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 0, 1>), g, b, 0, s, a);
+    else
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 0, R>), g, b, 0, s, a);
+  }
   return hipGetLastError();
 }
 

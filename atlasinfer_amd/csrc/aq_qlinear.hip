@@ -1330,9 +1330,11 @@ hipError_t launch_gemv_x(QLArgs a, int fmt, bool per_channel, int S, hipStream_t
   }
   for (int i = a.count; i <= kMaxGroup; i++) a.first[i] = wgs;
   if (a.M <= 16)
-    return S == 2 ? launch_gemv_x<1, 2>(a, fmt, per_channel, wgs, s) : launch_gemv_x<1, 4>(a, fmt, per_channel, wgs, s);
+    return S == 2 ? launch_gemv_x<1, 2>(a, fmt, per_channel, wgs, s)
+           : S == 4 ? launch_gemv_x<1, 4>(a, fmt, per_channel, wgs, s) : launch_gemv_x<1, 8>(a, fmt, per_channel, wgs, s);
   if (a.M <= 32)
-    return S == 2 ? launch_gemv_x<2, 2>(a, fmt, per_channel, wgs, s) : launch_gemv_x<2, 4>(a, fmt, per_channel, wgs, s);
+    return S == 2 ? launch_gemv_x<2, 2>(a, fmt, per_channel, wgs, s)
+           : S == 4 ? launch_gemv_x<2, 4>(a, fmt, per_channel, wgs, s) : launch_gemv_x<2, 8>(a, fmt, per_channel, wgs, s);
   return S == 2 ? launch_gemv_x<4, 2>(a, fmt, per_channel, wgs, s) : launch_gemv_x<4, 4>(a, fmt, per_channel, wgs, s);
 }
 
@@ -1495,11 +1497,14 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
   bool per_channel = true;
   for (int i = 0; i < count; i++) per_channel = per_channel && a.mat[i].kg == 1;
   if (M >= kGemvXMinM && M <= kGemvMaxM) {
-    // S = 2 waves per tile row for tall groups, 4 for short ones (measured
-    // on the Llama-3-8B shapes: S = 1 leaves the loads' latency exposed).
+    // S = 2 waves per tile row for tall groups, 4 for short ones and 8 for
+    // fewer than 384 tile rows up to M = 32 (one tile row per workgroup; at
+    // M = 64 its x stages do not fit LDS) (measured on the Llama-3-8B
+    // shapes: S = 1 leaves the loads' latency exposed, S = 4 on N = 4096
+    // leaves half the CUs idle).
     // Per decoder layer of those shapes it beats re-reading x per tile row
     // from M = 6 on (M = 6: 76 against 78 us, M = 16: 77 against 127 us)
-    const int S = blocks >= 768 ? 2 : 4;
+    const int S = blocks >= 768 ? 2 : (blocks >= 384 || M > 32) ? 4 : 8;
     return aq::check_hip(launch_gemv_x(a, fmt, per_channel, S, s), "aq_qlinear: gemv launch");
   }
   if (M <= kGemvMaxM) {

@@ -224,13 +224,14 @@ def test_qlinear_llama_shapes(N, K, M):
     assert_close(y, reference_linear(x, w_deq, None), x, w_deq)
 
 
-@pytest.mark.parametrize("N,K", [(1040, 640), (12304, 384)])
+@pytest.mark.parametrize("N,K", [(1040, 640), (6160, 384), (12304, 384)])
 @pytest.mark.parametrize("M", [9, 17, 48, 64])
 @pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128)])
 def test_gemv_shared_x_ragged_shapes(N, K, M, fmt, G):
     """6 <= M <= 64: tile-row counts that leave the last workgroup partly
     empty, chunk counts that leave the last chunk group partly past K, and
-    both split widths (12304 rows take 2 waves per tile row, 1040 take 4)."""
+    every split width (12304 rows take 2 waves per tile row, 6160 take 4,
+    1040 take 8 up to M = 32 and 4 above)."""
     rng = np.random.default_rng(N + K + M + abs(G))
     w = make_weights(rng, (N, K), frac=0.004)
     x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)

@@ -1365,38 +1365,57 @@ hipError_t launch_gemm(const QLArgs& a, int fmt, bool per_channel, bool dense, h
                             : launch_gemm<BM, AQ_FMT_INT8, 0>(a, per_channel, s);
 }
 
-// GEMM shape choice.  256 x 256 tiles (qlinear_gemm_wide_kernel) when they
-// give every CU at least one.  Otherwise 256 x 128 or 128 x 128 tiles: both
-// run one workgroup per CU (their three LDS stages take 144 or 96 KiB), and a
-// 128-row tile takes about 3/4 of the time of a 256-row one (measured on
-// gfx950), so 256-row tiles unless the 128-row grid needs less than 4/3 of
-// the rounds.  Then a grid that fills at most half the CUs splits K 2 to 8
-// ways (up to one full round, at least 4 chunks of 64 per part).
+// GEMM shapes: 256 x 256 tiles (qlinear_gemm_wide_kernel, one workgroup of
+// 8 waves per CU), 256 x 128 or 128 x 128 tiles (qlinear_gemm_kernel, one
+// workgroup per CU: three LDS stages of 144 or 96 KiB).
 enum { kTile256x128 = 0, kTile128x128 = 1, kTile256x256 = 2 };
 struct GemmPlan {
   int tile;
   int split;
 };
 
-GemmPlan plan_gemm(int64_t M, const int64_t* Ns, int64_t count, int64_t K) {
-  int64_t wgw = 0, wg256 = 0, wg128 = 0;
-  for (int i = 0; i < count; i++) {
-    wgw += aq::ceil_div(M, kWideBM) * aq::ceil_div(Ns[i], kWideBN);
-    wg256 += aq::ceil_div(M, 256) * aq::ceil_div(Ns[i], kGemmBN);
-    wg128 += aq::ceil_div(M, 128) * aq::ceil_div(Ns[i], kGemmBN);
-  }
+// The tile shape and K split of a GEMM launch, chosen by an estimate of its
+// time in microseconds: a fixed cost per launch, the rounds of the grid over
+// the CUs times the 64-wide K chunks per work unit times the time one CU
+// takes for one chunk of that tile (measured with every CU busy on the
+// Llama-3-8B shapes at M = 512 and 2048: 1.8 us for 256 x 256, 1.17 for
+// 256 x 128, 0.74 for 128 x 128), plus the split-K reduction's traffic
+// (4 split + 2 bytes per output at an effective 4 TB/s, launch included).
+// On those shapes (single and grouped, M = 512 and 2048) its pick comes
+// within 4 % of the fastest of all 24 tile / split combinations measured;
+// e.g. down_proj at M = 2048 takes 256 x 256 tiles split two ways (235 us
+// against 265 unsplit with 256 x 128 tiles) and grouped q/k/v at M = 2048
+// 256 x 256 tiles unsplit on 192 of the CUs (110 against 153 us with 384
+// tiles of 256 x 128).  Splits need an even number of chunks per part and at
+// least 4; max_split bounds the split (the caller's workspace).
+GemmPlan plan_gemm(int64_t M, const int64_t* Ns, int64_t count, int64_t K, int max_split) {
+  struct Shape {
+    int tile, bm, bn;
+    double chunk_us;
+  };
+  static constexpr Shape kShapes[] = {{kTile256x256, kWideBM, kWideBN, 1.8},
+                                      {kTile256x128, 256, kGemmBN, 1.17},
+                                      {kTile128x128, 128, kGemmBN, 0.74}};
   const int64_t slots = cu_count();
-  if (wgw >= slots) return GemmPlan{kTile256x256, 1};
-  GemmPlan p{4 * aq::ceil_div(wg256, slots) <= 3 * aq::ceil_div(wg128, slots) ? kTile256x128 : kTile128x128, 1};
-  const int64_t tiles = p.tile == kTile256x128 ? wg256 : wg128;
   const int64_t nch = K / kGemmBK;
-  if (2 * tiles <= slots)
-    for (int sp = 8; sp >= 2; sp /= 2)
-      if (tiles * sp <= slots && nch % (2 * sp) == 0 && nch / sp >= 4) {
-        p.split = sp;
-        break;
+  int64_t outs = 0;
+  for (int i = 0; i < count; i++) outs += M * Ns[i];
+  GemmPlan best{kTile256x256, 1};
+  double best_us = 0.0;
+  for (const Shape& sh : kShapes) {
+    int64_t tiles = 0;
+    for (int i = 0; i < count; i++) tiles += aq::ceil_div(M, sh.bm) * aq::ceil_div(Ns[i], sh.bn);
+    for (int sp = 1; sp <= 8 && sp <= max_split; sp *= 2) {
+      if (sp > 1 && (nch % (2 * sp) != 0 || nch / sp < 4)) break;
+      const double us = 15.0 + (double)aq::ceil_div(tiles * sp, slots) * (double)(nch / sp) * sh.chunk_us +
+                        (sp > 1 ? (double)(4 * sp + 2) * (double)outs / 4e6 : 0.0);
+      if (best_us == 0.0 || us < best_us) {
+        best = GemmPlan{sh.tile, sp};
+        best_us = us;
       }
-  return p;
+    }
+  }
+  return best;
 }
 
 template <int FMT, int DENSE>
@@ -1430,7 +1449,7 @@ extern "C" int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K) {
   // the GEMM's fp32 partial sums when it would split K for this shape on the
   // current device (0 for the GEMV and for unsplit grids)
   if (M <= kGemvMaxM || N <= 0 || K < 128 || K % 128) return 0;
-  const GemmPlan p = plan_gemm(M, &N, 1, K);
+  const GemmPlan p = plan_gemm(M, &N, 1, K, 8);
   return p.split > 1 ? p.split * M * N * 4 : 0;
 }
 
@@ -1520,16 +1539,15 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
   }
   bool dense = false;  // some 16 x 64 block holds more than 64 outliers
   for (int i = 0; i < count; i++) dense = dense || tile_maxes[i] > 64;
-  // 256-row tiles decode each weight half as often, but only pay off while
-  // they still give every CU a workgroup; smaller grids take 128-row tiles
-  // (two workgroups per CU)
-  // Split K (plan_gemm) as far as the workspace allows: each part's fp32
-  // partial sums go there and splitk_reduce_kernel adds them in a fixed order.
+  // Tile shape and K split from plan_gemm, the split as far as the workspace
+  // allows: each part's fp32 partial sums go there and splitk_reduce_kernel
+  // adds them in a fixed order.
   int64_t outs = 0;
   for (int i = 0; i < count; i++) outs += M * Ns[i];
-  const GemmPlan plan = plan_gemm(M, Ns, count, K);
-  a.split = workspace ? plan.split : 1;
-  while (a.split > 1 && workspace_bytes < a.split * outs * 4) a.split /= 2;
+  int max_split = 1;  // as far as the caller's workspace holds the partial sums
+  while (workspace && max_split < 8 && workspace_bytes >= 2 * max_split * outs * 4) max_split *= 2;
+  const GemmPlan plan = plan_gemm(M, Ns, count, K, max_split);
+  a.split = plan.split;
   if (a.split > 1) {
     AQ_CHECK_ARG((uintptr_t)workspace % 16 == 0, "aq_qlinear: workspace must be 16-byte aligned");
     float* p = (float*)workspace;

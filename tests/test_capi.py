@@ -83,10 +83,12 @@ def test_workspace_sizes(lib):
     assert lib.aq_quantize_workspace_size(0, 128) == 0
     assert lib.aq_qlinear_workspace_size(1, 4096, 4096) == 0  # the GEMV needs none
     assert lib.aq_qlinear_workspace_size(64, 4096, 4096) == 0
-    # the GEMM on 256 CUs (the count assumed without a device): 128 tiles of
-    # 128 x 128 split K two ways, fp32 partial sums of both parts; grids that
-    # fill the GPU need none
-    assert lib.aq_qlinear_workspace_size(2048, 1024, 4096) == 2 * 2048 * 1024 * 4
+    # the GEMM on 256 CUs (the count assumed without a device): k_proj's 64
+    # tiles of 256 x 128 split K four ways and down_proj's 128 tiles of
+    # 256 x 256 two ways, fp32 partial sums of every part; grids that fill
+    # the GPU unsplit need none
+    assert lib.aq_qlinear_workspace_size(2048, 1024, 4096) == 4 * 2048 * 1024 * 4
+    assert lib.aq_qlinear_workspace_size(2048, 4096, 14336) == 2 * 2048 * 4096 * 4
     assert lib.aq_qlinear_workspace_size(2048, 14336, 4096) == 0
     assert lib.aq_max_block_size() == 65536
 

@@ -123,8 +123,14 @@ class QuantizedLinear(nn.Module):
         self.quantized_weights = quantized_weights
         self.bias = bias
         self.original_shape = getattr(quantized_weights, "original_shape", None)
-        self._codes = None  # tiled codes on the compute device (int8: expanded and tiled once)
-        self._tiles = None  # outlier block lists on the compute device
+        # derived from the weight object _derived_from on its device: the tiled
+        # codes (int8: expanded and tiled once) and the outlier block lists
+        self._derived_from = None
+        self._codes = None
+        self._tiles = None
+        # the GEMV call's fixed arguments, valid while device, weight and bias
+        # objects stay the same: (device, bias, weight, K, N, entry, args, codes)
+        self._prep = None
 
     def _weights_on(self, device: torch.device) -> QuantizedTensor:
         q = self.quantized_weights
@@ -134,11 +140,30 @@ class QuantizedLinear(nn.Module):
             self.quantized_weights = q = q.to(device)
             self._codes = None
             self._tiles = None
+            self._prep = None
         if self.bias is not None and self.bias.device != device:
             self.bias = self.bias.to(device)
         return q
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        # decode fast path (M <= GEMV_MAX_M rows of x): one library call with
+        # the weight's arguments prepared by an earlier forward on this device
+        p = self._prep
+        if (p is not None and x.dtype == torch.float16 and self.bias is p[1] and self.quantized_weights is p[2]
+                and x.device == p[0] and x.shape[-1] == p[3]):
+            K, N = p[3], p[4]
+            x2 = x.reshape(-1, K)
+            M = x2.shape[0]
+            if 0 < M <= GEMV_MAX_M:
+                if not x2.is_contiguous() or x2.data_ptr() % 16:
+                    x2 = x2.contiguous()
+                y = torch.empty((M, N), dtype=torch.float16, device=p[0])
+                _lib.check(p[5](x2.data_ptr(), M, K, N, *p[6], y.data_ptr(), None, 0, _lib.stream_of(p[0])),
+                           "aq_qlinear")
+                return y.view(*x.shape[:-1], N)
+        return self._forward(x)
+
+    def _forward(self, x: torch.Tensor) -> torch.Tensor:
         dev = x.device
         if dev.type != "cuda":
             raise RuntimeError(f"QuantizedLinear runs on a HIP device; input is on {dev}")
@@ -151,10 +176,19 @@ class QuantizedLinear(nn.Module):
                                f"in_features {K})")
         if not fused_supported(q):
             return F.linear(x, dequantize_tensor(q, dev), self.bias)
+        if self._derived_from is not q:  # a weight assigned since (q is on dev here)
+            self._derived_from, self._codes, self._tiles = q, None, None
         if self._codes is None or self._codes.device != dev:
             self._codes = kernel_codes(q, dev)
         if x.numel() > GEMV_MAX_M * x.shape[-1] and (self._tiles is None or self._tiles[0].device != dev):
             self._tiles = outlier_tiles(q, dev)
+        if self._prep is None or self._prep[0] != dev or self._prep[1] is not self.bias or self._prep[2] is not q:
+            N = q.original_shape.numel() // K
+            # the tuple holds the codes, weight and bias objects its addresses point into
+            self._prep = (dev, self.bias, q, K, N, _lib.load().aq_qlinear,
+                          (self._codes.data_ptr(), q.scale_factors.data_ptr(), q.block_size,
+                           _format_id(q.code_format), q.outlier_row_ptr.data_ptr(), _lib.ptr(q.outlier_cols),
+                           _lib.ptr(q.fp16_outliers), None, None, 0, _lib.ptr(self.bias)), self._codes)
         return qlinear(x, q, self.bias, self._codes, self._tiles)
 
     def _apply(self, fn, recurse=True):

@@ -1,0 +1,63 @@
+"""QuantizedLinear's decode fast path (arguments prepared once per device,
+weight and bias) gives the same bits as the stateless qlinear call, and
+follows a new bias, a new weight, a device move and every shape of x."""
+import numpy as np
+import pytest
+import torch
+
+from atlasinfer_core.quant import adaptive_quantizer as AQ
+from integration import atlas_wrappers as AW
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _q(seed, N, K, fmt="e4m3", G=-1):
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(N, K, generator=g) * 0.02).half()
+    w.view(-1)[torch.randperm(N * K, generator=g)[: N * K // 500]] *= 40
+    return AQ.quantize_tensor(w.to(DEV), block_size=G, code_format=fmt)
+
+
+def test_fast_path_matches_and_tracks_changes():
+    N, K = 256, 1024
+    q1, q2 = _q(1, N, K), _q(2, N, K, "int8", 128)
+    b1 = torch.randn(N, device=DEV).half()
+    b2 = torch.randn(N, device=DEV).half()
+    ql = AW.QuantizedLinear(q1, b1)
+    x = torch.randn(3, K, device=DEV).half()
+    first = ql(x)                  # prepares the arguments
+    assert ql._prep is not None
+    for _ in range(2):             # fast path
+        assert torch.equal(ql(x), first)
+    assert torch.equal(first, AW.qlinear(x, q1, b1))
+    ql.bias = b2
+    assert torch.equal(ql(x), AW.qlinear(x, q1, b2))
+    ql.bias = None
+    assert torch.equal(ql(x), AW.qlinear(x, q1, None))
+    ql.quantized_weights = q2      # a new weight: codes and arguments rebuilt
+    assert torch.equal(ql(x), AW.qlinear(x, q2, None))
+    assert torch.equal(ql(x), AW.qlinear(x, q2, None))
+    # shapes: 1-D, 3-D, a non-contiguous view, M past the GEMV, empty
+    for xx in [x[0], x.view(1, 3, K), torch.randn(K, 4, device=DEV).half().t(),
+               torch.randn(100, K, device=DEV).half(), torch.empty(0, K, device=DEV).half()]:
+        assert torch.equal(ql(xx), AW.qlinear(xx, q2, None))
+    with pytest.raises(RuntimeError):
+        ql(x.float())
+    with pytest.raises(RuntimeError):
+        ql(torch.randn(2, K + 128, device=DEV).half())
+
+
+def test_fast_path_after_module_move():
+    q = _q(3, 128, 512)
+    b = torch.randn(128).half()
+    ql = AW.QuantizedLinear(q.to("cpu"), b).to(DEV)
+    x = torch.randn(2, 512, device=DEV).half()
+    y = ql(x)
+    assert torch.equal(ql(x), y)
+    assert torch.equal(y, AW.qlinear(x, q, b.to(DEV)))
+    ql.to("cpu")
+    with pytest.raises(RuntimeError):
+        ql(x.cpu())
+    ql.to(DEV)
+    assert torch.equal(ql(x), y)

@@ -40,6 +40,14 @@ using namespace aqk;
 // ------------------------------------------------------------ GEMV (M <= 64)
 
 constexpr int kGemvMaxM = 64;   // larger M takes the GEMM
+// From 33 rows of x on, grids of fewer than 384 tile rows take the GEMM when the
+// caller passes the outlier block lists: the GEMV's x stages for 64 rows fit
+// LDS only with 4 waves per tile row, which leaves half the CUs idle there
+// (down_proj [4096, 14336] at M = 33..64: 78 us against 29 with the GEMM;
+// q/o and k/v about equal; taller grids such as grouped q/k/v or gate+up stay
+// faster on the GEMV)
+constexpr int kGemvShortMaxM = 32;
+constexpr int kGemvShortRows = 384;
 constexpr int kGemvXMinM = 6;   // from here on the GEMV shares x through LDS (qlinear_gemv_x_kernel)
 constexpr int kGemvUnroll = 2;  // 128-wide K chunks per wave with loads in flight together
 constexpr int kGemvDirectMaxM = kGemvXMinM - 1;  // rows of x qlinear_gemv_kernel takes
@@ -1447,8 +1455,10 @@ hipError_t launch_gemm_wide(const QLArgs& a, int fmt, bool per_channel, bool den
 
 extern "C" int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K) {
   // the GEMM's fp32 partial sums when it would split K for this shape on the
-  // current device (0 for the GEMV and for unsplit grids)
-  if (M <= kGemvMaxM || N <= 0 || K < 128 || K % 128) return 0;
+  // current device (0 for the GEMV and for unsplit grids; for 33 <= M <= 64
+  // on short grids the GEMM takes the call if given the block lists)
+  if (N <= 0 || K < 128 || K % 128) return 0;
+  if (M <= kGemvShortMaxM || (M <= kGemvMaxM && N / 16 >= kGemvShortRows)) return 0;
   const GemmPlan p = plan_gemm(M, &N, 1, K, 8);
   return p.split > 1 ? p.split * M * N * 4 : 0;
 }
@@ -1515,7 +1525,10 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
   hipStream_t s = (hipStream_t)stream;
   bool per_channel = true;
   for (int i = 0; i < count; i++) per_channel = per_channel && a.mat[i].kg == 1;
-  if (M >= kGemvXMinM && M <= kGemvMaxM) {
+  bool have_lists = tile_ptrs && tile_ents && tile_maxes;
+  for (int i = 0; i < count && have_lists; i++) have_lists = tile_ptrs[i] && tile_ents[i];
+  const bool gemv = M <= kGemvShortMaxM || (M <= kGemvMaxM && (blocks >= kGemvShortRows || !have_lists));
+  if (gemv && M >= kGemvXMinM) {
     // S = 2 waves per tile row for tall groups, 4 for short ones and 8 for
     // fewer than 384 tile rows up to M = 32 (one tile row per workgroup; at
     // M = 64 its x stages do not fit LDS) (measured on the Llama-3-8B
@@ -1526,7 +1539,7 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
     const int S = blocks >= 768 ? 2 : (blocks >= 384 || M > 32) ? 4 : 8;
     return aq::check_hip(launch_gemv_x(a, fmt, per_channel, S, s), "aq_qlinear: gemv launch");
   }
-  if (M <= kGemvMaxM) {
+  if (gemv) {
     // tall groups fill the GPU with 4 streaming waves per tile row, short ones need 8
     // waves per tile row: enough for about 1536 waves in all (1.5 per SIMD),
     // at most 8; a tall group (gate+up) streams one tile row per wave

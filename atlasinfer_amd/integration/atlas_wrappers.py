@@ -30,14 +30,21 @@ from ..quant.adaptive_quantizer import (QuantizedTensor, _format_id, _rows_cols,
 
 
 GEMV_MAX_M = 64  # aq_qlinear runs the dequant-GEMV up to this many rows of x
+# from this many rows of x on, calls pass the outlier block lists and the
+# workspace: the library then runs the GEMM for grids too short for the GEMV
+# (and always past GEMV_MAX_M)
+LISTS_MIN_M = 33
 
 
 def _workspace(M: int, Ns, K: int, dev: torch.device):
-    """The GEMM's split-K workspace (None for the GEMV) and its size."""
-    if M <= GEMV_MAX_M:
+    """The GEMM's split-K workspace (None when the call needs none) and its size."""
+    if M < LISTS_MIN_M:
         return None, 0
-    L = _lib.load()
-    n = sum(int(L.aq_qlinear_workspace_size(M, N, K)) for N in Ns)
+    # one query for the whole group: the library plans a grouped call over
+    # all its output columns, and returns 0 when it runs the GEMV
+    n = int(_lib.load().aq_qlinear_workspace_size(M, sum(Ns), K))
+    if n == 0:
+        return None, 0
     return torch.empty(n, dtype=torch.uint8, device=dev), n
 
 
@@ -73,7 +80,7 @@ def qlinear_grouped(x: torch.Tensor, qts, biases=None, codes=None, tiles=None):
     ys = [torch.empty((M, N), dtype=torch.float16, device=dev) for N in Ns]
     if M > 0:
         arr = _lib.ptr_array
-        if M > GEMV_MAX_M:
+        if M >= LISTS_MIN_M:
             tiles = list(tiles) if tiles is not None else [outlier_tiles(q, dev) for q in qts]
         else:
             tiles = [(None, None, 0)] * n
@@ -105,7 +112,7 @@ def qlinear(x: torch.Tensor, qt: QuantizedTensor, bias: Optional[torch.Tensor],
         return y.view(*x.shape[:-1], N)
     if codes is None:
         codes = kernel_codes(qt, dev)
-    tp, te, tmax = (tiles if tiles is not None else outlier_tiles(qt, dev)) if M > GEMV_MAX_M else (None, None, 0)
+    tp, te, tmax = (tiles if tiles is not None else outlier_tiles(qt, dev)) if M >= LISTS_MIN_M else (None, None, 0)
     L = _lib.load()
     ws, ws_bytes = _workspace(M, [N], K, dev)
     _lib.check(L.aq_qlinear(x2.data_ptr(), M, K, N, codes.data_ptr(), qt.scale_factors.data_ptr(), qt.block_size,
@@ -146,7 +153,7 @@ class QuantizedLinear(nn.Module):
         return q
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        # decode fast path (M <= GEMV_MAX_M rows of x): one library call with
+        # decode fast path (M < LISTS_MIN_M rows of x): one library call with
         # the weight's arguments prepared by an earlier forward on this device
         p = self._prep
         if (p is not None and x.dtype == torch.float16 and self.bias is p[1] and self.quantized_weights is p[2]
@@ -154,7 +161,7 @@ class QuantizedLinear(nn.Module):
             K, N = p[3], p[4]
             x2 = x.reshape(-1, K)
             M = x2.shape[0]
-            if 0 < M <= GEMV_MAX_M:
+            if 0 < M < LISTS_MIN_M:
                 if not x2.is_contiguous() or x2.data_ptr() % 16:
                     x2 = x2.contiguous()
                 y = torch.empty((M, N), dtype=torch.float16, device=p[0])
@@ -180,7 +187,7 @@ class QuantizedLinear(nn.Module):
             self._derived_from, self._codes, self._tiles = q, None, None
         if self._codes is None or self._codes.device != dev:
             self._codes = kernel_codes(q, dev)
-        if x.numel() > GEMV_MAX_M * x.shape[-1] and (self._tiles is None or self._tiles[0].device != dev):
+        if x.numel() >= LISTS_MIN_M * x.shape[-1] and (self._tiles is None or self._tiles[0].device != dev):
             self._tiles = outlier_tiles(q, dev)
         if self._prep is None or self._prep[0] != dev or self._prep[1] is not self.bias or self._prep[2] is not q:
             N = q.original_shape.numel() // K

@@ -82,7 +82,9 @@ def test_workspace_sizes(lib):
     assert lib.aq_quantize_workspace_size(4096 * 4096, 4096) >= 4096 * 4096 * 6
     assert lib.aq_quantize_workspace_size(0, 128) == 0
     assert lib.aq_qlinear_workspace_size(1, 4096, 4096) == 0  # the GEMV needs none
-    assert lib.aq_qlinear_workspace_size(64, 4096, 4096) == 0
+    assert lib.aq_qlinear_workspace_size(32, 4096, 4096) == 0
+    assert lib.aq_qlinear_workspace_size(64, 14336, 4096) == 0  # tall grid: the GEMV even at M = 64
+    assert lib.aq_qlinear_workspace_size(64, 4096, 14336) > 0   # short grid: the GEMM, split K
     # the GEMM on 256 CUs (the count assumed without a device): k_proj's 64
     # tiles of 256 x 128 split K four ways and down_proj's 128 tiles of
     # 256 x 256 two ways, fp32 partial sums of every part; grids that fill

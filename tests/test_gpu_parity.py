@@ -278,6 +278,33 @@ def test_gemm_split_k_matches_unsplit(M, N, K):
     assert_close(y_plain, ref, x, w_deq)
 
 
+@pytest.mark.parametrize("M", [33, 48, 64])
+@pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128)])
+def test_short_grid_gemm_and_gemv_agree_with_reference(M, fmt, G):
+    """33 <= M <= 64 on a grid of fewer than 384 tile rows: given the block
+    lists (and its workspace) the library runs the GEMM, without them the
+    shared-x GEMV; both within the bounds of the reference."""
+    N, K = 1040, 1152
+    rng = np.random.default_rng(7 * M + abs(G))
+    w = make_weights(rng, (N, K), frac=0.004)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)
+    b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(DEV)
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=G, code_format=fmt)
+    AQ.clear_dequantized_cache()
+    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    L = _lib.load()
+    ref = reference_linear(x, w_deq, b)
+    y_gemm = AW.qlinear(x, q, b)
+    assert_close(y_gemm, ref, x, w_deq)
+    codes = AQ.kernel_codes(q, torch.device(DEV))
+    y_gemv = torch.empty(M, N, dtype=torch.float16, device=DEV)
+    _lib.check(L.aq_qlinear(x.data_ptr(), M, K, N, codes.data_ptr(), q.scale_factors.data_ptr(), q.block_size,
+                            _lib.FORMATS[fmt], q.outlier_row_ptr.data_ptr(), q.outlier_cols.data_ptr(),
+                            q.fp16_outliers.data_ptr(), None, None, 0, b.data_ptr(), y_gemv.data_ptr(), None, 0,
+                            _lib.stream_of(torch.device(DEV))), "aq_qlinear")
+    assert_close(y_gemv, ref, x, w_deq)
+
+
 def test_qlinear_heavy_outliers_and_3d_input():
     rng = np.random.default_rng(77)
     w = make_weights(rng, (512, 1024), frac=0.01, t_dof=3)

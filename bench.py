@@ -50,6 +50,24 @@ def gen_weight(N, K, gen, dev, sigma=0.02, frac=0.001):
     return w.view(N, K).to(torch.float16)
 
 
+def gen_weight_t3(N, K, gen, dev, sigma=0.02, frac=0.01):
+    """BASELINE config 4 weights: Student-t(3) * sigma, as z / sqrt(chi2_3 / 3)
+    from seeded normals, plus ``frac`` of the entries (uniform positions)
+    replaced by +-U(8, 20) * sigma (sigma taken as 0.02)."""
+    n = N * K
+    w = torch.empty(n, device=dev, dtype=torch.float32)
+    step = 1 << 26
+    for i in range(0, n, step):
+        m = min(step, n - i)
+        chi = torch.randn(3, m, generator=gen, device=dev).square_().sum(0).div_(3.0).sqrt_()
+        w[i:i + m] = torch.randn(m, generator=gen, device=dev).div_(chi).mul_(sigma)
+    k = int(round(frac * n))
+    pos = torch.randint(0, n, (k,), generator=gen, device=dev)
+    sign = torch.where(torch.rand(k, generator=gen, device=dev) < 0.5, -1.0, 1.0)
+    w[pos] = sign * (torch.rand(k, generator=gen, device=dev) * 12 + 8) * sigma
+    return w.view(N, K).to(torch.float16)
+
+
 def gen_x(M, K, gen, dev):
     x = torch.randn(M, K, generator=gen, device=dev, dtype=torch.float32)
     ch = torch.randperm(K, generator=gen, device=dev)[:4]
@@ -309,6 +327,81 @@ def bench_models(dev, which, log):
     return out
 
 
+def bench_config4(dev, gen, log, qlinear):
+    """BASELINE config 4.  Part 1: the quantize kernel over a full
+    Llama-3-8B-shaped weight set (32 layers of the seven linears, embedding
+    and lm_head [128256, 4096]; 8.03 B parameters) of Student-t(3) weights
+    with 1 % outliers, generated and quantized one layer at a time (graph of
+    one pass per layer, HIP events).  Part 2: the quantized linear on the
+    Gemma-2B lm_head [256000, 2048] and FFN ([16384, 2048] x 2, [2048, 16384])
+    at M = 1 (copies rotated past the 256 MB MALL, one HIP graph) and
+    M = 2048 (eager, 10 calls)."""
+    from atlasinfer_amd.quant import adaptive_quantizer as AQ
+    params, q_bytes, q_s = 0, 0, 0.0
+    shapes = [[(N, K) for _, N, K in LLAMA_LINEARS]] * 32 + [[(128256, 4096)], [(128256, 4096)]]
+    for li, sh in enumerate(shapes):
+        ws = [gen_weight_t3(N, K, gen, dev) for N, K in sh]
+        b, t = time_quantize_kernel(ws, reps=3)
+        q_bytes += b
+        q_s += t
+        params += sum(N * K for N, K in sh)
+        del ws
+        if li % 8 == 7:
+            log(f"config 4: {li + 1} of {len(shapes)} weight groups quantized")
+    torch.cuda.empty_cache()
+    part1 = {"params": params, "GBps": round(q_bytes / q_s / 1e9, 1),
+             "frac_hbm_peak": round(q_bytes / q_s / 1e9 / HBM_PEAK_GBS, 4), "ms": round(1e3 * q_s, 2),
+             "note": "quantize kernel (aq_quantize, per-channel e4m3, tiled) over 32 Llama-3-8B layers + "
+                     "embedding + lm_head, Student-t(3)*0.02 weights with 1% U(8,20)*0.02 outliers"}
+    log(f"config 4 part 1: {params / 1e9:.2f} B params quantized at {part1['GBps']} GB/s "
+        f"({part1['ms']} ms of kernel time)")
+    part2 = {}
+    for name, N, K in [("lm_head", 256000, 2048), ("gate_proj", 16384, 2048), ("up_proj", 16384, 2048),
+                       ("down_proj", 2048, 16384)]:
+        copies = max(1, -(-768 * 2 ** 20 // (N * K)))
+        qts = []
+        for _ in range(copies):
+            w = gen_weight(N, K, gen, dev)
+            qts.append(AQ.quantize_tensor(w, block_size=-1, code_format="e4m3"))
+            del w
+        x1 = gen_x(1, K, gen, dev)
+        for q in qts:
+            qlinear(x1, q, None)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for q in qts:
+                qlinear(x1, q, None)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        t1 = e0.elapsed_time(e1) / 1e3 / (5 * copies)
+        gbs = gemv_bytes(qts[0], 1) / t1 / 1e9
+        x2 = gen_x(2048, K, gen, dev)
+        qlinear(x2, qts[0], None)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(10):
+            qlinear(x2, qts[0], None)
+        e1.record()
+        torch.cuda.synchronize()
+        t2 = e0.elapsed_time(e1) / 1e3 / 10
+        tf = 2 * 2048 * N * K / t2 / 1e12
+        part2[name] = {"N": N, "K": K, "m1_us": round(1e6 * t1, 2), "m1_GBps": round(gbs, 1),
+                       "m1_frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "m2048_us": round(1e6 * t2, 1),
+                       "m2048_tflops": round(tf, 1), "m2048_frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)}
+        log(f"config 4 part 2 {name} [{N}, {K}]: M=1 {1e6 * t1:.1f} us ({gbs:.0f} GB/s), "
+            f"M=2048 {1e6 * t2:.0f} us ({tf:.0f} TFLOP/s)")
+        del qts
+        torch.cuda.empty_cache()
+    return {"quantize_8b": part1, "gemma2b": part2}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -319,6 +412,10 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--models", default="", help="comma list of opt,mistral: also run BASELINE configs 1 / 3 "
                                                   "(HF generate on random-init models; a few minutes)")
+    ap.add_argument("--config4", action="store_true",
+                    help="also run BASELINE config 4: quantize kernel over a full 8B Llama-3-shaped weight set "
+                         "(Student-t(3), 1%% outliers) and the Gemma-2B lm_head / FFN at M = 1 and 2048 "
+                         "(a minute or two)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant kernel (gate+up grouped GEMV, 4 rotated layers) and a 512 MiB "
                          "calibration copy, for counter runs")
@@ -482,6 +579,8 @@ def main():
                              "TFLOP/s": round(2 * Ms * N * K / s / 1e12, 1)}
             sweep[str(Ms)] = per
 
+    config4 = bench_config4(dev, gen, log, qlinear) if args.config4 else None
+
     models = None
     if args.models:
         import contextlib
@@ -539,6 +638,7 @@ def main():
             "quantize_note": "whole quantize_tensor call incl. host sync, outlier gather and block lists",
             "sweep": sweep or None,
             "models": models,
+            "config4": config4,
         },
     }
     print(json.dumps(result), flush=True)

@@ -1327,7 +1327,7 @@ hipError_t launch_gemv_x(const QLArgs& a, int fmt, bool per_channel, int blocks,
                             : launch_gemv_x<AQ_FMT_INT8, MG, S>(a, per_channel, blocks, s);
 }
 
-// 6 <= M <= 64: x row groups of 16 per MFMA (MG = 1, 2 or 4 for M up to 16, 32, 64),
+// 6 <= M <= 64: x row groups of 16 per MFMA (MG = 1, 2, 3 or 4 for M up to 16, 32, 48, 64),
 // S = 2 or 4 waves per tile row; a.first counts workgroups of 8 / S tile rows
 hipError_t launch_gemv_x(QLArgs a, int fmt, bool per_channel, int S, hipStream_t s) {
   const int TR = kXWaves / S;
@@ -1343,6 +1343,8 @@ hipError_t launch_gemv_x(QLArgs a, int fmt, bool per_channel, int S, hipStream_t
   if (a.M <= 32)
     return S == 2 ? launch_gemv_x<2, 2>(a, fmt, per_channel, wgs, s)
            : S == 4 ? launch_gemv_x<2, 4>(a, fmt, per_channel, wgs, s) : launch_gemv_x<2, 8>(a, fmt, per_channel, wgs, s);
+  if (a.M <= 48)
+    return S == 2 ? launch_gemv_x<3, 2>(a, fmt, per_channel, wgs, s) : launch_gemv_x<3, 4>(a, fmt, per_channel, wgs, s);
   return S == 2 ? launch_gemv_x<4, 2>(a, fmt, per_channel, wgs, s) : launch_gemv_x<4, 4>(a, fmt, per_channel, wgs, s);
 }
 

@@ -122,6 +122,74 @@ def qlinear(x: torch.Tensor, qt: QuantizedTensor, bias: Optional[torch.Tensor],
     return y.view(*x.shape[:-1], N)
 
 
+class SiblingGroup:
+    """QuantizedLinear modules that a model calls one after another on the
+    same input (q/k/v projections, gate/up): at decode sizes the first
+    member's forward runs one grouped launch for all of them and keeps the
+    other outputs for their own forward on that very tensor object (same
+    object, unchanged version); any other input computes as usual.  A kept
+    output lives until its member consumes it or the group runs again."""
+
+    def __init__(self, members):
+        self.members = list(members)
+        self.x = None
+        self.version = -1
+        self.out = {}
+
+    def _prepare(self, dev):
+        """The grouped call's fixed arguments for the members' current
+        weights and biases on ``dev`` (rebuilt when any of them changes)."""
+        qs, biases, codes = [], [], []
+        for m in self.members:
+            q = m._weights_on(dev)
+            m._ensure_codes(q, dev)
+            qs.append(q)
+            biases.append(m.bias)
+            codes.append(m._codes)
+        key = (dev, tuple(id(q) for q in qs), tuple(id(b) for b in biases))
+        p = getattr(self, "_prep", None)
+        if p is not None and p[0] == key:
+            return p
+        arr, n = _lib.ptr_array, len(qs)
+        K = int(qs[0].original_shape[-1])
+        Ns = [_rows_cols(q.original_shape)[0] for q in qs]
+        fixed = (_format_id(qs[0].code_format), n, arr(Ns, ctypes.c_int64), arr([c.data_ptr() for c in codes]),
+                 arr([q.scale_factors.data_ptr() for q in qs]), arr([q.block_size for q in qs], ctypes.c_int64),
+                 arr([q.outlier_row_ptr.data_ptr() for q in qs]), arr([_lib.ptr(q.outlier_cols) for q in qs]),
+                 arr([_lib.ptr(q.fp16_outliers) for q in qs]), None, None, None, arr([_lib.ptr(b) for b in biases]))
+        # the tuple keeps the weights, biases and codes its addresses point into
+        self._prep = p = (key, K, Ns, fixed, (qs, biases, codes))
+        return p
+
+    def run(self, leader, x):
+        dev = x.device
+        _, K, Ns, fixed, _keep = self._prepare(dev)
+        x2 = x.reshape(-1, K)
+        if not x2.is_contiguous() or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        M = x2.shape[0]
+        buf = torch.empty(M * sum(Ns), dtype=torch.float16, device=dev)
+        ys, off = [], 0
+        for N in Ns:  # each output a contiguous [M, N] piece of one allocation
+            ys.append(buf[off:off + M * N].view(M, N))
+            off += M * N
+        _lib.check(_lib.load().aq_qlinear_grouped(x2.data_ptr(), M, K, *fixed,
+                                                  _lib.ptr_array([y.data_ptr() for y in ys]), None, 0,
+                                                  _lib.stream_of(dev)), "aq_qlinear_grouped")
+        ys = [y.view(*x.shape[:-1], N) for y, N in zip(ys, Ns)]
+        self.x, self.version = x, x._version
+        self.out = {id(m): y for m, y in zip(self.members, ys) if m is not leader}
+        return ys[self.members.index(leader)]
+
+    def take(self, member, x):
+        if self.x is x and x._version == self.version:
+            y = self.out.pop(id(member), None)
+            if not self.out:
+                self.x = None
+            return y
+        return None
+
+
 class QuantizedLinear(nn.Module):
     """A Linear layer that uses a QuantizedTensor for weights."""
 
@@ -138,6 +206,7 @@ class QuantizedLinear(nn.Module):
         # the GEMV call's fixed arguments, valid while device, weight and bias
         # objects stay the same: (device, bias, weight, K, N, entry, args, codes)
         self._prep = None
+        self._group = None  # SiblingGroup this module leads or follows (decode-time grouped launch)
 
     def _weights_on(self, device: torch.device) -> QuantizedTensor:
         q = self.quantized_weights
@@ -152,7 +221,28 @@ class QuantizedLinear(nn.Module):
             self.bias = self.bias.to(device)
         return q
 
+    def _ensure_codes(self, q: QuantizedTensor, dev: torch.device) -> None:
+        if self._derived_from is not q:  # a weight assigned since (q is on dev here)
+            self._derived_from, self._codes, self._tiles = q, None, None
+        if self._codes is None or self._codes.device != dev:
+            self._codes = kernel_codes(q, dev)
+
+    def _grouped_forward(self, x: torch.Tensor) -> Optional[torch.Tensor]:
+        g = self._group
+        y = g.take(self, x)
+        if y is not None:
+            return y
+        if (g.members[0] is self and x.dtype == torch.float16 and x.device.type == "cuda"
+                and 0 < x.numel() < LISTS_MIN_M * x.shape[-1]
+                and all(fused_supported(m.quantized_weights) for m in g.members)):
+            return g.run(self, x)
+        return None
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self._group is not None:
+            y = self._grouped_forward(x)
+            if y is not None:
+                return y
         # decode fast path (M < LISTS_MIN_M rows of x): one library call with
         # the weight's arguments prepared by an earlier forward on this device
         p = self._prep
@@ -183,10 +273,7 @@ class QuantizedLinear(nn.Module):
                                f"in_features {K})")
         if not fused_supported(q):
             return F.linear(x, dequantize_tensor(q, dev), self.bias)
-        if self._derived_from is not q:  # a weight assigned since (q is on dev here)
-            self._derived_from, self._codes, self._tiles = q, None, None
-        if self._codes is None or self._codes.device != dev:
-            self._codes = kernel_codes(q, dev)
+        self._ensure_codes(q, dev)
         if x.numel() >= LISTS_MIN_M * x.shape[-1] and (self._tiles is None or self._tiles[0].device != dev):
             self._tiles = outlier_tiles(q, dev)
         if self._prep is None or self._prep[0] != dev or self._prep[1] is not self.bias or self._prep[2] is not q:

@@ -88,11 +88,13 @@ def find_modules(model: nn.Module, target_types: List[Type], target_names: List[
 
 def apply_atlas_quantization_to_model(model: nn.Module, model_type: str, quantization_config: Dict,
                                       excluded_layers: List[str] = ["lm_head", "embed_tokens", "embeddings"],
-                                      *, device: Optional[torch.device] = None):
+                                      *, device: Optional[torch.device] = None, fuse_siblings: bool = False):
     """Quantize every non-excluded nn.Linear of ``model`` in place
     (reference :95-143).  ``quantization_config`` is splatted into
     quantize_tensor (block_size, z_threshold, code_format).  Returns
-    (layers_replaced, layers_failed)."""
+    (layers_replaced, layers_failed).  ``fuse_siblings`` (not in the
+    reference) links q/k/v and gate/up projections of one parent into a
+    SiblingGroup (see link_sibling_linears)."""
     print(f"\n--- Applying Atlas Quantization ({model_type}) ---")
     patterns = _get_model_patterns(model_type)
     if patterns is None:
@@ -134,5 +136,33 @@ def apply_atlas_quantization_to_model(model: nn.Module, model_type: str, quantiz
             traceback.print_exc()
             failed += 1
     gc.collect()
+    if fuse_siblings:
+        print(f"Linked {link_sibling_linears(model)} sibling groups for grouped decode launches")
     print(f"--- Quantization complete. Replaced: {replaced}, Failed/Skipped: {failed} ---")
     return replaced, failed
+
+
+SIBLING_NAMES = (("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj"))
+
+
+def link_sibling_linears(model: nn.Module, names=SIBLING_NAMES) -> int:
+    """Link the QuantizedLinear children of one parent that a forward calls
+    in turn on the same input (``names``, first member first) into a
+    SiblingGroup: at decode sizes the first one's forward runs one grouped
+    launch and the others take their outputs.  Members must share
+    in_features and code format.  Returns the number of groups linked."""
+    from .atlas_wrappers import SiblingGroup
+    n = 0
+    for parent in model.modules():
+        for group in names:
+            mods = [getattr(parent, c, None) for c in group]
+            if not all(type(m).__name__ == "QuantizedLinear" for m in mods):
+                continue
+            qs = [m.quantized_weights for m in mods]
+            if len({int(q.original_shape[-1]) for q in qs}) != 1 or len({q.code_format for q in qs}) != 1:
+                continue
+            g = SiblingGroup(mods)
+            for m in mods:
+                m._group = g
+            n += 1
+    return n

@@ -149,7 +149,9 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* codes, cons
 __global__ __launch_bounds__(256) void scatter_outliers_kernel(const int64_t* idx, const uint16_t* vals, int64_t nnz,
                                                                int64_t numel, uint16_t* out) {
   const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (p < nnz && idx[p] < numel) out[idx[p]] = vals[p];
+  if (p >= nnz) return;
+  const int64_t j = idx[p];
+  if (j >= 0 && j < numel) out[j] = vals[p];
 }
 
 __device__ __forceinline__ int lower_bound_i32(const int32_t* a, int lo, int hi, int key) {

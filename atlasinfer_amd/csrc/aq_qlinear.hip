@@ -29,6 +29,7 @@
 //    LDS in MFMA operand order, each outlier written over its decoded zero,
 //    loads two 64-wide K chunks ahead.
 #include <algorithm>
+#include <atomic>
 
 #include "aq_common.h"
 #include "aq_qlinear_internal.h"
@@ -1259,15 +1260,20 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, i
   *reinterpret_cast<uint2*>(y + i) = make_uint2(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16));
 }
 
+// CU count of the current device, read once per device.  Any host thread
+// may call this: each slot is an atomic written with the same value by
+// whichever thread gets there first.
 int cu_count() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    int v = 0;
+    n = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0 ? v : 256;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 int log2_exact(int64_t g) {

@@ -232,13 +232,21 @@ class QuantizedLinear(nn.Module):
         y = g.take(self, x)
         if y is not None:
             return y
-        if (g.members[0] is self and x.dtype == torch.float16 and x.device.type == "cuda"
+        # an inference tensor has no version counter, so a kept output could
+        # not be matched to an unmodified input: such inputs compute alone
+        if (g.members[0] is self and not x.is_inference() and x.dtype == torch.float16 and x.device.type == "cuda"
                 and 0 < x.numel() < LISTS_MIN_M * x.shape[-1]
                 and all(fused_supported(m.quantized_weights) for m in g.members)):
             return g.run(self, x)
         return None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if torch.is_grad_enabled() and (x.requires_grad or (self.bias is not None and self.bias.requires_grad)):
+            # the fused kernels record no autograd graph: inputs that need
+            # gradients take the reference's own computation, F.linear on the
+            # dequantized weight (atlas_wrappers.py:56,67), whose backward
+            # reaches x and the bias
+            return self._forward_reference(x)
         if self._group is not None:
             y = self._grouped_forward(x)
             if y is not None:
@@ -260,7 +268,7 @@ class QuantizedLinear(nn.Module):
                 return y.view(*x.shape[:-1], N)
         return self._forward(x)
 
-    def _forward(self, x: torch.Tensor) -> torch.Tensor:
+    def _checked_weights(self, x: torch.Tensor) -> QuantizedTensor:
         dev = x.device
         if dev.type != "cuda":
             raise RuntimeError(f"QuantizedLinear runs on a HIP device; input is on {dev}")
@@ -271,6 +279,16 @@ class QuantizedLinear(nn.Module):
         if x.shape[-1] != K:
             raise RuntimeError(f"mat1 and mat2 shapes cannot be multiplied (input last dim {x.shape[-1]} vs "
                                f"in_features {K})")
+        return q
+
+    def _forward_reference(self, x: torch.Tensor) -> torch.Tensor:
+        q = self._checked_weights(x)
+        return F.linear(x, dequantize_tensor(q, x.device), self.bias)
+
+    def _forward(self, x: torch.Tensor) -> torch.Tensor:
+        dev = x.device
+        q = self._checked_weights(x)
+        K = int(q.original_shape[-1])
         if not fused_supported(q):
             return F.linear(x, dequantize_tensor(q, dev), self.bias)
         self._ensure_codes(q, dev)

@@ -331,7 +331,13 @@ def outlier_tiles(qt: QuantizedTensor, device: torch.device):
     return build_outlier_tiles(qt, device)
 
 
-# --- Dequantization cache (reference :153-154): id(QuantizedTensor) -> fp16 tensor
+# --- Dequantization cache (reference :153-154): id(QuantizedTensor) -> fp16 tensor.
+# Each entry also holds the QuantizedTensor it was computed from: while the
+# entry exists that object stays alive, so its id cannot be handed to another
+# object, and a lookup by id can never return another tensor's weights (the
+# reference, which stores only the fp16 tensor, can: ids are reused after
+# garbage collection).  The reference's API is unchanged: keys are ids, and
+# clear_dequantized_cache(id) / clear_dequantized_cache() drop entries.
 _dequantized_weights_cache = {}
 _cache_lock = threading.Lock()
 
@@ -345,12 +351,12 @@ def dequantize_tensor(quant_data: QuantizedTensor, target_device: torch.device) 
         target_device = torch.device("cuda", torch.cuda.current_device())
     cache_key = id(quant_data)
     with _cache_lock:
-        cached = _dequantized_weights_cache.get(cache_key)
-        if cached is not None and cached.device == target_device:
-            return cached
-        elif cached is not None:
-            cached = cached.to(target_device)
-            _dequantized_weights_cache[cache_key] = cached
+        entry = _dequantized_weights_cache.get(cache_key)
+        if entry is not None and entry[0] is quant_data:
+            cached = entry[1]
+            if cached.device != target_device:
+                cached = cached.to(target_device)
+                _dequantized_weights_cache[cache_key] = (quant_data, cached)
             return cached
 
     numel = quant_data.original_shape.numel()
@@ -372,7 +378,7 @@ def dequantize_tensor(quant_data: QuantizedTensor, target_device: torch.device) 
         final = out.view(q.original_shape).to(target_device)
 
     with _cache_lock:
-        _dequantized_weights_cache[cache_key] = final
+        _dequantized_weights_cache[cache_key] = (quant_data, final)
     return final
 
 

@@ -37,7 +37,7 @@ import torch.nn as nn
 from safetensors import safe_open
 from safetensors.torch import save_file
 
-from .adaptive_quantizer import QuantizedTensor
+from .adaptive_quantizer import QuantizedTensor, tiled_eligible, tiles_eligible
 
 FORMAT_NAME = "atlasinfer_amd.quantized"
 FORMAT_VERSION = 1
@@ -108,12 +108,56 @@ def _check_entry(name: str, q: QuantizedTensor) -> None:
         bad(f"{ncodes} e4m3 codes for {numel} elements")
     if q.code_layout not in ("flat", "tiled"):
         bad(f"code_layout {q.code_layout!r}")
+    if q.code_layout == "tiled" and not tiled_eligible(q.original_shape, G):
+        bad(f"tiled codes for shape {tuple(q.original_shape)} and block {G}")
+    # The index lists drive device reads (the GEMV reads x at each outlier's
+    # column, the dequantize kernel writes at each flat index): every value
+    # is checked here, on the host, before the tensors reach a kernel.
+    idx = q.outlier_indices
+    if nnz and (int(idx[0]) < 0 or int(idx[-1]) >= nblocks * G or (nnz > 1 and not bool((idx[1:] > idx[:-1]).all()))):
+        bad("outlier indices are not ascending inside the padded tensor")
+    K = int(q.original_shape[-1]) if len(q.original_shape) else 1
+    rows = numel // K if K else 0
+    inside = int((idx < rows * K).sum()) if nnz else 0  # outliers in the padding have no row
     if q.outlier_row_ptr is not None:
-        rows = numel // int(q.original_shape[-1]) if len(q.original_shape) and q.original_shape[-1] else 0
-        if q.outlier_row_ptr.numel() != rows + 1:
-            bad("row pointer length")
-        if q.outlier_cols is not None and q.outlier_cols.numel() != nnz:
-            bad("outlier column count")
+        rp = q.outlier_row_ptr
+        if rp.dtype != torch.int32 or rp.numel() != rows + 1:
+            bad("row pointer dtype or length")
+        if int(rp[0]) != 0 or int(rp[-1]) != inside or (rows and not bool((rp[1:] >= rp[:-1]).all())):
+            bad("row pointer is not a CSR pointer over the outliers")
+        if rows and not torch.equal(rp[1:].long() - rp[:-1].long(),
+                                    torch.bincount(idx[:inside] // K, minlength=rows)):
+            bad("row pointer does not match the outlier indices")
+    if q.outlier_cols is not None:
+        if q.outlier_cols.dtype != torch.int32 or q.outlier_cols.numel() != nnz:
+            bad("outlier column dtype or count")
+        if not torch.equal(q.outlier_cols[:inside].long(), idx[:inside] % K):
+            bad("outlier columns do not match the outlier indices")
+    if (q.outlier_tile_ptr is None) != (q.outlier_tile_ent is None):
+        bad("block list pointer and entries must come together")
+    if q.outlier_tile_ptr is not None:
+        if q.outlier_row_ptr is None or q.outlier_cols is None or not tiles_eligible(q.original_shape):
+            bad("block lists without CSR lists or for a shape without 16 x 64 blocks")
+        tp, te = q.outlier_tile_ptr, q.outlier_tile_ent
+        if tp.dtype != torch.int32 or te.dtype != torch.int32:
+            bad("block list dtype")
+        exp_ptr, exp_ent = _block_lists(idx[:inside], q.fp16_outliers[:inside], rows, K)
+        if not torch.equal(tp, exp_ptr) or te.numel() != inside + 64 or not torch.equal(te[:inside], exp_ent):
+            bad("block lists do not match the outliers")
+        if int(q.outlier_tile_max) != (int((tp[1:] - tp[:-1]).max()) if inside else 0):
+            bad(f"outlier_tile_max {q.outlier_tile_max} does not match the block lists")
+
+
+def _block_lists(idx: torch.Tensor, vals: torch.Tensor, N: int, K: int):
+    """The 16 x 64 block lists of aq_outlier_tiles, rebuilt on the host:
+    entry (fp16 value << 16) | r << 6 | k, ordered by block, row, column."""
+    n, c = idx // K, idx % K
+    blk = (n // 16) * (K // 64) + c // 64
+    ent = (vals.view(torch.int16).to(torch.int64) & 0xFFFF) << 16 | (n % 16) << 6 | (c % 64)
+    order = torch.sort(blk, stable=True).indices
+    ptr = torch.searchsorted(blk[order], torch.arange((N // 16) * (K // 64) + 1, dtype=torch.int64))
+    ent = ent[order]
+    return ptr.to(torch.int32), torch.where(ent >= 1 << 31, ent - (1 << 32), ent).to(torch.int32)
 
 
 def load_quantized(path: str, device="cpu") -> Tuple[Dict[str, QuantizedTensor], Dict[str, torch.Tensor]]:

@@ -113,6 +113,26 @@ uint8_t aqo_e4m3_encode(double v) {
   return (uint8_t)(sign | best);
 }
 
+/* The quantizer only ever encodes fp16 values (the fp16 quotient, clamped to
+ * +-448, which is itself an fp16 value), so the exhaustive search above is
+ * run once per fp16 bit pattern and memoised: same results, a table lookup
+ * per element.  Built on first use, single-threaded (aqo_init). */
+static uint8_t g_e4m3_of_f16[65536];
+static int g_e4m3_ready = 0;
+
+void aqo_init(void) {
+  if (g_e4m3_ready) return;
+  for (uint32_t b = 0; b < 65536u; b++) {
+    double v = (double)aqo_h2f((uint16_t)b);
+    if (v == v) {
+      if (v > 448.0) v = 448.0;
+      if (v < -448.0) v = -448.0;
+    }
+    g_e4m3_of_f16[b] = aqo_e4m3_encode(v);
+  }
+  g_e4m3_ready = 1;
+}
+
 /* --------------------------------------------------------- reductions */
 
 static double tree_sum(double* v, int64_t n) { /* n is a power of two */
@@ -188,6 +208,7 @@ void aqo_zscore(const uint16_t* x, int64_t n, float eps, uint16_t* z, uint16_t* 
 int64_t aqo_quantize(const uint16_t* x, int64_t numel, int64_t G, uint16_t thr16, int fmt,
                      uint8_t* codes, uint16_t* scales, uint8_t* outlier, uint16_t* stats) {
   int64_t nblocks = (numel + G - 1) / G;
+  aqo_init();
   double* scratch = (double*)malloc(sizeof(double) * (size_t)next_pow2(G));
   uint16_t* blk = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)G);
   const float qmax = fmt == 0 ? 127.0f : 448.0f;
@@ -235,9 +256,8 @@ int64_t aqo_quantize(const uint16_t* x, int64_t numel, int64_t G, uint16_t thr16
           if (r < -127.0f) r = -127.0f;
           c = (uint8_t)(int8_t)r;
         } else {
-          if (q > 448.0f) q = 448.0f;
-          if (q < -448.0f) q = -448.0f;
-          c = aqo_e4m3_encode((double)q);
+          /* e4m3(clamp(q, +-448)) by the memoised exhaustive search */
+          c = g_e4m3_of_f16[hdiv(blk[i], s16)];
         }
       }
       codes[base + i] = c;

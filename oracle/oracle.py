@@ -20,6 +20,7 @@ module wraps it with numpy and restates the reference's storage layout:
 """
 from __future__ import annotations
 
+import concurrent.futures as cf
 import ctypes
 import os
 import subprocess
@@ -64,6 +65,9 @@ def lib():
         L.aqo_quantize.restype = i64
         L.aqo_dequantize.argtypes = [P, P, i64, i64, ctypes.c_int, P, P, i64, P]
         L.aqo_dequantize.restype = None
+        L.aqo_init.argtypes = []
+        L.aqo_init.restype = None
+        L.aqo_init()  # the memoised E4M3 table, before any threaded call
         _lib = L
     return _lib
 
@@ -79,8 +83,10 @@ def threshold_f16(z_threshold: float) -> np.uint16:
 
 
 def quantize(w: np.ndarray, block_size: int = 128, z_threshold: float = 3.0, fmt: int = FMT_INT8,
-             with_stats: bool = False) -> dict:
-    """Quantize fp16 array ``w`` (any shape) as quantize_tensor does."""
+             with_stats: bool = False, threads: int | None = None) -> dict:
+    """Quantize fp16 array ``w`` (any shape) as quantize_tensor does.  Large
+    inputs are split over up to ``threads`` host threads on block boundaries
+    (results identical to one thread)."""
     x = np.ascontiguousarray(w, dtype=np.float16).reshape(-1).view(np.uint16)
     numel = x.size
     G = int(block_size)
@@ -97,8 +103,24 @@ def quantize(w: np.ndarray, block_size: int = 128, z_threshold: float = 3.0, fmt
     scales = np.zeros(nblocks, np.uint16)
     flags = np.zeros(padded, np.uint8)
     stats = np.zeros(nblocks * 3, np.uint16) if with_stats else None
-    lib().aqo_quantize(_ptr(x), numel, G, int(threshold_f16(z_threshold)), fmt, _ptr(codes),
-                       _ptr(scales), _ptr(flags), _ptr(stats) if stats is not None else None)
+    L = lib()
+    thr = int(threshold_f16(z_threshold))
+
+    def run(b0, b1):
+        # blocks [b0, b1): each block is independent, so disjoint block
+        # ranges can run in parallel threads (ctypes releases the GIL)
+        n = min(numel - b0 * G, (b1 - b0) * G)
+        off = lambda a, k: ctypes.c_void_p(a.ctypes.data + k * a.itemsize)  # noqa: E731
+        L.aqo_quantize(off(x, b0 * G), n, G, thr, fmt, off(codes, b0 * G), off(scales, b0), off(flags, b0 * G),
+                       off(stats, 3 * b0) if stats is not None else None)
+
+    nthreads = max(1, min(threads or (os.cpu_count() or 1), 16, numel // (1 << 18)))
+    if nthreads == 1:
+        run(0, nblocks)
+    else:
+        step = -(-nblocks // nthreads)
+        with cf.ThreadPoolExecutor(nthreads) as ex:
+            list(ex.map(lambda b0: run(b0, min(b0 + step, nblocks)), range(0, nblocks, step)))
     xp = np.zeros(padded, np.uint16)
     xp[:numel] = x
     is_out = flags.astype(bool)

@@ -1,6 +1,6 @@
 """Writes the golden fixtures in this directory from the reference itself.
 
-Run once, in the build container (where the reference is mounted read-only at
+Run in the build container (where the reference is mounted read-only at
 /root/reference):  python tests/golden/make_golden.py
 
 Why an import is needed: the reference's own tests
@@ -93,6 +93,14 @@ def cases():
     # 13-14. bulk: many blocks, to exercise the fp16 mean/std rounding
     out.append(("bulk_g128", weights(g, (256, 512)), 128, 3.0))
     out.append(("bulk_per_row_k1024", weights(g, (128, 1024), outlier_frac=0.01, t_dof=3), 1024, 3.0))
+    # 15-18. rows at the block sizes the product runs (one block per output
+    # channel of the Llama-3-8B shapes: K = 4096 and 14336), normal and
+    # Student-t weights; their own generator, so cases 1-14 stay as they were
+    g2 = torch.Generator().manual_seed(4096)
+    out.append(("per_row_k4096", weights(g2, (8, 4096)), 4096, 3.0))
+    out.append(("per_row_k4096_t3", weights(g2, (8, 4096), outlier_frac=0.01, t_dof=3), 4096, 3.0))
+    out.append(("per_row_k14336", weights(g2, (4, 14336)), 14336, 3.0))
+    out.append(("per_row_k14336_t3", weights(g2, (2, 14336), outlier_frac=0.01, t_dof=3), 14336, 3.0))
     return out
 
 

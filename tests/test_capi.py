@@ -100,3 +100,29 @@ def test_workspace_too_small_is_reported(lib):
     p = ctypes.c_void_p(16)
     assert lib.aq_quantize(p, 4096, 128, 0x4200, 1, 128, 0, p, p, p, p, 16, None) == AQ_EWORKSPACE
     assert b"workspace" in lib.aq_last_error()
+
+
+def integration_stub():
+    """The python block of INTEGRATION.md's reference-side binding section."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    sec = text[text.index("## 3. The reference-side binding"):]
+    m = re.search(r"```python\n(.*?)```", sec, flags=re.S)
+    assert m, "no python block in the binding section"
+    return m.group(1)
+
+
+def test_integration_stub_binds_the_built_library(lib):
+    """The documented ctypes binding, executed as written against the built
+    library (no GPU call is made: only argtypes and the ABI assert run), and
+    every argtypes list it sets equal to the header's signature."""
+    from atlasinfer_amd import _lib
+    src = integration_stub().replace('ctypes.CDLL("libatlasinfer_amd.so")', f"ctypes.CDLL({_lib.LIB_PATH!r})")
+    ns = {}
+    exec(compile(src, "INTEGRATION.md", "exec"), ns)
+    so = ns["_so"]
+    bound = re.findall(r"_so\.(aq_[a-z0-9_]+)\.argtypes", src)
+    assert len(bound) >= 8
+    for name in bound:
+        want = _lib.SIGNATURES[name][1]
+        got = getattr(so, name).argtypes
+        assert [t.__name__ for t in got] == [t.__name__ for t in want], name

@@ -1,10 +1,14 @@
 """QuantizedLinear's decode fast path (arguments prepared once per device,
-weight and bias) gives the same bits as the stateless qlinear call, and
-follows a new bias, a new weight, a device move and every shape of x."""
+weight and bias) gives the same bits as the stateless qlinear call, lies
+within the north-star bounds of F.linear on the oracle's weight, and follows
+a new bias, a new weight, a device move and every shape of x; inputs that
+need gradients take the reference's F.linear path, whose backward reaches
+x and the bias."""
 import numpy as np
 import pytest
 import torch
 
+import gpu_ref as R
 from atlasinfer_core.quant import adaptive_quantizer as AQ
 from integration import atlas_wrappers as AW
 
@@ -12,11 +16,15 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-def _q(seed, N, K, fmt="e4m3", G=-1):
+def _w(seed, N, K):
     g = torch.Generator().manual_seed(seed)
     w = (torch.randn(N, K, generator=g) * 0.02).half()
     w.view(-1)[torch.randperm(N * K, generator=g)[: N * K // 500]] *= 40
-    return AQ.quantize_tensor(w.to(DEV), block_size=G, code_format=fmt)
+    return w
+
+
+def _q(seed, N, K, fmt="e4m3", G=-1):
+    return AQ.quantize_tensor(_w(seed, N, K).to(DEV), block_size=G, code_format=fmt)
 
 
 def test_fast_path_matches_and_tracks_changes():
@@ -28,6 +36,8 @@ def test_fast_path_matches_and_tracks_changes():
     x = torch.randn(3, K, device=DEV).half()
     first = ql(x)                  # prepares the arguments
     assert ql._prep is not None
+    w_ref = R.oracle_reference(q1, _w(1, N, K).numpy(), K, "e4m3")
+    R.assert_close(first, R.reference_linear(x, w_ref, b1), x, w_ref)
     for _ in range(2):             # fast path
         assert torch.equal(ql(x), first)
     assert torch.equal(first, AW.qlinear(x, q1, b1))
@@ -61,3 +71,29 @@ def test_fast_path_after_module_move():
         ql(x.cpu())
     ql.to(DEV)
     assert torch.equal(ql(x), y)
+
+
+def test_inputs_needing_gradients_take_the_reference_path():
+    """x.requires_grad (or a bias that does) under grad mode: y and the
+    gradients are those of F.linear on the dequantized weight, as in the
+    reference (atlas_wrappers.py:67); under no_grad the fused kernel runs."""
+    N, K = 256, 1024
+    q = _q(5, N, K)
+    w_ref = R.oracle_reference(q, _w(5, N, K).numpy(), K, "e4m3")
+    b = torch.randn(N, device=DEV).half()
+    ql = AW.QuantizedLinear(q, b)
+    x = torch.randn(4, K, device=DEV).half().requires_grad_()
+    y = ql(x)
+    assert y.requires_grad and y.grad_fn is not None
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    assert x.grad is not None
+    gx = (dy.double() @ w_ref.double()).to(torch.float16)
+    assert torch.allclose(x.grad.double(), gx.double(), rtol=2e-3, atol=2e-3)
+    R.assert_close(y.detach(), R.reference_linear(x.detach(), w_ref, b), x.detach(), w_ref)
+    bg = b.clone().requires_grad_()
+    ql.bias = bg
+    ql(x.detach()).sum().backward()
+    assert bg.grad is not None and torch.all(bg.grad == 4)
+    with torch.no_grad():
+        assert not ql(x).requires_grad

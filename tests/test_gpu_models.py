@@ -1,0 +1,197 @@
+"""BASELINE configurations 1 and 3 end to end on the GPU: full-size
+random-init HF models with every Linear swapped by
+apply_atlas_quantization_to_model (integration/model_modifier.py:95-143),
+checked against the oracle.
+
+* Each QuantizedLinear's output on the model's own activations (prefill and
+  a decode step) is checked by a forward hook against F.linear on the
+  oracle-pinned weight (float64, north-star bounds plus the per-element
+  bound; tests/gpu_ref.py), on a sample of rows.
+* The logits of the prompt match the same model with every QuantizedLinear
+  computed as F.linear on those weights (the reference's forward,
+  atlas_wrappers.py:56,67) up to the fp16 rounding of 24-32 layers.
+* Greedy generate runs to the requested length.
+
+Config 1: OPT-1.3b (24 layers, hidden 2048, 32 heads, FFN 8192, vocab
+50272), excluded_layers=[] (lm_head quantized too), 32-token prompt, 128 new
+tokens; every weight checked against the oracle in full.  Config 3:
+Mistral-7B (32 layers, hidden 4096, 32 / 8 heads, FFN 14336, vocab 32000,
+RoPE 1e6), 512-token prompts at batch 1, 8 and 32; weights checked against
+the oracle on row slices (one whole tile row of 16 plus 3 single rows per
+weight; the full-weight checks of these shapes are in test_gpu_configs.py),
+reference weights from the torch restatement of dequantize_tensor.
+Weights: the HF init (N(0, 0.02)) with 0.1 % of each Linear's entries
+replaced by +-U(8, 20) * 0.02, as in BASELINE config 0.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+import gpu_ref as R
+
+pytestmark = pytest.mark.gpu
+DEV = R.DEV
+QCFG = {"block_size": -1, "z_threshold": 3.0, "code_format": "e4m3"}
+
+
+def plant_outliers(model, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    with torch.no_grad():
+        for m in model.modules():
+            if isinstance(m, nn.Linear):
+                w = m.weight.view(-1)
+                k = int(round(0.001 * w.numel()))
+                pos = torch.randperm(w.numel(), generator=g, device=DEV)[:k]
+                sign = torch.where(torch.rand(k, generator=g, device=DEV) < 0.5, -1.0, 1.0)
+                w[pos] = (sign * (torch.rand(k, generator=g, device=DEV) * 12 + 8) * 0.02).to(w.dtype)
+
+
+def sample_rows(M, n=16):
+    """Rows of x checked by the hooks: first, last and evenly spaced."""
+    return sorted(set(np.linspace(0, M - 1, min(n, M)).round().astype(int).tolist()))
+
+
+class LayerChecks:
+    """Forward hooks asserting every QuantizedLinear's output against
+    F.linear(x, w_ref, b) in float64 on sampled rows."""
+
+    def __init__(self, model, w_refs):
+        self.n = 0
+        self.handles = []
+        for name, m in model.named_modules():
+            if type(m).__name__ == "QuantizedLinear":
+                self.handles.append(m.register_forward_hook(self._hook(w_refs[name])))
+
+    def _hook(self, w_ref):
+        def hook(mod, inp, out):
+            x = inp[0].reshape(-1, w_ref.shape[1])
+            y = out.reshape(-1, w_ref.shape[0])
+            rows = torch.tensor(sample_rows(x.shape[0]), device=x.device)
+            xs = x.index_select(0, rows)
+            R.assert_close(y.index_select(0, rows), R.reference_linear(xs, w_ref, mod.bias), xs, w_ref)
+            self.n += 1
+        return hook
+
+    def remove(self):
+        for h in self.handles:
+            h.remove()
+
+
+def reference_logits(model, w_refs, **kw):
+    """Logits of the same model with every QuantizedLinear computed as
+    F.linear on its reference weight."""
+    from integration import atlas_wrappers as AW
+    by_module = {m: w_refs[n] for n, m in model.named_modules() if type(m).__name__ == "QuantizedLinear"}
+    saved = AW.QuantizedLinear.forward
+    AW.QuantizedLinear.forward = lambda self, x: F.linear(x, by_module[self], self.bias)
+    try:
+        return model(**kw).logits
+    finally:
+        AW.QuantizedLinear.forward = saved
+
+
+def rel_l2(a, b):
+    return ((a.double() - b.double()).norm() / b.double().norm()).item()
+
+
+def swap(model, model_type, excluded, full_oracle):
+    """Quantize every Linear (weights recorded first) and build each one's
+    reference weight, checked against the oracle in full or on row slices."""
+    from integration.model_modifier import apply_atlas_quantization_to_model
+    rng = np.random.default_rng(0)
+    kept, slices = {}, {}
+    for name, m in model.named_modules():
+        if isinstance(m, nn.Linear) and not any(e in name for e in excluded):
+            N = m.out_features
+            if full_oracle:
+                kept[name] = m.weight.detach().cpu().numpy()
+            else:
+                rb = int(rng.integers(0, N // 16))
+                rows = list(range(16 * rb, 16 * rb + 16)) + [0, int(rng.integers(0, N)), N - 1]
+                rows = sorted(set(rows))
+                slices[name] = (rows, m.weight.detach()[rows].cpu().numpy())
+    rep, fail = apply_atlas_quantization_to_model(model, model_type, QCFG, excluded_layers=excluded)
+    assert fail == 0
+    w_refs = {}
+    for name, m in model.named_modules():
+        if type(m).__name__ != "QuantizedLinear":
+            continue
+        q = m.quantized_weights
+        N, K = q.original_shape
+        if full_oracle:
+            w_refs[name] = R.oracle_reference(q, kept.pop(name), K, "e4m3")
+        else:
+            rows, w_rows = slices[name]
+            full = np.zeros((N, K), np.float16)  # only the checked rows are read
+            full[rows] = w_rows
+            R.assert_matches_oracle(q, full, K, "e4m3", rows=rows)
+            w_refs[name] = R.torch_dequant(q, N, K)
+    return rep, w_refs
+
+
+def test_config1_opt_1_3b_full_swap_generate():
+    transformers = pytest.importorskip("transformers")
+    cfg = transformers.OPTConfig(num_hidden_layers=24, hidden_size=2048, num_attention_heads=32, ffn_dim=8192,
+                                 vocab_size=50272, max_position_embeddings=2048, word_embed_proj_dim=2048)
+    torch.manual_seed(0)
+    with torch.device(DEV):
+        model = transformers.OPTForCausalLM(cfg).half().eval()
+    plant_outliers(model, 1)
+    rep, w_refs = swap(model, "opt", [], full_oracle=True)
+    assert rep == 24 * 6 + 1  # every Linear, lm_head included
+    assert type(model.lm_head).__name__ == "QuantizedLinear"
+    g = torch.Generator(device=DEV).manual_seed(3)
+    ids = torch.randint(0, cfg.vocab_size, (1, 32), generator=g, device=DEV)
+    with torch.no_grad():
+        checks = LayerChecks(model, w_refs)
+        logits = model(input_ids=ids).logits          # prompt: M = 32
+        model(input_ids=ids[:, :1])                   # one token: M = 1
+        checks.remove()
+        assert checks.n == 2 * rep
+        ref = reference_logits(model, w_refs, input_ids=ids)
+        rel = rel_l2(logits, ref)
+        print(f"OPT-1.3b logits rel-L2 vs F.linear on oracle weights: {rel:.2e}")
+        assert rel < 5e-3, rel
+        out = model.generate(ids, max_new_tokens=128, min_new_tokens=128, do_sample=False, pad_token_id=0)
+    assert out.shape == (1, 160)
+    assert torch.equal(out[:, :32], ids)
+
+
+@pytest.fixture(scope="module")
+def mistral():
+    transformers = pytest.importorskip("transformers")
+    cfg = transformers.MistralConfig(num_hidden_layers=32, hidden_size=4096, num_attention_heads=32,
+                                     num_key_value_heads=8, head_dim=128, intermediate_size=14336, vocab_size=32000,
+                                     rope_theta=1e6, max_position_embeddings=4096)
+    torch.manual_seed(0)
+    with torch.device(DEV):
+        model = transformers.MistralForCausalLM(cfg).half().eval()
+    plant_outliers(model, 2)
+    rep, w_refs = swap(model, "mistral", ["lm_head", "embed_tokens", "embeddings"], full_oracle=False)
+    assert rep == 32 * 7
+    yield cfg, model, rep, w_refs
+    del model, w_refs
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("B", [1, 8, 32])
+def test_config3_mistral_7b(mistral, B):
+    cfg, model, rep, w_refs = mistral
+    g = torch.Generator(device=DEV).manual_seed(10 + B)
+    ids = torch.randint(0, cfg.vocab_size, (B, 512), generator=g, device=DEV)
+    with torch.no_grad():
+        checks = LayerChecks(model, w_refs)
+        out = model(input_ids=ids, use_cache=True)          # prefill: M = 512 B
+        nxt = out.logits[:, -1:].argmax(-1)
+        model(input_ids=nxt, past_key_values=out.past_key_values, use_cache=True)  # decode step: M = B
+        checks.remove()
+        assert checks.n == 2 * rep
+        ref = reference_logits(model, w_refs, input_ids=ids)
+        rel = rel_l2(out.logits, ref)
+        print(f"Mistral-7B batch {B} logits rel-L2 vs F.linear on reference weights: {rel:.2e}")
+        assert rel < 5e-3, rel
+        del out, ref
+        gen = model.generate(ids, max_new_tokens=8, min_new_tokens=8, do_sample=False, pad_token_id=0)
+    assert gen.shape == (B, 520)

@@ -4,15 +4,19 @@ CPU oracle on the same seeded inputs.
 Bit-exact: codes, scales, outlier indices/values, dequantized weights,
 z-scores.  Tolerance (north star): layer outputs within
 max|dy| <= 2e-3 * max|x| * max|w| and ||dy||_2 / ||y||_2 <= 1e-3 of
-F.linear(x, dequantize_tensor(W), b) computed in float64.
+F.linear(x, W, b) computed in float64, W the oracle's dequantized weight
+after the GPU's quantized tensor matched the oracle bit for bit
+(tests/gpu_ref.py).
 """
 import numpy as np
 import pytest
 import torch
 
+import gpu_ref as R
 from atlasinfer_amd import _lib
 from atlasinfer_core.quant import adaptive_quantizer as AQ
 from conftest import golden_cases
+from gpu_ref import assert_close, bits, make_weights, reference_linear, tile_np
 from integration import atlas_wrappers as AW
 
 pytestmark = pytest.mark.gpu
@@ -20,28 +24,12 @@ DEV = "cuda:0"
 CASES = golden_cases()
 
 
-def bits(t):
-    if isinstance(t, torch.Tensor):
-        t = t.detach().cpu()
-        return t.view(torch.uint8).numpy() if t.element_size() == 1 else t.view(torch.int16).numpy().view(np.uint16)
-    return t.view(np.uint8) if t.dtype.itemsize == 1 else t.view(np.uint16)
-
-
-def tile_np(flat_codes, N, K):
-    """The tiled code layout restated with numpy reshapes: element (n, k) with
-    n = 16 rb + r, k = 128 c + 64 h + 16 g + e goes to tile (rb, c), byte
-    h*1024 + g*256 + r*16 + e."""
-    a = np.asarray(flat_codes, np.uint8).reshape(N // 16, 16, K // 128, 2, 4, 16)  # rb r c h g e
-    return np.ascontiguousarray(a.transpose(0, 2, 3, 4, 1, 5)).reshape(-1)
-
-
-def make_weights(rng, shape, sigma=0.02, frac=0.001, t_dof=None):
-    n = int(np.prod(shape))
-    w = rng.standard_t(t_dof, n) * sigma if t_dof else rng.standard_normal(n) * sigma
-    k = int(round(frac * n))
-    pos = rng.permutation(n)[:k]
-    w[pos] = rng.choice([-1.0, 1.0], k) * rng.uniform(8, 20, k) * sigma
-    return w.reshape(shape).astype(np.float16)
+def oref(q, w):
+    """The oracle's reference weight for GPU tensor ``q`` of weight ``w``
+    (bit-exact check of q against the oracle first; tests/gpu_ref.py)."""
+    K = int(q.original_shape[-1])
+    w16 = np.asarray(w).astype(np.float16).reshape(-1, K)
+    return R.oracle_reference(q, w16, q.block_size, q.code_format)
 
 
 @pytest.mark.parametrize("name,d", CASES, ids=[c[0] for c in CASES])
@@ -161,34 +149,6 @@ def test_compact_expand_round_trip():
     assert torch.all(dense[~mask] == 0)
 
 
-def reference_linear(x, w_deq, bias):
-    y = x.double() @ w_deq.double().t()
-    if bias is not None:
-        y = y + bias.double()
-    return y
-
-
-def fp16_ulp(v):
-    a = v.abs().clamp(min=2.0 ** -14)
-    return torch.exp2(torch.floor(torch.log2(a)) - 10)
-
-
-def assert_close(y, yref, x, w):
-    """North-star tolerance, plus a per-element bound: one fp16 ulp of the
-    exact result (the output rounding) plus the worst-case fp32 accumulation
-    error over the row, 2^-20 * sum_k |x_k| |w_nk|."""
-    d = (y.double() - yref).abs()
-    bound = 2e-3 * x.abs().max().double() * w.abs().max().double()
-    assert d.max() <= bound, (d.max().item(), bound.item())
-    rel = (y.double() - yref).norm() / yref.norm()
-    assert rel <= 1e-3, rel.item()
-    x2 = x.reshape(-1, x.shape[-1]).double().abs()
-    acc = (x2 @ w.double().abs().t()).reshape(yref.shape)
-    strict = fp16_ulp(yref) + 2.0 ** -20 * acc
-    worst = (d / strict).max().item()
-    assert worst <= 1.0, worst
-
-
 @pytest.mark.parametrize("M", [1, 2, 4, 5, 6, 8, 12, 16, 17, 33, 64, 65, 300])
 @pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128), ("e4m3", 64)])
 def test_qlinear_matches_reference_linear(M, fmt, G):
@@ -200,28 +160,12 @@ def test_qlinear_matches_reference_linear(M, fmt, G):
     x = torch.from_numpy(xs.astype(np.float16)).to(DEV)
     b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(DEV)
     q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=G, code_format=fmt)
-    AQ.clear_dequantized_cache()
-    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    w_deq = oref(q, w)
     for bias in (None, b):
         layer = AW.QuantizedLinear(q, bias)
         y = layer(x)
         assert y.shape == (M, N) and y.dtype == torch.float16
         assert_close(y, reference_linear(x, w_deq, bias), x, w_deq)
-
-
-@pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (4096, 14336), (14336, 4096)])
-@pytest.mark.parametrize("M", [1, 16, 40, 64, 512, 2048])
-def test_qlinear_llama_shapes(N, K, M):
-    rng = np.random.default_rng(N + K + M)
-    w = make_weights(rng, (N, K))
-    xs = rng.standard_normal((M, K)).astype(np.float32)
-    xs[:, rng.permutation(K)[:4]] *= 30  # BASELINE config 2 activations
-    x = torch.from_numpy(xs.astype(np.float16)).to(DEV)
-    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, code_format="e4m3")
-    AQ.clear_dequantized_cache()
-    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
-    y = AW.QuantizedLinear(q, None)(x)
-    assert_close(y, reference_linear(x, w_deq, None), x, w_deq)
 
 
 @pytest.mark.parametrize("N,K", [(1040, 640), (6160, 384), (12304, 384)])
@@ -237,8 +181,7 @@ def test_gemv_shared_x_ragged_shapes(N, K, M, fmt, G):
     x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)
     b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(DEV)
     q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=G, code_format=fmt)
-    AQ.clear_dequantized_cache()
-    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    w_deq = oref(q, w)
     y = AW.QuantizedLinear(q, b)(x)
     assert_close(y, reference_linear(x, w_deq, b), x, w_deq)
 
@@ -253,8 +196,7 @@ def test_gemm_split_k_matches_unsplit(M, N, K):
     x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)
     b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(DEV)
     q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, code_format="e4m3")
-    AQ.clear_dequantized_cache()
-    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    w_deq = oref(q, w)
     L = _lib.load()
     codes = AQ.kernel_codes(q, torch.device(DEV))
     tp, te, tmax = AQ.outlier_tiles(q, torch.device(DEV))
@@ -290,8 +232,7 @@ def test_short_grid_gemm_and_gemv_agree_with_reference(M, fmt, G):
     x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)
     b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(DEV)
     q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=G, code_format=fmt)
-    AQ.clear_dequantized_cache()
-    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    w_deq = oref(q, w)
     L = _lib.load()
     ref = reference_linear(x, w_deq, b)
     y_gemm = AW.qlinear(x, q, b)
@@ -311,8 +252,7 @@ def test_qlinear_heavy_outliers_and_3d_input():
     q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=128, code_format="int8")
     x = torch.from_numpy(rng.standard_normal((2, 3, 1024)).astype(np.float16)).to(DEV)
     b = torch.from_numpy(rng.standard_normal(512).astype(np.float16)).to(DEV)
-    AQ.clear_dequantized_cache()
-    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    w_deq = oref(q, w)
     y = AW.QuantizedLinear(q, b)(x)
     assert y.shape == (2, 3, 512)
     yref = reference_linear(x.reshape(-1, 1024), w_deq, b).reshape(2, 3, 512)
@@ -368,8 +308,7 @@ def test_gemm_crowded_outlier_blocks(M):
     # the N(0, 0.02) background adds a few outliers of its own
     assert counts[0, 0] >= 48 and counts[3, 15] >= 32 and counts[1, 5] >= 16 and counts[5, 9] >= 1
     x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)
-    AQ.clear_dequantized_cache()
-    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    w_deq = oref(q, w)
     assert_close(AW.QuantizedLinear(q, None)(x), reference_linear(x, w_deq, None), x, w_deq)
 
 
@@ -386,8 +325,7 @@ def test_gemm_tile_shapes(M, N):
     xs[:, rng.permutation(K)[:4]] *= 30
     x = torch.from_numpy(xs.astype(np.float16)).to(DEV)
     b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(DEV)
-    AQ.clear_dequantized_cache()
-    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    w_deq = oref(q, w)
     assert_close(AW.QuantizedLinear(q, b)(x), reference_linear(x, w_deq, b), x, w_deq)
 
 
@@ -408,8 +346,7 @@ def test_gemm_wide_tiles(fmt, G, M, N, K):
     xs[:, rng.permutation(K)[:4]] *= 30
     x = torch.from_numpy(xs.astype(np.float16)).to(DEV)
     b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(DEV)
-    AQ.clear_dequantized_cache()
-    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    w_deq = oref(q, w)
     assert_close(AW.QuantizedLinear(q, b)(x), reference_linear(x, w_deq, b), x, w_deq)
 
 
@@ -422,8 +359,7 @@ def test_gemm_dense_outliers_long_rows():
     q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, code_format="e4m3")
     assert q.outlier_indices.numel() > 0.015 * N * K
     x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)
-    AQ.clear_dequantized_cache()
-    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    w_deq = oref(q, w)
     assert_close(AW.QuantizedLinear(q, None)(x), reference_linear(x, w_deq, None), x, w_deq)
 
 
@@ -433,8 +369,7 @@ def test_qlinear_fallback_for_ragged_blocks():
     w = make_weights(rng, (64, 1000))
     q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=100, code_format="e4m3")
     x = torch.from_numpy(rng.standard_normal((5, 1000)).astype(np.float16)).to(DEV)
-    AQ.clear_dequantized_cache()
-    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    w_deq = oref(q, w)
     assert_close(AW.QuantizedLinear(q, None)(x), reference_linear(x, w_deq, None), x, w_deq)
 
 
@@ -467,16 +402,17 @@ def test_model_swap_tiny_opt():
     torch.manual_seed(0)
     model = transformers.OPTForCausalLM(cfg).half().to(DEV).eval()
     ids = torch.randint(0, 256, (1, 12), device=DEV)
+    before = {n: m.weight.detach().cpu().numpy() for n, m in model.named_modules()
+              if isinstance(m, torch.nn.Linear) and n != "lm_head"}
     replaced, failed = apply_atlas_quantization_to_model(model, "opt", {"block_size": -1, "z_threshold": 3.0})
     assert (replaced, failed) == (12, 0)
-    qlin = [m for m in model.modules() if type(m).__name__ == "QuantizedLinear"]
-    assert len(qlin) == 12
+    qlin = {n: m for n, m in model.named_modules() if type(m).__name__ == "QuantizedLinear"}
+    assert sorted(qlin) == sorted(before)
     with torch.no_grad():
         logits = model(ids).logits
-        # same model with every QuantizedLinear computed as F.linear on the dequantized weight
-        for m in qlin:
-            AQ.clear_dequantized_cache()
-            m._ref_w = AQ.dequantize_tensor(m.quantized_weights, torch.device(DEV)).clone()
+        # same model with every QuantizedLinear computed as F.linear on the oracle's weight
+        for n, m in qlin.items():
+            m._ref_w = oref(m.quantized_weights, before[n])
         saved = AW.QuantizedLinear.forward
         AW.QuantizedLinear.forward = lambda self, x: torch.nn.functional.linear(x, self._ref_w, self.bias)
         try:
@@ -610,14 +546,13 @@ def test_tile_untile_round_trip():
 def test_grouped_launch_matches_single_calls(M):
     rng = np.random.default_rng(M)
     K = 1024
-    qts = [AQ.quantize_tensor(torch.from_numpy(make_weights(rng, (N, K))).to(DEV), block_size=-1)
-           for N in (512, 128, 128)]
+    ws = [make_weights(rng, (N, K)) for N in (512, 128, 128)]
+    qts = [AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1) for w in ws]
     bias = [None, torch.from_numpy(rng.standard_normal(128).astype(np.float16)).to(DEV), None]
     x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)
     ys = AW.qlinear_grouped(x, qts, bias)
-    for q, b, y in zip(qts, bias, ys):
-        AQ.clear_dequantized_cache()
-        w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    for q, w, b, y in zip(qts, ws, bias, ys):
+        w_deq = oref(q, w)
         assert_close(y, reference_linear(x, w_deq, b), x, w_deq)
         assert torch.allclose(y, AW.QuantizedLinear(q, b)(x), rtol=2e-3, atol=1e-3)
 
@@ -630,6 +565,5 @@ def test_int8_weights_run_through_tiled_kernels():
     q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=128, code_format="int8")
     assert q.code_layout == "flat"
     x = torch.from_numpy(rng.standard_normal((3, 512)).astype(np.float16)).to(DEV)
-    AQ.clear_dequantized_cache()
-    w_deq = AQ.dequantize_tensor(q, torch.device(DEV))
+    w_deq = oref(q, w)
     assert_close(AW.QuantizedLinear(q, None)(x), reference_linear(x, w_deq, None), x, w_deq)

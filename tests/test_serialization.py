@@ -68,21 +68,82 @@ def test_round_trip_fields(tmp_path, oracle, fmt, G):
     assert torch.equal(extra["a.bias"], bias)
 
 
+def consistent_tiled_qt(seed=0, N=32, K=256, nnz=40):
+    """A tiled e4m3 QuantizedTensor with random codes and outliers whose CSR
+    and 16 x 64 block lists agree with the flat indices."""
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.sort(torch.randperm(N * K, generator=g)[:nnz]).values
+    vals = torch.randn(nnz, generator=g).half()
+    row_ptr = torch.zeros(N + 1, dtype=torch.int32)
+    row_ptr[1:] = torch.cumsum(torch.bincount(idx // K, minlength=N), 0).to(torch.int32)
+    tp, te = S._block_lists(idx, vals, N, K)
+    return AQ.QuantizedTensor(torch.randint(0, 255, (N * K,), dtype=torch.uint8, generator=g).view(torch.float8_e4m3fn),
+                              vals, idx, torch.rand(N, generator=g).half(), torch.Size([N, K]), K, "e4m3",
+                              row_ptr, (idx % K).to(torch.int32), "tiled", tp,
+                              torch.cat([te, torch.zeros(64, dtype=torch.int32)]), int((tp[1:] - tp[:-1]).max()))
+
+
 def test_round_trip_tiled_and_block_lists(tmp_path):
     """Every optional field (tiled codes, 16 x 64 block lists) survives."""
-    g = torch.Generator().manual_seed(0)
-    N, K, nnz = 32, 256, 5
-    q = AQ.QuantizedTensor(torch.randint(0, 255, (N * K,), dtype=torch.uint8, generator=g).view(torch.float8_e4m3fn),
-                           torch.randn(nnz, generator=g).half(), torch.arange(nnz, dtype=torch.int64) * 97,
-                           torch.rand(N, generator=g).half(), torch.Size([N, K]), K, "e4m3",
-                           torch.zeros(N + 1, dtype=torch.int32), torch.arange(nnz, dtype=torch.int32), "tiled",
-                           torch.arange((N // 16) * (K // 64) + 1, dtype=torch.int32),
-                           torch.arange(nnz + 64, dtype=torch.int32), 3)
+    q = consistent_tiled_qt()
     p = str(tmp_path / "t.safetensors")
     S.save_quantized({"w": q}, p)
     got, extra = S.load_quantized(p)
     same_qt(q, got["w"])
     assert extra == {}
+
+
+def test_block_lists_match_expected_tiles_restatement():
+    """_block_lists (the loader's check) against the numpy restatement the
+    GPU tests use for aq_outlier_tiles."""
+    q = consistent_tiled_qt(3, 48, 384, 300)
+    N, K = 48, 384
+    idx = q.outlier_indices.numpy()
+    vals = q.fp16_outliers.numpy().view(np.uint16).astype(np.uint32)
+    n, c = idx // K, idx % K
+    blk = (n // 16) * (K // 64) + c // 64
+    ent = (vals << 16) | (n % 16).astype(np.uint32) << 6 | (c % 64).astype(np.uint32)
+    order = np.argsort(blk, kind="stable")
+    ptr = np.searchsorted(blk[order], np.arange((N // 16) * (K // 64) + 1))
+    assert np.array_equal(q.outlier_tile_ptr.numpy(), ptr)
+    assert np.array_equal(q.outlier_tile_ent[:300].numpy().view(np.uint32), ent[order])
+
+
+CORRUPTIONS = [
+    # (field, how to corrupt it, message)
+    ("outlier_row_ptr", lambda t: t.flip(0).contiguous(), "CSR pointer"),
+    ("outlier_row_ptr", lambda t: t.to(torch.int64), "row pointer dtype"),
+    ("outlier_row_ptr", lambda t: torch.cat([t[:1], t[2:], t[-1:]]), "does not match"),
+    ("outlier_cols", lambda t: t + 300, "columns do not match"),
+    ("outlier_cols", lambda t: t - 1000, "columns do not match"),
+    ("outlier_indices", lambda t: t.flip(0).contiguous(), "ascending"),
+    ("outlier_indices", lambda t: torch.cat([t[:-1], t[-1:] + (1 << 20)]), "ascending"),
+    ("outlier_indices", lambda t: torch.cat([-t[:1] - 1, t[1:]]), "ascending"),
+    ("outlier_tile_ptr", lambda t: torch.cat([t[:-1], t[-1:] - 1]), "block lists"),
+    ("outlier_tile_ent", lambda t: torch.cat([t[:5] ^ 1, t[5:]]), "block lists"),
+    ("outlier_tile_ent", lambda t: t[:-1].contiguous(), "block lists"),
+]
+
+
+@pytest.mark.parametrize("field,corrupt,match", CORRUPTIONS)
+def test_corrupted_index_lists_rejected(tmp_path, field, corrupt, match):
+    """Index lists that would drive out-of-range or wrong device reads are
+    caught on the host before any tensor moves to a device."""
+    q = consistent_tiled_qt(1)
+    q = q._replace(**{field: corrupt(getattr(q, field))})
+    p = str(tmp_path / "c.safetensors")
+    S.save_quantized({"w": q}, p)
+    with pytest.raises(ValueError, match=match):
+        S.load_quantized(p)
+
+
+def test_understated_tile_max_rejected(tmp_path):
+    q = consistent_tiled_qt(2)
+    q = q._replace(outlier_tile_max=q.outlier_tile_max - 1)
+    p = str(tmp_path / "m.safetensors")
+    S.save_quantized({"w": q}, p)
+    with pytest.raises(ValueError, match="outlier_tile_max"):
+        S.load_quantized(p)
 
 
 def test_empty_tensor_round_trip(tmp_path):

@@ -114,7 +114,81 @@ def cpu_baseline(layer_w_cpu, budget_s=12.0):
     return passes, dt, torch.get_num_threads()
 
 
+def cpu_reference_extras(w_gate_cpu, x2048_cpu, budget_s):
+    """The reference's other CPU costs on this host, each time-boxed to about
+    ``budget_s`` and labelled as extrapolated where it is:
+    * the per-block quantize loop (adaptive_quantizer.py:102-133) on the
+      first blocks of gate_proj [14336, 4096], at the reference's default
+      block of 128 and per output channel (block 4096); linear in blocks,
+      so the whole-weight time is blocks x time per block;
+    * the per-block dequantize loop (:188-239) on the same weight's int8
+      tensor at block 128, with the weight's full outlier list (its mask
+      over all outliers per block is what makes it O(blocks x nnz)): time
+      per block x blocks;
+    * warm F.linear (atlas_wrappers.py:67) at M = 2048 on gate_proj.
+    Quantize bytes per element: 2 read + 1 code + 2 / G scale, as the GPU
+    figure counts them."""
+    from oracle import ref_loop
+    out = {}
+    N, K = w_gate_cpu.shape
+    for G in (128, 4096):
+        ref_loop.quantize_loop(w_gate_cpu, G, 3.0, max_blocks=4)
+        t0 = time.perf_counter()
+        n = 0
+        step = 64 if G == 128 else 8
+        total = N * K // G
+        while time.perf_counter() - t0 < budget_s:
+            b0 = n % (total - step)  # wraps on a host fast enough to reach the end
+            ref_loop.quantize_loop(w_gate_cpu.view(-1)[b0 * G:(b0 + step) * G], G, 3.0)
+            n += step
+        dt = time.perf_counter() - t0
+        per = dt / n
+        out[f"quantize_loop_g{G}"] = {
+            "blocks_timed": n, "s_per_block": per, "GBps": round(n * (3 * G + 2) / dt / 1e9, 6),
+            "extrapolated_s_whole_weight": round(per * total, 1),
+            "note": f"gate_proj [{N}, {K}], block {G}: {n} blocks timed, whole weight extrapolated linearly"}
+    from atlasinfer_amd.quant import adaptive_quantizer as AQ
+    q = AQ.quantize_tensor(w_gate_cpu.to("cuda"), block_size=128, code_format="int8")
+    codes, outs, idx, sc = (q.fp8_data.cpu(), q.fp16_outliers.cpu(), q.outlier_indices.cpu(), q.scale_factors.cpu())
+    ref_loop.dequantize_loop(codes, outs, idx, sc, N * K, 128, max_blocks=2)
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < budget_s:
+        n += ref_loop.dequantize_loop(codes, outs, idx, sc, N * K, 128, max_blocks=n + 16)[1] - n
+    dt = time.perf_counter() - t0
+    per = dt / n
+    out["dequantize_loop_g128"] = {
+        "blocks_timed": n, "s_per_block": per, "nnz": int(idx.numel()),
+        "extrapolated_s_whole_weight": round(per * (N * K // 128), 1),
+        "note": "gate_proj int8 block 128, per-block loop with the full outlier list; whole weight extrapolated"}
+    ref_loop.forward_warm(x2048_cpu[:8], w_gate_cpu)
+    t0 = time.perf_counter()
+    n = 0
+    while n == 0 or time.perf_counter() - t0 < budget_s:
+        ref_loop.forward_warm(x2048_cpu, w_gate_cpu)
+        n += 1
+    dt = time.perf_counter() - t0
+    out["forward_warm_m2048"] = {"calls": n, "TFLOPs": round(2 * x2048_cpu.shape[0] * N * K * n / dt / 1e12, 4),
+                                 "note": f"F.linear fp16 [2048, {K}] x [{N}, {K}]^T on the host cores"}
+    return out
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qlinear_gemv_gateup_llama3_8b_m1_traffic.txt")
+TRACE_FILE = os.path.join(ROOT, "profiles", "bench_llama3_8b_kernel_trace.txt")
+
+
+def profiled_us_per_launch():
+    """rocprof's kernel-only average duration of the dominant kernel from the
+    committed kernel-trace summary (line ``dominant_kernel_rocprof_avg_us:``),
+    or None."""
+    try:
+        with open(TRACE_FILE) as f:
+            for line in f:
+                if line.startswith("dominant_kernel_rocprof_avg_us:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def time_quantize_kernel(weights, reps=5):
@@ -410,8 +484,9 @@ def main():
     ap.add_argument("--sweep", action="store_true", help="also time M in {4,16,32,64,512} per shape")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
-    ap.add_argument("--models", default="", help="comma list of opt,mistral: also run BASELINE configs 1 / 3 "
-                                                  "(HF generate on random-init models; a few minutes)")
+    ap.add_argument("--models", default="opt", help="comma list of opt,mistral (or none): BASELINE configs 1 / 3 "
+                                                     "(HF generate on random-init models; opt takes about half a "
+                                                     "minute, mistral a few minutes)")
     ap.add_argument("--config4", action="store_true",
                     help="also run BASELINE config 4: quantize kernel over a full 8B Llama-3-shaped weight set "
                          "(Student-t(3), 1%% outliers) and the Gemma-2B lm_head / FFN at M = 1 and 2048 "
@@ -582,13 +657,14 @@ def main():
     config4 = bench_config4(dev, gen, log, qlinear) if args.config4 else None
 
     models = None
-    if args.models:
+    if args.models and args.models != "none":
         import contextlib
         with contextlib.redirect_stdout(sys.stderr):  # stdout carries only the result line
             models = bench_models(dev, args.models.split(","), log)
 
     # ---- the reference's CPU path on this host (warm F.linear, M=1)
     cpu = None
+    cpu_extra = None
     if not args.no_cpu:
         w_cpu = {name: keep_fp16[name].cpu() for name, _, _ in LLAMA_LINEARS}
         passes, dt, threads = cpu_baseline(w_cpu, args.cpu_budget)
@@ -596,7 +672,11 @@ def main():
         cpu = {"value": round(cpu_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
                "sample": f"{passes} passes of the 7 Llama-3-8B linears at M=1, F.linear on the cached fp16 "
                          f"weights (reference steady state, atlas_wrappers.py:67), {dt:.1f} s"}
+        cpu_extra = cpu_reference_extras(w_cpu["gate_proj"], xg[4096].cpu(), args.cpu_budget / 3)
+        cpu_extra["cores"] = threads
+        log(f"CPU reference loops: {json.dumps(cpu_extra)}")
 
+    prof_us = profiled_us_per_launch()
     result = {
         "metric": "dequant-GEMM GB/s @M=1 & TFLOP/s @M=2048 (Llama-3-8B linears); decode tok/s",
         "value": round(value, 1),
@@ -616,7 +696,12 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "qlinear_gemv_kernel (one wave per 16-row tile, E4M3, per-channel): gate+up grouped, 2x[14336,4096], M=1",
-                     "algorithmic_bytes_per_launch": dom_bytes, "us_per_launch": round(1e6 * dom_s, 3)},
+                     "algorithmic_bytes_per_launch": dom_bytes, "us_per_launch": round(1e6 * dom_s, 3),
+                     "timing": "HIP events on the launch stream around graph replays (includes the gap between "
+                               "dispatches); rocprof's kernel-only average from profiles/ beside it",
+                     "rocprof_us_per_launch": prof_us,
+                     "rocprof_frac": (round(dom_bytes / (prof_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                                      if prof_us else None)},
         "cpu_baseline": cpu,
         "extra": {
             "gemm_m2048_tflops": round(gemm_tflops, 1),
@@ -637,6 +722,7 @@ def main():
             "quantize_GBps": round(q_bytes / q_time / 1e9, 1),
             "quantize_note": "whole quantize_tensor call incl. host sync, outlier gather and block lists",
             "sweep": sweep or None,
+            "cpu_reference": cpu_extra,
             "models": models,
             "config4": config4,
         },

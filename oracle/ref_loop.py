@@ -5,9 +5,11 @@ reference's per-block torch loop and its forward so that their cost can be
 timed on the GPU box's host cores; the reference itself never leaves the
 build container.
 
-* ``quantize_loop``  -- adaptive_quantizer.py:84-148 (one Python iteration
+* ``quantize_loop``    -- adaptive_quantizer.py:84-148 (one Python iteration
   per block, ~20 torch ops each)
-* ``forward_warm``   -- atlas_wrappers.py:67, F.linear on the cached fp16
+* ``dequantize_loop``  -- adaptive_quantizer.py:175-245 (one Python iteration
+  per block, each with a mask over ALL outlier indices and a host sync)
+* ``forward_warm``     -- atlas_wrappers.py:67, F.linear on the cached fp16
   weight (the reference's steady state after the first call, :161-171)
 """
 from __future__ import annotations
@@ -51,6 +53,37 @@ def quantize_loop(fp16_tensor: torch.Tensor, block_size: int = 128, z_threshold:
         codes.append(q)
         scales.append(s.unsqueeze(0))
     return torch.cat(codes), torch.cat(outs), torch.cat(idxs), torch.cat(scales), nb
+
+
+def dequantize_loop(fp8_data: torch.Tensor, fp16_outliers: torch.Tensor, outlier_indices: torch.Tensor,
+                    scale_factors: torch.Tensor, numel: int, block_size: int, max_blocks: int | None = None):
+    """Per-block loop of dequantize_tensor on CPU (the reference's int8
+    layout: compacted codes of the non-outliers); stops after ``max_blocks``
+    blocks.  Returns (flat fp16 tensor of the padded length, blocks_done)."""
+    padded = (numel + block_size - 1) // block_size * block_size
+    nb = padded // block_size if max_blocks is None else min(max_blocks, padded // block_size)
+    out = torch.zeros(padded, dtype=torch.float16)
+    pos = 0
+    for i in range(nb):
+        s = scale_factors[i]
+        b0, b1 = i * block_size, (i + 1) * block_size
+        in_block = (outlier_indices >= b0) & (outlier_indices < b1)  # :194-196, over all outliers
+        sel = torch.where(in_block)[0]
+        rel = outlier_indices[in_block] - b0
+        vals = fp16_outliers[sel]
+        n_codes = max(block_size - rel.numel(), 0)
+        codes = fp8_data[pos:pos + n_codes]
+        pos += n_codes
+        deq = codes.to(torch.float16) * s if n_codes > 0 else torch.empty((0,), dtype=torch.float16)
+        blk = torch.zeros(block_size, dtype=torch.float16)
+        keep = torch.ones(block_size, dtype=torch.bool)
+        if rel.numel() > 0:
+            keep[rel] = False
+            blk[rel] = vals
+        n_keep = keep.sum().item()  # :234, the host sync of every block
+        blk[keep] = deq[:n_keep]
+        out[b0:b1] = blk
+    return out, nb
 
 
 def forward_warm(x: torch.Tensor, w_fp16: torch.Tensor, bias=None) -> torch.Tensor:

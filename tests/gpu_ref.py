@@ -10,9 +10,10 @@ oracle's dequantized weight is then the F.linear operand the layer output is
 compared with (the reference's forward is F.linear(x, dequantize_tensor(W),
 b), integration/atlas_wrappers.py:56,67).
 
-Tolerance (north star): max|dy| <= 2e-3 max|x| max|w| and rel-L2 <= 1e-3
-against the float64 product, plus a per-element bound of one fp16 ulp of the
-exact result and the worst-case fp32 accumulation error 2^-20 sum|x||w|.
+Tolerance (north star): max|dy| <= 2e-3 max|x| max|w| (plus one fp16 ulp
+of the result: the output rounding, see north_star_abs_bound) and rel-L2 <=
+1e-3 against the float64 product, plus a per-element bound of one fp16 ulp of
+the exact result and the worst-case fp32 accumulation error 2^-20 sum|x||w|.
 """
 from __future__ import annotations
 
@@ -162,13 +163,26 @@ def fp16_ulp(v):
     return torch.exp2(torch.floor(torch.log2(a)) - 10)
 
 
+def north_star_abs_bound(yref, x, w):
+    """Per-element form of the north-star max-abs bound used here:
+    2e-3 max|x| max|w| plus one fp16 ulp of the exact result.  The ulp term
+    is the output rounding every fp16-output linear incurs, the reference's
+    own F.linear included: half an ulp of |y| exceeds 2e-3 max|x| max|w|
+    alone once |y| > 4 max|x| max|w| (e.g. outlier-free layers with a few
+    thousand inputs), where no fp16 result can meet the bound without it
+    (test_gpu_configs.py::test_literal_bound_misses_fp16_output_rounding
+    shows torch's F.linear missing it on such inputs)."""
+    return 2e-3 * x.abs().max().double() * w.abs().max().double() + fp16_ulp(yref)
+
+
 def assert_close(y, yref, x, w):
-    """North-star tolerance, plus a per-element bound: one fp16 ulp of the
-    exact result (the output rounding) plus the worst-case fp32 accumulation
-    error over the row, 2^-20 * sum_k |x_k| |w_nk|."""
+    """North-star tolerance (max-abs with the output-rounding term, see
+    north_star_abs_bound; rel-L2 <= 1e-3), plus a per-element bound: one
+    fp16 ulp of the exact result (the output rounding) plus the worst-case
+    fp32 accumulation error over the row, 2^-20 * sum_k |x_k| |w_nk|."""
     d = (y.double() - yref).abs()
-    bound = 2e-3 * x.abs().max().double() * w.abs().max().double()
-    assert d.max() <= bound, (d.max().item(), bound.item())
+    excess = (d / north_star_abs_bound(yref, x, w)).max().item()
+    assert excess <= 1.0, excess
     rel = (y.double() - yref).norm() / yref.norm()
     assert rel <= 1e-3, rel.item()
     x2 = x.reshape(-1, x.shape[-1]).double().abs()

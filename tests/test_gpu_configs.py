@@ -133,8 +133,14 @@ def test_config4_student_t(name, N, K):
     seed = 400 + sum(map(ord, name))
     q, w, w_ref = quantized(("t3", name), lambda: gpu_weights(N, K, seed, t_dof=3, frac=0.01), -1, "e4m3")
     per_tile_row = tile_row_outliers(q, N)
-    # heavy tails: every tile row holds more entries than the GEMV kernels stage
-    assert per_tile_row.min() > 512, per_tile_row.min()
+    # heavy tails: tile rows hold more entries than the GEMV kernels stage
+    # (every one from K = 4096 on; at K = 2048 about half of them)
+    print(f"{name}: outliers per 16-row tile row min {per_tile_row.min()} mean {per_tile_row.mean():.0f} "
+          f"max {per_tile_row.max()}")
+    if K >= 4096:
+        assert per_tile_row.min() > 512, per_tile_row.min()
+    else:
+        assert (per_tile_row > 512).mean() > 0.2, per_tile_row.mean()
     for M in (1, 5, 16, 48, 64, 2048):
         check_layer(q, w_ref, activations(M, K, seed + M))
 
@@ -204,3 +210,23 @@ def test_gemv_crowded_tile_row_every_path(fmt, G):
         yref = R.reference_linear(x, w_ref, None)
         R.assert_close(raw_qlinear(q, x, with_lists=False), yref, x, w_ref)
         R.assert_close(raw_qlinear(q, x, with_lists=True), yref, x, w_ref)
+
+
+def test_literal_bound_misses_fp16_output_rounding():
+    """Why the max-abs check carries one fp16 ulp of the result: on an
+    outlier-free layer with |y| up to ~4 max|x| max|w|, torch's own fp16
+    F.linear (the reference's forward, atlas_wrappers.py:67) misses the
+    literal 2e-3 max|x| max|w| bound against the exact product, and meets
+    the bound with the ulp term -- as does the quantized layer."""
+    rng = np.random.default_rng(5)
+    N, K = 512, 4096
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, code_format="e4m3")
+    w_ref = R.oracle_reference(q, w, K, "e4m3")
+    x = torch.from_numpy(rng.standard_normal((8, K)).astype(np.float16)).to(DEV)
+    exact = R.reference_linear(x, w_ref, None)
+    literal = 2e-3 * x.abs().max().double() * w_ref.abs().max().double()
+    y_torch = torch.nn.functional.linear(x, w_ref)
+    assert (y_torch.double() - exact).abs().max() > literal
+    assert ((y_torch.double() - exact).abs() <= R.north_star_abs_bound(exact, x, w_ref)).all()
+    check_layer(q, w_ref, x)

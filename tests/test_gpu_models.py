@@ -79,17 +79,38 @@ class LayerChecks:
             h.remove()
 
 
-def reference_logits(model, w_refs, **kw):
+def reference_logits(model, w_refs, fp32=False, **kw):
     """Logits of the same model with every QuantizedLinear computed as
-    F.linear on its reference weight."""
+    F.linear on its reference weight: in fp16 (the reference's forward), or
+    in fp32 rounded to fp16 once (another fp32-accumulating implementation,
+    whose distance to the first is the noise floor of fp16 rounding through
+    the whole model)."""
     from integration import atlas_wrappers as AW
     by_module = {m: w_refs[n] for n, m in model.named_modules() if type(m).__name__ == "QuantizedLinear"}
     saved = AW.QuantizedLinear.forward
-    AW.QuantizedLinear.forward = lambda self, x: F.linear(x, by_module[self], self.bias)
+    if fp32:
+        AW.QuantizedLinear.forward = lambda self, x: F.linear(
+            x.float(), by_module[self].float(), None if self.bias is None else self.bias.float()).half()
+    else:
+        AW.QuantizedLinear.forward = lambda self, x: F.linear(x, by_module[self], self.bias)
     try:
         return model(**kw).logits
     finally:
         AW.QuantizedLinear.forward = saved
+
+
+def assert_logits_close(logits, model, w_refs, what, **kw):
+    """Our logits against the reference's forward on the reference weights,
+    within 3x the distance between two equally valid fp32-accumulating
+    implementations of that forward (fp16 F.linear and fp32 F.linear rounded
+    once), floor 2e-3: the per-linear hooks check each layer against the
+    north-star bounds; through 24-32 layers fp16 roundings compound."""
+    ref = reference_logits(model, w_refs, **kw)
+    ref32 = reference_logits(model, w_refs, fp32=True, **kw)
+    rel, floor = rel_l2(logits, ref), rel_l2(ref32, ref)
+    print(f"{what}: logits rel-L2 vs F.linear fp16 on the reference weights {rel:.2e} "
+          f"(fp32 F.linear vs fp16 F.linear: {floor:.2e})")
+    assert rel <= max(3 * floor, 2e-3), (rel, floor)
 
 
 def rel_l2(a, b):
@@ -150,10 +171,7 @@ def test_config1_opt_1_3b_full_swap_generate():
         model(input_ids=ids[:, :1])                   # one token: M = 1
         checks.remove()
         assert checks.n == 2 * rep
-        ref = reference_logits(model, w_refs, input_ids=ids)
-        rel = rel_l2(logits, ref)
-        print(f"OPT-1.3b logits rel-L2 vs F.linear on oracle weights: {rel:.2e}")
-        assert rel < 5e-3, rel
+        assert_logits_close(logits, model, w_refs, "OPT-1.3b", input_ids=ids)
         out = model.generate(ids, max_new_tokens=128, min_new_tokens=128, do_sample=False, pad_token_id=0)
     assert out.shape == (1, 160)
     assert torch.equal(out[:, :32], ids)
@@ -188,10 +206,7 @@ def test_config3_mistral_7b(mistral, B):
         model(input_ids=nxt, past_key_values=out.past_key_values, use_cache=True)  # decode step: M = B
         checks.remove()
         assert checks.n == 2 * rep
-        ref = reference_logits(model, w_refs, input_ids=ids)
-        rel = rel_l2(out.logits, ref)
-        print(f"Mistral-7B batch {B} logits rel-L2 vs F.linear on reference weights: {rel:.2e}")
-        assert rel < 5e-3, rel
-        del out, ref
+        assert_logits_close(out.logits, model, w_refs, f"Mistral-7B batch {B}", input_ids=ids)
+        del out
         gen = model.generate(ids, max_new_tokens=8, min_new_tokens=8, do_sample=False, pad_token_id=0)
     assert gen.shape == (B, 520)

@@ -300,6 +300,24 @@ def kernel_only(args, dev, gen, qlinear_grouped, AQ):
           flush=True)
 
 
+def quantize_only(args, dev, gen):
+    """Counter-run workload of the quantize kernel: aq_quantize (per-channel
+    E4M3, tiled) over 4 rotated gate_proj weights [14336, 4096] (470 MB of
+    fp16, past the 256 MB MALL), each pass one HIP graph, plus the same
+    512 MiB calibration copy as --kernel-only."""
+    ws = [gen_weight(14336, 4096, gen, dev) for _ in range(4)]
+    nbytes, secs = time_quantize_kernel(ws, reps=max(args.steps // 4, 1))
+    src = torch.empty(512 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"quantize_only": True, "algorithmic_bytes_per_launch": nbytes // 4,
+                      "us_per_launch": round(1e6 * secs / 4, 3), "GBps": round(nbytes / secs / 1e9, 1),
+                      "copy_bytes": src.numel()}), flush=True)
+
+
 def plant_outliers(model, gen, sigma=0.02, frac=0.001):
     """BASELINE weight recipe on a random-init model: every Linear weight
     gets round(frac * numel) entries replaced by +-U(8, 20) * sigma."""
@@ -494,6 +512,9 @@ def main():
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant kernel (gate+up grouped GEMV, 4 rotated layers) and a 512 MiB "
                          "calibration copy, for counter runs")
+    ap.add_argument("--quantize-only", action="store_true",
+                    help="only the quantize kernel (4 rotated gate_proj weights) and a 512 MiB calibration copy, "
+                         "for counter runs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the quantized-linear path is single-GPU here; "
@@ -511,6 +532,9 @@ def main():
 
     if args.kernel_only:
         kernel_only(args, dev, gen, qlinear_grouped, AQ)
+        return
+    if args.quantize_only:
+        quantize_only(args, dev, gen)
         return
 
     # ---- weights: 4 layers x 7 linears, quantized on the GPU (also timed)

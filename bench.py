@@ -318,6 +318,33 @@ def quantize_only(args, dev, gen):
                       "copy_bytes": src.numel()}), flush=True)
 
 
+def gemm_only(args, dev, gen, qlinear, qlinear_grouped, AQ):
+    """Counter-run workload of the dequant-GEMM: the M = 2048 prefill launch
+    pattern of one Llama-3-8B layer (q/k/v grouped, o, gate/up grouped,
+    down), ``--steps`` times, eager."""
+    layer = {name: AQ.quantize_tensor(gen_weight(N, K, gen, dev), block_size=-1, code_format="e4m3")
+             for name, N, K in LLAMA_LINEARS}
+    xg = {K: gen_x(2048, K, gen, dev) for K in {K for _, _, K in LLAMA_LINEARS}}
+
+    def step():
+        qlinear_grouped(xg[4096], [layer["q_proj"], layer["k_proj"], layer["v_proj"]])
+        qlinear(xg[4096], layer["o_proj"], None)
+        qlinear_grouped(xg[4096], [layer["gate_proj"], layer["up_proj"]])
+        qlinear(xg[14336], layer["down_proj"], None)
+    step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    secs = e0.elapsed_time(e1) / 1e3 / args.steps
+    flops = sum(2 * 2048 * N * K for _, N, K in LLAMA_LINEARS)
+    print(json.dumps({"gemm_only": True, "us_per_layer": round(1e6 * secs, 1),
+                      "TFLOPs": round(flops / secs / 1e12, 1)}), flush=True)
+
+
 def plant_outliers(model, gen, sigma=0.02, frac=0.001):
     """BASELINE weight recipe on a random-init model: every Linear weight
     gets round(frac * numel) entries replaced by +-U(8, 20) * sigma."""
@@ -515,6 +542,8 @@ def main():
     ap.add_argument("--quantize-only", action="store_true",
                     help="only the quantize kernel (4 rotated gate_proj weights) and a 512 MiB calibration copy, "
                          "for counter runs")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the M=2048 prefill launches of one Llama-3-8B layer, for counter runs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the quantized-linear path is single-GPU here; "
@@ -535,6 +564,9 @@ def main():
         return
     if args.quantize_only:
         quantize_only(args, dev, gen)
+        return
+    if args.gemm_only:
+        gemm_only(args, dev, gen, qlinear, qlinear_grouped, AQ)
         return
 
     # ---- weights: 4 layers x 7 linears, quantized on the GPU (also timed)

@@ -17,7 +17,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libatlasinfer_amd.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 FMT_INT8 = 0
 FMT_E4M3 = 1
@@ -53,7 +53,10 @@ SIGNATURES = {
                                   _I64, _P, _P, _P, _I64, _P]),
     "aq_qlinear_grouped": (ctypes.c_int, [_P, _I64, _I64, ctypes.c_int, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                           _P, _P, _P, _P, _I64, _P]),
+    "aq_qlinear_noalloc": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, _I64, ctypes.c_int, _I32P, _I32P, _P,
+                                          _I32P, _P, _I64, _P, _P, _P]),
 }
+NOALLOC_SCRATCH_BYTES = 64 << 20  # AQ_NOALLOC_SCRATCH_BYTES
 
 
 def ptr_array(values, ctype=ctypes.c_void_p):

@@ -5,9 +5,11 @@
  * Conventions
  *   - extern "C", plain pointers and sizes; no C++ or torch types.
  *   - Every pointer argument is device memory owned by the caller, unless the
- *     comment says otherwise.  The library never allocates device memory;
- *     scratch space comes in through a caller-owned workspace argument whose
- *     size the matching *_workspace_size() call returns.
+ *     comment says otherwise.  No call allocates device memory; scratch space
+ *     comes in through a caller-owned workspace argument whose size the
+ *     matching *_workspace_size() call returns, except for
+ *     aq_qlinear_noalloc, whose scratch is a static device array of the
+ *     library (AQ_NOALLOC_SCRATCH_BYTES per GPU, held until process exit).
  *   - Every call enqueues work on `stream` (a hipStream_t, passed as void*)
  *     and returns without synchronising.
  *   - Return value: AQ_OK (0) or a negative AQ_E* code; aq_last_error()
@@ -42,7 +44,7 @@
 extern "C" {
 #endif
 
-#define AQ_ABI_VERSION 4
+#define AQ_ABI_VERSION 5
 
 enum { AQ_FMT_INT8 = 0, AQ_FMT_E4M3 = 1 };
 enum { AQ_LAYOUT_FLAT = 0, AQ_LAYOUT_TILED = 1 };
@@ -203,6 +205,25 @@ int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, int64_t cou
                        const int32_t* const* tile_ptrs, const uint32_t* const* tile_ents,
                        const int64_t* tile_maxes, const void* const* biases, void* const* ys, void* workspace,
                        int64_t workspace_bytes, void* stream);
+
+/*
+ * aq_qlinear without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Same arguments, kernels and results as aq_qlinear given a workspace of
+ * AQ_NOALLOC_SCRATCH_BYTES: the GEMM's split-K partial sums go to a static
+ * device array of that size inside the library, one per GPU, held from the
+ * first use on a GPU until the process ends.  The split is planned within
+ * that size (as aq_qlinear's within its workspace), so no call is too large
+ * for it; the call allocates nothing (no hipMalloc, no allocating library
+ * call).  Calls that overlap in time on one GPU share the array and race:
+ * serialise them (one stream, or your own ordering).
+ */
+#define AQ_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int aq_qlinear_noalloc(const void* x, int64_t M, int64_t K, int64_t N, const void* codes, const void* scales,
+                       int64_t G, int fmt, const int32_t* row_ptr, const int32_t* cols, const void* vals,
+                       const int32_t* tile_ptr, const uint32_t* tile_ent, int64_t tile_max, const void* bias,
+                       void* y, void* stream);
 
 #ifdef __cplusplus
 }

@@ -386,43 +386,104 @@ __device__ __forceinline__ void finish_block_any(const QuantArgs& a, Elems<E>& x
   }
 }
 
-// mean / std / std + eps as block_stats computes them, with one pass less:
-// S is the same exact-order f64 tree, but the variance comes from
-// Q = sum x^2 (products exact in f32, four f32 chains per thread, f64 across
-// threads) as V = Q - S mu, whose error is below Q 2^-19.  std16 is a
-// monotone function of V (f64 division, sqrt, rounding to f32 and to fp16),
-// so when both ends of V +- Q 2^-16 give the same std16 that is the value
-// the two-pass tree gives.  Otherwise (a near-tie, large |mean| / std, or a
-// non-finite sum) the team runs the two-pass tree.  The decision is the
-// same in every lane of the team (its sums are).
+// f32 fused multiply-adds with fp16 sources taken from the halves of packed
+// pairs (v_fma_mix_f32: the fp16 operands enter exactly, one f32 rounding).
+// Written out because the compiler splits x * 1 + y into two conversions and
+// an add.
+__device__ __forceinline__ float pair_sum_f32(uint32_t p) {  // lo + hi
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %1 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(p));
+  return r;
+}
+__device__ __forceinline__ float sq_acc_lo(uint32_t p, float c) {  // lo * lo + c
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %1, %2 op_sel:[0,0,0] op_sel_hi:[1,1,0]" : "=v"(r) : "v"(p), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float sq_acc_hi(uint32_t p, float c) {  // hi * hi + c
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %1, %2 op_sel:[1,1,0] op_sel_hi:[1,1,0]" : "=v"(r) : "v"(p), "v"(c));
+  return r;
+}
+
+// The reference's mean of a block whose sum is S: fp16(f32(S / G)).  A
+// monotone non-decreasing function of S (f64 division by G > 0, then two
+// round-to-nearest conversions).
+__device__ __forceinline__ f16 mean_of_sum(double S, int64_t G) { return rn_h((float)(S / (double)G)); }
+
+// mean / std / std + eps as block_stats computes them, from one pass of
+// single-precision sums in the common case:
+//   S  = sum x   as an f32 tree (leaf pairs by one fused multiply-add of the
+//        fp16 values, x0 * 1 + x1, then a balanced tree): depth d = log2(E)
+//        roundings of u = 2^-24 per thread, so |S_f32 - S| <= d u sum|x|
+//        (the f64 sum across the team adds under 2^-46 relative), and
+//        sum|x| <= sqrt(G Q) by Cauchy-Schwarz;
+//   Q  = sum x^2 (products exact in f32, four f32 chains per thread, f64
+//        across threads), within Q 2^-19 of the exact sum.
+// mean16 is a monotone function of S, so when both ends of S_f32 +- errS
+// give the same mean16, that is the value the exact sum gives; std16 is a
+// monotone function of V = Q - S mu, accepted when both ends of V +- errV
+// (errV covers Q's error and S's) give the same std16.  Otherwise (a
+// near-tie, a non-finite sum, G < 2) the team falls back to the exact-order
+// f64 trees of block_stats: the sum, and the two-pass variance when std16
+// is the open one.  Every decision is the same in all lanes of the team (its
+// sums are), and for teams of several waves sharing a workgroup's barriers
+// it is taken by the whole workgroup.
 template <int TAU, int E, int MODE>
 __device__ __forceinline__ BlockStats block_stats_fast(Elems<E>& xs, int i0, int64_t G, float eps, double* lds_d) {
 #pragma clang fp contract(off)
-  const double s_loc = thread_tree_sum<E, MODE>(xs, i0, G, false, 0.0);
+  constexpr int NT = TAU > kWG ? TAU : kWG;
+  constexpr bool kSyncedTeams = TAU > 64 && NT / TAU > 1;
+  constexpr int kDepth = E == 16 ? 4 : E == 32 ? 5 : 6;
+  static_assert(E == 16 || E == 32 || E == 64, "tree depth");
+  // padding elements are zeros: every E elements enter the sums
+  float sp[E / 2];
+#pragma unroll
+  for (int i = 0; i < E / 2; i++) sp[i] = pair_sum_f32(xs.p[i]);
+#pragma unroll
+  for (int w = E / 2; w > 1; w >>= 1)
+#pragma unroll
+    for (int i = 0; i < w / 2; i++) sp[i] = sp[2 * i] + sp[2 * i + 1];
   float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int e = 0; e < E; e++) {
-    const float v = (float)xs[e];  // padding elements are zeros
-    q[e & 3] = __builtin_fmaf(v, v, q[e & 3]);
+  for (int i = 0; i < E / 2; i++) {
+    q[(2 * i) & 3] = sq_acc_lo(xs.p[i], q[(2 * i) & 3]);
+    q[(2 * i + 1) & 3] = sq_acc_hi(xs.p[i], q[(2 * i + 1) & 3]);
   }
-  const double S = team_sum_f64<TAU>(s_loc, lds_d);
+  const double Sf = team_sum_f64<TAU>((double)sp[0], lds_d);
   const double Q = team_sum_f64<TAU>((double)((q[0] + q[1]) + (q[2] + q[3])), lds_d);
+  const double absum = sqrt((double)G * Q * (1.0 + 0x1p-16));
+  const double errS = (double)(kDepth + 1) * 0x1p-24 * absum + fabs(Sf) * 0x1p-50;
+  const f16 m_lo = mean_of_sum(Sf - errS, G), m_hi = mean_of_sum(Sf + errS, G);
+  bool need_exact = !(h_to_bits(m_lo) == h_to_bits(m_hi) && !isnan((float)m_lo));
+  if constexpr (kSyncedTeams) need_exact = __syncthreads_or(need_exact);
+  double S = Sf, dS = errS;
+  if (need_exact) {
+    xs.fence();
+    S = team_sum_f64<TAU>(thread_tree_sum<E, MODE>(xs, i0, G, false, 0.0), lds_d);
+    dS = 0.0;
+  }
   const double mu = S / (double)G;
   auto std_of = [&](double V) { return rn_h((float)sqrt(V / (double)(G - 1))); };
   BlockStats st;
   st.mean16 = rn_h((float)mu);
-  bool pinned = false;
+  bool open = true;
   if (G >= 2) {
     const double V = Q - S * mu;
-    const double err = Q * 0x1p-16;
+    const double err = Q * 0x1p-16 + (2.0 * fabs(S) + dS) * dS / (double)G + fabs(V) * 0x1p-50;
     const f16 lo = std_of(fmax(V - err, 0.0));
     const f16 hi = std_of(V + err);
-    pinned = h_to_bits(lo) == h_to_bits(hi) && !isnan((float)lo);
+    open = !(h_to_bits(lo) == h_to_bits(hi) && !isnan((float)lo));
     st.std16 = lo;
   }
-  if (!pinned) {
+  if constexpr (kSyncedTeams) open = __syncthreads_or(open);
+  if (open) {
     xs.fence();
-    const double v_loc = thread_tree_sum<E, MODE>(xs, i0, G, true, mu);
+    double Se = S;
+    if (dS != 0.0) Se = team_sum_f64<TAU>(thread_tree_sum<E, MODE>(xs, i0, G, false, 0.0), lds_d);
+    const double mue = Se / (double)G;
+    xs.fence();
+    const double v_loc = thread_tree_sum<E, MODE>(xs, i0, G, true, mue);
     st.std16 = std_of(team_sum_f64<TAU>(v_loc, lds_d));
   }
   st.den16 = rn_h((float)st.std16 + eps);
@@ -452,17 +513,26 @@ __device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
   return d;
 }
 
-// fp16(x / s) for both halves of a pair, s > 0, r = fl(1 / s): the f32
-// quotient with one Newton step (the correctly rounded f32 quotient), then
-// fp16.  The fp16 x enters the fused multiply-adds directly; a zero x gives
-// +0 there, so the sign bits are taken from x (for any other x the
-// quotient already carries x's sign).
-__device__ __forceinline__ uint32_t quot2(uint32_t xp, float s, float r) {
-  const half2v x = as_h2(xp);
-  const float q00 = __builtin_fmaf((float)x.x, r, 0.0f), q01 = __builtin_fmaf((float)x.y, r, 0.0f);
-  const float e0 = __builtin_fmaf(q00, s, -(float)x.x), e1 = __builtin_fmaf(q01, s, -(float)x.y);
-  const uint32_t q = h2_bits((half2v){(f16)__builtin_fmaf(-e0, r, q00), (f16)__builtin_fmaf(-e1, r, q01)});
-  return (q & 0x7FFF7FFFu) | (xp & 0x80008000u);
+// fp16(x / s) for both halves of a pair, s > 0, r = RN32(1 / s): one mixed
+// fused multiply-add per half, x * r + (-0), the fp16 x entering exactly and
+// the product rounded to fp16.  Why one product suffices: a quotient x / s
+// can lie near an fp16 rounding midpoint m (odd 12-bit significand) only as
+// x / s = m (1 + e) with |e| > 2^-23, since m s has a significand below 2^23
+// that x (11 bits) cannot equal; x * r = (x / s)(1 + d) with |d| <= 2^-24,
+// and a rounding through f32 on the way adds at most another 2^-24, so the
+// product rounds to the same fp16 value as RN32(x / s) wherever that value
+// is an fp16 normal.  Below, in the fp16 subnormal range, the two can differ
+// only on exact ties, and every such quotient (|q| < 2^-14) encodes to code
+// 0 in either format.  The -0 addend keeps the sign of a zero x (x * r = -0
+// for x = -0).  Checked over all fp16 x and s with |x / s| <= 448.25, under
+// both rounding behaviours (tests/c_kernel_math_check.c).
+__device__ __forceinline__ uint32_t quot2(uint32_t xp, float r) {
+  uint32_t q;
+  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "=&v"(q)
+      : "v"(xp), "v"(r), "v"(-0.0f));
+  return q;
 }
 
 // The rest of a block after its elements are loaded, when a thread's E
@@ -580,10 +650,10 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
         // quotient is at most 448.25, which the conversion (round to nearest
         // even) takes to 448 as the clamp to +-448 would
         typedef short short2v __attribute__((vector_size(4)));
-        const uint32_t q0 = quot2(p0, s, r);
+        const uint32_t q0 = quot2(p0, r);
         // both halves of c are written; its initial value is never seen
         short2v c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(__builtin_bit_cast(short2v, q0), as_h2(q0), 1.0f, false);
-        c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(c, as_h2(quot2(p1, s, r)), 1.0f, true);
+        c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(c, as_h2(quot2(p1, r)), 1.0f, true);
         w[k] = __builtin_bit_cast(uint32_t, c);
       }
     }

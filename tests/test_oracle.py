@@ -164,10 +164,12 @@ def test_brute_force_tiny_blocks_against_float64(oracle):
 
 
 def test_kernel_arithmetic_identities():
-    """The quantize kernel replaces two literal divisions by cheaper forms;
-    check both identities against the literal arithmetic: every fp16 x for
-    every 16th positive fp16 scale, and the outlier cut for 100 random dens
-    x 9 thresholds x every fp16 |x - mean|."""
+    """The quantize kernel replaces literal divisions by cheaper forms; check
+    the identities against the literal arithmetic: the Newton-corrected and
+    the single fused-product quotients for every fp16 x and every 16th
+    positive fp16 scale (every scale: `c_kernel_math_check 1`, about 3e9
+    pairs, run during development with 0 differences), and the outlier cut
+    for 100 random dens x 9 thresholds x every fp16 |x - mean|."""
     build = os.path.join(ROOT, "oracle", "_build")
     os.makedirs(build, exist_ok=True)
     exe = os.path.join(build, "c_kernel_math_check")
@@ -175,4 +177,7 @@ def test_kernel_arithmetic_identities():
                     os.path.join(ROOT, "oracle", "aq_oracle.c"), "-lm"], check=True)
     r = subprocess.run([exe, "16", "100"], capture_output=True, text=True)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert "0 code differences" in r.stdout and "0 differences" in r.stdout, r.stdout
+    assert "quotient:" in r.stdout and "product:" in r.stdout and "threshold:" in r.stdout, r.stdout
+    for line in r.stdout.splitlines():
+        assert " 0 code differences" in line or line.startswith("threshold"), line
+    assert "0 normal-quotient differences" in r.stdout and "pairs, 0 differences" in r.stdout, r.stdout

@@ -738,17 +738,6 @@ __device__ __forceinline__ void gemm_load_ent(GemmRegs<BM>& R, const GemmSrc<BM>
   __builtin_amdgcn_sched_barrier(0);  // ahead of the next bulk loads: loads complete in issue order
 }
 
-// Byte offset of (row, 16-byte piece) in an A or B tile: 128-byte rows,
-// piece p stored at p ^ (row & 7) ^ ((row >> 3) & 1).  Measured on gfx950:
-// 16-byte LDS reads serve 16 lanes per cycle over 64 banks, 16-byte writes
-// 8 lanes over 128 bytes.  Reads of 16 consecutive rows at one piece then
-// fall on 8 distinct pieces among the even rows and 8 among the odd rows,
-// and writes of 8 consecutive rows at one piece (or of one row's 8 pieces)
-// on 8 distinct pieces.
-__device__ __forceinline__ uint32_t tile_off(int row, int piece) {
-  return (uint32_t)(row * 128 + ((piece ^ (row & 7) ^ ((row >> 3) & 1)) << 4));
-}
-
 // R -> one LDS stage: x pieces into the A tile, decoded weights into the B
 // tile, then the outliers over them.  Lanes past a block's count write to the
 // spare slot instead of branching.
@@ -988,14 +977,18 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qlinear_gemm_kernel(QLArgs a)
 // kernel above, which is what bounds it.  8 waves, each computing a 128 x 64
 // tile (2 x 4 layout) and each also staging a share of the next chunk; two
 // LDS stages, one barrier per chunk.  Per chunk c a wave reads the fragments
-// of chunk c one k-step ahead of its MFMAs, stages chunk c + 1 (x pieces,
-// decoded weights, outlier patches) into the other stage, and reloads its
-// registers with chunk c + 2.  With two stages the first fragments of a chunk
-// are read after its barrier; each wave then has 32 MFMAs (1024 cycles of the
-// SIMD's matrix unit per wave pair) to hide them.
+// of chunk c one k-step ahead of its MFMAs and fills its share of the other
+// stage with chunk c + 1: the x pieces by direct-to-LDS loads (buffer_load
+// ... lds, 1 KiB per wave and instruction, each lane's source piece chosen so
+// the data lands in tile_off's layout: no registers, no LDS write
+// instructions), the decoded weights and their outlier patches from
+// registers loaded a chunk earlier; it then reloads those registers with
+// chunk c + 2, loads that stay in flight across the barrier.  With two
+// stages the first fragments of a chunk are read after its barrier; each
+// wave then has 32 MFMAs (1024 cycles of the SIMD's matrix unit per wave
+// pair) to hide them.
 
 struct WideRegs {
-  u32x4 a[4];      // x pieces
   u32x4 q[2];      // codes of the wave's two block rows
   uint32_t s[2];   // their scales (block-wise scales only)
   int e0[2], e1[2];
@@ -1004,7 +997,7 @@ struct WideRegs {
 
 struct WideSrc {
   __amdgpu_buffer_rsrc_t xr, cr, tr, er, sr;
-  int xo[4];
+  uint32_t xo[4];  // byte offsets of this lane's 4 x pieces of chunk 0 (direct-to-LDS loads)
   int co[2], to[2], so[2];
 };
 
@@ -1015,11 +1008,16 @@ __device__ __forceinline__ void wide_src_init(WideSrc& S, const QLMat& W, const 
                                               int m_first, int nbase, int nch128, int t) {
   const int l = t & 63, w = t >> 6;
   const int rows = min(M - m_first, kWideBM);
+  // x rows past M lie past the end of this range: their pieces read as zero
   S.xr = __builtin_amdgcn_make_buffer_rsrc((void*)(x + (size_t)m_first * K), (short)0, rows * K * 2, kBufferDword3);
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const int row = min(64 * i + (t >> 3), rows - 1);
-    S.xo[i] = (row * K + 8 * (t & 7)) * 2;
+    // direct load i of wave w fills A-tile bytes (4 w + i) KiB + 16 l: row
+    // 8 (4 w + i) + l / 8, stored piece l % 8, which tile_off assigns the
+    // logical piece (l % 8) ^ (row & 7) ^ ((row >> 3) & 1)
+    const int row = 8 * (4 * w + i) + (l >> 3);
+    const int piece = (l & 7) ^ (row & 7) ^ ((row >> 3) & 1);
+    S.xo[i] = (uint32_t)(row * K + 8 * piece) * 2;
   }
   const int rb0 = nbase / 16, rb_last = W.N / 16 - 1;
   const int nrb = min(rb_last - rb0 + 1, kWideBN / 16);
@@ -1052,8 +1050,6 @@ __device__ __forceinline__ void wide_load(WideRegs& R, const WideSrc& S, const Q
   __builtin_amdgcn_sched_barrier(0);
   const int k0 = c * kGemmBK;
 #pragma unroll
-  for (int i = 0; i < 4; i++) R.a[i] = __builtin_amdgcn_raw_buffer_load_b128(S.xr, S.xo[i], k0 * 2, 0);
-#pragma unroll
   for (int i = 0; i < 2; i++) {
     R.q[i] = __builtin_amdgcn_raw_buffer_load_b128(S.cr, S.co[i], ((c >> 1) << 11) + ((c & 1) << 10), 0);
     if (!PC) {
@@ -1062,6 +1058,15 @@ __device__ __forceinline__ void wide_load(WideRegs& R, const WideSrc& S, const Q
       R.s[i] = __builtin_amdgcn_raw_buffer_load_b16(S.sr, S.so[i] + kb * 2, 0, 0);
     }
   }
+}
+
+// Chunk c's x straight into a stage's A tile: 4 direct-to-LDS loads of 1 KiB
+// per wave, no registers and no LDS write instructions.
+__device__ __forceinline__ void wide_load_x(const WideSrc& S, uint8_t* stage, int c, int w) {
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(S.xr, (void*)(stage + (4 * w + i) * 1024), 16, S.xo[i], c * kGemmBK * 2,
+                                             0, 0);
 }
 
 __device__ __forceinline__ void wide_load_ent(WideRegs& R, const WideSrc& S, int l) {
@@ -1078,12 +1083,8 @@ __device__ __forceinline__ void wide_load_ent(WideRegs& R, const WideSrc& S, int
 template <int FMT, int PC, int DENSE>
 __device__ __forceinline__ void wide_stage(const WideRegs& R, const WideSrc& S, uint8_t* stage, uint8_t* spare,
                                            const half2v (&srow)[2], int t) {
-  uint8_t* As = stage;
   uint8_t* Bs = stage + kWideA;
   const int l = t & 63, w = t >> 6, g = l >> 4;
-  const uint32_t xo = tile_off(t >> 3, t & 7);  // rows 64 i + t / 8 share the permutation
-#pragma unroll
-  for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4*>(As + xo + i * 64 * 128) = R.a[i];
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     const int n = 16 * (2 * w + i) + (l & 15);
@@ -1178,18 +1179,28 @@ __global__ __launch_bounds__(512, 1) void qlinear_gemm_wide_kernel(QLArgs a) {
       for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(F.a[i], F.b[j], acc[i][j], 0, 0, 0);
   };
 
-  // prologue: chunk c_first staged, chunk c_first + 1 loading
+  // The barrier at the end of each chunk waits for the stage just written
+  // (its direct x loads and this wave's LDS writes) but not for the weight
+  // loads issued after them (2 block pointers + 2 code pieces, + 2 scales
+  // for block-wise scales), which stay in flight into the next chunk.
+#define AQ_WIDE_BARRIER() \
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(PC ? 4 : 6) : "memory")
+  // prologue: chunk c_first staged, chunk c_first + 1's weights loading
   WideRegs R;
+  wide_load_x(S, lds, c_first, wave);
   wide_load<PC>(R, S, W, c_first, lane);
   wide_load_ent(R, S, lane);
   wide_stage<FMT, PC, DENSE>(R, S, lds, spare, srow, t);
   wide_load<PC>(R, S, W, min(c_first + 1, c_end - 1), lane);
-  __syncthreads();
+  AQ_WIDE_BARRIER();
 
   Frags F0, F1;
   uint32_t cur = 0;
   for (int c = c_first; c < c_end; c++) {
     const uint32_t oth = cur ^ kWideStage;
+    // chunk c + 1's x into the other stage (its last reads were before the
+    // previous barrier); past the last chunk, a harmless reload
+    wide_load_x(S, lds + oth, min(c + 1, c_end - 1), wave);
     wide_load_ent(R, S, lane);  // entries of chunk c + 1
     read_frags(F0, cur, 0);
     read_frags(F1, cur, 1);
@@ -1209,9 +1220,10 @@ __global__ __launch_bounds__(512, 1) void qlinear_gemm_wide_kernel(QLArgs a) {
     mma(F0);
     __builtin_amdgcn_sched_barrier(0);
     mma(F1);
-    __syncthreads();
+    AQ_WIDE_BARRIER();
     cur = oth;
   }
+#undef AQ_WIDE_BARRIER
 
   const int hi = lane >> 5, lc = lane & 31;
   if (a.split > 1) {

@@ -85,6 +85,17 @@ __device__ __forceinline__ int scale_index(const QLMat& w, int n, int k) {
   return n * w.kg + (w.gshift >= 0 ? (k >> w.gshift) : (k / w.G));
 }
 
+// Byte offset of (row, 16-byte piece) in an A or B tile of the dequant-GEMMs:
+// 128-byte rows, piece p stored at p ^ (row & 7) ^ ((row >> 3) & 1).
+// Measured on gfx950: 16-byte LDS reads serve 16 lanes per cycle over 64
+// banks, 16-byte writes 8 lanes over 128 bytes.  Reads of 16 consecutive rows
+// at one piece then fall on 8 distinct pieces among the even rows and 8 among
+// the odd rows, and writes of 8 consecutive rows at one piece (or of one
+// row's 8 pieces) on 8 distinct pieces.
+__device__ __forceinline__ uint32_t tile_off(int row, int piece) {
+  return (uint32_t)(row * 128 + ((piece ^ (row & 7) ^ ((row >> 3) & 1)) << 4));
+}
+
 constexpr uint32_t kOutOfRange = 0x80000000u;  // a buffer offset past every range used here
 constexpr int kBufferDword3 = 0x00020000;      // raw (untyped) buffer access on gfx9
 

@@ -11,15 +11,16 @@
 // code 0; their fp16 values are added from the CSR lists in fp32, then the
 // bias, then one rounding to fp16.
 //
-//  * M <= 16: dequant-GEMV.  One workgroup per 16-row tile row: NS waves
-//    stream its tiles (1 KiB contiguous per load instruction, two 128-wide
+//  * M <= 5: dequant-GEMV.  One workgroup per 16-row tile row: NS waves
+//    stream its tiles (1 KiB contiguous per load instruction, four 128-wide
 //    K chunks in flight per wave) with the M rows of x as the MFMA A operand
 //    (rows >= M are zero), and their partial tiles are summed through LDS in
-//    a fixed order.  Wave 0 then stages the rows' CSR outlier lists and the
-//    x values they multiply into LDS for the epilogue.  NS (1, 2, 4 or 8)
-//    gives the launch about 1536 waves: one per tile row for a tall group.
-//    Several matrices that read the same x (q/k/v, gate/up) share one
-//    launch.
+//    a fixed order.  Wave 0 also sums the rows' CSR outliers.  NS (1, 2, 4
+//    or 8) gives the launch about 1536 waves: one per tile row for a tall
+//    group.  Several matrices that read the same x (q/k/v, gate/up) share
+//    one launch, cut into pieces of equal tile-row count, one grid row
+//    (blockIdx.y) per piece, so that a wave finds its matrix without
+//    loading anything first.
 //  * 6 <= M <= 64: the same streaming, but 8 waves per workgroup share each
 //    chunk of x through LDS (details at its kernel below), since x is then
 //    comparable to or larger than the codes it multiplies.  (M = 1..5 re-read
@@ -40,6 +41,30 @@ using namespace aqk;
 
 // ------------------------------------------------------------ GEMV (M <= 64)
 
+// The GEMV's arguments: its piece of the group (blockIdx.y, known at wave
+// start) and the shared x, M, K, all read in one round of scalar loads and
+// held in scalar registers (the asm below keeps the compiler from placing
+// each load next to its first use, which costs a full round trip to the
+// argument block per use: the first code load of a wave would wait for
+// several in turn).
+struct GemvIn {
+  QLMat w;
+  const uint16_t* x;
+  int M, K;
+};
+__device__ __forceinline__ GemvIn gemv_in(const QLArgs& a) {
+  GemvIn g;
+  g.w = a.mat[blockIdx.y];
+  g.x = a.x;
+  g.M = a.M;
+  g.K = a.K;
+  asm volatile(""
+               : "+s"(g.w.codes), "+s"(g.w.scales), "+s"(g.w.row_ptr), "+s"(g.w.cols), "+s"(g.w.vals),
+                 "+s"(g.w.bias), "+s"(g.w.y), "+s"(g.w.N), "+s"(g.w.G), "+s"(g.w.kg), "+s"(g.w.gshift),
+                 "+s"(g.w.ldy), "+s"(g.x), "+s"(g.M), "+s"(g.K));
+  return g;
+}
+
 constexpr int kGemvMaxM = 64;   // larger M takes the GEMM
 // From 33 rows of x on, grids of fewer than 384 tile rows take the GEMM when the
 // caller passes the outlier block lists: the GEMV's x stages for 64 rows fit
@@ -57,6 +82,10 @@ constexpr int kGemvDirectMaxM = kGemvXMinM - 1;  // rows of x qlinear_gemv_kerne
 constexpr int kStageBatch = 8;
 constexpr int kGemvX1MaxK = 16384;  // decode keeps x in LDS up to this row length (32 KiB)
 
+// s_waitcnt operand on gfx9: vmcnt(N) only (expcnt and lgkmcnt at their maxima)
+template <int N>
+constexpr int kVmcnt = (N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00;
+
 // MM: the most rows of x (1 for decode, kGemvDirectMaxM otherwise)
 template <int NS, int FMT, int PC, int X1, int MM>
 __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
@@ -69,16 +98,14 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   __shared__ float s_prod[MM][64 * kStageBatch];  // x * value of the tile's first entries
   __shared__ float s_osum[MM][16];                // outlier sum per (row of x, output column)
 
-  int mi = 0;
-#pragma unroll
-  for (int j = 1; j < kMaxGroup; j++)
-    if (j < a.count && (int)blockIdx.x >= a.first[j]) mi = j;
-  const QLMat W = pick(a, mi);
-  const int rb = blockIdx.x - a.first[mi];
+  const GemvIn in = gemv_in(a);
+  const QLMat& W = in.w;
+  const int rb = blockIdx.x;  // tile row in the piece
+  if (rb * 16 >= W.N) return;  // the grid is as wide as the longest piece
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: chunk tests stay scalar
   const int n0 = rb * 16;
-  const int M = a.M, K = a.K, N = W.N;
+  const int M = in.M, K = in.K;
   const int nchunks = K >> 7;
   const int grp = lane >> 4;
   const int li = lane & 15;
@@ -90,7 +117,7 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   // condition (which would make the compiler wait for all loads in flight).
   const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W.codes + ((size_t)rb * nchunks << 11)), (short)0, nchunks * 2048, kBufferDword3);
-  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, M * K * 2, kBufferDword3);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)in.x, (short)0, M * K * 2, kBufferDword3);
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W.scales + (size_t)n0 * W.kg), (short)0, 16 * W.kg * 2, kBufferDword3);
   const uint32_t code_lane = lane * 16;
@@ -172,7 +199,7 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
         const float wv = (float)bits_to_h(W.vals[p0 + e]);
 #pragma unroll
         for (int m = 0; m < MM; m++)
-          if (m < M) v[m] += (float)bits_to_h(X1 ? x_lds[col] : a.x[(size_t)m * K + col]) * wv;
+          if (m < M) v[m] += (float)bits_to_h(X1 ? x_lds[col] : in.x[(size_t)m * K + col]) * wv;
       }
     }
 #pragma unroll
@@ -262,27 +289,33 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   if (X1) {
     {
       // x in 16-byte pieces (K / 8 of x, then 4 of zeros: pieces past x are
-      // out of range and read as zero), XB pieces per lane at a time.  The
-      // first XB go out ahead of the first two batches of codes, so their
-      // wait (x comes from L2) leaves the codes in flight; longer rows take
-      // further rounds of XB.
-      constexpr int XB = 8;
+      // out of range and read as zero), XB pieces per thread at a time,
+      // enough for a row of 4096 with 64 threads, 10208 with 256 and 16352
+      // with 512.
+      // They go out ahead of the first two batches of codes, so their wait
+      // (x comes from L2) leaves the codes in flight; longer rows take
+      // further rounds.  Each thread issues only the loads its share needs
+      // (a uniform test): every load instruction costs the CU's address unit
+      // the same time, in range or not.
+      constexpr int XB = NS >= 4 ? 5 : 9;
       const int nxp = (K >> 3) + 4;
-      const __amdgpu_buffer_rsrc_t xr1 = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, K * 2, kBufferDword3);
+      const int per = min(XB, (nxp + 64 * NS - 1) / (64 * NS));  // pieces per thread and round
+      const __amdgpu_buffer_rsrc_t xr1 = __builtin_amdgcn_make_buffer_rsrc((void*)in.x, (short)0, K * 2, kBufferDword3);
       u32x4 xv[XB];
       auto x_round = [&](int i0) {
 #pragma unroll
         for (int j = 0; j < XB; j++) {
           const int i = i0 + 64 * NS * j;
-          xv[j] = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr1, i < (K >> 3) ? (uint32_t)i * 16 : kOutOfRange, 0, 0));
+          if (j < per)
+            xv[j] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr1, i < (K >> 3) ? (uint32_t)i * 16 : kOutOfRange, 0, 0));
         }
       };
       auto x_store = [&](int i0) {
 #pragma unroll
         for (int j = 0; j < XB; j++) {
           const int i = i0 + 64 * NS * j;
-          if (i < nxp) *reinterpret_cast<u32x4*>(x_lds + 8 * i) = xv[j];
+          if (j < per && i < nxp) *reinterpret_cast<u32x4*>(x_lds + 8 * i) = xv[j];
         }
       };
       x_round(threadIdx.x);
@@ -290,24 +323,38 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       load_q(B0, wave);
       load_q(B1, wave + step);
       __builtin_amdgcn_sched_barrier(0);
+      // x arrived, the codes may not have: the loads after x are 2 U code
+      // pieces per batch, + 2 U scales with block-wise scales (the
+      // compiler's own count gives up on the conditional loads above)
+      if (PC)
+        __builtin_amdgcn_s_waitcnt(kVmcnt<4 * U>);
+      else
+        __builtin_amdgcn_s_waitcnt(kVmcnt<8 * U>);
       x_store(threadIdx.x);
-      for (int i0 = threadIdx.x + 64 * NS * XB; i0 < nxp; i0 += 64 * NS * XB) {
+      for (int i0 = threadIdx.x + 64 * NS * per; i0 < nxp; i0 += 64 * NS * per) {
         x_round(i0);
         x_store(i0);
       }
+      // wave 0: the tile row's outlier entries load while the codes stream
+      if (wave == 0) stage_first_batch();
       __syncthreads();
     }
     load_x(B0, wave);
     load_x(B1, wave + step);
-    if (wave == 0) stage_first_batch();
+    // wave 0 sums the outliers' products in its third pass of the loop (or
+    // its last, if sooner): by then their entries have arrived, and the
+    // loads of the passes before went out without waiting for them (summed
+    // in the first pass, their round trips held up the stream; after the
+    // last, they added a tail)
+    const int c_out = wave + 2 * step * min(2, (nchunks - 1 - wave) / (2 * step));
     for (int c0 = wave; c0 < nchunks; c0 += 2 * step) {
       __builtin_amdgcn_sched_barrier(0);
-      if (wave == 0 && c0 == 0) gather_x();
+      if (wave == 0 && c0 == c_out) gather_x();
       compute(B0);
       __builtin_amdgcn_sched_barrier(0);
       load(B0, c0 + 2 * step);
       __builtin_amdgcn_sched_barrier(0);
-      if (wave == 0 && c0 == 0) outlier_sums();
+      if (wave == 0 && c0 == c_out) outlier_sums();
       __builtin_amdgcn_sched_barrier(0);
       compute(B1);
       __builtin_amdgcn_sched_barrier(0);
@@ -352,7 +399,7 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
 #pragma unroll
     for (int w = 0; w < NS; w++) dense += red[w][(16 * (m >> 2) + nl) * 4 + (m & 3)];
     const float v = dense + s_osum[m][nl] + (float)bits_to_h((uint16_t)bias_v);
-    W.y[(size_t)m * N + n0 + nl] = h_to_bits(rn_h(v));
+    W.y[(size_t)m * W.ldy + n0 + nl] = h_to_bits(rn_h(v));
   }
 }
 
@@ -368,7 +415,7 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
 // barrier does not wait for them, so the loads of groups j + 1 and j + 2 stay
 // in flight while group j is computed, and the zero that an out-of-range
 // buffer load returns stands in for the rows of x past M, the chunks past K
-// and the tile rows past N (no memory is read for them).  The S partial
+// and the tile rows past the piece (no memory is read for them).  The S partial
 // sums meet in LDS; outliers are added per lane in the epilogue, where a
 // lane owns one output column and 4 MG of its rows.
 
@@ -386,31 +433,29 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   __shared__ __attribute__((aligned(16))) uint16_t xs[2][XR * XW];
   __shared__ uint32_t x_ent[TR][kXCsrCap];  // (value << 16) | column of the tile row's first outliers
 
-  int mi = 0;
-#pragma unroll
-  for (int j = 1; j < kMaxGroup; j++)
-    if (j < a.count && (int)blockIdx.x >= a.first[j]) mi = j;
-  const QLMat W = pick(a, mi);
+  const GemvIn in = gemv_in(a);
+  const QLMat& W = in.w;
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int tr = wave % TR, sp = wave / TR;
-  const int M = a.M, K = a.K, N = W.N;
+  const int M = in.M, K = in.K;
   const int nchunks = K >> 7;
-  const int nrb = N / 16;
-  const int rb0 = (blockIdx.x - a.first[mi]) * TR;
-  const int rows_here = min(TR, nrb - rb0);  // tile rows of this workgroup inside N
+  const int nrb = W.N / 16;
+  const int rb0 = blockIdx.x * TR;  // in the piece
+  if (rb0 >= nrb) return;  // the grid is as wide as the longest piece
+  const int rows_here = min(TR, nrb - rb0);  // tile rows of this workgroup inside the piece
   const int grp = lane >> 4, li = lane & 15;
   const int ngroups = (nchunks + S - 1) / S;
   const int nsteps = (ngroups + 1) & ~1;    // even: the loop body handles two groups
 
   const __amdgpu_buffer_rsrc_t xr =
-      __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, M * K * 2, kBufferDword3);
+      __builtin_amdgcn_make_buffer_rsrc((void*)in.x, (short)0, M * K * 2, kBufferDword3);
   const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W.codes + ((size_t)rb0 * nchunks << 11)), (short)0, rows_here * nchunks * 2048, kBufferDword3);
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W.scales + (size_t)rb0 * 16 * W.kg), (short)0, rows_here * 16 * W.kg * 2, kBufferDword3);
-  // tile rows past N: every code load of the wave is out of range (zero)
+  // tile rows past the piece: every code load of the wave is out of range (zero)
   const uint32_t code_base = tr < rows_here ? (uint32_t)(tr * nchunks * 2048 + lane * 16) : kOutOfRange;
   const uint32_t scale_row = (uint32_t)(tr * 16 + li) * W.kg;
   uint16_t sb_row = 0;
@@ -582,7 +627,7 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
         const int m = min(16 * gi + 4 * grp + i, M - 1);
         float xg[8];
 #pragma unroll
-        for (int b = 0; b < 8; b++) xg[b] = (float)bits_to_h(a.x[(size_t)m * K + col[b]]);
+        for (int b = 0; b < 8; b++) xg[b] = (float)bits_to_h(in.x[(size_t)m * K + col[b]]);
 #pragma unroll
         for (int b = 0; b < 8; b++) acc[gi][i] = __builtin_fmaf(xg[b], wv[b], acc[gi][i]);
       }
@@ -593,7 +638,7 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int m = 16 * gi + 4 * grp + i;
-      if (m < M) W.y[(size_t)m * N + n] = h_to_bits(rn_h(acc[gi][i] + bv));
+      if (m < M) W.y[(size_t)m * W.ldy + n] = h_to_bits(rn_h(acc[gi][i] + bv));
     }
 }
 
@@ -1295,75 +1340,118 @@ int log2_exact(int64_t g) {
   return s;
 }
 
+// GEMV launches take their matrix from blockIdx.y: the group's matrices are
+// cut into pieces of at most P tile rows, one grid row per piece, with P a
+// multiple of `unit` (the tile rows of one workgroup) chosen so that at most
+// kMaxPieces pieces leave the fewest workgroups idle (the grid is as wide as
+// the longest piece).  Returns the grid; *g gets the pieces.
+dim3 gemv_pieces(const QLArgs& a, int unit, QLArgs* g) {
+  const int64_t nch = a.K >> 7;
+  int rmax = 0;
+  for (int i = 0; i < a.count; i++) rmax = std::max(rmax, a.mat[i].N / 16);
+  int P = 0;
+  int64_t best = INT64_MAX;
+  // d = 1 always fits: a group holds at most kMaxGroup <= kMaxPieces matrices
+  for (int d = 1; d <= kMaxPieces; d++) {
+    const int p = (int)(aq::ceil_div(aq::ceil_div(rmax, d), unit) * unit);
+    int n = 0;
+    for (int i = 0; i < a.count; i++) n += (int)aq::ceil_div(a.mat[i].N / 16, p);
+    const int64_t idle_and_busy = aq::ceil_div(p, unit) * (int64_t)n;
+    if (n <= kMaxPieces && idle_and_busy < best) {
+      best = idle_and_busy;
+      P = p;
+    }
+  }
+  *g = a;
+  int n = 0;
+  for (int i = 0; i < a.count; i++) {
+    const QLMat& w = a.mat[i];
+    for (int r0 = 0; r0 < w.N / 16; r0 += P) {
+      QLMat& q = g->mat[n++];
+      const int row0 = 16 * r0;
+      q = w;
+      q.codes = w.codes + ((size_t)r0 * nch << 11);
+      q.scales = w.scales + (size_t)row0 * w.kg;
+      q.row_ptr = w.row_ptr + row0;
+      q.bias = w.bias ? w.bias + row0 : nullptr;
+      q.y = w.y + row0;
+      q.N = 16 * std::min(P, w.N / 16 - r0);
+      q.ldy = w.N;
+      q.tptr = nullptr;
+      q.tent = nullptr;
+    }
+  }
+  g->count = n;
+  return dim3((unsigned)aq::ceil_div(P, unit), (unsigned)n);
+}
+
 template <int NS, int FMT>
-hipError_t launch_gemv(const QLArgs& a, bool per_channel, int blocks, hipStream_t s) {
-  // decode (M = 1) with x small enough and at most 4 waves per tile row: x in
-  // LDS (dynamic size).  With 8 waves per tile row (short matrices, 1 to 2
-  // workgroups per CU) the staging latency costs more than the x loads it
-  // saves (measured).
-  // Decode gets instances for one row of x (no registers or loads for more).
-  const bool x1 = a.M == 1 && a.K <= kGemvX1MaxK && NS <= 4;
+hipError_t launch_gemv(const QLArgs& a, bool per_channel, hipStream_t s) {
+  // decode (M = 1) with x small enough: x in LDS (dynamic size), read by
+  // every wave from there instead of by 4 loads per chunk and lane of which
+  // 60 of 64 lanes are out of range (each load instruction occupies the
+  // CU's address unit the same time: on short matrices, whose 8 waves per
+  // tile row issue all their loads at once, those loads were the start-up
+  // queue).  Decode gets instances for one row of x (no registers or loads
+  // for more).
+  const bool x1 = a.M == 1 && a.K <= kGemvX1MaxK;
   const size_t lds = x1 ? (size_t)a.K * 2 + 64 : 0;
   constexpr int R = kGemvDirectMaxM;
-  const dim3 g(blocks), b(64 * NS);
+  QLArgs p;
+  const dim3 g = gemv_pieces(a, 1, &p), b(64 * NS);
   if (per_channel) {
     if (x1)
-      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 1, 1>), g, b, lds, s, a);
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 1, 1>), g, b, lds, s, p);
     else if (a.M == 1)
-      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 0, 1>), g, b, 0, s, a);
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 0, 1>), g, b, 0, s, p);
     else
-      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 0, R>), g, b, 0, s, a);
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 0, R>), g, b, 0, s, p);
   } else {
     if (x1)
-      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 1, 1>), g, b, lds, s, a);
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 1, 1>), g, b, lds, s, p);
     else if (a.M == 1)
-      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 0, 1>), g, b, 0, s, a);
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 0, 1>), g, b, 0, s, p);
     else
-      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 0, R>), g, b, 0, s, a);
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 0, R>), g, b, 0, s, p);
   }
   return hipGetLastError();
 }
 
 template <int NS>
-hipError_t launch_gemv(const QLArgs& a, int fmt, bool per_channel, int blocks, hipStream_t s) {
-  return fmt == AQ_FMT_E4M3 ? launch_gemv<NS, AQ_FMT_E4M3>(a, per_channel, blocks, s)
-                            : launch_gemv<NS, AQ_FMT_INT8>(a, per_channel, blocks, s);
+hipError_t launch_gemv(const QLArgs& a, int fmt, bool per_channel, hipStream_t s) {
+  return fmt == AQ_FMT_E4M3 ? launch_gemv<NS, AQ_FMT_E4M3>(a, per_channel, s)
+                            : launch_gemv<NS, AQ_FMT_INT8>(a, per_channel, s);
 }
 
 template <int FMT, int MG, int S>
-hipError_t launch_gemv_x(const QLArgs& a, bool per_channel, int blocks, hipStream_t s) {
+hipError_t launch_gemv_x(const QLArgs& a, bool per_channel, hipStream_t s) {
+  QLArgs p;
+  const dim3 g = gemv_pieces(a, kXWaves / S, &p);  // workgroups of 8 / S tile rows
   if (per_channel)
-    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 1, MG, S>), dim3(blocks), dim3(64 * kXWaves), 0, s, a);
+    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 1, MG, S>), g, dim3(64 * kXWaves), 0, s, p);
   else
-    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 0, MG, S>), dim3(blocks), dim3(64 * kXWaves), 0, s, a);
+    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 0, MG, S>), g, dim3(64 * kXWaves), 0, s, p);
   return hipGetLastError();
 }
 
 template <int MG, int S>
-hipError_t launch_gemv_x(const QLArgs& a, int fmt, bool per_channel, int blocks, hipStream_t s) {
-  return fmt == AQ_FMT_E4M3 ? launch_gemv_x<AQ_FMT_E4M3, MG, S>(a, per_channel, blocks, s)
-                            : launch_gemv_x<AQ_FMT_INT8, MG, S>(a, per_channel, blocks, s);
+hipError_t launch_gemv_x(const QLArgs& a, int fmt, bool per_channel, hipStream_t s) {
+  return fmt == AQ_FMT_E4M3 ? launch_gemv_x<AQ_FMT_E4M3, MG, S>(a, per_channel, s)
+                            : launch_gemv_x<AQ_FMT_INT8, MG, S>(a, per_channel, s);
 }
 
 // 6 <= M <= 64: x row groups of 16 per MFMA (MG = 1, 2, 3 or 4 for M up to 16, 32, 48, 64),
-// S = 2 or 4 waves per tile row; a.first counts workgroups of 8 / S tile rows
-hipError_t launch_gemv_x(QLArgs a, int fmt, bool per_channel, int S, hipStream_t s) {
-  const int TR = kXWaves / S;
-  int wgs = 0;
-  for (int i = 0; i < a.count; i++) {
-    a.first[i] = wgs;
-    wgs += (int)aq::ceil_div(a.mat[i].N / 16, TR);
-  }
-  for (int i = a.count; i <= kMaxGroup; i++) a.first[i] = wgs;
+// S = 2 or 4 waves per tile row
+hipError_t launch_gemv_x(const QLArgs& a, int fmt, bool per_channel, int S, hipStream_t s) {
   if (a.M <= 16)
-    return S == 2 ? launch_gemv_x<1, 2>(a, fmt, per_channel, wgs, s)
-           : S == 4 ? launch_gemv_x<1, 4>(a, fmt, per_channel, wgs, s) : launch_gemv_x<1, 8>(a, fmt, per_channel, wgs, s);
+    return S == 2 ? launch_gemv_x<1, 2>(a, fmt, per_channel, s)
+           : S == 4 ? launch_gemv_x<1, 4>(a, fmt, per_channel, s) : launch_gemv_x<1, 8>(a, fmt, per_channel, s);
   if (a.M <= 32)
-    return S == 2 ? launch_gemv_x<2, 2>(a, fmt, per_channel, wgs, s)
-           : S == 4 ? launch_gemv_x<2, 4>(a, fmt, per_channel, wgs, s) : launch_gemv_x<2, 8>(a, fmt, per_channel, wgs, s);
+    return S == 2 ? launch_gemv_x<2, 2>(a, fmt, per_channel, s)
+           : S == 4 ? launch_gemv_x<2, 4>(a, fmt, per_channel, s) : launch_gemv_x<2, 8>(a, fmt, per_channel, s);
   if (a.M <= 48)
-    return S == 2 ? launch_gemv_x<3, 2>(a, fmt, per_channel, wgs, s) : launch_gemv_x<3, 4>(a, fmt, per_channel, wgs, s);
-  return S == 2 ? launch_gemv_x<4, 2>(a, fmt, per_channel, wgs, s) : launch_gemv_x<4, 4>(a, fmt, per_channel, wgs, s);
+    return S == 2 ? launch_gemv_x<3, 2>(a, fmt, per_channel, s) : launch_gemv_x<3, 4>(a, fmt, per_channel, s);
+  return S == 2 ? launch_gemv_x<4, 2>(a, fmt, per_channel, s) : launch_gemv_x<4, 4>(a, fmt, per_channel, s);
 }
 
 template <int BM, int FMT, int DENSE>
@@ -1501,7 +1589,7 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
   AQ_CHECK_ARG(fmt == AQ_FMT_INT8 || fmt == AQ_FMT_E4M3, "aq_qlinear: unknown code format %d", fmt);
   AQ_CHECK_ARG(x && Ns && codes && scales && Gs && row_ptrs && cols && vals && ys, "aq_qlinear: null pointer argument");
   AQ_CHECK_ARG((uintptr_t)x % 16 == 0, "aq_qlinear: x must be 16-byte aligned");
-  QLArgs a;
+  QLArgs a{};
   a.x = (const uint16_t*)x;
   a.M = (int)M;
   a.K = (int)K;
@@ -1535,6 +1623,7 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
     w.y = (uint16_t*)ys[j];
     w.part = nullptr;
     w.N = (int)N;
+    w.ldy = (int)N;
     w.G = (int)G;
     w.kg = (int)(K / G);
     w.gshift = log2_exact(G);
@@ -1564,10 +1653,10 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
     // waves per tile row: enough for about 1536 waves in all (1.5 per SIMD),
     // at most 8; a tall group (gate+up) streams one tile row per wave
     const int64_t want = (1536 + blocks - 1) / blocks;
-    const hipError_t e = want <= 1 ? launch_gemv<1>(a, fmt, per_channel, (int)blocks, s)
-                       : want <= 2 ? launch_gemv<2>(a, fmt, per_channel, (int)blocks, s)
-                       : want <= 4 ? launch_gemv<4>(a, fmt, per_channel, (int)blocks, s)
-                                   : launch_gemv<8>(a, fmt, per_channel, (int)blocks, s);
+    const hipError_t e = want <= 1 ? launch_gemv<1>(a, fmt, per_channel, s)
+                       : want <= 2 ? launch_gemv<2>(a, fmt, per_channel, s)
+                       : want <= 4 ? launch_gemv<4>(a, fmt, per_channel, s)
+                                   : launch_gemv<8>(a, fmt, per_channel, s);
     return aq::check_hip(e, "aq_qlinear: gemv launch");
   }
   bool dense = false;  // some 16 x 64 block holds more than 64 outliers

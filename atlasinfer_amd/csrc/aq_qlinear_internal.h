@@ -14,6 +14,9 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int kMaxGroup = 4;
+// GEMV launches cut a group's matrices into up to this many pieces of equal
+// tile-row count, one grid row (blockIdx.y) per piece
+constexpr int kMaxPieces = 8;
 
 struct QLMat {
   const uint8_t* codes;  // tiled
@@ -26,18 +29,19 @@ struct QLMat {
   const uint16_t* bias;
   uint16_t* y;
   float* part;  // GEMM split over K: this matrix's fp32 partial sums [split][M][N]
-  int N;
+  int N;       // rows (of a GEMV piece: the rows it covers)
   int G;
   int kg;      // K / G, scale blocks per row
   int gshift;  // log2(G) when G is a power of two, else -1
+  int ldy;     // row stride of y: the whole matrix's N
 };
 
 struct QLArgs {
   const uint16_t* x;
   int M, K, count;
   int split;                 // GEMM: ways the K chunks are split (1: none)
-  int first[kMaxGroup + 1];  // GEMV: first workgroup of each matrix
-  QLMat mat[kMaxGroup];
+  int first[kMaxGroup + 1];  // GEMM: first output tile of each matrix
+  QLMat mat[kMaxPieces];     // GEMM: the group's matrices; GEMV: their pieces
 };
 
 // The matrix a workgroup works on (workgroup-uniform selection, no dynamic

@@ -170,17 +170,23 @@ int aq_zscore(const void* x, int64_t n, float eps, void* z, void* stats, void* s
  *   tile_max              the largest entry count of any block (max of
  *                         tile_ptr[b+1] - tile_ptr[b]); above 64 the GEMM
  *                         takes a variant that reads the excess from memory
- * M <= 64 runs the dequant-GEMV, which adds the outliers from the CSR lists in
- * fp32; larger M the dequant-GEMM, which writes each outlier's fp16 value over
- * its decoded zero in the weight tile it multiplies.  Either way the result is
- * x times the dequantized weight accumulated in fp32, plus the bias, rounded
- * once to fp16.
+ * Which kernels run:
+ *   M <= 5        dequant-GEMV, each 16-row tile row reading x directly;
+ *   6 <= M <= 64  dequant-GEMV sharing x through LDS, except that from
+ *                 M = 33 on, grids of fewer than 384 tile rows (N < 6144,
+ *                 summed over a group) take the dequant-GEMM when tile_ptr
+ *                 and tile_ent are given;
+ *   M > 64        dequant-GEMM (tile_ptr, tile_ent required).
+ * The GEMV adds the outliers from the CSR lists in fp32; the GEMM writes each
+ * outlier's fp16 value over its decoded zero in the weight tile it
+ * multiplies.  Either way the result is x times the dequantized weight
+ * accumulated in fp32, plus the bias, rounded once to fp16.
  * workspace: aq_qlinear_workspace_size(M, N, K) bytes, 16-byte aligned, or
- * NULL.  The GEMM splits K 2 or 4 ways when its grid would leave CUs idle
- * (k/v projections at M = 2048, most weights at M = 512) and keeps the fp32
+ * NULL.  A nonzero size means the GEMM would split K (2, 4 or 8 ways, chosen
+ * from a time estimate of the shape on the current device) and keep the fp32
  * partial sums there; a second kernel adds them in a fixed order, so results
- * are deterministic.  With NULL (or too small a workspace) it runs unsplit.
- * The GEMV (M <= 64) uses none.
+ * are deterministic.  A smaller workspace, or NULL, only limits the split (to
+ * what it holds, down to none).  0 for every GEMV call.
  */
 int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K);
 int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const void* codes, const void* scales,
@@ -195,9 +201,10 @@ int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const void* codes
  * cols[i], vals[i], tile_ptrs[i], tile_ents[i], tile_maxes[i], biases[i]
  * (entries may be NULL), Ns[i] rows.  All W_i share K and fmt.  count <= 4.
  * The arrays themselves are host memory; tile_ptrs/tile_ents/tile_maxes may
- * be NULL when M <= 64.  workspace: the sum over i of
- * aq_qlinear_workspace_size(M, Ns[i], K) bytes, or NULL (as for aq_qlinear).
- * Same per-matrix requirements as aq_qlinear.
+ * be NULL when M <= 64.  workspace: aq_qlinear_workspace_size(M, N, K)
+ * bytes with N the sum of Ns (the group is planned over all its output
+ * columns), or less, or NULL (as for aq_qlinear).  Same per-matrix
+ * requirements as aq_qlinear.
  */
 int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, int64_t count, const int64_t* Ns,
                        const void* const* codes, const void* const* scales, const int64_t* Gs,

@@ -221,6 +221,19 @@ class QuantizedLinear(nn.Module):
             self.bias = self.bias.to(device)
         return q
 
+    def _set_weights(self, q: QuantizedTensor, bias: Optional[torch.Tensor]) -> None:
+        """Assign weight and bias, dropping everything derived from the
+        previous ones (codes, block lists, prepared arguments, the sibling
+        group's prepared call and kept outputs)."""
+        self.quantized_weights = q
+        self.bias = bias
+        self._derived_from = self._codes = self._tiles = self._prep = None
+        g = self._group
+        if g is not None:
+            g._prep = None
+            g.out = {}
+            g.x = None
+
     def _ensure_codes(self, q: QuantizedTensor, dev: torch.device) -> None:
         if self._derived_from is not q:  # a weight assigned since (q is on dev here)
             self._derived_from, self._codes, self._tiles = q, None, None

@@ -166,3 +166,76 @@ def link_sibling_linears(model: nn.Module, names=SIBLING_NAMES) -> int:
                 m._group = g
             n += 1
     return n
+
+
+FINAL_NORM_PATHS = ("model.decoder.final_layer_norm", "model.norm", "decoder.norm")
+
+
+def _shares_parameters(module: nn.Module, model: nn.Module) -> bool:
+    """Whether a parameter of ``module`` also belongs to a module outside it
+    (a tied lm_head / embedding weight)."""
+    own = {id(p) for p in module.parameters()}
+    inside = {id(m) for m in module.modules()}
+    for m in model.modules():
+        if id(m) in inside:
+            continue
+        if any(id(p) in own for p in m.parameters(recurse=False)):
+            return True
+    return False
+
+
+def setup_offloading_hooks(model: nn.Module, model_type: str, gpu_device: torch.device, prefetch_depth: int = 1):
+    """Stream the weights of the decoder blocks, the final norm and the
+    lm_head from pinned host memory (reference :211-268, which attaches
+    QuantizedTensorOffloadHook with offload=True to the same modules).
+
+    Every hooked module's parameters, buffers and QuantizedLinear weights
+    move to pinned host memory now; in a forward, each module's weights are
+    on ``gpu_device`` only for its own forward, and the next
+    ``prefetch_depth`` modules (in forward order, the first blocks again
+    after the lm_head) are copied on a side stream meanwhile (0: each
+    module's copy is issued at its own forward).  Unlike the reference, the
+    final norm is hooked whatever its type and the lm_head whatever its type
+    unless its weight is tied to a module outside it (that one stays where
+    it is).  Modules that are not hooked (embeddings, rotary tables) stay
+    where they are.  Returns the WeightStreamer (its ``stats`` count the
+    prefetched and on-demand copies and the bytes copied)."""
+    from accelerate.hooks import add_hook_to_module
+
+    from ..utils.weight_offloader import QuantizedTensorOffloadHook, WeightStreamer
+
+    print("\n--- Setting up weight streaming hooks ---")
+    patterns = _get_model_patterns(model_type)
+    if patterns is None:
+        print("ERROR: No patterns.")
+        return None
+    path = patterns.get("decoder_block_path")
+    try:
+        blocks = model.get_submodule(path)
+    except AttributeError:
+        print(f"Warn: decoder block path '{path}' not found.")
+        return None
+    if not isinstance(blocks, nn.ModuleList):
+        print("Warn: decoder blocks are not an nn.ModuleList.")
+        return None
+    streamer = WeightStreamer(gpu_device, depth=prefetch_depth)
+    hooked = list(blocks)
+    for p in FINAL_NORM_PATHS:
+        try:
+            hooked.append(model.get_submodule(p))
+            break
+        except AttributeError:
+            continue
+    lm_head = getattr(model, "lm_head", None)
+    if lm_head is not None:
+        if _shares_parameters(lm_head, model):
+            print("lm_head shares its weight with another module: left in place.")
+        else:
+            hooked.append(lm_head)
+    for m in hooked:
+        streamer.register(m)
+        add_hook_to_module(m, QuantizedTensorOffloadHook(execution_device=streamer.device, offload=True,
+                                                         streamer=streamer))
+    print(f"--- Streaming {len(hooked)} modules ({streamer.host_bytes() / 2**20:.1f} MiB pinned), "
+          f"prefetch depth {prefetch_depth} ---")
+    return streamer

@@ -382,6 +382,14 @@ def dequantize_tensor(quant_data: QuantizedTensor, target_device: torch.device) 
     return final
 
 
+def discard_dequantized(quant_data_id: int) -> None:
+    """Drop the cached fp16 copy of one QuantizedTensor (by id), without
+    returning the allocator's cached blocks to the device (the per-layer
+    counterpart of clear_dequantized_cache for code that runs every step)."""
+    with _cache_lock:
+        _dequantized_weights_cache.pop(quant_data_id, None)
+
+
 def clear_dequantized_cache(quant_data_id=None):
     """Clear one entry (by id) or the whole cache (reference :253-263)."""
     global _dequantized_weights_cache

@@ -381,6 +381,45 @@ def linear_flops(model, tokens):
     return sum(2 * m.in_features * m.out_features for m in model.modules() if isinstance(m, torch.nn.Linear)) * tokens
 
 
+def host_link_gbs(dev, nbytes=256 << 20, reps=5):
+    """Pinned host -> device copy rate on a side stream: the ceiling of
+    weight streaming."""
+    h = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    d = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    s = torch.cuda.Stream(device=dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        d.copy_(h, non_blocking=True)
+        e0.record(s)
+        for _ in range(reps):
+            d.copy_(h, non_blocking=True)
+        e1.record(s)
+    e1.synchronize()
+    return nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+
+
+def bench_streaming(model, ids, dev, log, new_tokens=32):
+    """The quantized model of config 1 with its decoder blocks, final norm
+    and lm_head streamed from pinned host memory (setup_offloading_hooks):
+    decode tok/s and the host -> device rate it implies (every streamed byte
+    is copied once per token), at prefetch depth 1 and 0, against the
+    pinned-copy rate of the link."""
+    from atlasinfer_amd.integration.model_modifier import setup_offloading_hooks
+    link = host_link_gbs(dev)
+    streamer = setup_offloading_hooks(model, "opt", dev, prefetch_depth=1)
+    per_token = streamer.host_bytes()
+    res = {"bytes_per_token": per_token, "link_gbs": round(link, 1), "new_tokens": new_tokens}
+    for depth in (1, 0):
+        streamer.depth = depth
+        tps, _ = generate_tokps(model, ids, new_tokens)
+        rate = tps * per_token / 1e9
+        res[f"depth{depth}_decode_tok_s"] = round(tps, 2)
+        res[f"depth{depth}_h2d_gbs"] = round(rate, 1)
+        res[f"depth{depth}_frac_of_link"] = round(rate / link, 3)
+    res["stats"] = dict(streamer.stats)
+    return res
+
+
 def bench_models(dev, which, log):
     """BASELINE configs 1 (OPT-1.3b, every Linear quantized, 32-token prompt,
     128 greedy tokens, batch 1) and 3 (Mistral-7B, 512-token prompts, 256
@@ -412,6 +451,8 @@ def bench_models(dev, which, log):
                           "linears_quantized": rep, "failed": fail, "quantize_s": round(t_q, 2),
                           "prompt": 32, "new_tokens": 128, "batch": 1}
         log(f"OPT-1.3b: {out['opt1.3b']}")
+        out["opt1.3b_streamed"] = bench_streaming(model, ids, dev, log)
+        log(f"OPT-1.3b streamed from host memory: {out['opt1.3b_streamed']}")
         del model
         torch.cuda.empty_cache()
     if "mistral" in which:

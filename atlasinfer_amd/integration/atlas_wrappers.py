@@ -14,6 +14,9 @@ registers and never written back as fp16.  Weights that do not tile
 (out_features % 16, in_features % 128, or a block size that is not a
 multiple of 32 dividing in_features) take the dequantize kernel followed by
 F.linear on the GPU.
+
+``AtlasAttentionWrapper`` (reference :84-262) keeps an attention module's
+key/value history in a UnifiedMemoryManager (tiered KV cache).
 """
 from __future__ import annotations
 
@@ -339,3 +342,67 @@ class QuantizedLinear(nn.Module):
             except AttributeError:
                 pass
         return f"quantized_shape={q_shape}, bias={self.bias is not None}, device={q_device}"
+
+
+class AtlasAttentionWrapper(nn.Module):
+    """An attention module whose key/value history lives in a
+    UnifiedMemoryManager (reference :84-262).
+
+    Constructor as the reference's: ``(q_proj, k_proj, v_proj, o_proj,
+    parent_layer, memory_manager, layer_idx, model_type)``.  The wrapped
+    module is the decoder layer's own attention (``parent_layer.self_attn``),
+    whose forward still does the projections (QuantizedLinear after the
+    swap), the rotary embedding, the masks and the attention itself; the
+    wrapper makes the HF cache it is handed keep this layer's keys and
+    values in the manager (``KVCacheLayer``: appended in place in HBM,
+    demoted to host memory or disk when the manager's limits say so).  A new
+    cache object starts the layer's history afresh.
+
+    Unlike the reference's, which recomputed attention itself: the rotary
+    embedding is applied to the new positions only (the reference applied
+    it again to the whole concatenated history each step), the causal mask
+    of a prompt is kept, OPT's query scaling is applied once, and Llama's
+    ``o_proj`` is found as well as OPT's ``out_proj``.  Results equal the
+    unwrapped model's on the same inputs."""
+
+    def __init__(self, q_proj: nn.Module, k_proj: nn.Module, v_proj: nn.Module, o_proj: nn.Module,
+                 parent_layer: nn.Module, memory_manager, layer_idx: int, model_type: str):
+        super().__init__()
+        inner = getattr(parent_layer, "self_attn", None)
+        if inner is None or not all(p is not None for p in (q_proj, k_proj, v_proj, o_proj)):
+            raise ValueError(f"CRITICAL: no attention module or projections in layer {layer_idx}")
+        # the wrapped module's children under their own names (state-dict keys
+        # unchanged); the module itself stays outside the module tree
+        for name, child in inner.named_children():
+            setattr(self, name, child)
+        object.__setattr__(self, "_inner", inner)
+        self.memory_manager = memory_manager
+        self.layer_idx = layer_idx
+        self.model_type = model_type
+        self._bound = None  # the HF cache whose layer entry is the manager's
+
+    def _bind(self, cache) -> None:
+        from ..memory.unified_memory_manager import KVCacheLayer
+        idx = getattr(self._inner, "layer_idx", self.layer_idx)
+        layers = getattr(cache, "layers", None)
+        if layers is None:
+            raise TypeError(f"AtlasAttentionWrapper: unsupported cache type {type(cache).__name__}")
+        while len(layers) <= idx:
+            layers.append(cache.layer_class_to_replicate())
+        cur = layers[idx]
+        if isinstance(cur, KVCacheLayer) and cur.manager is self.memory_manager:
+            return
+        if getattr(cur, "is_sliding", False):
+            raise NotImplementedError("AtlasAttentionWrapper: sliding-window cache layers are not supported")
+        self.memory_manager.reset_layer(idx)  # a new cache: a new history
+        layers[idx] = KVCacheLayer(self.memory_manager, idx)
+
+    def forward(self, hidden_states, *args, **kwargs):
+        for key in ("past_key_values", "past_key_value"):
+            cache = kwargs.get(key)
+            if cache is not None:
+                if cache is not self._bound:
+                    self._bind(cache)
+                    self._bound = cache
+                break
+        return self._inner(hidden_states, *args, **kwargs)

@@ -239,3 +239,49 @@ def setup_offloading_hooks(model: nn.Module, model_type: str, gpu_device: torch.
     print(f"--- Streaming {len(hooked)} modules ({streamer.host_bytes() / 2**20:.1f} MiB pinned), "
           f"prefetch depth {prefetch_depth} ---")
     return streamer
+
+
+def apply_atlas_attention_wrapper(model: nn.Module, model_type: str, memory_manager) -> Tuple[int, int]:
+    """Wrap every decoder layer's attention (the pattern's attention class
+    names) in an AtlasAttentionWrapper bound to ``memory_manager``, in place
+    (reference :146-208).  Returns (wrapped, failed)."""
+    from .atlas_wrappers import AtlasAttentionWrapper
+
+    print(f"\n--- Applying Atlas Attention Wrapper ({model_type}) ---")
+    patterns = _get_model_patterns(model_type)
+    if patterns is None:
+        print("ERROR: No patterns.")
+        return 0, 0
+    names = patterns.get("attention_type", [])
+    names = names if isinstance(names, list) else [names]
+    path, sub = patterns.get("decoder_block_path"), patterns.get("attention_subpath")
+    try:
+        layers = model.get_submodule(path)
+    except AttributeError:
+        print(f"Warn: Path not found: {path}")
+        return 0, 0
+    wrapped, failed = 0, 0
+    for idx, layer in enumerate(layers):
+        chain = sub.split(".")
+        parent = layer.get_submodule(".".join(chain[:-1])) if len(chain) > 1 else layer
+        attn = getattr(parent, chain[-1], None)
+        if isinstance(attn, AtlasAttentionWrapper):
+            print(f"Skipping wrapped layer {idx}.")
+            continue
+        if attn is None or type(attn).__name__ not in names:
+            print(f"Warn: Type {type(attn).__name__} layer {idx} not target. Skip.")
+            failed += 1
+            continue
+        q, k, v = (getattr(attn, n, None) for n in ("q_proj", "k_proj", "v_proj"))
+        o = getattr(attn, "o_proj", None) or getattr(attn, "out_proj", None)
+        try:
+            w = AtlasAttentionWrapper(q, k, v, o, parent_layer=layer, memory_manager=memory_manager,
+                                      layer_idx=idx, model_type=model_type)
+        except ValueError as e:
+            print(f"!! FAILED WRAP layer {idx}: {e}")
+            failed += 1
+            continue
+        _replace_module(parent, chain[-1], w)
+        wrapped += 1
+    print(f"--- Attention wrapping complete. Wrapped: {wrapped}, Failed/Skipped: {failed} ---")
+    return wrapped, failed

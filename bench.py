@@ -420,6 +420,49 @@ def bench_streaming(model, ids, dev, log, new_tokens=32):
     return res
 
 
+def bench_kv_cache(dev, log, steps=64):
+    """Per decode step, the key/value cache update of all 32 layers of
+    Mistral-7B (batch 1, 8 KV heads of 128, fp16) after a prompt of S
+    positions: HF's DynamicCache (the history concatenated with the new
+    position each step, as the reference's attention did) against the tiered
+    cache's in-place append (capacity doubled when full, the doubling copy
+    included in the average).  Wall clock per step, GPU synchronised."""
+    from transformers import DynamicCache
+    from atlasinfer_amd.memory.unified_memory_manager import UnifiedMemoryManager
+    L, H, D = 32, 8, 128
+    out = {}
+    for S in (4096, 32768):
+        pre = [torch.randn(1, H, S, D, device=dev).half() for _ in range(2)]
+        new = [torch.randn(1, H, 1, D, device=dev).half() for _ in range(2)]
+        res = {}
+        for kind in ("dynamic_cache", "tiered"):
+            if kind == "dynamic_cache":
+                c = DynamicCache()
+                upd = lambda i, k, v, c=c: c.update(k, v, i)  # noqa: E731
+            else:
+                m = UnifiedMemoryManager(64.0, 1.0, None, gpu_device=dev)
+                upd = m.append_kv
+            for i in range(L):
+                upd(i, pre[0], pre[1])
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                for i in range(L):
+                    upd(i, new[0], new[1])
+            torch.cuda.synchronize()
+            res[f"{kind}_ms_per_step"] = round((time.perf_counter() - t0) / steps * 1e3, 3)
+            del upd
+            if kind == "dynamic_cache":
+                del c
+            else:
+                m.close()
+                del m
+            torch.cuda.empty_cache()
+        out[f"S{S}"] = res
+        log(f"KV cache update, Mistral-7B shapes, prompt {S}: {res}")
+    return out
+
+
 def bench_models(dev, which, log):
     """BASELINE configs 1 (OPT-1.3b, every Linear quantized, 32-token prompt,
     128 greedy tokens, batch 1) and 3 (Mistral-7B, 512-token prompts, 256
@@ -758,6 +801,7 @@ def main():
         import contextlib
         with contextlib.redirect_stdout(sys.stderr):  # stdout carries only the result line
             models = bench_models(dev, args.models.split(","), log)
+            models["kv_cache_update"] = bench_kv_cache(dev, log)
 
     # ---- the reference's CPU path on this host (warm F.linear, M=1)
     cpu = None

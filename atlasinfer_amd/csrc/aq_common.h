@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/atlasinfer_amd.h"
 
 typedef _Float16 f16;
@@ -29,6 +31,21 @@ int check_hip(hipError_t e, const char* what);
   } while (0)
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Compute units of the current device, queried once per device (any host
+// thread; the cache is atomic).
+inline int cu_count() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    int v = 0;
+    n = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0 ? v : 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 
 }  // namespace aq
 
@@ -168,6 +185,18 @@ __device__ __forceinline__ double xlane_level_sum_f64(double v) {
 }
 
 template <int L>
+__device__ __forceinline__ float xlane_level_sum_f32(float v) {
+  const uint32_t x = __builtin_bit_cast(uint32_t, v);
+  if constexpr (L <= 4) {
+    return v + __builtin_bit_cast(float, xlane_partner_u32<L>(x));
+  } else {
+    uint32_t a, b;
+    xlane_swap_u32<L>(x, a, b);
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+  }
+}
+
+template <int L>
 __device__ __forceinline__ float xlane_level_max_f32(float v) {
   const uint32_t x = __builtin_bit_cast(uint32_t, v);
   if constexpr (L <= 4) {
@@ -188,6 +217,17 @@ __device__ __forceinline__ double wave_group_sum_f64(double v) {
   if constexpr (WL > 8) v = xlane_level_sum_f64<4>(v);
   if constexpr (WL > 16) v = xlane_level_sum_f64<5>(v);
   if constexpr (WL > 32) v = xlane_level_sum_f64<6>(v);
+  return v;
+}
+
+template <int WL>
+__device__ __forceinline__ float wave_group_sum_f32(float v) {
+  if constexpr (WL > 1) v = xlane_level_sum_f32<1>(v);
+  if constexpr (WL > 2) v = xlane_level_sum_f32<2>(v);
+  if constexpr (WL > 4) v = xlane_level_sum_f32<3>(v);
+  if constexpr (WL > 8) v = xlane_level_sum_f32<4>(v);
+  if constexpr (WL > 16) v = xlane_level_sum_f32<5>(v);
+  if constexpr (WL > 32) v = xlane_level_sum_f32<6>(v);
   return v;
 }
 
@@ -214,6 +254,31 @@ __device__ __forceinline__ double team_sum_f64(double v, double* lds_team) {
     if (lane == 0) lds_team[w] = v;
     __syncthreads();
     double t[NW];
+#pragma unroll
+    for (int i = 0; i < NW; i++) t[i] = lds_team[i];
+#pragma unroll
+    for (int s = NW; s > 1; s >>= 1)
+#pragma unroll
+      for (int i = 0; i < s / 2; i++) t[i] = t[2 * i] + t[2 * i + 1];
+    v = t[0];
+  }
+  return v;
+}
+
+// f32 sum over the team, the same value in every lane (the wave part is a
+// butterfly, the waves' partial sums are added in a fixed tree order).
+template <int TAU>
+__device__ __forceinline__ float team_sum_f32(float v, float* lds_team) {
+  constexpr int WL = TAU < 64 ? TAU : 64;
+  v = wave_group_sum_f32<WL>(v);
+  if constexpr (TAU > 64) {
+    constexpr int NW = TAU / 64;
+    const int lane = threadIdx.x & 63;
+    const int w = (threadIdx.x % TAU) >> 6;
+    __syncthreads();
+    if (lane == 0) lds_team[w] = v;
+    __syncthreads();
+    float t[NW];
 #pragma unroll
     for (int i = 0; i < NW; i++) t[i] = lds_team[i];
 #pragma unroll

@@ -1320,19 +1320,6 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, i
 // CU count of the current device, read once per device.  Any host thread
 // may call this: each slot is an atomic written with the same value by
 // whichever thread gets there first.
-int cu_count() {
-  static std::atomic<int> cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int n = cached[dev].load(std::memory_order_relaxed);
-  if (n == 0) {
-    int v = 0;
-    n = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0 ? v : 256;
-    cached[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
 int log2_exact(int64_t g) {
   if (g <= 0 || (g & (g - 1))) return -1;
   int s = 0;
@@ -1512,7 +1499,7 @@ GemmPlan plan_gemm(int64_t M, const int64_t* Ns, int64_t count, int64_t K, int m
   static constexpr Shape kShapes[] = {{kTile256x256, kWideBM, kWideBN, 1.8},
                                       {kTile256x128, 256, kGemmBN, 1.17},
                                       {kTile128x128, 128, kGemmBN, 0.74}};
-  const int64_t slots = cu_count();
+  const int64_t slots = aq::cu_count();
   const int64_t nch = K / kGemmBK;
   int64_t outs = 0;
   for (int i = 0; i < count; i++) outs += M * Ns[i];

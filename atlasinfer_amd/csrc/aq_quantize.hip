@@ -52,6 +52,8 @@ struct QuantArgs {
   int64_t K;        // row length for the tiled layout
   int64_t nchunks;  // K / 128
   int64_t bpr;      // tiled layout: blocks per row, K / G
+  double inv_g;     // RN64(1 / G)
+  float inv_g1;     // RN32(1 / (G - 1)) (G >= 2)
   uint8_t* codes;
   uint16_t* scales;
   int32_t* block_cnt;  // block_off, holds counts until the scan
@@ -406,10 +408,12 @@ __device__ __forceinline__ float sq_acc_hi(uint32_t p, float c) {  // hi * hi + 
   return r;
 }
 
-// The reference's mean of a block whose sum is S: fp16(f32(S / G)).  A
-// monotone non-decreasing function of S (f64 division by G > 0, then two
-// round-to-nearest conversions).
+// The reference's mean of a block whose sum is S: fp16(f32(S / G)), and its
+// std from V = sum (x - mean)^2: fp16(f32(sqrt(V / (G - 1)))).  Both are
+// monotone non-decreasing functions (f64 operations and round-to-nearest
+// conversions, each monotone).
 __device__ __forceinline__ f16 mean_of_sum(double S, int64_t G) { return rn_h((float)(S / (double)G)); }
+__device__ __forceinline__ f16 std_of_var(double V, int64_t G) { return rn_h((float)sqrt(V / (double)(G - 1))); }
 
 // mean / std / std + eps as block_stats computes them, from one pass of
 // single-precision sums in the common case:
@@ -418,24 +422,30 @@ __device__ __forceinline__ f16 mean_of_sum(double S, int64_t G) { return rn_h((f
 //        roundings of u = 2^-24 per thread, so |S_f32 - S| <= d u sum|x|
 //        (the f64 sum across the team adds under 2^-46 relative), and
 //        sum|x| <= sqrt(G Q) by Cauchy-Schwarz;
-//   Q  = sum x^2 (products exact in f32, four f32 chains per thread, f64
-//        across threads), within Q 2^-19 of the exact sum.
+//   Q  = sum x^2 (products exact in f32, four f32 chains of E / 8 per
+//        thread, then f32 across the team): a sum of non-negative terms
+//        with at most E / 8 + 2 + log2(TAU) roundings, within Q 2^-19.
 // mean16 is a monotone function of S, so when both ends of S_f32 +- errS
 // give the same mean16, that is the value the exact sum gives; std16 is a
 // monotone function of V = Q - S mu, accepted when both ends of V +- errV
-// (errV covers Q's error and S's) give the same std16.  Otherwise (a
-// near-tie, a non-finite sum, G < 2) the team falls back to the exact-order
-// f64 trees of block_stats: the sum, and the two-pass variance when std16
-// is the open one.  Every decision is the same in all lanes of the team (its
-// sums are), and for teams of several waves sharing a workgroup's barriers
-// it is taken by the whole workgroup.
+// (errV covers Q's error and S's) give the same std16.  The two ends are
+// evaluated with cheaper arithmetic than the functions themselves, on
+// arguments pushed outward by more than that arithmetic's error, so each end
+// still bounds the function's value at the true argument (see the comments
+// at each step).  Otherwise (a near-tie, a non-finite sum, G < 2) the team
+// falls back to the exact-order f64 trees of block_stats: the sum, and the
+// two-pass variance when std16 is the open one.  Every decision is the same
+// in all lanes of the team (its sums are), and for teams of several waves
+// sharing a workgroup's barriers it is taken by the whole workgroup.
 template <int TAU, int E, int MODE>
-__device__ __forceinline__ BlockStats block_stats_fast(Elems<E>& xs, int i0, int64_t G, float eps, double* lds_d) {
+__device__ __forceinline__ BlockStats block_stats_fast(Elems<E>& xs, int i0, const QuantArgs& a, float eps,
+                                                       double* lds_d, float* lds_f) {
 #pragma clang fp contract(off)
   constexpr int NT = TAU > kWG ? TAU : kWG;
   constexpr bool kSyncedTeams = TAU > 64 && NT / TAU > 1;
   constexpr int kDepth = E == 16 ? 4 : E == 32 ? 5 : 6;
   static_assert(E == 16 || E == 32 || E == 64, "tree depth");
+  const int64_t G = a.G;
   // padding elements are zeros: every E elements enter the sums
   float sp[E / 2];
 #pragma unroll
@@ -451,28 +461,50 @@ __device__ __forceinline__ BlockStats block_stats_fast(Elems<E>& xs, int i0, int
     q[(2 * i + 1) & 3] = sq_acc_hi(xs.p[i], q[(2 * i + 1) & 3]);
   }
   const double Sf = team_sum_f64<TAU>((double)sp[0], lds_d);
-  const double Q = team_sum_f64<TAU>((double)((q[0] + q[1]) + (q[2] + q[3])), lds_d);
-  const double absum = sqrt((double)G * Q * (1.0 + 0x1p-16));
-  const double errS = (double)(kDepth + 1) * 0x1p-24 * absum + fabs(Sf) * 0x1p-50;
-  const f16 m_lo = mean_of_sum(Sf - errS, G), m_hi = mean_of_sum(Sf + errS, G);
+  const float Qf = team_sum_f32<TAU>((q[0] + q[1]) + (q[2] + q[3]), lds_f);
+  const double Q = (double)Qf;
+  // sqrt(G Q) from above: (1 + 2^-14) covers Q's 2^-19 and the two f32
+  // products' roundings, (1 + 2^-20) the square root's one ulp and the last
+  // rounding (G Q stays below 2^47: no overflow; an inf or NaN propagates)
+  const float absum = __builtin_amdgcn_sqrtf((float)G * Qf * (1.0f + 0x1p-14f)) * (1.0f + 0x1p-20f);
+  const double errS = (double)(kDepth + 1) * 0x1p-24 * (double)absum + fabs(Sf) * 0x1p-50;
+  // the bracket's ends as (Sf -+ errS2) * RN64(1 / G): three f64 roundings
+  // move a product by at most 3.1 * 2^-53 of |Sf| + errS2, which the extra
+  // |Sf| 2^-49 and errS 2^-48 exceed, so lo_t <= (Sf - errS) / G and
+  // hi_t >= (Sf + errS) / G as real numbers, and the f64 quotient of the
+  // exact sum (between those) rounds between fp16(f32(lo_t)) and
+  // fp16(f32(hi_t))
+  const double errS2 = (errS + fabs(Sf) * 0x1p-49) * (1.0 + 0x1p-48);
+  const f16 m_lo = rn_h((float)((Sf - errS2) * a.inv_g)), m_hi = rn_h((float)((Sf + errS2) * a.inv_g));
   bool need_exact = !(h_to_bits(m_lo) == h_to_bits(m_hi) && !isnan((float)m_lo));
   if constexpr (kSyncedTeams) need_exact = __syncthreads_or(need_exact);
   double S = Sf, dS = errS;
+  BlockStats st;
+  st.mean16 = m_lo;
   if (need_exact) {
     xs.fence();
     S = team_sum_f64<TAU>(thread_tree_sum<E, MODE>(xs, i0, G, false, 0.0), lds_d);
     dS = 0.0;
+    st.mean16 = mean_of_sum(S, G);
   }
-  const double mu = S / (double)G;
-  auto std_of = [&](double V) { return rn_h((float)sqrt(V / (double)(G - 1))); };
-  BlockStats st;
-  st.mean16 = rn_h((float)mu);
   bool open = true;
   if (G >= 2) {
+    // |S * mu| <= Q (Cauchy-Schwarz): every rounding below, and mu taken as
+    // S * RN64(1 / G), stays far inside the Q 2^-16 term
+    const double mu = S * a.inv_g;
     const double V = Q - S * mu;
-    const double err = Q * 0x1p-16 + (2.0 * fabs(S) + dS) * dS / (double)G + fabs(V) * 0x1p-50;
-    const f16 lo = std_of(fmax(V - err, 0.0));
-    const f16 hi = std_of(V + err);
+    const double err = Q * 0x1p-16 + (2.0 * fabs(S) + dS) * dS * a.inv_g + fabs(V) * 0x1p-50;
+    // sqrt((V -+ err) / (G - 1)) in f32 with c = RN32(1 / (G - 1)): the
+    // conversions, the product and the square root (one ulp) stay within
+    // 2^-22 relative, so the 2^-20 pulls put ylo below and yhi above the
+    // exact roots at V - err and V + err, and below / above the f64 results
+    // there (2^-52 from the exact roots); fp16 rounding of an f32 value
+    // equals fp16(f32(.)) of it, so lo <= std16 <= hi.  (An f32 argument
+    // small enough to be flushed has a root below 2^-63, which rounds to
+    // fp16 0 either way.)
+    const float ylo = __builtin_amdgcn_sqrtf((float)fmax(V - err, 0.0) * a.inv_g1) * (1.0f - 0x1p-20f);
+    const float yhi = __builtin_amdgcn_sqrtf((float)(V + err) * a.inv_g1) * (1.0f + 0x1p-20f);
+    const f16 lo = rn_h(ylo), hi = rn_h(yhi);
     open = !(h_to_bits(lo) == h_to_bits(hi) && !isnan((float)lo));
     st.std16 = lo;
   }
@@ -484,7 +516,7 @@ __device__ __forceinline__ BlockStats block_stats_fast(Elems<E>& xs, int i0, int
     const double mue = Se / (double)G;
     xs.fence();
     const double v_loc = thread_tree_sum<E, MODE>(xs, i0, G, true, mue);
-    st.std16 = std_of(team_sum_f64<TAU>(v_loc, lds_d));
+    st.std16 = std_of_var(team_sum_f64<TAU>(v_loc, lds_d), G);
   }
   st.den16 = rn_h((float)st.std16 + eps);
   return st;
@@ -507,9 +539,16 @@ __device__ __forceinline__ uint32_t pk_min_u16(uint32_t a, uint32_t b) {
   asm("v_pk_min_u16 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
   return d;
 }
-__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+// gfx950 three-operand packed fp16 maximum / minimum (IEEE maximum and
+// minimum per half: -0 < +0, a NaN operand gives NaN)
+__device__ __forceinline__ uint32_t pk_maximum3_f16(uint32_t a, uint32_t b, uint32_t c) {
   uint32_t d;
-  asm("v_pk_max_u16 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+  asm("v_pk_maximum3_f16 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+__device__ __forceinline__ uint32_t pk_minimum3_f16(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t d;
+  asm("v_pk_minimum3_f16 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
   return d;
 }
 
@@ -555,13 +594,16 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
   const int64_t G = a.G;
   const bool tvalid = MODE == kFullBlocks || i0 < G;
 
-  const BlockStats st = block_stats_fast<TAU, E, MODE>(xs, i0, G, 1e-6f, lds_d);
+  const BlockStats st = block_stats_fast<TAU, E, MODE>(xs, i0, a, 1e-6f, lds_d, lds_f);
   xs.fence();
   const f16 thr = bits_to_h(a.thr_bits);
   const float cut = outlier_cut_team<TAU>(st.den16, thr);
 
   uint32_t obits[NWD];
-  uint32_t amax2 = 0;  // packed |x| of non-outliers, as bit patterns
+  // packed fp16 maximum and minimum of the pairs after the outliers are
+  // zeroed, two pairs per instruction; starting from +0 is harmless since
+  // the absmax below is max(max, -min) >= 0
+  uint32_t mx = 0, mn = 0;
   if (cut >= 0.0f) {
     // cut is an fp16 value or +inf (none are outliers)
     const uint32_t th = (uint32_t)h_to_bits((f16)cut) * 0x00010001u;
@@ -576,7 +618,10 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
         const uint32_t m = pk_min_u16(pk_sub_sat_u16(ad, th), 0x00010001u);
         xs.p[i] &= ~pk_sub_u16(0u, m);  // 0xFFFF in each outlier half
         acc = 2 * acc + m;
-        amax2 = pk_max_u16(amax2, xs.p[i] & 0x7FFF7FFFu);
+        if (j & 1) {
+          mx = pk_maximum3_f16(mx, xs.p[i - 1], xs.p[i]);
+          mn = pk_minimum3_f16(mn, xs.p[i - 1], xs.p[i]);
+        }
       }
       obits[w] = acc;
       if (NWD > 1) xs.fence();
@@ -598,7 +643,10 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
         }
         xs.p[i] &= ~(m * 0xFFFFu);
         acc = 2 * acc + m;
-        amax2 = pk_max_u16(amax2, xs.p[i] & 0x7FFF7FFFu);
+        if (j & 1) {
+          mx = pk_maximum3_f16(mx, xs.p[i - 1], xs.p[i]);
+          mn = pk_minimum3_f16(mn, xs.p[i - 1], xs.p[i]);
+        }
       }
       obits[w] = acc;
     }
@@ -609,70 +657,6 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
     if (!tvalid) obits[w] = 0;  // padding threads hold zeros that may pass the test
     nout += __builtin_popcount(obits[w]);
   }
-  // the absmax over non-outliers; -1 when the thread has none
-  float amax = tvalid && nout < E ? fmaxf((float)as_h2(amax2).x, (float)as_h2(amax2).y) : -1.0f;
-  amax = team_max_f32<TAU>(amax, lds_f);
-  xs.fence();
-
-  const float qmax = a.fmt == AQ_FMT_INT8 ? 127.0f : 448.0f;
-  f16 s16 = (f16)1.0f;
-  if (amax >= 0.0f) {
-    s16 = rn_h(amax / qmax);
-    if ((float)s16 < 1e-6f) s16 = rn_h(1e-6f);
-  }
-  const float s = (float)s16;
-  const float r = 1.0f / s;
-
-  int64_t row = 0, col0 = 0;  // where the thread's elements sit in the [rows, K] matrix (tiled layout)
-  if (a.tiled) {
-    row = a.bpr == 1 ? g : g / a.bpr;
-    col0 = (g - row * a.bpr) * G + i0;
-  }
-  // codes, 16 elements (8 pairs, four words) at a time
-#pragma unroll
-  for (int v = 0; v < E / 16; v++) {
-    uint32_t w[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const uint32_t p0 = xs.p[8 * v + 2 * k], p1 = xs.p[8 * v + 2 * k + 1];
-      if (a.fmt == AQ_FMT_INT8) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-          const f16 xe = xs[16 * v + 4 * k + b];
-          float rr = __builtin_rintf((float)h_div_fast((float)xe, s, r));
-          rr = fminf(fmaxf(rr, -127.0f), 127.0f);
-          word |= (uint32_t)(uint8_t)(int8_t)(int)rr << (8 * b);
-        }
-        w[k] = word;
-      } else {
-        // |x| <= amax and s = fp16(amax / 448) give |x / s| < 448.25, so the
-        // quotient is at most 448.25, which the conversion (round to nearest
-        // even) takes to 448 as the clamp to +-448 would
-        typedef short short2v __attribute__((vector_size(4)));
-        const uint32_t q0 = quot2(p0, r);
-        // both halves of c are written; its initial value is never seen
-        short2v c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(__builtin_bit_cast(short2v, q0), as_h2(q0), 1.0f, false);
-        c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(c, as_h2(quot2(p1, r)), 1.0f, true);
-        w[k] = __builtin_bit_cast(uint32_t, c);
-      }
-    }
-    if (E > 16) xs.fence();
-    if (gvalid && tvalid) {
-      // 16 consecutive elements of one row land in 16 consecutive bytes of either layout
-      const int64_t j = base + i0 + 16 * v;
-      if (a.vec) {
-        const int64_t off = a.tiled ? tiled_offset(row, col0 + 16 * v, a.nchunks) : j;
-        *reinterpret_cast<uint4*>(a.codes + off) = make_uint4(w[0], w[1], w[2], w[3]);
-      } else {
-#pragma unroll
-        for (int b = 0; b < 16; b++)
-          a.codes[a.tiled ? tiled_offset(row, col0 + 16 * v + b, a.nchunks) : j + b] =
-              (uint8_t)(w[b / 4] >> (8 * (b % 4)));
-      }
-    }
-  }
-
   // outlier compaction: team prefix sum, then the block's staging slot in
   // element order (flag word w: pair PW w + j low / high at bit PW - 1 - j /
   // 16 + PW - 1 - j, so after a bit reversal L and H below hold them at bit j)
@@ -704,10 +688,99 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
         k++;
       }
     }
-    if (t == 0) {
-      a.scales[g] = h_to_bits(s16);
-      a.block_cnt[g] = total;
+  }
+  // the outlier stores go out before the code stores (see the end)
+  asm volatile("" ::: "memory");
+
+  // the absmax over non-outliers (NaN and, past a finite cut, infinities are
+  // outliers, so the extremes are ordered values); -1 when the thread has none
+  float amax = -1.0f;
+  if (tvalid && nout < E) {
+    const half2v hx = as_h2(mx), hn = as_h2(mn);
+    amax = fmaxf(fmaxf((float)hx.x, (float)hx.y), -fminf((float)hn.x, (float)hn.y));
+  }
+  amax = team_max_f32<TAU>(amax, lds_f);
+  xs.fence();
+
+  const float qmax = a.fmt == AQ_FMT_INT8 ? 127.0f : 448.0f;
+  f16 s16 = (f16)1.0f;
+  if (amax >= 0.0f) {
+    s16 = rn_h(amax / qmax);
+    if ((float)s16 < 1e-6f) s16 = rn_h(1e-6f);
+  }
+  const float s = (float)s16;
+  const float r = 1.0f / s;
+
+  int64_t row = 0, col0 = 0;  // where the thread's elements sit in the [rows, K] matrix (tiled layout)
+  if (a.tiled) {
+    row = a.bpr == 1 ? g : g / a.bpr;
+    col0 = (g - row * a.bpr) * G + i0;
+  }
+  // Where the thread's first 16 codes go; group v of 16 follows at v * 256
+  // bytes in the tiled layout (E divides G, so col0 is a multiple of E and
+  // the thread's columns col0 .. col0 + E - 1 lie in one 64-column half of a
+  // tile, 16-byte piece v = ((col0 + 16 v) >> 4) & 3 of it), at v * 16 in
+  // element order.
+  uint8_t* const dst = a.codes + (a.tiled ? tiled_offset(row, col0, a.nchunks) : base + i0);
+  const int vstep = a.tiled ? 256 : 16;
+  auto store16 = [&](int v, const uint32_t (&w)[4]) {
+    if (!(gvalid && tvalid)) return;
+    if (a.vec) {
+      *reinterpret_cast<uint4*>(dst + v * vstep) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+      const int64_t j = base + i0 + 16 * v;
+#pragma unroll
+      for (int b = 0; b < 16; b++)
+        a.codes[a.tiled ? tiled_offset(row, col0 + 16 * v + b, a.nchunks) : j + b] =
+            (uint8_t)(w[b / 4] >> (8 * (b % 4)));
     }
+  };
+  // codes, 16 elements (8 pairs, four words) at a time; one loop per format
+  if (a.fmt == AQ_FMT_INT8) {
+#pragma unroll
+    for (int v = 0; v < E / 16; v++) {
+      uint32_t w[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+          const f16 xe = xs[16 * v + 4 * k + b];
+          float rr = __builtin_rintf((float)h_div_fast((float)xe, s, r));
+          rr = fminf(fmaxf(rr, -127.0f), 127.0f);
+          word |= (uint32_t)(uint8_t)(int8_t)(int)rr << (8 * b);
+        }
+        w[k] = word;
+      }
+      if (E > 16) xs.fence();
+      store16(v, w);
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < E / 16; v++) {
+      uint32_t w[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        // |x| <= amax and s = fp16(amax / 448) give |x / s| < 448.25, so the
+        // quotient is at most 448.25, which the conversion (round to nearest
+        // even) takes to 448 as the clamp to +-448 would
+        typedef short short2v __attribute__((vector_size(4)));
+        const uint32_t q0 = quot2(xs.p[8 * v + 2 * k], r);
+        // both halves of c are written; its initial value is never seen
+        short2v c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(__builtin_bit_cast(short2v, q0), as_h2(q0), 1.0f, false);
+        c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(c, as_h2(quot2(xs.p[8 * v + 2 * k + 1], r)), 1.0f, true);
+        w[k] = __builtin_bit_cast(uint32_t, c);
+      }
+      if (E > 16) xs.fence();
+      store16(v, w);
+    }
+  }
+
+  // the block's scale and count (the same values in every lane of the team:
+  // all lanes store them, no branch around the stores)
+  if (gvalid) {
+    a.scales[g] = h_to_bits(s16);
+    a.block_cnt[g] = total;
   }
 }
 
@@ -1027,6 +1100,8 @@ extern "C" int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_t
   a.K = K;
   a.nchunks = K / 128;
   a.bpr = a.tiled ? K / G : 1;
+  a.inv_g = 1.0 / (double)G;
+  a.inv_g1 = G >= 2 ? (float)(1.0 / (double)(G - 1)) : 0.0f;
   a.codes = (uint8_t*)codes;
   a.scales = (uint16_t*)scales;
   a.block_cnt = block_off;

@@ -1,0 +1,253 @@
+"""Greedy decoding with each step captured in one HIP graph.
+
+The reference decodes with HF ``generate`` (examples/run_atlas_inference.py
+:244-264), one eager forward per token; on a GPU as fast as this one that
+loop is bound by the host (Python and launch overhead), not by the bytes a
+token moves.  ``GraphDecoder`` takes a model whose Linears were swapped by
+``apply_atlas_quantization_to_model`` (or any HF OPT / Llama / Mistral
+model), runs the prompt through the model's own forward, then records one
+decode step -- embeddings, every layer (the QuantizedLinear launches, the
+attention over a static key/value cache, the norms and activations), the
+final norm, the lm_head and the greedy choice -- in a HIP graph and replays
+it once per token.
+
+Everything a replay reads that changes from token to token is device
+memory updated in place by the graph itself: the current token ``tok``
+(written by the argmax at the end of a step), the position ``pos`` (the
+index of the key/value slot and of the positional embedding, incremented at
+the end of a step), the output slot index, and the key/value cache
+(``index_copy_`` at ``pos``).  No host value is baked into the graph
+except the shapes: batch, cache length, model dimensions.  The host only
+guards that a replay never runs past the cache (``max_len``), so no index
+leaves its buffer.
+
+Limits: greedy decoding, equal-length prompts without padding (batch rows
+share ``pos``), no beam search, no sliding-window attention.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+
+def _kind(model) -> str:
+    t = getattr(model.config, "model_type", "")
+    if t == "opt":
+        return "opt"
+    if t in ("llama", "mistral"):
+        return "llama"
+    raise NotImplementedError(f"GraphDecoder: model type {t!r} (opt, llama, mistral supported)")
+
+
+class GraphDecoder:
+    """Greedy decode of ``model`` for ``batch`` sequences of up to
+    ``max_len`` positions (prompt + new tokens), one HIP graph replay per
+    token.  ``graph=False`` runs the same step eagerly (no capture), which is
+    also how it runs on a CPU."""
+
+    def __init__(self, model, batch: int, max_len: int, graph: bool = True):
+        self.model = model
+        self.kind = _kind(model)
+        cfg = model.config
+        self.B, self.L = int(batch), int(max_len)
+        p = next(model.parameters())
+        self.dev, self.dtype = p.device, p.dtype
+        self.use_graph = graph and self.dev.type == "cuda"
+        if self.kind == "opt":
+            dec = model.model.decoder
+            if dec.project_in is not None or dec.project_out is not None or not dec.layers[0].do_layer_norm_before:
+                raise NotImplementedError("GraphDecoder: OPT variants with projections or post-norm (350m)")
+            self.layers = list(dec.layers)
+            self.H = cfg.num_attention_heads
+            self.Hkv = self.H
+            self.D = cfg.hidden_size // self.H
+        else:
+            self.layers = list(model.model.layers)
+            if getattr(cfg, "sliding_window", None) not in (None, 0) and cfg.sliding_window < self.L:
+                raise NotImplementedError("GraphDecoder: sliding-window attention shorter than max_len")
+            self.H = cfg.num_attention_heads
+            self.Hkv = getattr(cfg, "num_key_value_heads", None) or self.H
+            self.D = getattr(cfg, "head_dim", None) or cfg.hidden_size // self.H
+        B, L, dev = self.B, self.L, self.dev
+        # the state every replay reads and updates in place
+        self.tok = torch.zeros(B, dtype=torch.long, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.long, device=dev)
+        self.slot = torch.zeros(1, dtype=torch.long, device=dev)  # index of the next output token
+        self.out = torch.zeros(B, L, dtype=torch.long, device=dev)
+        self.logits = None  # the last step's logits (a static buffer once captured)
+        self.ar = torch.arange(L, device=dev)
+        # keys stored [B, Hkv, D, L] so that the score product reads a plain
+        # (not transposed) right operand; values [B, Hkv, L, D]
+        self.k = [torch.zeros(B, self.Hkv, self.D, L, dtype=self.dtype, device=dev) for _ in self.layers]
+        self.v = [torch.zeros(B, self.Hkv, L, self.D, dtype=self.dtype, device=dev) for _ in self.layers]
+        if self.kind == "llama":
+            rot = model.model.rotary_emb
+            pos_ids = torch.arange(L, device=dev)[None]
+            with torch.no_grad():
+                cos, sin = rot(torch.zeros(1, dtype=self.dtype, device=dev), pos_ids)
+            self.cos, self.sin = cos[0].contiguous(), sin[0].contiguous()  # [L, D]
+        self.graph = None
+        self.captured = False
+        self.S, self._n = 0, 0
+
+    # ------------------------------------------------------------ one step
+
+    def _attend(self, li: int, q, k, v, scale: float = 1.0):
+        """Attention of the step's queries q [B, H, D] over positions
+        0..pos after writing k, v [B, Hkv, D] at pos (scores in f32, times
+        ``scale``, softmax in f32 as HF's eager attention does)."""
+        B, H, Hkv, D = self.B, self.H, self.Hkv, self.D
+        K, V = self.k[li], self.v[li]
+        K.index_copy_(3, self.pos, k.reshape(B, Hkv, D, 1))
+        V.index_copy_(2, self.pos, v.reshape(B, Hkv, 1, D))
+        qg = q.reshape(B, Hkv, H // Hkv, D)
+        s = torch.matmul(qg, K).float()  # [B, Hkv, G, L]
+        if scale != 1.0:
+            s = s * scale
+        s = s.masked_fill(self.ar > self.pos, float("-inf"))
+        p = torch.softmax(s, dim=-1).to(self.dtype)
+        o = torch.matmul(p, V)  # [B, Hkv, G, D]
+        return o.reshape(B, H * D)
+
+    def _layer_opt(self, li, layer, x):
+        at = layer.self_attn
+        h = layer.self_attn_layer_norm(x)
+        q = at.q_proj(h) * at.scaling
+        k = at.k_proj(h)
+        v = at.v_proj(h)
+        B = self.B
+        o = self._attend(li, q.view(B, self.H, self.D), k.view(B, self.Hkv, self.D), v.view(B, self.Hkv, self.D))
+        x = x + at.out_proj(o)
+        h = layer.final_layer_norm(x)
+        h = layer.fc2(layer.activation_fn(layer.fc1(h)))
+        return x + h
+
+    def _rope(self, t, cos, sin):
+        # HF's rotate-half form on [B, heads, D] with cos / sin [D]
+        half = t.shape[-1] // 2
+        rot = torch.cat((-t[..., half:], t[..., :half]), dim=-1)
+        return t * cos + rot * sin
+
+    def _layer_llama(self, li, layer, x):
+        at = layer.self_attn
+        h = layer.input_layernorm(x)
+        B = self.B
+        q = at.q_proj(h).view(B, self.H, self.D)
+        k = at.k_proj(h).view(B, self.Hkv, self.D)
+        v = at.v_proj(h).view(B, self.Hkv, self.D)
+        cos = self.cos.index_select(0, self.pos)  # [1, D]
+        sin = self.sin.index_select(0, self.pos)
+        q = self._rope(q, cos, sin)
+        k = self._rope(k, cos, sin)
+        o = self._attend(li, q, k, v, at.scaling)
+        x = x + at.o_proj(o)
+        h = layer.post_attention_layernorm(x)
+        h = layer.mlp.down_proj(layer.mlp.act_fn(layer.mlp.gate_proj(h)) * layer.mlp.up_proj(h))
+        return x + h
+
+    def _step(self):
+        m = self.model
+        if self.kind == "opt":
+            dec = m.model.decoder
+            x = dec.embed_tokens(self.tok)
+            x = x + dec.embed_positions.weight.index_select(0, self.pos + 2)
+            for li, layer in enumerate(self.layers):
+                x = self._layer_opt(li, layer, x)
+            x = dec.final_layer_norm(x)
+        else:
+            x = m.model.embed_tokens(self.tok)
+            for li, layer in enumerate(self.layers):
+                x = self._layer_llama(li, layer, x)
+            x = m.model.norm(x)
+        logits = m.lm_head(x)  # [B, V]
+        nxt = self._argmax(logits)
+        self.tok.copy_(nxt)
+        self.out.index_copy_(1, self.slot, nxt.view(self.B, 1))
+        self.pos.add_(1)
+        self.slot.add_(1)
+        return logits
+
+    @staticmethod
+    def _argmax(logits):
+        """Greedy choice (first maximum) in two single-pass reductions over
+        short rows: the row split into 64 parts, then the parts' maxima."""
+        B, V = logits.shape
+        n = 64
+        w = (V + n - 1) // n
+        x = logits.float()
+        if w * n != V:
+            x = F.pad(x, (0, w * n - V), value=float("-inf"))
+        mx, ix = x.view(B, n, w).max(dim=-1)  # [B, n]
+        best, part = mx.max(dim=-1)  # first part holding the maximum
+        return part * w + ix.gather(1, part.view(B, 1)).view(B)
+
+    # ------------------------------------------------------------ driving
+
+    def _capture(self):
+        """Record one step.  A few eager steps first (allocations, the
+        layers' prepared arguments), on scratch positions; the caller's
+        prefill then sets the real state."""
+        s = torch.cuda.Stream(device=self.dev)
+        s.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(s), torch.no_grad():
+            for _ in range(2):
+                self._step()
+        torch.cuda.current_stream(self.dev).wait_stream(s)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph), torch.no_grad():
+            self.logits = self._step()
+        self.captured = True
+
+    @torch.no_grad()
+    def prefill(self, input_ids: torch.Tensor) -> torch.Tensor:
+        """Run the prompt [B, S] through the model's own forward, fill the
+        static cache and set tok / pos / slot; returns the first new token."""
+        B, S = input_ids.shape
+        if B != self.B or S >= self.L:
+            raise ValueError(f"prefill: batch {B} (decoder built for {self.B}), prompt {S} (cache {self.L})")
+        if self.use_graph and not self.captured:
+            self._capture()
+        from transformers import DynamicCache
+        cache = DynamicCache()
+        out = self.model(input_ids=input_ids.to(self.dev), past_key_values=cache, use_cache=True)
+        for li in range(len(self.layers)):
+            kl, vl = cache.layers[li].keys, cache.layers[li].values  # [B, Hkv, S, D]
+            self.k[li][:, :, :, :S].copy_(kl.transpose(2, 3))
+            self.v[li][:, :, :S].copy_(vl)
+        first = self._argmax(out.logits[:, -1])
+        self.tok.copy_(first)
+        self.out.zero_()
+        self.out[:, 0].copy_(first)
+        self.pos.fill_(S)
+        self.slot.fill_(1)
+        self.S, self._n = S, 0
+        return first
+
+    @torch.no_grad()
+    def step(self) -> torch.Tensor:
+        """One decode step (a graph replay when captured): the token chosen
+        last goes in at position pos; returns the step's logits [B, V] (the
+        static buffer when captured)."""
+        # host-side guard: the step writes the cache at pos = S + n and the
+        # output at slot 1 + n, both below L
+        if self.S + self._n >= self.L:
+            raise RuntimeError(f"GraphDecoder: cache of {self.L} positions is full")
+        self._n += 1
+        if self.use_graph:
+            self.graph.replay()
+            return self.logits
+        self.logits = self._step()
+        return self.logits
+
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int) -> torch.Tensor:
+        """Prompt + ``max_new_tokens`` greedy tokens, [B, S + max_new_tokens]."""
+        S = input_ids.shape[1]
+        if S + max_new_tokens > self.L:
+            raise ValueError(f"generate: {S} + {max_new_tokens} positions exceed the cache ({self.L})")
+        self.prefill(input_ids)
+        for _ in range(max_new_tokens - 1):
+            self.step()
+        return torch.cat([input_ids.to(self.dev), self.out[:, :max_new_tokens]], dim=1)

@@ -463,6 +463,37 @@ def bench_kv_cache(dev, log, steps=64):
     return out
 
 
+def graph_decode_tokps(model, ids, new_tokens):
+    """GraphDecoder (one HIP graph replay per token, greedy): decode tokens
+    per second per sequence (prefill excluded) and the generated tokens."""
+    from atlasinfer_amd.integration.decode_graph import GraphDecoder
+    B, S = ids.shape
+    gd = GraphDecoder(model, batch=B, max_len=S + new_tokens)
+    with torch.no_grad():
+        gd.generate(ids, 4)  # capture and warm
+        gd.prefill(ids)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(new_tokens - 1):
+            gd.step()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+    out = torch.cat([ids, gd.out[:, :new_tokens]], dim=1)
+    del gd
+    return (new_tokens - 1) / dt, out
+
+
+def agree_until(a, b, start):
+    """Positions from ``start`` on where two token sequences [B, T] agree in
+    every row, up to the first difference."""
+    n = 0
+    for t in range(start, min(a.shape[1], b.shape[1])):
+        if not torch.equal(a[:, t], b[:, t]):
+            break
+        n += 1
+    return n
+
+
 def bench_models(dev, which, log):
     """BASELINE configs 1 (OPT-1.3b, every Linear quantized, 32-token prompt,
     128 greedy tokens, batch 1) and 3 (Mistral-7B, 512-token prompts, 256
@@ -490,7 +521,12 @@ def bench_models(dev, which, log):
         torch.cuda.synchronize()
         t_q = time.perf_counter() - t0
         q_tps, _ = generate_tokps(model, ids, 128)
+        with torch.no_grad():
+            hf_seq = model.generate(ids, max_new_tokens=128, min_new_tokens=128, do_sample=False, pad_token_id=0)
+        g_tps, g_seq = graph_decode_tokps(model, ids, 128)
         out["opt1.3b"] = {"decode_tok_s": round(q_tps, 1), "fp16_decode_tok_s": round(fp16_tps, 1),
+                          "graph_decode_tok_s": round(g_tps, 1),
+                          "graph_tokens_agreeing_with_hf_generate": agree_until(g_seq, hf_seq, 32),
                           "linears_quantized": rep, "failed": fail, "quantize_s": round(t_q, 2),
                           "prompt": 32, "new_tokens": 128, "batch": 1}
         log(f"OPT-1.3b: {out['opt1.3b']}")
@@ -520,6 +556,8 @@ def bench_models(dev, which, log):
                 tps, t_pre = generate_tokps(model, ids, 256)
                 flops = linear_flops(model, B * 512) if phase == "fp16" else res[f"fp16_b{B}_prefill_flops"]
                 res[f"{phase}_b{B}_decode_tok_s"] = round(tps * B, 1)
+                g_tps, _ = graph_decode_tokps(model, ids, 256)
+                res[f"{phase}_b{B}_graph_decode_tok_s"] = round(g_tps * B, 1)
                 res[f"{phase}_b{B}_prefill_tflops"] = round(flops / t_pre / 1e12, 1)
                 if phase == "fp16":
                     res[f"fp16_b{B}_prefill_flops"] = flops

@@ -55,6 +55,8 @@ SIGNATURES = {
                                           _P, _P, _P, _P, _I64, _P]),
     "aq_qlinear_noalloc": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, _I64, ctypes.c_int, _I32P, _I32P, _P,
                                           _I32P, _P, _I64, _P, _P, _P]),
+    "aq_decode_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
+                                           _P, _P]),
 }
 NOALLOC_SCRATCH_BYTES = 64 << 20  # AQ_NOALLOC_SCRATCH_BYTES
 

@@ -16,10 +16,17 @@ memory updated in place by the graph itself: the current token ``tok``
 (written by the argmax at the end of a step), the position ``pos`` (the
 index of the key/value slot and of the positional embedding, incremented at
 the end of a step), the output slot index, and the key/value cache
-(``index_copy_`` at ``pos``).  No host value is baked into the graph
+(written at ``pos``).  No host value is baked into the graph
 except the shapes: batch, cache length, model dimensions.  The host only
 guards that a replay never runs past the cache (``max_len``), so no index
 leaves its buffer.
+
+On the GPU with an fp16 model a step's attention is one kernel
+(``aq_decode_attention``: the new key/value written at ``pos``, scores,
+softmax and the weighted sum of values in one pass over the cache), and the
+q/k/v and gate/up projections are one grouped QuantizedLinear launch each.
+Elsewhere (CPU, other dtypes, head sizes other than 64 and 128) the same
+step runs as torch operations.
 
 Limits: greedy decoding, equal-length prompts without padding (batch rows
 share ``pos``), no beam search, no sliding-window attention.
@@ -28,8 +35,12 @@ from __future__ import annotations
 
 from typing import Optional
 
+import ctypes
+
 import torch
 import torch.nn.functional as F
+
+from .. import _lib
 
 
 def _kind(model) -> str:
@@ -78,9 +89,8 @@ class GraphDecoder:
         self.out = torch.zeros(B, L, dtype=torch.long, device=dev)
         self.logits = None  # the last step's logits (a static buffer once captured)
         self.ar = torch.arange(L, device=dev)
-        # keys stored [B, Hkv, D, L] so that the score product reads a plain
-        # (not transposed) right operand; values [B, Hkv, L, D]
-        self.k = [torch.zeros(B, self.Hkv, self.D, L, dtype=self.dtype, device=dev) for _ in self.layers]
+        # keys and values [B, Hkv, L, D]: a position's key is one row
+        self.k = [torch.zeros(B, self.Hkv, L, self.D, dtype=self.dtype, device=dev) for _ in self.layers]
         self.v = [torch.zeros(B, self.Hkv, L, self.D, dtype=self.dtype, device=dev) for _ in self.layers]
         if self.kind == "llama":
             rot = model.model.rotary_emb
@@ -91,19 +101,33 @@ class GraphDecoder:
         self.graph = None
         self.captured = False
         self.S, self._n = 0, 0
+        # on the GPU: the attention of a step in one HIP kernel
+        # (aq_decode_attention), q/k/v and gate/up in one grouped launch each
+        self.fused = (self.dev.type == "cuda" and self.dtype == torch.float16 and self.D in (64, 128)
+                      and self.H // self.Hkv in (1, 2, 4, 8))
+        if self.dev.type == "cuda":
+            self._lib = _lib.load()
 
     # ------------------------------------------------------------ one step
 
     def _attend(self, li: int, q, k, v, scale: float = 1.0):
         """Attention of the step's queries q [B, H, D] over positions
-        0..pos after writing k, v [B, Hkv, D] at pos (scores in f32, times
-        ``scale``, softmax in f32 as HF's eager attention does)."""
+        0..pos after writing k, v [B, Hkv, D] at pos (scores rounded to fp16
+        as a half-precision product returns them, times ``scale``, softmax
+        in f32)."""
         B, H, Hkv, D = self.B, self.H, self.Hkv, self.D
         K, V = self.k[li], self.v[li]
-        K.index_copy_(3, self.pos, k.reshape(B, Hkv, D, 1))
+        if self.fused:
+            q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+            o = torch.empty(B, H * D, dtype=self.dtype, device=self.dev)
+            _lib.check(self._lib.aq_decode_attention(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), K.data_ptr(), V.data_ptr(), self.pos.data_ptr(), B, H, Hkv,
+                D, self.L, ctypes.c_float(scale), o.data_ptr(), _lib.stream_of(self.dev)), "aq_decode_attention")
+            return o
+        K.index_copy_(2, self.pos, k.reshape(B, Hkv, 1, D))
         V.index_copy_(2, self.pos, v.reshape(B, Hkv, 1, D))
         qg = q.reshape(B, Hkv, H // Hkv, D)
-        s = torch.matmul(qg, K).float()  # [B, Hkv, G, L]
+        s = torch.matmul(qg, K.transpose(2, 3).contiguous()).float()  # [B, Hkv, G, L]
         if scale != 1.0:
             s = s * scale
         s = s.masked_fill(self.ar > self.pos, float("-inf"))
@@ -111,12 +135,25 @@ class GraphDecoder:
         o = torch.matmul(p, V)  # [B, Hkv, G, D]
         return o.reshape(B, H * D)
 
+    def _linears(self, mods, h):
+        """The outputs of several linears on the same input: one grouped
+        launch when they are all QuantizedLinear layers the fused kernels
+        take (on the GPU), else one call each."""
+        from .atlas_wrappers import fused_supported, qlinear_grouped
+        if self.dev.type == "cuda" and len(mods) > 1 and all(type(m).__name__ == "QuantizedLinear" for m in mods):
+            qs = [m._weights_on(self.dev) for m in mods]
+            if (all(fused_supported(q) for q in qs) and len({int(q.original_shape[-1]) for q in qs}) == 1
+                    and len({q.code_format for q in qs}) == 1):
+                for m, q in zip(mods, qs):
+                    m._ensure_codes(q, self.dev)
+                return qlinear_grouped(h, qs, [m.bias for m in mods], [m._codes for m in mods])
+        return [m(h) for m in mods]
+
     def _layer_opt(self, li, layer, x):
         at = layer.self_attn
         h = layer.self_attn_layer_norm(x)
-        q = at.q_proj(h) * at.scaling
-        k = at.k_proj(h)
-        v = at.v_proj(h)
+        q, k, v = self._linears([at.q_proj, at.k_proj, at.v_proj], h)
+        q = q * at.scaling
         B = self.B
         o = self._attend(li, q.view(B, self.H, self.D), k.view(B, self.Hkv, self.D), v.view(B, self.Hkv, self.D))
         x = x + at.out_proj(o)
@@ -134,9 +171,10 @@ class GraphDecoder:
         at = layer.self_attn
         h = layer.input_layernorm(x)
         B = self.B
-        q = at.q_proj(h).view(B, self.H, self.D)
-        k = at.k_proj(h).view(B, self.Hkv, self.D)
-        v = at.v_proj(h).view(B, self.Hkv, self.D)
+        q, k, v = self._linears([at.q_proj, at.k_proj, at.v_proj], h)
+        q = q.view(B, self.H, self.D)
+        k = k.view(B, self.Hkv, self.D)
+        v = v.view(B, self.Hkv, self.D)
         cos = self.cos.index_select(0, self.pos)  # [1, D]
         sin = self.sin.index_select(0, self.pos)
         q = self._rope(q, cos, sin)
@@ -144,7 +182,8 @@ class GraphDecoder:
         o = self._attend(li, q, k, v, at.scaling)
         x = x + at.o_proj(o)
         h = layer.post_attention_layernorm(x)
-        h = layer.mlp.down_proj(layer.mlp.act_fn(layer.mlp.gate_proj(h)) * layer.mlp.up_proj(h))
+        g, u = self._linears([layer.mlp.gate_proj, layer.mlp.up_proj], h)
+        h = layer.mlp.down_proj(layer.mlp.act_fn(g) * u)
         return x + h
 
     def _step(self):
@@ -214,7 +253,7 @@ class GraphDecoder:
         out = self.model(input_ids=input_ids.to(self.dev), past_key_values=cache, use_cache=True)
         for li in range(len(self.layers)):
             kl, vl = cache.layers[li].keys, cache.layers[li].values  # [B, Hkv, S, D]
-            self.k[li][:, :, :, :S].copy_(kl.transpose(2, 3))
+            self.k[li][:, :, :S].copy_(kl)
             self.v[li][:, :, :S].copy_(vl)
         first = self._argmax(out.logits[:, -1])
         self.tok.copy_(first)

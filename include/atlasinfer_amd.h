@@ -232,6 +232,28 @@ int aq_qlinear_noalloc(const void* x, int64_t M, int64_t K, int64_t N, const voi
                        const int32_t* tile_ptr, const uint32_t* tile_ent, int64_t tile_max, const void* bias,
                        void* y, void* stream);
 
+/*
+ * Attention of one decode step over a static key/value cache, the position
+ * read from device memory (so that a captured HIP graph replays it for
+ * every token).  Replaces the attention part of a decode step's forward:
+ * the reference's AtlasAttentionWrapper.forward concatenates the cached
+ * history with the new key/value, rotates, and runs SDPA or a BMM softmax
+ * (integration/atlas_wrappers.py:161-262); HF's own attention modules do
+ * the equivalent.  For batch row b and key/value head j (query heads
+ * j G .. j G + G - 1, G = H / Hkv <= 8):
+ *   k_cache[b, j, pos, :] = k_new[b, j, :];  v_cache[b, j, pos, :] = v_new[b, j, :]
+ *   s_p = fp16(q . k_p) * scale, p = 0 .. pos;  w = softmax(s) in f32
+ *   out[b, h, :] = fp16(sum_p w_p v_p)   (f32 accumulation, one rounding)
+ *   q      fp16 [B, H, D]          k_new, v_new fp16 [B, Hkv, D]
+ *   k_cache, v_cache fp16 [B, Hkv, L, D] (16-byte aligned)
+ *   pos    int64 device scalar, 0 <= pos < L
+ *   out    fp16 [B, H, D]          D = 64 or 128
+ * A pos outside [0, L) leaves everything untouched (callers keep it inside).
+ */
+int aq_decode_attention(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                        const int64_t* pos, int64_t B, int64_t H, int64_t Hkv, int64_t D, int64_t L, float scale,
+                        void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

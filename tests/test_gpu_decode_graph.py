@@ -72,3 +72,51 @@ def test_graph_generate_follows_hf_generate(kind):
                 gap = (top2[row, 0] - top2[row, 1]).item()
                 assert gap < 2e-2 * top2[row, 0].abs().item() + 1e-2, (t, row, gap)
                 return
+
+
+@pytest.mark.parametrize("B,H,Hkv,D,L,pos", [(1, 32, 32, 64, 160, 0), (1, 32, 32, 64, 160, 47), (2, 32, 8, 128, 768, 511),
+                                             (3, 8, 1, 128, 600, 257), (2, 16, 4, 64, 1000, 999),
+                                             (1, 64, 8, 128, 300, 299), (2, 16, 2, 64, 40, 0)])
+def test_decode_attention_kernel(B, H, Hkv, D, L, pos):
+    """aq_decode_attention against the same attention computed in float64
+    from the same fp16 data (scores rounded to fp16 as the kernel's contract
+    says); the new key and value land at pos and nothing else in the caches
+    changes."""
+    import ctypes
+    from atlasinfer_amd import _lib
+    g = torch.Generator(device=DEV).manual_seed(B * 1000 + pos)
+    q = torch.randn(B, H, D, generator=g, device=DEV).half()
+    kn = torch.randn(B, Hkv, D, generator=g, device=DEV).half()
+    vn = torch.randn(B, Hkv, D, generator=g, device=DEV).half()
+    K = torch.randn(B, Hkv, L, D, generator=g, device=DEV).half()
+    V = torch.randn(B, Hkv, L, D, generator=g, device=DEV).half()
+    K0, V0 = K.clone(), V.clone()
+    p = torch.tensor([pos], dtype=torch.long, device=DEV)
+    out = torch.empty(B, H, D, dtype=torch.float16, device=DEV)
+    scale = D ** -0.5
+    _lib.check(_lib.load().aq_decode_attention(q.data_ptr(), kn.data_ptr(), vn.data_ptr(), K.data_ptr(), V.data_ptr(),
+                                               p.data_ptr(), B, H, Hkv, D, L, ctypes.c_float(scale), out.data_ptr(),
+                                               _lib.stream_of(torch.device(DEV))), "aq_decode_attention")
+    torch.cuda.synchronize()
+    K0[:, :, pos, :] = kn
+    V0[:, :, pos, :] = vn
+    assert torch.equal(K, K0) and torch.equal(V, V0)
+    G = H // Hkv
+    qd = q.double().view(B, Hkv, G, D)
+    s = (qd @ K0[:, :, :pos + 1].double().transpose(2, 3)).half().double() * scale  # [B, Hkv, G, pos+1]
+    w = torch.softmax(s, dim=-1)
+    ref = (w @ V0[:, :, :pos + 1].double()).view(B, H, D)
+    err = (out.double() - ref).abs().max().item()
+    assert err < 2e-3 * ref.abs().max().item() + 1e-3, err
+
+
+def test_decode_attention_rejects_group_sizes():
+    """Query groups other than 1, 2, 4 and 8 heads per key/value head are
+    refused before any launch."""
+    from atlasinfer_amd import _lib
+    t = torch.zeros(64, dtype=torch.float16, device=DEV)
+    p = torch.zeros(1, dtype=torch.long, device=DEV)
+    with pytest.raises(_lib.AQError, match="times Hkv"):
+        _lib.check(_lib.load().aq_decode_attention(t.data_ptr(), t.data_ptr(), t.data_ptr(), t.data_ptr(), t.data_ptr(),
+                                                   p.data_ptr(), 1, 3, 1, 64, 1, 1.0, t.data_ptr(), None),
+                   "aq_decode_attention")

@@ -56,7 +56,10 @@ SIGNATURES = {
     "aq_qlinear_noalloc": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, _I64, ctypes.c_int, _I32P, _I32P, _P,
                                           _I32P, _P, _I64, _P, _P, _P]),
     "aq_decode_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
-                                           _P, _P]),
+                                           ctypes.c_float, _P, _P, _P, _I64, _P, _P]),
+    "aq_decode_norm": (ctypes.c_int, [_P, _P, _P, _P, ctypes.c_float, _I64, _I64, ctypes.c_int, _P, _P]),
+    "aq_silu_mul": (ctypes.c_int, [_P, _P, _P, _I64, _P]),
+    "aq_decode_attention_workspace": (ctypes.c_int64, [_I64, _I64, _I64, _I64, _I64]),
 }
 NOALLOC_SCRATCH_BYTES = 64 << 20  # AQ_NOALLOC_SCRATCH_BYTES
 

@@ -21,12 +21,15 @@ except the shapes: batch, cache length, model dimensions.  The host only
 guards that a replay never runs past the cache (``max_len``), so no index
 leaves its buffer.
 
-On the GPU with an fp16 model a step's attention is one kernel
-(``aq_decode_attention``: the new key/value written at ``pos``, scores,
-softmax and the weighted sum of values in one pass over the cache), and the
-q/k/v and gate/up projections are one grouped QuantizedLinear launch each.
-Elsewhere (CPU, other dtypes, head sizes other than 64 and 128) the same
-step runs as torch operations.
+On the GPU with an fp16 model a layer's step is about nine launches: one
+residual add + norm (``aq_decode_norm``) before the attention and one
+before the MLP, the q/k/v and gate/up projections as one grouped
+QuantizedLinear launch each, the attention (``aq_decode_attention``: query
+scaling or rotary embedding, the new key/value written at ``pos``, scores,
+softmax and the weighted sum of values over the cache, plus a merge of the
+cache spans' partial results), the output projection, the SiLU product
+(``aq_silu_mul``) and the down projection.  Elsewhere (CPU, other dtypes,
+head sizes other than 64 and 128) the same step runs as torch operations.
 
 Limits: greedy decoding, equal-length prompts without padding (batch rows
 share ``pos``), no beam search, no sliding-window attention.
@@ -104,26 +107,91 @@ class GraphDecoder:
         # on the GPU: the attention of a step in one HIP kernel
         # (aq_decode_attention), q/k/v and gate/up in one grouped launch each
         self.fused = (self.dev.type == "cuda" and self.dtype == torch.float16 and self.D in (64, 128)
-                      and self.H // self.Hkv in (1, 2, 4, 8))
+                      and self.H % self.Hkv == 0 and self.H // self.Hkv in (1, 2, 4, 8))
         if self.dev.type == "cuda":
             self._lib = _lib.load()
+        if self.fused:
+            # the attention kernel's per-span partial results: one workspace
+            # for every layer (the layers' calls follow each other on one
+            # stream)
+            nb = self._lib.aq_decode_attention_workspace(B, self.H, self.Hkv, self.D, L)
+            if nb < 0:
+                raise ValueError("aq_decode_attention_workspace refused these sizes")
+            self.ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
 
     # ------------------------------------------------------------ one step
+
+    def _attend_fused(self, li: int, q, k, v, scale: float, q_scale: float, rope: bool):
+        """aq_decode_attention: q [B, H, D] scaled by q_scale (rounded to
+        fp16) and, with ``rope``, q and the new key k [B, Hkv, D] rotated at
+        pos; k, v written at pos; attention over positions 0..pos."""
+        B, H, Hkv, D = self.B, self.H, self.Hkv, self.D
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        o = torch.empty(B, H * D, dtype=self.dtype, device=self.dev)
+        cs, sn = (self.cos.data_ptr(), self.sin.data_ptr()) if rope else (None, None)
+        _lib.check(self._lib.aq_decode_attention(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), self.k[li].data_ptr(), self.v[li].data_ptr(),
+            self.pos.data_ptr(), B, H, Hkv, D, self.L, ctypes.c_float(scale), ctypes.c_float(q_scale), cs, sn,
+            self.ws.data_ptr(), self.ws.numel(), o.data_ptr(), _lib.stream_of(self.dev)), "aq_decode_attention")
+        return o
+
+    def _addnorm(self, x, delta, mod):
+        """x += delta in place (fp16 add; none when delta is None), then
+        mod(x): one aq_decode_norm launch for HF's Llama/Mistral RMSNorm and
+        for LayerNorm with weight and bias, else the torch add and module."""
+        name = type(mod).__name__
+        rms = name in ("LlamaRMSNorm", "MistralRMSNorm")
+        ln = isinstance(mod, torch.nn.LayerNorm) and mod.weight is not None and mod.bias is not None
+        if (rms or ln) and mod.weight.dtype == self.dtype and x.shape[-1] % 8 == 0 and x.shape[-1] <= 16384:
+            y = torch.empty_like(x)
+            eps = mod.variance_epsilon if rms else mod.eps
+            _lib.check(self._lib.aq_decode_norm(
+                x.data_ptr(), None if delta is None else delta.data_ptr(), mod.weight.data_ptr(),
+                None if rms else mod.bias.data_ptr(), ctypes.c_float(eps), x.shape[0], x.shape[-1], 0 if rms else 1,
+                y.data_ptr(), _lib.stream_of(self.dev)), "aq_decode_norm")
+            return y
+        if delta is not None:
+            x.add_(delta)
+        return mod(x)
+
+    def _silu_mul(self, act, g, u):
+        """act(g) * u: one aq_silu_mul launch for SiLU, else torch."""
+        if type(act).__name__ in ("SiLU", "SiLUActivation") and g.numel() % 8 == 0:
+            out = torch.empty_like(g)
+            _lib.check(self._lib.aq_silu_mul(g.data_ptr(), u.data_ptr(), out.data_ptr(), g.numel(),
+                                             _lib.stream_of(self.dev)), "aq_silu_mul")
+            return out
+        return act(g) * u
+
+    def _layer_fused(self, li, layer, x, delta):
+        """One layer on the GPU path: the residual stream x [B, hidden] is
+        updated in place by the norm launches (x += the previous layer's
+        output delta, then x += this layer's attention output); returns x
+        and the MLP output, which the next norm adds."""
+        B, H, Hkv, D = self.B, self.H, self.Hkv, self.D
+        at = layer.self_attn
+        if self.kind == "opt":
+            h = self._addnorm(x, delta, layer.self_attn_layer_norm)
+            q, k, v = self._linears([at.q_proj, at.k_proj, at.v_proj], h)
+            o = self._attend_fused(li, q.view(B, H, D), k.view(B, Hkv, D), v.view(B, Hkv, D), 1.0, at.scaling,
+                                   rope=False)
+            h = self._addnorm(x, at.out_proj(o), layer.final_layer_norm)
+            return x, layer.fc2(layer.activation_fn(layer.fc1(h)))
+        h = self._addnorm(x, delta, layer.input_layernorm)
+        q, k, v = self._linears([at.q_proj, at.k_proj, at.v_proj], h)
+        o = self._attend_fused(li, q.view(B, H, D), k.view(B, Hkv, D), v.view(B, Hkv, D), at.scaling, 1.0,
+                               rope=True)
+        h = self._addnorm(x, at.o_proj(o), layer.post_attention_layernorm)
+        g, u = self._linears([layer.mlp.gate_proj, layer.mlp.up_proj], h)
+        return x, layer.mlp.down_proj(self._silu_mul(layer.mlp.act_fn, g, u))
 
     def _attend(self, li: int, q, k, v, scale: float = 1.0):
         """Attention of the step's queries q [B, H, D] over positions
         0..pos after writing k, v [B, Hkv, D] at pos (scores rounded to fp16
         as a half-precision product returns them, times ``scale``, softmax
-        in f32)."""
+        in f32) -- the torch form of the step."""
         B, H, Hkv, D = self.B, self.H, self.Hkv, self.D
         K, V = self.k[li], self.v[li]
-        if self.fused:
-            q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-            o = torch.empty(B, H * D, dtype=self.dtype, device=self.dev)
-            _lib.check(self._lib.aq_decode_attention(
-                q.data_ptr(), k.data_ptr(), v.data_ptr(), K.data_ptr(), V.data_ptr(), self.pos.data_ptr(), B, H, Hkv,
-                D, self.L, ctypes.c_float(scale), o.data_ptr(), _lib.stream_of(self.dev)), "aq_decode_attention")
-            return o
         K.index_copy_(2, self.pos, k.reshape(B, Hkv, 1, D))
         V.index_copy_(2, self.pos, v.reshape(B, Hkv, 1, D))
         qg = q.reshape(B, Hkv, H // Hkv, D)
@@ -192,14 +260,20 @@ class GraphDecoder:
             dec = m.model.decoder
             x = dec.embed_tokens(self.tok)
             x = x + dec.embed_positions.weight.index_select(0, self.pos + 2)
-            for li, layer in enumerate(self.layers):
-                x = self._layer_opt(li, layer, x)
-            x = dec.final_layer_norm(x)
+            final, layer_fn = dec.final_layer_norm, self._layer_opt
         else:
             x = m.model.embed_tokens(self.tok)
+            final, layer_fn = m.model.norm, self._layer_llama
+        if self.fused:
+            x = x.contiguous()
+            delta = None
             for li, layer in enumerate(self.layers):
-                x = self._layer_llama(li, layer, x)
-            x = m.model.norm(x)
+                x, delta = self._layer_fused(li, layer, x, delta)
+            x = self._addnorm(x, delta, final)
+        else:
+            for li, layer in enumerate(self.layers):
+                x = layer_fn(li, layer, x)
+            x = final(x)
         logits = m.lm_head(x)  # [B, V]
         nxt = self._argmax(logits)
         self.tok.copy_(nxt)

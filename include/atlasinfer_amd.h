@@ -240,19 +240,56 @@ int aq_qlinear_noalloc(const void* x, int64_t M, int64_t K, int64_t N, const voi
  * history with the new key/value, rotates, and runs SDPA or a BMM softmax
  * (integration/atlas_wrappers.py:161-262); HF's own attention modules do
  * the equivalent.  For batch row b and key/value head j (query heads
- * j G .. j G + G - 1, G = H / Hkv <= 8):
+ * j G .. j G + G - 1, G = H / Hkv in {1, 2, 4, 8}):
  *   k_cache[b, j, pos, :] = k_new[b, j, :];  v_cache[b, j, pos, :] = v_new[b, j, :]
  *   s_p = fp16(q . k_p) * scale, p = 0 .. pos;  w = softmax(s) in f32
  *   out[b, h, :] = fp16(sum_p w_p v_p)   (f32 accumulation, one rounding)
+ * Before that, q is multiplied by q_scale (rounded to fp16; 1 skips it:
+ * OPT's query scaling) and, given rope_cos / rope_sin (fp16 [L, D]), q and
+ * the new key are rotated at pos in the rotate-half form of Llama/Mistral,
+ * x' = fp16(fp16(x cos) + fp16(r sin)), r = (-x[D/2:], x[:D/2]); the cache
+ * receives the rotated key.
  *   q      fp16 [B, H, D]          k_new, v_new fp16 [B, Hkv, D]
  *   k_cache, v_cache fp16 [B, Hkv, L, D] (16-byte aligned)
  *   pos    int64 device scalar, 0 <= pos < L
  *   out    fp16 [B, H, D]          D = 64 or 128
+ *   workspace  at least aq_decode_attention_workspace(B, H, Hkv, D, L)
+ *          bytes, 16-byte aligned: the cache is split into spans of
+ *          positions (one workgroup each) whose partial results a second
+ *          kernel on the same stream merges.  No initial contents needed;
+ *          calls that overlap in time must not share one.
  * A pos outside [0, L) leaves everything untouched (callers keep it inside).
  */
 int aq_decode_attention(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
                         const int64_t* pos, int64_t B, int64_t H, int64_t Hkv, int64_t D, int64_t L, float scale,
+                        float q_scale, const void* rope_cos, const void* rope_sin, void* workspace, int64_t ws_bytes,
                         void* out, void* stream);
+
+/* Bytes of workspace aq_decode_attention needs for these sizes (-1 for
+ * sizes it cannot take).  No counterpart in the reference. */
+int64_t aq_decode_attention_workspace(int64_t B, int64_t H, int64_t Hkv, int64_t D, int64_t L);
+
+/*
+ * Residual add and normalisation of `rows` rows of n fp16 (n a multiple of
+ * 8, at most 16384), one launch.  With delta: x = fp16(x + delta), in place
+ * (the residual stream).  Then y = norm(x):
+ *   mode 0  RMSNorm of Llama/Mistral: y = fp16(w fp16(x / sqrt(mean(x^2) + eps)))
+ *   mode 1  LayerNorm of OPT: y = fp16((x - mean) / sqrt(var + eps) w + bias)
+ * (statistics in f32).  Replaces the norm modules and `x + residual` adds of
+ * HF's OPT / Llama / Mistral decoder layers in the decode steps the reference
+ * drives through model.generate (examples/run_atlas_inference.py:244-264);
+ * the reference's own code has no kernel of its own here.
+ */
+int aq_decode_norm(void* x, const void* delta, const void* weight, const void* bias, float eps, int64_t rows,
+                   int64_t n, int mode, void* y, void* stream);
+
+/*
+ * out = fp16(fp16(silu(g)) u) over n fp16 (n a multiple of 8): the SwiGLU
+ * activation of HF's Llama/Mistral MLPs, act_fn(gate_proj(x)) * up_proj(x),
+ * between two of the reference's quantized linears (no counterpart in the
+ * reference's own code).
+ */
+int aq_silu_mul(const void* g, const void* u, void* out, int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

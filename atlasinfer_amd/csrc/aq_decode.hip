@@ -368,6 +368,16 @@ __global__ __launch_bounds__(kNormThreads) void decode_norm_kernel(uint16_t* __r
   uint16_t* yr = y + (int64_t)blockIdx.x * n;
   float v[kNormChunks][8];
   float s = 0.0f;
+  // the weights (and bias) go out with x, ahead of the reduction
+  uint4 wv[kNormChunks], bv[kNormChunks];
+#pragma unroll
+  for (int c = 0; c < kNormChunks; c++) {
+    const int i = (c * kNormThreads + t) * 8;
+    if (i < n) {
+      wv[c] = *reinterpret_cast<const uint4*>(w + i);
+      bv[c] = MODE == 1 ? *reinterpret_cast<const uint4*>(bias + i) : make_uint4(0, 0, 0, 0);
+    }
+  }
 #pragma unroll
   for (int c = 0; c < kNormChunks; c++) {
     const int i = (c * kNormThreads + t) * 8;
@@ -412,10 +422,7 @@ __global__ __launch_bounds__(kNormThreads) void decode_norm_kernel(uint16_t* __r
   for (int c = 0; c < kNormChunks; c++) {
     const int i = (c * kNormThreads + t) * 8;
     if (i < n) {
-      const uint4 wv = *reinterpret_cast<const uint4*>(w + i);
-      uint4 bv = make_uint4(0, 0, 0, 0);
-      if (MODE == 1) bv = *reinterpret_cast<const uint4*>(bias + i);
-      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w};
+      const uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w}, bw[4] = {bv[c].x, bv[c].y, bv[c].z, bv[c].w};
       uint32_t ow[4] = {0, 0, 0, 0};
 #pragma unroll
       for (int k = 0; k < 8; k++) {

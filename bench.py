@@ -494,6 +494,44 @@ def agree_until(a, b, start):
     return n
 
 
+def config_model(kind, dev, gen):
+    """The fp16 random-init model of BASELINE config 1 (OPT-1.3b) or 3
+    (Mistral-7B), outliers planted as in config 2."""
+    from transformers import MistralConfig, MistralForCausalLM, OPTConfig, OPTForCausalLM
+    if kind == "opt":
+        cfg = OPTConfig(num_hidden_layers=24, hidden_size=2048, num_attention_heads=32, ffn_dim=8192,
+                        vocab_size=50272, max_position_embeddings=2048, word_embed_proj_dim=2048)
+        cls = OPTForCausalLM
+    else:
+        cfg = MistralConfig(num_hidden_layers=32, hidden_size=4096, num_attention_heads=32, num_key_value_heads=8,
+                            head_dim=128, intermediate_size=14336, vocab_size=32000, rope_theta=1e6,
+                            max_position_embeddings=4096)
+        cls = MistralForCausalLM
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = cls(cfg).half().eval()
+    plant_outliers(model, gen)
+    return model, cfg
+
+
+def graph_decode_only(args, dev, log):
+    """Only GraphDecoder on the quantized model of config 1 (``opt``: 32-token
+    prompt, 128 new tokens) or 3 (``mistral``: 512-token prompts, 256 new),
+    at --batch: the run a kernel trace of the decode step is taken from."""
+    from atlasinfer_amd.integration.model_modifier import apply_atlas_quantization_to_model
+    gen = torch.Generator(device=dev).manual_seed(7)
+    model, cfg = config_model(args.graph_decode, dev, gen)
+    apply_atlas_quantization_to_model(model, args.graph_decode, {"block_size": -1, "z_threshold": 3.0,
+                                                                 "code_format": "e4m3"},
+                                      **({"excluded_layers": []} if args.graph_decode == "opt" else {}))
+    S, new = (32, 128) if args.graph_decode == "opt" else (512, 256)
+    ids = torch.randint(0, cfg.vocab_size, (args.batch, S), generator=gen, device=dev)
+    tps, _ = graph_decode_tokps(model, ids, new)
+    log(f"graph decode {args.graph_decode} batch {args.batch}: {tps * args.batch:.1f} tok/s")
+    print(json.dumps({"graph_decode": args.graph_decode, "batch": args.batch, "prompt": S, "new_tokens": new,
+                      "tok_s": round(tps * args.batch, 1)}))
+
+
 def bench_models(dev, which, log):
     """BASELINE configs 1 (OPT-1.3b, every Linear quantized, 32-token prompt,
     128 greedy tokens, batch 1) and 3 (Mistral-7B, 512-token prompts, 256
@@ -502,18 +540,12 @@ def bench_models(dev, which, log):
     Linears swapped by apply_atlas_quantization_to_model (per-channel E4M3).
     HF generate runs eagerly: tok/s there includes the framework's per-token
     Python work, identical in both columns."""
-    from transformers import MistralConfig, MistralForCausalLM, OPTConfig, OPTForCausalLM
     from atlasinfer_amd.integration.model_modifier import apply_atlas_quantization_to_model
     out = {}
     gen = torch.Generator(device=dev).manual_seed(7)
     qcfg = {"block_size": -1, "z_threshold": 3.0, "code_format": "e4m3"}
     if "opt" in which:
-        cfg = OPTConfig(num_hidden_layers=24, hidden_size=2048, num_attention_heads=32, ffn_dim=8192,
-                        vocab_size=50272, max_position_embeddings=2048, word_embed_proj_dim=2048)
-        torch.manual_seed(0)
-        with torch.device(dev):
-            model = OPTForCausalLM(cfg).half().eval()
-        plant_outliers(model, gen)
+        model, cfg = config_model("opt", dev, gen)
         ids = torch.randint(0, cfg.vocab_size, (1, 32), generator=gen, device=dev)
         fp16_tps, _ = generate_tokps(model, ids, 128)
         t0 = time.perf_counter()
@@ -535,13 +567,7 @@ def bench_models(dev, which, log):
         del model
         torch.cuda.empty_cache()
     if "mistral" in which:
-        cfg = MistralConfig(num_hidden_layers=32, hidden_size=4096, num_attention_heads=32, num_key_value_heads=8,
-                            head_dim=128, intermediate_size=14336, vocab_size=32000, rope_theta=1e6,
-                            max_position_embeddings=4096)
-        torch.manual_seed(0)
-        with torch.device(dev):
-            model = MistralForCausalLM(cfg).half().eval()
-        plant_outliers(model, gen)
+        model, cfg = config_model("mistral", dev, gen)
         res = {}
         for phase in ("fp16", "quantized"):
             if phase == "quantized":
@@ -666,6 +692,9 @@ def main():
                          "for counter runs")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the M=2048 prefill launches of one Llama-3-8B layer, for counter runs")
+    ap.add_argument("--graph-decode", choices=["opt", "mistral"],
+                    help="only graph-captured greedy decode of the quantized config-1 / config-3 model, for traces")
+    ap.add_argument("--batch", type=int, default=1, help="batch of --graph-decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the quantized-linear path is single-GPU here; "
@@ -689,6 +718,9 @@ def main():
         return
     if args.gemm_only:
         gemm_only(args, dev, gen, qlinear, qlinear_grouped, AQ)
+        return
+    if args.graph_decode:
+        graph_decode_only(args, dev, log)
         return
 
     # ---- weights: 4 layers x 7 linears, quantized on the GPU (also timed)

@@ -57,6 +57,8 @@ SIGNATURES = {
                                           _I32P, _P, _I64, _P, _P, _P]),
     "aq_decode_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
                                            ctypes.c_float, _P, _P, _P, _I64, _P, _P]),
+    "aq_qlinear_decode": (ctypes.c_int, [_P, _I64, ctypes.c_int, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int,
+                                         _P, _P, _P, ctypes.c_float, _P, _P, _P]),
     "aq_decode_norm": (ctypes.c_int, [_P, _P, _P, _P, ctypes.c_float, _I64, _I64, ctypes.c_int, _P, _P]),
     "aq_silu_mul": (ctypes.c_int, [_P, _P, _P, _I64, _P]),
     "aq_decode_attention_workspace": (ctypes.c_int64, [_I64, _I64, _I64, _I64, _I64]),

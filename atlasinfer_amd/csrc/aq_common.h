@@ -82,6 +82,13 @@ __device__ __forceinline__ f16 rn_h(float f) { return (f16)f; }
 
 // fp16 tensor arithmetic as torch's CPU kernels do it: compute in f32,
 // round once to fp16.
+// fp16(fp16(silu(g)) u), silu(g) = g / (1 + exp(-g)) in f32: the SwiGLU
+// product of fp16 tensors (act_fn(gate) * up).
+__device__ __forceinline__ f16 silu_mul_h(float g, float u) {
+  const f16 a = rn_h(g / (1.0f + __expf(-g)));
+  return rn_h((float)a * u);
+}
+
 __device__ __forceinline__ f16 h_sub(f16 a, f16 b) { return rn_h((float)a - (float)b); }
 __device__ __forceinline__ f16 h_div(f16 a, f16 b) { return rn_h((float)a / (float)b); }  // IEEE f32 div
 

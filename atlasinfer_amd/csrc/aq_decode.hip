@@ -455,8 +455,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
   for (int k = 0; k < 8; k++) {
     const float gk = (float)bits_to_h((uint16_t)(gw[k >> 1] >> (16 * (k & 1))));
     const float uk = (float)bits_to_h((uint16_t)(uw[k >> 1] >> (16 * (k & 1))));
-    const f16 a = rn_h(gk / (1.0f + __expf(-gk)));
-    ow[k >> 1] |= (uint32_t)h_to_bits(rn_h((float)a * uk)) << (16 * (k & 1));
+    ow[k >> 1] |= (uint32_t)h_to_bits(silu_mul_h(gk, uk)) << (16 * (k & 1));
   }
   reinterpret_cast<uint4*>(out)[i] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
 }

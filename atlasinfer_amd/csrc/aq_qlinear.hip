@@ -90,6 +90,7 @@ constexpr int kVmcnt = (N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00;
 template <int NS, int FMT, int PC, int X1, int MM>
 __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   static_assert(!X1 || MM == 1, "x in LDS is for decode");
+  // X1 = 2: x in LDS with aq_qlinear_decode's prologue and epilogue
   constexpr int U = kGemvUnroll;
   // X1 (M = 1): x is staged in LDS once, K fp16 followed by 64 zero bytes
   // that the lanes of rows 1..15 of the MFMA A operand read instead
@@ -301,21 +302,50 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       const int nxp = (K >> 3) + 4;
       const int per = min(XB, (nxp + 64 * NS - 1) / (64 * NS));  // pieces per thread and round
       const __amdgpu_buffer_rsrc_t xr1 = __builtin_amdgcn_make_buffer_rsrc((void*)in.x, (short)0, K * 2, kBufferDword3);
-      u32x4 xv[XB];
+      // Prologue (decode launches of aq_qlinear_decode): what LDS receives
+      // in place of x.  kProSwiGlu: fp16(fp16(silu(x)) u) from x and a.x2,
+      // piece by piece.  kProRms / kProLayerNorm: x itself first, its sum
+      // (of squares) gathered on the way; after a workgroup reduction each
+      // thread rewrites its own pieces as the normalised row.  The norm
+      // weight (and bias) pieces of the first round load with x, ahead of
+      // the codes, so the code loads stay in flight through all of this.
+      // The zero pieces after x stay zero.
+      const int pro = X1 == 2 ? a.pro : kProNone;  // uniform; instances without a prologue drop its code
+      const __amdgpu_buffer_rsrc_t ur = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(pro == kProSwiGlu ? a.x2 : pro != kProNone ? a.nw : in.x), (short)0, pro != kProNone ? K * 2 : 0,
+          kBufferDword3);
+      const __amdgpu_buffer_rsrc_t br1 = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(pro == kProLayerNorm ? a.nb : in.x), (short)0, pro == kProLayerNorm ? K * 2 : 0, kBufferDword3);
+      u32x4 xv[XB], uv[XB], bv[XB];
+      float stat = 0.0f;  // this thread's sum (LayerNorm) or sum of squares (RMSNorm)
       auto x_round = [&](int i0) {
 #pragma unroll
         for (int j = 0; j < XB; j++) {
           const int i = i0 + 64 * NS * j;
-          if (j < per)
-            xv[j] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr1, i < (K >> 3) ? (uint32_t)i * 16 : kOutOfRange, 0, 0));
+          const uint32_t off = i < (K >> 3) ? (uint32_t)i * 16 : kOutOfRange;
+          if (j < per) {
+            xv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr1, off, 0, 0));
+            if (pro != kProNone) uv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ur, off, 0, 0));
+            if (pro == kProLayerNorm)
+              bv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(br1, off, 0, 0));
+          }
         }
       };
       auto x_store = [&](int i0) {
 #pragma unroll
         for (int j = 0; j < XB; j++) {
           const int i = i0 + 64 * NS * j;
-          if (j < per && i < nxp) *reinterpret_cast<u32x4*>(x_lds + 8 * i) = xv[j];
+          if (j < per && i < nxp) {
+            u32x4 v = xv[j];
+            if (pro == kProSwiGlu) {
+              v = swiglu8(xv[j], uv[j]);
+            } else if (pro != kProNone) {
+              const half8 h = __builtin_bit_cast(half8, xv[j]);
+#pragma unroll
+              for (int e = 0; e < 8; e++) stat += pro == kProRms ? (float)h[e] * (float)h[e] : (float)h[e];
+            }
+            *reinterpret_cast<u32x4*>(x_lds + 8 * i) = v;
+          }
         }
       };
       x_round(threadIdx.x);
@@ -337,6 +367,56 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       }
       // wave 0: the tile row's outlier entries load while the codes stream
       if (wave == 0) stage_first_batch();
+      if (pro == kProRms || pro == kProLayerNorm) {
+        // the row's statistics: waves' sums in a fixed order
+        const float sw = wave_group_sum_f32<64>(stat);
+        if (lane == 0) red[wave][0] = sw;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NS; w++) tot += red[w][0];
+        float mean = 0.0f, r;
+        if (pro == kProRms) {
+          r = 1.0f / sqrtf(tot / (float)K + a.eps);
+        } else {
+          mean = tot / (float)K;
+          float q = 0.0f;
+          for (int i = threadIdx.x; i < (K >> 3); i += 64 * NS) {
+            const half8 h = *reinterpret_cast<const half8*>(x_lds + 8 * i);
+#pragma unroll
+            for (int e = 0; e < 8; e++) q += ((float)h[e] - mean) * ((float)h[e] - mean);
+          }
+          const float qw = wave_group_sum_f32<64>(q);
+          if (lane == 0) red[wave][1] = qw;
+          __syncthreads();
+          float qt = 0.0f;
+#pragma unroll
+          for (int w = 0; w < NS; w++) qt += red[w][1];
+          r = 1.0f / sqrtf(qt / (float)K + a.eps);
+        }
+        // each thread rewrites the pieces it stored (with one round, the
+        // weights are still in registers; with more, the later rounds
+        // replaced them and every round loads its own again)
+        const bool one_round = 64 * NS * per >= nxp;
+        for (int i0 = threadIdx.x; i0 < (K >> 3); i0 += 64 * NS * per) {
+          if (!one_round) x_round(i0);
+#pragma unroll
+          for (int j = 0; j < XB; j++) {
+            const int i = i0 + 64 * NS * j;
+            if (j < per && i < (K >> 3)) {
+              const half8 h = *reinterpret_cast<const half8*>(x_lds + 8 * i);
+              const half8 wh = __builtin_bit_cast(half8, uv[j]);
+              const half8 bh = __builtin_bit_cast(half8, bv[j]);
+              half8 o;
+#pragma unroll
+              for (int e = 0; e < 8; e++)
+                o[e] = pro == kProRms ? rn_h((float)wh[e] * (float)rn_h((float)h[e] * r))
+                                      : rn_h(((float)h[e] - mean) * r * (float)wh[e] + (float)bh[e]);
+              *reinterpret_cast<half8*>(x_lds + 8 * i) = o;
+            }
+          }
+        }
+      }
       __syncthreads();
     }
     load_x(B0, wave);
@@ -387,7 +467,12 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
 #pragma unroll
       for (int w = 0; w < NS; w++) dense += red[w][lane * 4];
       const float v = dense + s_osum[0][lane] + (float)bits_to_h((uint16_t)bias_v);
-      W.y[n0 + lane] = h_to_bits(rn_h(v));
+      f16 o = rn_h(v);
+      if (X1 == 2) {
+        if (W.act == 1 && (float)o < 0.0f) o = (f16)0.0f;                   // ReLU
+        if (W.res) o = rn_h((float)bits_to_h(W.res[n0 + lane]) + (float)o);  // residual add
+      }
+      W.y[n0 + lane] = h_to_bits(o);
     }
     return;
   }
@@ -1361,6 +1446,7 @@ dim3 gemv_pieces(const QLArgs& a, int unit, QLArgs* g) {
       q.scales = w.scales + (size_t)row0 * w.kg;
       q.row_ptr = w.row_ptr + row0;
       q.bias = w.bias ? w.bias + row0 : nullptr;
+      q.res = w.res ? w.res + row0 : nullptr;
       q.y = w.y + row0;
       q.N = 16 * std::min(P, w.N / 16 - r0);
       q.ldy = w.N;
@@ -1386,6 +1472,15 @@ hipError_t launch_gemv(const QLArgs& a, bool per_channel, hipStream_t s) {
   constexpr int R = kGemvDirectMaxM;
   QLArgs p;
   const dim3 g = gemv_pieces(a, 1, &p), b(64 * NS);
+  bool fused = a.pro != kProNone;
+  for (int i = 0; i < a.count; i++) fused = fused || a.mat[i].res || a.mat[i].act;
+  if (fused) {  // aq_qlinear_decode: M = 1 and K within the x-in-LDS limit, checked there
+    if (per_channel)
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 2, 1>), g, b, lds, s, p);
+    else
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 2, 1>), g, b, lds, s, p);
+    return hipGetLastError();
+  }
   if (per_channel) {
     if (x1)
       hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 1, 1>), g, b, lds, s, p);
@@ -1560,13 +1655,23 @@ extern "C" int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K) {
 
 
 
-extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, int64_t count, const int64_t* Ns,
-                                  const void* const* codes, const void* const* scales, const int64_t* Gs,
-                                  const int32_t* const* row_ptrs, const int32_t* const* cols,
-                                  const void* const* vals, const int32_t* const* tile_ptrs,
-                                  const uint32_t* const* tile_ents, const int64_t* tile_maxes,
-                                  const void* const* biases, void* const* ys, void* workspace,
-                                  int64_t workspace_bytes, void* stream) {
+// aq_qlinear_decode's additions to a grouped launch
+struct DecodeFuse {
+  int pro;
+  const void* x2;
+  const void* nw;
+  const void* nb;
+  float eps;
+  const void* const* res;
+  const int32_t* act;
+};
+
+static int qlinear_grouped_impl(const void* x, int64_t M, int64_t K, int fmt, int64_t count, const int64_t* Ns,
+                                const void* const* codes, const void* const* scales, const int64_t* Gs,
+                                const int32_t* const* row_ptrs, const int32_t* const* cols, const void* const* vals,
+                                const int32_t* const* tile_ptrs, const uint32_t* const* tile_ents,
+                                const int64_t* tile_maxes, const void* const* biases, void* const* ys,
+                                void* workspace, int64_t workspace_bytes, void* stream, const DecodeFuse* fz) {
   AQ_CHECK_ARG(count >= 1 && count <= kMaxGroup, "aq_qlinear: 1..%d matrices per call (got %lld)", kMaxGroup,
                (long long)count);
   AQ_CHECK_ARG(M >= 0 && M < (1 << 30) && K >= 128 && K % 128 == 0,
@@ -1617,6 +1722,30 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
   }
   for (int i = (int)count; i <= kMaxGroup; i++) a.first[i] = (int)blocks;
   a.split = 1;
+  if (fz) {
+    // decode: the M = 1 GEMV with x in LDS (the only kernel with the prologue / epilogue)
+    AQ_CHECK_ARG(M == 1 && K <= kGemvX1MaxK, "aq_qlinear_decode: M = 1 and K <= %d (M=%lld K=%lld)", kGemvX1MaxK,
+                 (long long)M, (long long)K);
+    AQ_CHECK_ARG(fz->pro >= kProNone && fz->pro <= kProSwiGlu, "aq_qlinear_decode: unknown prologue %d", fz->pro);
+    AQ_CHECK_ARG(fz->pro != kProSwiGlu || (fz->x2 && (uintptr_t)fz->x2 % 16 == 0),
+                 "aq_qlinear_decode: SwiGLU needs u (16-byte aligned)");
+    AQ_CHECK_ARG((fz->pro != kProRms && fz->pro != kProLayerNorm) || (fz->nw && (uintptr_t)fz->nw % 16 == 0),
+                 "aq_qlinear_decode: the norm needs its weight (16-byte aligned)");
+    AQ_CHECK_ARG(fz->pro != kProLayerNorm || (fz->nb && (uintptr_t)fz->nb % 16 == 0),
+                 "aq_qlinear_decode: LayerNorm needs its bias (16-byte aligned)");
+    a.pro = fz->pro;
+    a.x2 = (const uint16_t*)fz->x2;
+    a.nw = (const uint16_t*)fz->nw;
+    a.nb = (const uint16_t*)fz->nb;
+    a.eps = fz->eps;
+    for (int i = 0; i < count; i++) {
+      a.mat[i].res = fz->res ? (const uint16_t*)fz->res[i] : nullptr;
+      a.mat[i].act = fz->act ? fz->act[i] : 0;
+      AQ_CHECK_ARG(a.mat[i].act == 0 || a.mat[i].act == 1, "aq_qlinear_decode: activation %d (0 none, 1 ReLU)",
+                   a.mat[i].act);
+      AQ_CHECK_ARG(a.mat[i].res != ys[i], "aq_qlinear_decode: the residual must not be the output");
+    }
+  }
   if (M == 0) return AQ_OK;
   hipStream_t s = (hipStream_t)stream;
   bool per_channel = true;
@@ -1676,6 +1805,28 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
     e = hipGetLastError();
   }
   return aq::check_hip(e, "aq_qlinear: split-K reduce launch");
+}
+
+extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, int64_t count, const int64_t* Ns,
+                                  const void* const* codes, const void* const* scales, const int64_t* Gs,
+                                  const int32_t* const* row_ptrs, const int32_t* const* cols,
+                                  const void* const* vals, const int32_t* const* tile_ptrs,
+                                  const uint32_t* const* tile_ents, const int64_t* tile_maxes,
+                                  const void* const* biases, void* const* ys, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  return qlinear_grouped_impl(x, M, K, fmt, count, Ns, codes, scales, Gs, row_ptrs, cols, vals, tile_ptrs, tile_ents,
+                              tile_maxes, biases, ys, workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int aq_qlinear_decode(const void* x, int64_t K, int fmt, int64_t count, const int64_t* Ns,
+                                 const void* const* codes, const void* const* scales, const int64_t* Gs,
+                                 const int32_t* const* row_ptrs, const int32_t* const* cols, const void* const* vals,
+                                 const void* const* biases, void* const* ys, int prologue, const void* x2,
+                                 const void* norm_weight, const void* norm_bias, float eps,
+                                 const void* const* residuals, const int32_t* relu, void* stream) {
+  const DecodeFuse fz{prologue, x2, norm_weight, norm_bias, eps, residuals, relu};
+  return qlinear_grouped_impl(x, 1, K, fmt, count, Ns, codes, scales, Gs, row_ptrs, cols, vals, nullptr, nullptr,
+                              nullptr, biases, ys, nullptr, 0, stream, &fz);
 }
 
 extern "C" int aq_qlinear(const void* x, int64_t M, int64_t K, int64_t N, const void* codes, const void* scales,

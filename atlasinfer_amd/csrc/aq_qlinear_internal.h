@@ -34,11 +34,23 @@ struct QLMat {
   int kg;      // K / G, scale blocks per row
   int gshift;  // log2(G) when G is a power of two, else -1
   int ldy;     // row stride of y: the whole matrix's N
+  // decode epilogue (M = 1 GEMV only; zero elsewhere): act 1 = ReLU of the
+  // fp16 output, then res (fp16 [N], this piece's rows) added in fp16
+  const uint16_t* res;
+  int act;
 };
+
+// Prologue of the M = 1 GEMV: what is staged in LDS in place of x.
+enum : int { kProNone = 0, kProRms = 1, kProLayerNorm = 2, kProSwiGlu = 3 };
 
 struct QLArgs {
   const uint16_t* x;
   int M, K, count;
+  int pro;              // kPro*: 0 stages x as given
+  const uint16_t* x2;   // kProSwiGlu: u (x holds the gate g)
+  const uint16_t* nw;   // kProRms / kProLayerNorm: weight [K]
+  const uint16_t* nb;   // kProLayerNorm: bias [K]
+  float eps;
   int split;                 // GEMM: ways the K chunks are split (1: none)
   int first[kMaxGroup + 1];  // GEMM: first output tile of each matrix
   QLMat mat[kMaxPieces];     // GEMM: the group's matrices; GEMV: their pieces
@@ -58,6 +70,15 @@ __device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(
 __device__ __forceinline__ uint32_t h2_bits(half2v h) { return __builtin_bit_cast(uint32_t, h); }
 
 // 8 codes (two dwords) -> 8 fp16 weights value(code) * s.
+// eight fp16 pairs (g, u) -> fp16(fp16(silu(g)) u)
+__device__ __forceinline__ u32x4 swiglu8(u32x4 g, u32x4 u) {
+  const half8 gh = __builtin_bit_cast(half8, g), uh = __builtin_bit_cast(half8, u);
+  half8 o;
+#pragma unroll
+  for (int e = 0; e < 8; e++) o[e] = silu_mul_h((float)gh[e], (float)uh[e]);
+  return __builtin_bit_cast(u32x4, o);
+}
+
 template <int FMT>
 __device__ __forceinline__ half8 deq8(uint32_t w0, uint32_t w1, half2v s2) {
   uint32_t r[4];

@@ -99,6 +99,44 @@ def qlinear_grouped(x: torch.Tensor, qts, biases=None, codes=None, tiles=None):
     return [y.view(*x.shape[:-1], N) for y, N in zip(ys, Ns)]
 
 
+PRO_NONE, PRO_RMS, PRO_LAYERNORM, PRO_SWIGLU = 0, 1, 2, 3
+
+
+def qlinear_decode(x: torch.Tensor, qts, biases, codes, prologue: int = PRO_NONE, x2=None, norm_weight=None,
+                   norm_bias=None, eps: float = 0.0, residuals=None, relu=None):
+    """One M = 1 launch of aq_qlinear_decode: [f(x) W_i^T + b_i] for up to 4
+    quantized W_i sharing in_features, where f is the prologue (none,
+    RMSNorm / LayerNorm with ``norm_weight`` / ``norm_bias`` and ``eps``, or
+    the SwiGLU product silu(x) * x2), each output optionally passed through
+    ReLU (``relu[i]``) and added to ``residuals[i]`` (fp16 [1, N_i]).
+    ``codes`` are the weights' tiled code arrays."""
+    dev = x.device
+    L = _lib.load()
+    n = len(qts)
+    K = int(qts[0].original_shape[-1])
+    fmt = qts[0].code_format
+    for q in qts:
+        if int(q.original_shape[-1]) != K or q.code_format != fmt or not fused_supported(q):
+            raise ValueError("qlinear_decode: weights must share in_features and code format and tile")
+    xs = [x.reshape(-1, K)] + ([x2.reshape(-1, K)] if x2 is not None else [])
+    for t in xs:
+        if t.shape[0] != 1 or not t.is_contiguous() or t.data_ptr() % 16 or t.dtype != torch.float16:
+            raise ValueError("qlinear_decode: x (and x2) must be one contiguous, 16-byte aligned fp16 row")
+    Ns = [_rows_cols(q.original_shape)[0] for q in qts]
+    ys = [torch.empty((1, N), dtype=torch.float16, device=dev) for N in Ns]
+    arr = _lib.ptr_array
+    res = None if residuals is None else arr([_lib.ptr(r) for r in residuals])
+    acts = None if relu is None else arr([int(bool(r)) for r in relu], ctypes.c_int32)
+    _lib.check(L.aq_qlinear_decode(
+        xs[0].data_ptr(), K, _format_id(fmt), n, arr(Ns, ctypes.c_int64), arr([c.data_ptr() for c in codes]),
+        arr([q.scale_factors.data_ptr() for q in qts]), arr([q.block_size for q in qts], ctypes.c_int64),
+        arr([q.outlier_row_ptr.data_ptr() for q in qts]), arr([_lib.ptr(q.outlier_cols) for q in qts]),
+        arr([_lib.ptr(q.fp16_outliers) for q in qts]), arr([_lib.ptr(b) for b in biases]),
+        arr([y.data_ptr() for y in ys]), int(prologue), None if x2 is None else xs[1].data_ptr(), _lib.ptr(norm_weight),
+        _lib.ptr(norm_bias), ctypes.c_float(eps), res, acts, _lib.stream_of(dev)), "aq_qlinear_decode")
+    return ys
+
+
 def qlinear(x: torch.Tensor, qt: QuantizedTensor, bias: Optional[torch.Tensor],
             codes: Optional[torch.Tensor] = None, tiles=None) -> torch.Tensor:
     """y = x W^T + b for W in quantized form, through aq_qlinear.  ``codes``

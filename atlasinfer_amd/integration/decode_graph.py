@@ -21,7 +21,10 @@ except the shapes: batch, cache length, model dimensions.  The host only
 guards that a replay never runs past the cache (``max_len``), so no index
 leaves its buffer.
 
-On the GPU with an fp16 model a layer's step is about nine launches: one
+At batch 1 with quantized linears a layer is five launches (six with the
+attention's span merge): the norms, the SwiGLU product (OPT: ReLU) and the
+residual adds run inside the GEMV launches (``aq_qlinear_decode``).
+Otherwise, on the GPU with an fp16 model, a layer's step is about nine launches: one
 residual add + norm (``aq_decode_norm``) before the attention and one
 before the MLP, the q/k/v and gate/up projections as one grouped
 QuantizedLinear launch each, the attention (``aq_decode_attention``: query
@@ -118,6 +121,9 @@ class GraphDecoder:
             if nb < 0:
                 raise ValueError("aq_decode_attention_workspace refused these sizes")
             self.ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
+        # batch 1 with quantized linears: norms, SwiGLU / ReLU and residual
+        # adds folded into the GEMV launches (aq_qlinear_decode)
+        self.b1 = self._decode_ready()
 
     # ------------------------------------------------------------ one step
 
@@ -162,6 +168,85 @@ class GraphDecoder:
                                              _lib.stream_of(self.dev)), "aq_silu_mul")
             return out
         return act(g) * u
+
+    # ---------------------------------------------- batch 1: five launches a layer
+
+    def _decode_ready(self) -> bool:
+        """Whether every layer can take the batch-1 form: all its linears
+        QuantizedLinear weights the fused GEMV takes (K <= 16384), the norms
+        HF's RMSNorm (Llama / Mistral, SiLU MLP) or LayerNorm with bias and
+        ReLU (OPT)."""
+        from .atlas_wrappers import fused_supported
+        if not (self.fused and self.B == 1):
+            return False
+
+        def lin_ok(*mods):
+            if not all(type(m).__name__ == "QuantizedLinear" for m in mods):
+                return False
+            qs = [m.quantized_weights for m in mods]
+            return (all(fused_supported(q) for q in qs) and len({int(q.original_shape[-1]) for q in qs}) == 1
+                    and len({q.code_format for q in qs}) == 1 and int(qs[0].original_shape[-1]) <= 16384)
+
+        def norm_ok(mod):
+            if self.kind == "opt":
+                return isinstance(mod, torch.nn.LayerNorm) and mod.weight is not None and mod.bias is not None
+            return type(mod).__name__ in ("LlamaRMSNorm", "MistralRMSNorm")
+
+        for layer in self.layers:
+            at = layer.self_attn
+            if self.kind == "opt":
+                ok = (lin_ok(at.q_proj, at.k_proj, at.v_proj) and lin_ok(at.out_proj) and lin_ok(layer.fc1)
+                      and lin_ok(layer.fc2) and norm_ok(layer.self_attn_layer_norm) and norm_ok(layer.final_layer_norm)
+                      and isinstance(layer.activation_fn, torch.nn.ReLU))
+            else:
+                ok = (lin_ok(at.q_proj, at.k_proj, at.v_proj) and lin_ok(at.o_proj)
+                      and lin_ok(layer.mlp.gate_proj, layer.mlp.up_proj) and lin_ok(layer.mlp.down_proj)
+                      and norm_ok(layer.input_layernorm) and norm_ok(layer.post_attention_layernorm)
+                      and type(layer.mlp.act_fn).__name__ in ("SiLU", "SiLUActivation"))
+            if not ok:
+                return False
+        return True
+
+    def _qdec(self, mods, x, norm=None, u=None, res=None, relu=None):
+        """aq_qlinear_decode over ``mods`` (QuantizedLinear sharing x): the
+        norm module or the SwiGLU product with u applied to x first, ReLU
+        and residual adds on the outputs."""
+        from .atlas_wrappers import PRO_LAYERNORM, PRO_NONE, PRO_RMS, PRO_SWIGLU, qlinear_decode
+        qs = [m._weights_on(self.dev) for m in mods]
+        for m, q in zip(mods, qs):
+            m._ensure_codes(q, self.dev)
+        pro, nw, nb, eps = PRO_NONE, None, None, 0.0
+        if norm is not None:
+            if isinstance(norm, torch.nn.LayerNorm):
+                pro, nw, nb, eps = PRO_LAYERNORM, norm.weight, norm.bias, norm.eps
+            else:
+                pro, nw, eps = PRO_RMS, norm.weight, norm.variance_epsilon
+        elif u is not None:
+            pro = PRO_SWIGLU
+        return qlinear_decode(x, qs, [m.bias for m in mods], [m._codes for m in mods], pro, u, nw, nb, eps, res,
+                              relu)
+
+    def _layer_b1(self, li, layer, x):
+        """One layer at batch 1 in five launches (OPT: five, plus none for
+        the ReLU): norm + q/k/v, attention (+ span merge), o_proj + residual,
+        norm + gate/up (OPT: norm + fc1 + ReLU), SwiGLU + down + residual
+        (OPT: fc2 + residual).  x [1, hidden] is the residual stream; returns
+        the next one."""
+        B, H, Hkv, D = self.B, self.H, self.Hkv, self.D
+        at = layer.self_attn
+        if self.kind == "opt":
+            q, k, v = self._qdec([at.q_proj, at.k_proj, at.v_proj], x, norm=layer.self_attn_layer_norm)
+            o = self._attend_fused(li, q.view(B, H, D), k.view(B, Hkv, D), v.view(B, Hkv, D), 1.0, at.scaling,
+                                   rope=False)
+            x1 = self._qdec([at.out_proj], o, res=[x])[0]
+            f = self._qdec([layer.fc1], x1, norm=layer.final_layer_norm, relu=[1])[0]
+            return self._qdec([layer.fc2], f, res=[x1])[0]
+        q, k, v = self._qdec([at.q_proj, at.k_proj, at.v_proj], x, norm=layer.input_layernorm)
+        o = self._attend_fused(li, q.view(B, H, D), k.view(B, Hkv, D), v.view(B, Hkv, D), at.scaling, 1.0,
+                               rope=True)
+        x1 = self._qdec([at.o_proj], o, res=[x])[0]
+        g, u = self._qdec([layer.mlp.gate_proj, layer.mlp.up_proj], x1, norm=layer.post_attention_layernorm)
+        return self._qdec([layer.mlp.down_proj], g, u=u, res=[x1])[0]
 
     def _layer_fused(self, li, layer, x, delta):
         """One layer on the GPU path: the residual stream x [B, hidden] is
@@ -264,7 +349,12 @@ class GraphDecoder:
         else:
             x = m.model.embed_tokens(self.tok)
             final, layer_fn = m.model.norm, self._layer_llama
-        if self.fused:
+        if self.b1:
+            x = x.contiguous()
+            for li, layer in enumerate(self.layers):
+                x = self._layer_b1(li, layer, x)
+            x = self._addnorm(x, None, final)
+        elif self.fused:
             x = x.contiguous()
             delta = None
             for li, layer in enumerate(self.layers):

@@ -233,6 +233,31 @@ int aq_qlinear_noalloc(const void* x, int64_t M, int64_t K, int64_t N, const voi
                        void* y, void* stream);
 
 /*
+ * One decode-step launch of up to 4 quantized linears sharing x (M = 1
+ * row, K <= 16384), with the layer's neighbouring elementwise work folded
+ * in: the M = 1 path of aq_qlinear_grouped (the reference's
+ * QuantizedLinear.forward, integration/atlas_wrappers.py:56-67, at one
+ * token) plus
+ *   prologue  what the linears read instead of x:
+ *             0  x as given
+ *             1  RMSNorm(x): fp16(w fp16(x / sqrt(mean(x^2) + eps)))   (norm_weight)
+ *             2  LayerNorm(x): fp16((x - mean) / sqrt(var + eps) w + b) (norm_weight, norm_bias)
+ *             3  fp16(fp16(silu(x)) x2)  (x the gate, x2 the up projection)
+ *             (the statistics in f32 over the row; the HF modules' order)
+ *   epilogue  per member i: relu[i] = 1 applies ReLU to the fp16 output,
+ *             then residuals[i] (fp16 [N_i], or NULL) is added in fp16.
+ * relu and residuals may be NULL (none for every member).  The residual
+ * must not be the output.  Replaces, at decode, the norm / activation /
+ * residual operations of HF's decoder layers around the reference's
+ * QuantizedLinear calls (no counterpart of its own in the reference).
+ */
+int aq_qlinear_decode(const void* x, int64_t K, int fmt, int64_t count, const int64_t* Ns, const void* const* codes,
+                      const void* const* scales, const int64_t* Gs, const int32_t* const* row_ptrs,
+                      const int32_t* const* cols, const void* const* vals, const void* const* biases, void* const* ys,
+                      int prologue, const void* x2, const void* norm_weight, const void* norm_bias, float eps,
+                      const void* const* residuals, const int32_t* relu, void* stream);
+
+/*
  * Attention of one decode step over a static key/value cache, the position
  * read from device memory (so that a captured HIP graph replays it for
  * every token).  Replaces the attention part of a decode step's forward:

@@ -40,6 +40,7 @@ def test_graph_replays_match_eager_steps(kind, batch):
     ids = torch.randint(0, 512, (batch, 9), device=DEV)
     g = GraphDecoder(m, batch=batch, max_len=40, graph=True)
     e = GraphDecoder(m, batch=batch, max_len=40, graph=False)
+    assert g.b1 == e.b1 == (batch == 1)
     for _ in range(2):  # a second sequence reuses the captured graph
         assert torch.equal(g.prefill(ids), e.prefill(ids))
         for t in range(20):
@@ -52,21 +53,25 @@ def test_graph_replays_match_eager_steps(kind, batch):
 
 
 @pytest.mark.parametrize("kind", ["opt", "llama"])
-def test_graph_generate_follows_hf_generate(kind):
+@pytest.mark.parametrize("batch", [1, 2])
+def test_graph_generate_follows_hf_generate(kind, batch):
+    """Batch 1 takes the five-launch layers (norms, activation and residual
+    adds inside the GEMV launches), batch 2 the nine-launch ones."""
     m = _model(kind, 2)
-    ids = torch.randint(0, 512, (2, 12), device=DEV)
+    ids = torch.randint(0, 512, (batch, 12), device=DEV)
     n = 16
     with torch.no_grad():
         ref = m.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=n, do_sample=False,
                          return_dict_in_generate=True, output_logits=True)
-    g = GraphDecoder(m, batch=2, max_len=64)
+    g = GraphDecoder(m, batch=batch, max_len=64)
+    assert g.b1 == (batch == 1)
     out = g.generate(ids, n)
     assert out.shape == ref.sequences.shape
     for t in range(n):
         a, b = out[:, 12 + t], ref.sequences[:, 12 + t]
         lg = ref.logits[t].float()
         top2 = lg.topk(2, dim=-1).values
-        for row in range(2):
+        for row in range(batch):
             if a[row] != b[row]:
                 # only a near-tie of HF's two best logits may flip the choice
                 gap = (top2[row, 0] - top2[row, 1]).item()

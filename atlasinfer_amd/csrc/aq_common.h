@@ -82,10 +82,12 @@ __device__ __forceinline__ f16 rn_h(float f) { return (f16)f; }
 
 // fp16 tensor arithmetic as torch's CPU kernels do it: compute in f32,
 // round once to fp16.
-// fp16(fp16(silu(g)) u), silu(g) = g / (1 + exp(-g)) in f32: the SwiGLU
-// product of fp16 tensors (act_fn(gate) * up).
+// fp16(fp16(silu(g)) u), silu(g) = g / (1 + exp(-g)) in f32 with the
+// hardware reciprocal (1 ulp) for the division: the SwiGLU product of fp16
+// tensors (act_fn(gate) * up).  The second product of two fp16 values is
+// exact in f32, so its one rounding is the fp16 multiply's.
 __device__ __forceinline__ f16 silu_mul_h(float g, float u) {
-  const f16 a = rn_h(g / (1.0f + __expf(-g)));
+  const f16 a = rn_h(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)));
   return rn_h((float)a * u);
 }
 

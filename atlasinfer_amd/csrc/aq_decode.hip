@@ -30,30 +30,57 @@ __device__ __forceinline__ f16 rope_h(f16 x, f16 partner, bool lo, uint16_t c, u
   return rn_h((float)a + (float)b2);
 }
 
-// Splitting of the cache among workgroups: one wave per workgroup takes a
-// span of nt chunks of 64 positions, nt the smallest power of two that
-// leaves ns = ceil(L / (64 nt)) <= 64 spans per head and B Hkv ns <= 4096
-// workgroups (or one span for the whole cache).
+// Splitting of the cache among workgroups.  A cache of at most 16 chunks of
+// 64 positions may be one span per head, its chunks dealt to nw = min(4,
+// chunks) waves of one workgroup that merge their results in LDS (no
+// second kernel): taken when a wave's serial share is short -- at most 4
+// chunk-units of work, a chunk costing G D / 64 units (scores and value
+// sums of 64 positions per lane, about 1000 vector instructions at G = 4,
+// D = 128) -- or when B Hkv >= 256 workgroups keep every SIMD busy anyway.
+// (Measured: OPT-1.3b batch 1, 32 heads of D = 64, 3 chunks: one span
+// 1168 against 1119 tok/s; Mistral-7B batch 32, 256 heads x batch rows:
+// 8116 against 7531; Mistral-7B batch 1, 8 key/value heads of G = 4,
+// D = 128, 12 chunks: 398 against 439, so split.)  Otherwise the cache is
+// split into spans of nt chunks, one wave each, nt the smallest power of
+// two that leaves ns = ceil(L / (64 nt)) <= 64 spans per head and
+// B Hkv ns <= 4096 workgroups (or one span for the whole cache);
+// decode_combine_kernel merges the spans.
 constexpr int kChunk = 64;
+constexpr int kOneSpanChunks = 16;
+constexpr int kMaxWaves = 4;  // one per SIMD: 8 would halve the registers a wave may hold (D = 128 then spills)
 constexpr int64_t kMaxGroups = 4096;
 constexpr int64_t kMaxSpans = 64;
 
 struct Split {
-  int64_t nt, ns, part_floats, bytes;
+  int64_t nt, ns, nw, part_floats, bytes;
 };
 
 // G query heads share a key/value head; a span's partial result is its
 // running maximum and denominator per query head and its G x D weighted sum.
 inline Split split_of(int64_t B, int64_t Hkv, int64_t G, int64_t D, int64_t L) {
   Split sp;
-  sp.nt = 1;
-  auto spans = [&](int64_t nt) { return (L + kChunk * nt - 1) / (kChunk * nt); };
-  while (kChunk * sp.nt < L && (spans(sp.nt) > kMaxSpans || B * Hkv * spans(sp.nt) > kMaxGroups)) sp.nt *= 2;
-  sp.ns = spans(sp.nt);
+  const int64_t chunks = (L + kChunk - 1) / kChunk;
   sp.part_floats = G * D + 2 * G;
+  const int64_t nw1 = std::min<int64_t>(kMaxWaves, chunks);
+  const int64_t serial_units = (chunks + nw1 - 1) / nw1 * G * D / 64;
+  if (chunks <= kOneSpanChunks && (serial_units <= 4 || B * Hkv >= 256)) {
+    sp.nt = chunks;
+    sp.ns = 1;
+    sp.nw = nw1;
+  } else {
+    sp.nw = 1;
+    sp.nt = 1;
+    auto spans = [&](int64_t nt) { return (L + kChunk * nt - 1) / (kChunk * nt); };
+    while (kChunk * sp.nt < L && (spans(sp.nt) > kMaxSpans || B * Hkv * spans(sp.nt) > kMaxGroups)) sp.nt *= 2;
+    sp.ns = spans(sp.nt);
+  }
   sp.bytes = B * Hkv * sp.ns * sp.part_floats * 4;
   return sp;
 }
+
+// LDS of one workgroup of nw waves: per wave a chunk's softmax numerators
+// [G][64] and its merged result [G D + 2 G] (floats).
+inline size_t attention_lds(int64_t G, int64_t D, int64_t nw) { return (size_t)nw * (G * kChunk + G * D + 2 * G) * 4; }
 
 // Workgroup (j, b, z) takes key/value head j of batch row b (query heads
 // j G .. j G + G - 1) and cache positions z span .. z span + span - 1
@@ -64,8 +91,9 @@ inline Split split_of(int64_t B, int64_t Hkv, int64_t G, int64_t D, int64_t L) {
 // fp16, as a half-precision matrix product returns it), softmax over them in
 // f32 and o = sum_p softmax_p v_p accumulated in f32, rounded to fp16 once.
 //
-// Within a span, chunk by chunk with a running maximum (the sums so far are
-// rescaled by exp(m_old - m_new)):
+// Wave w of the workgroup takes chunks w, w + nw, ... of the span, chunk
+// by chunk with a running maximum (the sums so far are rescaled by
+// exp(m_old - m_new)):
 //   scores  lane ln takes position t0 + ln, its key row in D / 8 loads of
 //           16 bytes, the queries as 16-byte LDS broadcasts;
 //   values  lane ln takes the 16-byte chunk ln % (D / 8) of rows
@@ -79,14 +107,16 @@ inline Split split_of(int64_t B, int64_t Hkv, int64_t G, int64_t D, int64_t L) {
 // x' = fp16(fp16(x c) + fp16(r s)), r = (-x[D/2:], x[:D/2]) -- the order
 // and roundings of fp16 tensor arithmetic.
 //
-// With one span holding positions the span writes out itself; otherwise
-// every span with positions writes (m, l, sum) to its slot of part and
+// The waves' results meet in LDS (maximum M over the waves, each wave's
+// sums scaled by exp(m_w - M), waves in order).  With one span holding
+// positions the workgroup writes out itself; otherwise every span with
+// positions writes (M, l, sum) to its slot of part and
 // decode_combine_kernel, launched next on the same stream, merges them.  (A
 // merge inside this kernel by the last span to arrive would need an
 // agent-scope release per span, which writes back the whole L2 of the
 // span's XCD; the kernel boundary orders the slots for free.)
 template <int D, int G>
-__global__ __launch_bounds__(64) void decode_attention_kernel(
+__global__ __launch_bounds__(64 * kMaxWaves) void decode_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, const int64_t* __restrict__ pos_p, int H, int Hkv,
     int L, float scale, float q_scale, const uint16_t* __restrict__ rcos, const uint16_t* __restrict__ rsin, int nt,
@@ -95,7 +125,9 @@ __global__ __launch_bounds__(64) void decode_attention_kernel(
   constexpr int RPW = 64 / KV;  // rows one wave-wide load covers
   constexpr int NL = KV;        // loads per lane for 64 rows
   constexpr int PF = G * D + 2 * G;
-  const int j = blockIdx.x, b = blockIdx.y, z = blockIdx.z, ln = threadIdx.x;
+  const int j = blockIdx.x, b = blockIdx.y, z = blockIdx.z, t = threadIdx.x;
+  const int nw = blockDim.x >> 6, ln = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int64_t pos = *pos_p;
   if (pos < 0 || pos >= L) return;  // the caller guards this; no access outside the cache
   const int64_t span = (int64_t)kChunk * nt, z0 = (int64_t)z * span;
@@ -110,12 +142,14 @@ __global__ __launch_bounds__(64) void decode_attention_kernel(
 
   __shared__ uint4 qs[G][KV];    // the group's queries, fp16
   __shared__ uint4 krot[KV];     // position pos's key as cached (last span only)
-  __shared__ float w[G][kChunk]; // a chunk's softmax numerators
+  extern __shared__ float dyn[];
+  float* w = dyn + wave * G * kChunk;     // this wave's numerators [G][64]
+  float* res = dyn + nw * G * kChunk;     // the waves' results [nw][PF]
 
   const uint16_t* cs = rcos ? rcos + pos * D : nullptr;
   const uint16_t* sn = rsin ? rsin + pos * D : nullptr;
   const uint16_t* qb = q + ((int64_t)b * H + (int64_t)j * G) * D;
-  for (int i = ln; i < G * D; i += 64) {
+  for (int i = t; i < G * D; i += 64 * nw) {
     const int d = i % D;
     f16 v = scale_h(bits_to_h(qb[i]), q_scale);
     if (cs) v = rope_h(v, scale_h(bits_to_h(qb[i - d + (d + D / 2) % D]), q_scale), d < D / 2, cs[d], sn[d]);
@@ -124,16 +158,16 @@ __global__ __launch_bounds__(64) void decode_attention_kernel(
   const bool last = z == nact - 1;  // the span holding pos
   if (last) {
     const uint16_t* kb = k_new + kv * D;
-    for (int d = ln; d < D; d += 64) {
+    for (int d = t; d < D; d += 64 * nw) {
       f16 v = bits_to_h(kb[d]);
       if (cs) v = rope_h(v, bits_to_h(kb[(d + D / 2) % D]), d < D / 2, cs[d], sn[d]);
       reinterpret_cast<uint16_t*>(krot)[d] = h_to_bits(v);
     }
   }
   __syncthreads();
-  if (last && ln < KV) {
-    reinterpret_cast<uint4*>(Kc + pos * D)[ln] = krot[ln];
-    reinterpret_cast<uint4*>(Vc + pos * D)[ln] = vn[ln];
+  if (last && t < KV) {
+    reinterpret_cast<uint4*>(Kc + pos * D)[t] = krot[t];
+    reinterpret_cast<uint4*>(Vc + pos * D)[t] = vn[t];
   }
 
   const int ch = ln % KV, rs = ln / KV;
@@ -146,7 +180,7 @@ __global__ __launch_bounds__(64) void decode_attention_kernel(
     for (int h = 0; h < 8; h++) acc[g][h] = 0.0f;
   }
 
-  for (int it = 0; it < nt; it++) {
+  for (int it = wave; it < nt; it += nw) {
     const int64_t t0 = z0 + (int64_t)it * kChunk;
     if (t0 > pos) break;
     const int64_t p = t0 + ln;
@@ -185,10 +219,14 @@ __global__ __launch_bounds__(64) void decode_attention_kernel(
       c[g] = m[g] == -INFINITY ? 0.0f : __expf(m[g] - mn);
       const float e = valid ? __expf(sg - mn) : 0.0f;
       lt[g] = lt[g] * c[g] + e;
-      w[g][ln] = e;
+      w[g * kChunk + ln] = e;
       m[g] = mn;
     }
-    __syncthreads();
+    // w is this wave's own: its LDS writes complete before its reads, in
+    // order; the compiler keeps the reads after the writes (and later
+    // chunks' loads out of this one)
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int n = 0; n < NL; n++) {
       const int r = RPW * n + rs;
@@ -198,15 +236,16 @@ __global__ __launch_bounds__(64) void decode_attention_kernel(
       for (int h = 0; h < 8; h++) vf[h] = h2f((uint16_t)(wd[h >> 1] >> (16 * (h & 1))));
 #pragma unroll
       for (int g = 0; g < G; g++) {
-        const float wg = w[g][r];
+        const float wg = w[g * kChunk + r];
 #pragma unroll
         for (int h = 0; h < 8; h++) acc[g][h] = fmaf(wg, vf[h], n == 0 ? acc[g][h] * c[g] : acc[g][h]);
       }
     }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();  // this chunk's reads of w before the next chunk's writes
+    asm volatile("" ::: "memory");
   }
 
-  // the span's sums: the lanes' denominators, the RPW row groups' outputs
+  // the wave's sums: the lanes' denominators, the RPW row groups' outputs
 #pragma unroll
   for (int g = 0; g < G; g++) {
     lt[g] = wave_group_sum_f32<64>(lt[g]);
@@ -215,7 +254,7 @@ __global__ __launch_bounds__(64) void decode_attention_kernel(
 #pragma unroll
       for (int off = KV; off < 64; off <<= 1) acc[g][h] += __shfl_xor(acc[g][h], off);
   }
-  if (nact == 1) {
+  if (nw == 1 && nact == 1) {
     if (rs == 0) {
 #pragma unroll
       for (int g = 0; g < G; g++)
@@ -224,7 +263,7 @@ __global__ __launch_bounds__(64) void decode_attention_kernel(
     }
     return;
   }
-  float* pp = part + (kv * ns + z) * PF;
+  float* pp = nw == 1 ? part + (kv * ns + z) * PF : res + wave * PF;
   if (rs == 0) {
 #pragma unroll
     for (int g = 0; g < G; g++)
@@ -236,6 +275,32 @@ __global__ __launch_bounds__(64) void decode_attention_kernel(
     for (int g = 0; g < G; g++) {
       pp[G * D + g] = m[g];
       pp[G * D + G + g] = lt[g];
+    }
+  }
+  if (nw == 1) return;  // the span's partial is in part; decode_combine_kernel merges
+  __syncthreads();
+  // the waves' results, merged in wave order: out when one span holds every
+  // position, else the span's partial (M, l, sum) into part
+  float* sp = part + (kv * ns + z) * PF;
+  for (int i = t; i < G * D + G; i += 64 * nw) {
+    const int g = i < G * D ? i / D : i - G * D;
+    float mx = -INFINITY;
+    for (int v = 0; v < nw; v++) mx = fmaxf(mx, res[v * PF + G * D + g]);
+    float num = 0.0f, den = 0.0f;
+    for (int v = 0; v < nw; v++) {
+      const float mv = res[v * PF + G * D + g];
+      const float f = mv == -INFINITY ? 0.0f : __expf(mv - mx);
+      den = fmaf(res[v * PF + G * D + G + g], f, den);
+      if (i < G * D) num = fmaf(res[v * PF + i], f, num);
+    }
+    if (i < G * D) {
+      if (nact == 1)
+        o[i] = h_to_bits(rn_h(num / den));
+      else
+        sp[i] = num;
+    } else if (nact > 1) {
+      sp[G * D + g] = mx;
+      sp[G * D + G + g] = den;
     }
   }
 }
@@ -310,7 +375,8 @@ extern "C" int aq_decode_attention(const void* q, const void* k_new, const void*
   float* part = (float*)workspace;
 #define AQ_DECODE_LAUNCH(DD, GG)                                                                                     \
   do {                                                                                                               \
-    hipLaunchKernelGGL((decode_attention_kernel<DD, GG>), grid, dim3(64), 0, s, (const uint16_t*)q,                \
+    hipLaunchKernelGGL((decode_attention_kernel<DD, GG>), grid, dim3(64 * (unsigned)sp.nw),                       \
+                       attention_lds(GG, DD, sp.nw), s, (const uint16_t*)q,                                          \
                        (const uint16_t*)k_new, (const uint16_t*)v_new, (uint16_t*)k_cache, (uint16_t*)v_cache, pos, \
                        (int)H, (int)Hkv, (int)L, scale, q_scale, (const uint16_t*)rope_cos,                        \
                        (const uint16_t*)rope_sin, (int)sp.nt, (int)sp.ns, part, (uint16_t*)out);                    \
@@ -429,7 +495,7 @@ __global__ __launch_bounds__(kNormThreads) void decode_norm_kernel(uint16_t* __r
         const float wk = (float)bits_to_h((uint16_t)(ww[k >> 1] >> (16 * (k & 1))));
         f16 o;
         if (MODE == 0) {
-          o = rn_h(wk * (float)rn_h(v[c][k] * r));
+          o = bits_to_h((uint16_t)(ww[k >> 1] >> (16 * (k & 1)))) * rn_h(v[c][k] * r);  // fp16 multiply: same rounding
         } else {
           const float bk = (float)bits_to_h((uint16_t)(bw[k >> 1] >> (16 * (k & 1))));
           o = rn_h((v[c][k] - mean) * r * wk + bk);

@@ -408,10 +408,17 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
               const half8 wh = __builtin_bit_cast(half8, uv[j]);
               const half8 bh = __builtin_bit_cast(half8, bv[j]);
               half8 o;
+              if (pro == kProRms) {
+                // fp16(w fp16(x r)): the outer product of two fp16 values
+                // rounds as the fp16 multiply (packed)
+                half8 t;
 #pragma unroll
-              for (int e = 0; e < 8; e++)
-                o[e] = pro == kProRms ? rn_h((float)wh[e] * (float)rn_h((float)h[e] * r))
-                                      : rn_h(((float)h[e] - mean) * r * (float)wh[e] + (float)bh[e]);
+                for (int e = 0; e < 8; e++) t[e] = rn_h((float)h[e] * r);
+                o = wh * t;
+              } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) o[e] = rn_h(((float)h[e] - mean) * r * (float)wh[e] + (float)bh[e]);
+              }
               *reinterpret_cast<half8*>(x_lds + 8 * i) = o;
             }
           }

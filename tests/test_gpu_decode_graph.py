@@ -106,12 +106,16 @@ def _rope_tables(L, D, theta=10000.0):
 @pytest.mark.parametrize("B,H,Hkv,D,L,pos", [(1, 32, 32, 64, 160, 0), (1, 32, 32, 64, 160, 47), (2, 32, 8, 128, 768, 511),
                                              (3, 8, 1, 128, 600, 257), (2, 16, 4, 64, 1000, 999),
                                              (1, 64, 8, 128, 300, 299), (2, 16, 2, 64, 40, 0),
-                                             (1, 32, 8, 128, 9000, 8191), (40, 8, 8, 64, 2000, 1500)])
+                                             (1, 32, 8, 128, 9000, 8191), (40, 8, 8, 64, 2000, 1500),
+                                             (32, 32, 8, 128, 200, 150), (1, 16, 8, 64, 100, 99)])
 def test_decode_attention_kernel(B, H, Hkv, D, L, pos):
     """aq_decode_attention against the same attention computed in float64
     from the same fp16 data (scores rounded to fp16 as the kernel's contract
     says); the new key and value land at pos and nothing else in the caches
-    changes.  A second call on the same workspace at an earlier position
+    changes.  The cases take both ways of splitting the cache: one span per
+    head shared by the waves of a workgroup (short caches with little work
+    per wave, or 256+ heads x batch rows) and spans merged by a second
+    kernel.  A second call on the same workspace at an earlier position
     (fewer spans) checks that nothing of the first call's partial results
     leaks into it."""
     from atlasinfer_amd import _lib

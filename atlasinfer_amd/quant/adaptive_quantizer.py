@@ -45,6 +45,58 @@ DEFAULT_CODE_FORMAT = "e4m3"
 PER_CHANNEL = -1
 
 
+class DeviceInt:
+    """An int that still lives in a one-element device tensor: read (one host
+    sync) the first time it is used as a number, then kept.  Lets
+    quantize_tensor hand back the largest block-list count without waiting
+    for it; the first consumer (the GEMM's kernel choice, serialization)
+    pays the wait."""
+    __slots__ = ("_t", "_v")
+
+    def __init__(self, t: torch.Tensor):
+        self._t, self._v = t, None
+
+    def _get(self) -> int:
+        if self._v is None:
+            self._v = int(self._t.item())
+            self._t = None
+        return self._v
+
+    def __int__(self):
+        return self._get()
+
+    __index__ = __int__
+
+    def __eq__(self, o):
+        return self._get() == int(o)
+
+    def __lt__(self, o):
+        return self._get() < int(o)
+
+    def __le__(self, o):
+        return self._get() <= int(o)
+
+    def __gt__(self, o):
+        return self._get() > int(o)
+
+    def __ge__(self, o):
+        return self._get() >= int(o)
+
+    def __hash__(self):
+        return hash(self._get())
+
+    def __add__(self, o):
+        return self._get() + o
+
+    __radd__ = __add__
+
+    def __sub__(self, o):
+        return self._get() - o
+
+    def __repr__(self):
+        return repr(self._get())
+
+
 class QuantizedTensor(NamedTuple):
     """A tensor quantized into the hybrid FP8/FP16 format (reference :8-18)."""
     fp8_data: torch.Tensor          # codes (int8 compacted stream, or dense e4m3)
@@ -59,7 +111,7 @@ class QuantizedTensor(NamedTuple):
     code_layout: str = "flat"                       # "flat" (element order) or "tiled"
     outlier_tile_ptr: Optional[torch.Tensor] = None  # int32 [(N/16)*(K/64) + 1]
     outlier_tile_ent: Optional[torch.Tensor] = None  # int32 [nnz + 64], packed entries
-    outlier_tile_max: int = 0                        # most entries in one block
+    outlier_tile_max: int = 0                        # most entries in one block (an int or a DeviceInt)
 
     def to(self, device):
         """Move every tensor to ``device``; returns self when already there
@@ -221,9 +273,15 @@ def quantize_tensor(
     _lib.check(L.aq_quantize_finish(numel, G, K, block_off.data_ptr(), nnz, ws.data_ptr(), ws_bytes,
                                     _lib.ptr(flat_idx), _lib.ptr(vals), _lib.ptr(cols), stream),
                "aq_quantize_finish")
-    row_ptr = torch.empty(N + 1, dtype=torch.int32, device=dev)
-    _lib.check(L.aq_segment_offsets(_lib.ptr(flat_idx), nnz, N, K, row_ptr.data_ptr(), stream),
-               "aq_segment_offsets")
+    if K % G == 0:
+        # blocks tile the rows, so a row's first outlier is its first block's:
+        # the CSR row pointers are every (K / G)-th block offset (per output
+        # channel, the block offsets themselves)
+        row_ptr = block_off if G == K else block_off[::K // G].contiguous()
+    else:
+        row_ptr = torch.empty(N + 1, dtype=torch.int32, device=dev)
+        _lib.check(L.aq_segment_offsets(_lib.ptr(flat_idx), nnz, N, K, row_ptr.data_ptr(), stream),
+                   "aq_segment_offsets")
     if fmt == _lib.FMT_INT8:
         fp8_data = torch.empty(padded - nnz, dtype=torch.int8, device=dev)
         _lib.check(L.aq_compact_codes(codes.data_ptr(), padded, _lib.ptr(flat_idx), nnz, _lib.ptr(fp8_data),
@@ -244,7 +302,7 @@ def quantize_tensor(
         code_layout=layout,
     )
     if layout == "tiled":
-        tp, te, tmax = build_outlier_tiles(qt, dev)
+        tp, te, tmax = build_outlier_tiles(qt, dev, lazy_max=True)
         qt = qt._replace(outlier_tile_ptr=tp, outlier_tile_ent=te, outlier_tile_max=tmax)
     return qt.to(input_device)
 
@@ -304,10 +362,11 @@ def tiles_eligible(shape) -> bool:
     return N >= 16 and N % 16 == 0 and K >= 64 and K % 64 == 0
 
 
-def build_outlier_tiles(qt: QuantizedTensor, device: torch.device):
+def build_outlier_tiles(qt: QuantizedTensor, device: torch.device, lazy_max: bool = False):
     """(tile_ptr, tile_ent, tile_max): the outliers of ``qt`` per block of 16
     rows x 64 columns (aq_outlier_tiles), from its CSR lists, on ``device``,
-    and the largest count in one block (one host sync)."""
+    and the largest count in one block (one host sync, or with ``lazy_max`` a
+    DeviceInt read when first used)."""
     q = qt.to(device)
     if not tiles_eligible(q.original_shape) or q.outlier_row_ptr is None:
         raise ValueError(f"shape {tuple(q.original_shape)} has no 16 x 64 outlier blocks")
@@ -319,8 +378,10 @@ def build_outlier_tiles(qt: QuantizedTensor, device: torch.device):
     _lib.check(L.aq_outlier_tiles(q.outlier_row_ptr.data_ptr(), _lib.ptr(q.outlier_cols), _lib.ptr(q.fp16_outliers),
                                   N, K, tile_ptr.data_ptr(), tile_ent.data_ptr(), _lib.stream_of(device)),
                "aq_outlier_tiles")
-    tile_max = int((tile_ptr[1:] - tile_ptr[:-1]).max().item()) if nnz else 0
-    return tile_ptr, tile_ent, tile_max
+    if not nnz:
+        return tile_ptr, tile_ent, 0
+    tmax = (tile_ptr[1:] - tile_ptr[:-1]).max()
+    return tile_ptr, tile_ent, DeviceInt(tmax) if lazy_max else int(tmax.item())
 
 
 def outlier_tiles(qt: QuantizedTensor, device: torch.device):

@@ -1255,10 +1255,20 @@ __global__ __launch_bounds__(512, 1) void qlinear_gemm_wide_kernel(QLArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kWideStage + 128];
   uint8_t* const spare = lds + 2 * kWideStage;
 
-  // tiles: as in qlinear_gemm_kernel, with 256-column n-tiles
+  // tiles: as in qlinear_gemm_kernel, with 256-column n-tiles.  With a tail
+  // (unsplit grids only), the last `tail` tiles of each XCD's run come as
+  // two work units each, one per half of K (a work unit past the others:
+  // `half` 0 or 1, partial sums into a.tpart slot `tslot`)
   const int ntiles = a.first[a.count];
-  const int per = (ntiles + 7) / 8;
-  const int tile = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  const int per = a.tail ? a.per : (ntiles + 7) / 8;
+  const int xcd = (int)(blockIdx.x % 8), unit = (int)(blockIdx.x / 8);
+  int tile = xcd * per + unit, half = -1, tslot = 0;
+  if (a.tail && unit >= per - a.tail) {
+    const int v = unit - (per - a.tail);
+    tile = xcd * per + per - a.tail + (v >> 1);
+    half = v & 1;
+    tslot = xcd * a.tail + (v >> 1);
+  }
   if (tile >= ntiles) return;
   int mi = 0;
 #pragma unroll
@@ -1277,8 +1287,13 @@ __global__ __launch_bounds__(512, 1) void qlinear_gemm_wide_kernel(QLArgs a) {
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int nch128 = K >> 7;
-  const int nch_split = (K / kGemmBK) / a.split;
-  const int c_first = ks * nch_split, c_end = c_first + nch_split;
+  int nch_split = (K / kGemmBK) / a.split;
+  int c_first = ks * nch_split, c_end = c_first + nch_split;
+  if (half >= 0) {  // a tail unit: one half of K
+    nch_split = (K / kGemmBK) / 2;
+    c_first = half * nch_split;
+    c_end = c_first + nch_split;
+  }
 
   WideSrc S;
   wide_src_init(S, W, a.x, M, K, m_first, nbase, nch128, t);
@@ -1363,6 +1378,23 @@ __global__ __launch_bounds__(512, 1) void qlinear_gemm_wide_kernel(QLArgs a) {
 #undef AQ_WIDE_BARRIER
 
   const int hi = lane >> 5, lc = lane & 31;
+  if (half >= 0) {
+    // the tile's fp32 partial sums over this half of K: slot tslot, half,
+    // row-major 256 x 256 (tail_reduce_kernel adds the halves)
+    float* tp = a.tpart + ((size_t)tslot * 2 + half) * kWideBM * kWideBN;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int nl = wn * 64 + j * 32 + lc;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int ml = wm * 128 + i * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+          tp[ml * kWideBN + nl] = acc[i][j][e];
+        }
+    }
+    return;
+  }
   if (a.split > 1) {
     float* part = W.part + (size_t)ks * M * N;
 #pragma unroll
@@ -1407,6 +1439,45 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, i
 #pragma unroll
   for (int j = 0; j < 4; j++) o[j] = h_to_bits(rn_h(v[j] + (bias ? (float)bits_to_h(bias[n + j]) : 0.0f)));
   *reinterpret_cast<uint2*>(y + i) = make_uint2(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16));
+}
+
+// The tail tiles of a 256 x 256 GEMM (qlinear_gemm_wide_kernel with
+// a.tail): y = fp16(half 0 + half 1 + bias) over each tile's rows < M and
+// columns < N, the halves added in order.  Workgroup (tile slot, row band of
+// 16): 256 threads x 4 columns x 4 rows.
+__global__ __launch_bounds__(256) void tail_reduce_kernel(QLArgs a) {
+  const int ntiles = a.first[a.count];
+  const int slot = blockIdx.x, xcd = slot / a.tail, r = slot % a.tail;
+  const int tile = xcd * a.per + a.per - a.tail + r;
+  if (tile >= ntiles) return;
+  int mi = 0;
+#pragma unroll
+  for (int j = 1; j < kMaxGroup; j++)
+    if (j < a.count && tile >= a.first[j]) mi = j;
+  const QLMat W = pick(a, mi);
+  const int N = W.N, M = a.M;
+  const int mbands = (M + kWideBM - 1) / kWideBM;
+  const int local = tile - a.first[mi];
+  const int nbase = (local / mbands) * kWideBN, m_first = (local % mbands) * kWideBM;
+  const float* p0 = a.tpart + (size_t)slot * 2 * kWideBM * kWideBN;
+  const float* p1 = p0 + kWideBM * kWideBN;
+  const int nl = (threadIdx.x & 63) * 4;
+  const int n = nbase + nl;
+  if (n >= N) return;  // N is a multiple of 16: a group of 4 columns is all in or all out
+  float bv[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) bv[c] = W.bias ? (float)bits_to_h(W.bias[n + c]) : 0.0f;
+  for (int ml = (int)blockIdx.y * 16 + (threadIdx.x >> 6); ml < (int)blockIdx.y * 16 + 16; ml += 4) {
+    const int m = m_first + ml;
+    if (m >= M) break;
+    const float4v u = *reinterpret_cast<const float4v*>(p0 + ml * kWideBN + nl);
+    const float4v v = *reinterpret_cast<const float4v*>(p1 + ml * kWideBN + nl);
+    uint16_t o[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) o[c] = h_to_bits(rn_h(u[c] + v[c] + bv[c]));
+    *reinterpret_cast<uint2*>(W.y + (size_t)m * N + n) =
+        make_uint2(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16));
+  }
 }
 
 // CU count of the current device, read once per device.  Any host thread
@@ -1623,8 +1694,22 @@ GemmPlan plan_gemm(int64_t M, const int64_t* Ns, int64_t count, int64_t K, int m
   return best;
 }
 
+// The tail of an unsplit 256 x 256 grid (tiles dealt to the 8 XCDs in runs
+// of `per`): when each XCD's last round holds at most half its CUs' worth of
+// tiles, those tiles run as two K halves each, so that round has twice the
+// work units at half the length.  Returns the tail tiles per XCD (0: none)
+// and their partial sums' bytes.
+int wide_tail(int64_t ntiles, int64_t K, int64_t* bytes) {
+  const int64_t per = aq::ceil_div(ntiles, 8), cpx = std::max(1, aq::cu_count() / 8);
+  const int64_t tail = per % cpx, nch = K / kGemmBK;
+  *bytes = 0;
+  if (tail == 0 || 2 * tail > cpx || nch % 2 != 0 || nch < 8) return 0;
+  *bytes = 8 * tail * 2 * (int64_t)kWideBM * kWideBN * 4;
+  return (int)tail;
+}
+
 template <int FMT, int DENSE>
-hipError_t launch_gemm_wide(QLArgs a, bool per_channel, hipStream_t s) {
+hipError_t launch_gemm_wide(QLArgs a, bool per_channel, void* ws, int64_t ws_bytes, hipStream_t s) {
   const int mbands = (int)aq::ceil_div(a.M, kWideBM);
   int ntiles = 0;
   for (int i = 0; i < a.count; i++) {
@@ -1632,20 +1717,37 @@ hipError_t launch_gemm_wide(QLArgs a, bool per_channel, hipStream_t s) {
     ntiles += (int)aq::ceil_div(a.mat[i].N, kWideBN) * mbands * a.split;
   }
   for (int i = a.count; i <= kMaxGroup; i++) a.first[i] = ntiles;
-  const dim3 grid((unsigned)(8 * aq::ceil_div(ntiles, 8)));
+  a.tail = 0;
+  a.per = (int)aq::ceil_div(ntiles, 8);
+  a.tpart = nullptr;
+  if (a.split == 1 && ws && (uintptr_t)ws % 16 == 0) {
+    int64_t need = 0;
+    const int tail = wide_tail(ntiles, a.K, &need);
+    if (tail > 0 && ws_bytes >= need) {
+      a.tail = tail;
+      a.tpart = (float*)ws;
+    }
+  }
+  const dim3 grid((unsigned)(8 * (a.per + a.tail)));
   if (per_channel)
     hipLaunchKernelGGL((qlinear_gemm_wide_kernel<FMT, 1, DENSE>), grid, dim3(512), 0, s, a);
   else
     hipLaunchKernelGGL((qlinear_gemm_wide_kernel<FMT, 0, DENSE>), grid, dim3(512), 0, s, a);
-  return hipGetLastError();
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess && a.tail) {
+    hipLaunchKernelGGL(tail_reduce_kernel, dim3((unsigned)(8 * a.tail), kWideBM / 16), dim3(256), 0, s, a);
+    e = hipGetLastError();
+  }
+  return e;
 }
 
-hipError_t launch_gemm_wide(const QLArgs& a, int fmt, bool per_channel, bool dense, hipStream_t s) {
+hipError_t launch_gemm_wide(const QLArgs& a, int fmt, bool per_channel, bool dense, void* ws, int64_t ws_bytes,
+                            hipStream_t s) {
   if (dense)
-    return fmt == AQ_FMT_E4M3 ? launch_gemm_wide<AQ_FMT_E4M3, 1>(a, per_channel, s)
-                              : launch_gemm_wide<AQ_FMT_INT8, 1>(a, per_channel, s);
-  return fmt == AQ_FMT_E4M3 ? launch_gemm_wide<AQ_FMT_E4M3, 0>(a, per_channel, s)
-                            : launch_gemm_wide<AQ_FMT_INT8, 0>(a, per_channel, s);
+    return fmt == AQ_FMT_E4M3 ? launch_gemm_wide<AQ_FMT_E4M3, 1>(a, per_channel, ws, ws_bytes, s)
+                              : launch_gemm_wide<AQ_FMT_INT8, 1>(a, per_channel, ws, ws_bytes, s);
+  return fmt == AQ_FMT_E4M3 ? launch_gemm_wide<AQ_FMT_E4M3, 0>(a, per_channel, ws, ws_bytes, s)
+                            : launch_gemm_wide<AQ_FMT_INT8, 0>(a, per_channel, ws, ws_bytes, s);
 }
 
 }  // namespace
@@ -1657,7 +1759,10 @@ extern "C" int64_t aq_qlinear_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (N <= 0 || K < 128 || K % 128) return 0;
   if (M <= kGemvShortMaxM || (M <= kGemvMaxM && N / 16 >= kGemvShortRows)) return 0;
   const GemmPlan p = plan_gemm(M, &N, 1, K, 8);
-  return p.split > 1 ? p.split * M * N * 4 : 0;
+  if (p.split > 1) return p.split * M * N * 4;
+  int64_t tail_bytes = 0;  // an unsplit 256 x 256 grid's tail tiles, run as two K halves
+  if (p.tile == kTile256x256) wide_tail(aq::ceil_div(N, kWideBN) * aq::ceil_div(M, kWideBM), K, &tail_bytes);
+  return tail_bytes;
 }
 
 
@@ -1801,7 +1906,8 @@ static int qlinear_grouped_impl(const void* x, int64_t M, int64_t K, int fmt, in
       p += (size_t)a.split * M * Ns[i];
     }
   }
-  hipError_t e = plan.tile == kTile256x256   ? launch_gemm_wide(a, fmt, per_channel, dense, s)
+  hipError_t e = plan.tile == kTile256x256   ? launch_gemm_wide(a, fmt, per_channel, dense, workspace,
+                                                                 workspace_bytes, s)
                  : plan.tile == kTile256x128 ? launch_gemm<256>(a, fmt, per_channel, dense, s)
                                              : launch_gemm<128>(a, fmt, per_channel, dense, s);
   if (e != hipSuccess || a.split == 1) return aq::check_hip(e, "aq_qlinear: gemm launch");

@@ -51,6 +51,10 @@ struct QLArgs {
   const uint16_t* nw;   // kProRms / kProLayerNorm: weight [K]
   const uint16_t* nb;   // kProLayerNorm: bias [K]
   float eps;
+  // 256 x 256 GEMM, unsplit: the last `tail` tiles of each XCD's run of
+  // `per` run as two K halves, their fp32 partial sums in tpart (0: none)
+  int tail, per;
+  float* tpart;
   int split;                 // GEMM: ways the K chunks are split (1: none)
   int first[kMaxGroup + 1];  // GEMM: first output tile of each matrix
   QLMat mat[kMaxPieces];     // GEMM: the group's matrices; GEMV: their pieces

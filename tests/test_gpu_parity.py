@@ -350,6 +350,38 @@ def test_gemm_wide_tiles(fmt, G, M, N, K):
     assert_close(AW.QuantizedLinear(q, b)(x), reference_linear(x, w_deq, b), x, w_deq)
 
 
+@pytest.mark.parametrize("M,N,K", [(256, 8192, 2048), (2048, 16640, 512)])
+def test_gemm_wide_tail_in_k_halves(M, N, K):
+    """An unsplit 256 x 256 grid whose last round per XCD is at most half
+    full runs those tiles as two halves of K, added by a second kernel
+    (256 x 8192: every tile; 2048 x 16640: one tile per XCD), given the
+    workspace aq_qlinear_workspace_size asks for: against the
+    oracle-dequantized reference, and the same call without the workspace
+    (whole tiles) within the same bound."""
+    assert _lib.load().aq_qlinear_workspace_size(M, N, K) > 0  # the halves are planned
+    rng = np.random.default_rng(M * 7 + N)
+    w = make_weights(rng, (N, K))
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=-1, code_format="e4m3")
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    xs[:, rng.permutation(K)[:4]] *= 30
+    x = torch.from_numpy(xs.astype(np.float16)).to(DEV)
+    b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(DEV)
+    w_deq = oref(q, w)
+    ref = reference_linear(x, w_deq, b)
+    y = AW.qlinear(x, q, b)
+    assert_close(y, ref, x, w_deq)
+    tiles = AQ.outlier_tiles(q, torch.device(DEV))
+    codes = AQ.kernel_codes(q, torch.device(DEV))
+    y0 = torch.empty_like(y)
+    _lib.check(_lib.load().aq_qlinear(x.data_ptr(), M, K, N, codes.data_ptr(), q.scale_factors.data_ptr(),
+                                      q.block_size, _lib.FORMATS["e4m3"], q.outlier_row_ptr.data_ptr(),
+                                      q.outlier_cols.data_ptr(), q.fp16_outliers.data_ptr(), tiles[0].data_ptr(),
+                                      tiles[1].data_ptr(), int(tiles[2]), b.data_ptr(), y0.data_ptr(), None, 0,
+                                      _lib.stream_of(torch.device(DEV))), "aq_qlinear")
+    torch.cuda.synchronize()
+    assert_close(y0, ref, x, w_deq)
+
+
 def test_gemm_dense_outliers_long_rows():
     """Student-t(3) weights with 1% planted outliers (about 2% outliers in
     all) over 14336-wide rows."""

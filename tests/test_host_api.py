@@ -84,3 +84,23 @@ def test_extra_repr_format():
     q = AQ.quantize_tensor(torch.empty(0, 4, dtype=torch.float16))
     r = AW.QuantizedLinear(q, None).extra_repr()
     assert r.startswith("quantized_shape=torch.Size([0, 4]), bias=False, device=")
+
+
+def test_device_int_reads_once_and_acts_as_int():
+    """quantize_tensor hands back the block lists' largest count as a
+    DeviceInt (read from its one-element tensor when first used): it
+    compares, adds, converts for ctypes, copies and pickles like the int it
+    holds, and reads the tensor only once."""
+    import copy
+    import ctypes
+    import pickle
+    from atlasinfer_amd.quant.adaptive_quantizer import DeviceInt
+    t = torch.tensor(70, dtype=torch.int32)
+    d = DeviceInt(t)
+    assert d > 64 and d >= 70 and d == 70 and not d < 70 and d <= 70
+    assert d - 1 == 69 and 1 + d == 71 and int(d) == 70 and hash(d) == hash(70)
+    t.fill_(3)  # already read: later changes to the tensor do not matter
+    assert int(d) == 70
+    assert (ctypes.c_int64 * 1)(DeviceInt(torch.tensor(9)))[0] == 9
+    assert int(copy.deepcopy(DeviceInt(torch.tensor(5)))) == 5
+    assert int(pickle.loads(pickle.dumps(DeviceInt(torch.tensor(6))))) == 6

@@ -1,5 +1,7 @@
-// aq_decode.hip -- attention of one decode step over a static key/value cache
-// (the position read from device memory, so that a HIP graph replays it).
+// aq_decode.hip -- the work of one decode step around the quantized linears:
+// attention over a static key/value cache (the position read from device
+// memory, so that a HIP graph replays it), the residual add + RMSNorm /
+// LayerNorm of a row, and the SwiGLU product.
 #include "aq_common.h"
 
 namespace {

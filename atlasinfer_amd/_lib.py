@@ -17,7 +17,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libatlasinfer_amd.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 FMT_INT8 = 0
 FMT_E4M3 = 1
@@ -57,7 +57,8 @@ SIGNATURES = {
                                           _I32P, _P, _I64, _P, _P, _P]),
     "aq_decode_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
                                            ctypes.c_float, _P, _P, _P, _I64, _P, _P]),
-    "aq_qlinear_decode": (ctypes.c_int, [_P, _I64, ctypes.c_int, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int,
+    "aq_qlinear_decode": (ctypes.c_int, [_P, _I64, _I64, ctypes.c_int, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                         _P, _P, ctypes.c_int,
                                          _P, _P, _P, ctypes.c_float, _P, _P, _P]),
     "aq_decode_norm": (ctypes.c_int, [_P, _P, _P, _P, ctypes.c_float, _I64, _I64, ctypes.c_int, _P, _P]),
     "aq_silu_mul": (ctypes.c_int, [_P, _P, _P, _I64, _P]),

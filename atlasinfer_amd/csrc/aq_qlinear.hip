@@ -508,14 +508,27 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
 // in flight while group j is computed, and the zero that an out-of-range
 // buffer load returns stands in for the rows of x past M, the chunks past K
 // and the tile rows past the piece (no memory is read for them).  The S partial
-// sums meet in LDS; outliers are added per lane in the epilogue, where a
-// lane owns one output column and 4 MG of its rows.
+// sums meet in LDS.
+//
+// Outliers (OT = 1, from the block lists of aq_outlier_tiles): each wave
+// adds the outliers of its own chunk with one more MFMA per 16-row group of
+// x.  The chunk's entries (its two 16 x 64 blocks, contiguous in the lists)
+// are taken 32 at a time as the MFMA's k slots (as many slots per lane as
+// the batch needs): the A operand gathers the x
+// column of each entry from LDS, the B operand holds the entry's value in the
+// column of its row and zero elsewhere, so the product adds x[m][col] * value
+// to output (m, row) for every row m of x.  The entry ranges of a wave's
+// chunks are loaded once, one chunk group per lane (64 groups at a time),
+// and each chunk's first 64 entries travel with its codes.  Without the
+// lists (OT = 0) one wave per tile row adds its rows' outliers from the CSR
+// lists (see stage_outliers), the rest in the epilogue, where a lane owns
+// one output column and 4 MG of its rows.
 
 constexpr int kXWaves = 8;
 constexpr int kXPad = 8;  // halves of padding per LDS row of x
 constexpr int kXCsrCap = 512;  // outlier entries of a tile row staged in LDS (the rest: epilogue)
 
-template <int FMT, int PC, int MG, int S>
+template <int FMT, int PC, int MG, int S, int OT>
 __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) {
   constexpr int TR = kXWaves / S;
   constexpr int XR = 16 * MG;              // staged rows of x
@@ -553,10 +566,30 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   uint16_t sb_row = 0;
   if (PC) sb_row = tr < rows_here ? W.scales[(size_t)(rb0 + tr) * 16 + li] : (uint16_t)0;
 
+  // OT: the block lists (tile_ptr offset to the piece's first tile row;
+  // tile_ent holds 64 entries of read padding past the last)
+  const int nb64 = K >> 6;
+  const __amdgpu_buffer_rsrc_t tpr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)W.tptr, (short)0, OT ? (nrb * nb64 + 1) * 4 : 0, kBufferDword3);
+  const __amdgpu_buffer_rsrc_t ter =
+      __builtin_amdgcn_make_buffer_rsrc((void*)W.tent, (short)0, OT ? 0x7FFFFFFF : 0, kBufferDword3);
+  // lane i: first entry, first entry of the second block and end of chunk
+  // group g0 + i of this wave (chunk S (g0 + i) + sp); zero past the piece
+  uint32_t rg_s = 0, rg_m = 0, rg_e = 0;
+  auto load_ranges = [&](int g0) {
+    const int c = (g0 + lane) * S + sp;
+    const uint32_t off =
+        tr < rows_here && c < nchunks ? (uint32_t)((rb0 + tr) * nb64 + 2 * c) * 4 : kOutOfRange;
+    rg_s = __builtin_amdgcn_raw_buffer_load_b32(tpr, off, 0, 0);
+    rg_m = __builtin_amdgcn_raw_buffer_load_b32(tpr, off + 4, 0, 0);
+    rg_e = __builtin_amdgcn_raw_buffer_load_b32(tpr, off + 8, 0, 0);
+  };
   struct Slot {
     u32x4 q0, q1;
     uint32_t s0, s1;
     u32x4 x[XP];
+    uint32_t ent;          // OT: entry `lane` of the chunk (0 past its end)
+    int e_start, e_mid, e_cnt;  // OT: the chunk's entries (wave-uniform)
   };
   auto load = [&](Slot& sl, int j) {
     const int c = j * S + sp;
@@ -579,11 +612,54 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
       const uint32_t xo = col < K ? (uint32_t)(row * K + col) * 2 : kOutOfRange;
       sl.x[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo, 0, 0));
     }
+    if (OT) {
+      const int gl = j & 63;
+      const int e0 = __builtin_amdgcn_readlane((int)rg_s, gl);
+      sl.e_start = e0;
+      sl.e_mid = __builtin_amdgcn_readlane((int)rg_m, gl) - e0;
+      sl.e_cnt = __builtin_amdgcn_readlane((int)rg_e, gl) - e0;
+      sl.ent = __builtin_amdgcn_raw_buffer_load_b32(ter, lane < sl.e_cnt ? (uint32_t)(e0 + lane) * 4 : kOutOfRange, 0,
+                                                    0);
+    }
   };
 
   float4v acc[MG];
 #pragma unroll
   for (int gi = 0; gi < MG; gi++) acc[gi] = (float4v){0.f, 0.f, 0.f, 0.f};
+
+  // the entries of the current chunk 32 at a time as one MFMA's k slots:
+  // slot (grp, b) holds entry base + 4 b + grp, so that a batch of n entries
+  // fills the first ceil(n / 4) slots of each lane and the rest stay zero
+  // (a chunk typically holds a few entries)
+  auto add_block_outliers = [&](uint32_t ent_lane, int e_start, int e_mid, int e_cnt, const uint16_t* xb) {
+    for (int base = 0; base < e_cnt; base += 32) {
+      const int nb = min(8, (e_cnt - base + 3) >> 2);  // slots in use per lane (wave-uniform)
+      half8 bv = {};
+      half8 av[MG];
+#pragma unroll
+      for (int gi = 0; gi < MG; gi++) av[gi] = (half8){};
+#pragma unroll
+      for (int b = 0; b < 8; b++) {
+        if (b >= nb) break;
+        const int e = base + 4 * b + grp;
+        const bool valid = e < e_cnt;
+        // the first 64 entries came with the codes; later ones (blocks this
+        // crowded are rare) are read here
+        const uint32_t ent = base < 64 ? (uint32_t)__shfl((int)ent_lane, (base + 4 * b + grp) & 63, 64)
+                                       : __builtin_amdgcn_raw_buffer_load_b32(
+                                             ter, valid ? (uint32_t)(e_start + e) * 4 : kOutOfRange, 0, 0);
+        const int k = (int)(ent & 63u) + (e >= e_mid ? 64 : 0);
+        bv[b] = valid && (int)((ent >> 6) & 15u) == li ? bits_to_h((uint16_t)(ent >> 16)) : (f16)0.0f;
+#pragma unroll
+        for (int gi = 0; gi < MG; gi++) {
+          const f16 xv = bits_to_h(xb[(16 * gi + li) * XW + sp * 128 + k]);
+          av[gi][b] = valid ? xv : (f16)0.0f;
+        }
+      }
+#pragma unroll
+      for (int gi = 0; gi < MG; gi++) acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[gi], bv, acc[gi], 0, 0, 0);
+    }
+  };
 
   auto step = [&](Slot& sl, int j, uint16_t* xb) {
     const half2v s0 = scale2(PC ? sb_row : (uint16_t)sl.s0);
@@ -592,6 +668,9 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
     const half8 w1 = deq8<FMT>(sl.q0.z, sl.q0.w, s0);
     const half8 w2 = deq8<FMT>(sl.q1.x, sl.q1.y, s1);
     const half8 w3 = deq8<FMT>(sl.q1.z, sl.q1.w, s1);
+    // this chunk's entries, read before the slot is reloaded
+    const uint32_t ent = sl.ent;
+    const int e_start = sl.e_start, e_mid = sl.e_mid, e_cnt = sl.e_cnt;
 #pragma unroll
     for (int i = 0; i < XP; i++) {
       const int p = t + 64 * kXWaves * i;
@@ -613,9 +692,10 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
       acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(xp + 64), w2, acc[gi], 0, 0, 0);
       acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(xp + 72), w3, acc[gi], 0, 0, 0);
     }
+    if (OT) add_block_outliers(ent, e_start, e_mid, e_cnt, xb);
   };
 
-  // Outliers: wave sp = 0 of each tile row copies the tile row's first
+  // Outliers (OT = 0): wave sp = 0 of each tile row copies the tile row's first
   // kXCsrCap entries (from the CSR lists, fetched behind the first code
   // loads) into LDS for itself, and in each chunk group adds, per lane, the
   // products of its row's entries in the group's columns with the x values
@@ -668,14 +748,17 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   };
 
   Slot sa, sb;
+  if (OT) load_ranges(0);
   load(sa, 0);
   load(sb, 1);
-  if (sp == 0) stage_outliers();
+  if (!OT && sp == 0) stage_outliers();
   for (int j = 0; j < nsteps; j += 2) {
+    // the next 64 chunk groups' entry ranges, before load(j + 2) reads them
+    if (OT && ((j + 2) & 63) == 0) load_ranges(j + 2);
     step(sa, j, xs[0]);
-    if (sp == 0) add_outliers(j, xs[0]);
+    if (!OT && sp == 0) add_outliers(j, xs[0]);
     step(sb, j + 1, xs[1]);
-    if (sp == 0) add_outliers(j + 1, xs[1]);
+    if (!OT && sp == 0) add_outliers(j + 1, xs[1]);
   }
 
   // the S partial sums of each tile row meet in LDS (x is no longer read)
@@ -701,9 +784,9 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   // Outliers of row n, eight entries at a time: their loads, then all the x
   // loads they need, then the FMAs.
   const int n = (rb0 + tr) * 16 + li;
-  const int p_end = W.row_ptr[n + 1];
+  const int p_end = OT ? 0 : W.row_ptr[n + 1];
   // the row's entries past the staged ones
-  for (int p = W.row_ptr[n] + staged_row; p < p_end; p += 8) {
+  for (int p = OT ? 0 : W.row_ptr[n] + staged_row; p < p_end; p += 8) {
     int col[8];
     float wv[8];
 #pragma unroll
@@ -730,7 +813,13 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int m = 16 * gi + 4 * grp + i;
-      if (m < M) W.y[(size_t)m * W.ldy + n] = h_to_bits(rn_h(acc[gi][i] + bv));
+      if (m < M) {
+        f16 o = rn_h(acc[gi][i] + bv);
+        // aq_qlinear_decode's epilogue (zero / null for other calls)
+        if (W.act == 1 && (float)o < 0.0f) o = (f16)0.0f;                                 // ReLU
+        if (W.res) o = rn_h((float)bits_to_h(W.res[(size_t)m * W.ldy + n]) + (float)o);  // residual add
+        W.y[(size_t)m * W.ldy + n] = h_to_bits(o);
+      }
     }
 }
 
@@ -1525,11 +1614,10 @@ dim3 gemv_pieces(const QLArgs& a, int unit, QLArgs* g) {
       q.row_ptr = w.row_ptr + row0;
       q.bias = w.bias ? w.bias + row0 : nullptr;
       q.res = w.res ? w.res + row0 : nullptr;
+      q.tptr = w.tptr ? w.tptr + (size_t)r0 * (nch * 2) : nullptr;  // blocks of 16 x 64: 2 per chunk
       q.y = w.y + row0;
       q.N = 16 * std::min(P, w.N / 16 - r0);
       q.ldy = w.N;
-      q.tptr = nullptr;
-      q.tent = nullptr;
     }
   }
   g->count = n;
@@ -1587,10 +1675,26 @@ template <int FMT, int MG, int S>
 hipError_t launch_gemv_x(const QLArgs& a, bool per_channel, hipStream_t s) {
   QLArgs p;
   const dim3 g = gemv_pieces(a, kXWaves / S, &p);  // workgroups of 8 / S tile rows
+  // Every member's block lists given: the MFMA outlier path, except with 3
+  // or 4 row groups of x at S = 2, where the gathers (one per row group and
+  // entry) cost more than the CSR walk of a wave shared by only two
+  // (measured on the Mistral-7B / Llama-3-8B shapes: gate+up at M = 64 52 against 43 us;
+  // down at M = 8 18 against 31 us, q/k/v 10 against 12 us)
+  if constexpr (S >= 4 || MG <= 2) {
+    bool lists = true;
+    for (int i = 0; i < a.count; i++) lists = lists && a.mat[i].tptr && a.mat[i].tent;
+    if (lists) {
+      if (per_channel)
+        hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 1, MG, S, 1>), g, dim3(64 * kXWaves), 0, s, p);
+      else
+        hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 0, MG, S, 1>), g, dim3(64 * kXWaves), 0, s, p);
+      return hipGetLastError();
+    }
+  }
   if (per_channel)
-    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 1, MG, S>), g, dim3(64 * kXWaves), 0, s, p);
+    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 1, MG, S, 0>), g, dim3(64 * kXWaves), 0, s, p);
   else
-    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 0, MG, S>), g, dim3(64 * kXWaves), 0, s, p);
+    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 0, MG, S, 0>), g, dim3(64 * kXWaves), 0, s, p);
   return hipGetLastError();
 }
 
@@ -1835,10 +1939,15 @@ static int qlinear_grouped_impl(const void* x, int64_t M, int64_t K, int fmt, in
   for (int i = (int)count; i <= kMaxGroup; i++) a.first[i] = (int)blocks;
   a.split = 1;
   if (fz) {
-    // decode: the M = 1 GEMV with x in LDS (the only kernel with the prologue / epilogue)
-    AQ_CHECK_ARG(M == 1 && K <= kGemvX1MaxK, "aq_qlinear_decode: M = 1 and K <= %d (M=%lld K=%lld)", kGemvX1MaxK,
-                 (long long)M, (long long)K);
+    // decode: the M = 1 GEMV with x in LDS (every prologue) or the shared-x
+    // GEMV for 6 <= M <= 64 (epilogue only: each of its workgroups stages all
+    // of x, so a prologue there would be computed once per workgroup)
+    AQ_CHECK_ARG((M == 1 && K <= kGemvX1MaxK) || (M >= kGemvXMinM && M <= kGemvMaxM),
+                 "aq_qlinear_decode: M = 1 with K <= %d, or 6 <= M <= 64 (M=%lld K=%lld)", kGemvX1MaxK, (long long)M,
+                 (long long)K);
     AQ_CHECK_ARG(fz->pro >= kProNone && fz->pro <= kProSwiGlu, "aq_qlinear_decode: unknown prologue %d", fz->pro);
+    AQ_CHECK_ARG(M == 1 || fz->pro == kProNone, "aq_qlinear_decode: prologues take one row (M=%lld)",
+                 (long long)M);
     AQ_CHECK_ARG(fz->pro != kProSwiGlu || (fz->x2 && (uintptr_t)fz->x2 % 16 == 0),
                  "aq_qlinear_decode: SwiGLU needs u (16-byte aligned)");
     AQ_CHECK_ARG((fz->pro != kProRms && fz->pro != kProLayerNorm) || (fz->nw && (uintptr_t)fz->nw % 16 == 0),
@@ -1931,14 +2040,16 @@ extern "C" int aq_qlinear_grouped(const void* x, int64_t M, int64_t K, int fmt, 
                               tile_maxes, biases, ys, workspace, workspace_bytes, stream, nullptr);
 }
 
-extern "C" int aq_qlinear_decode(const void* x, int64_t K, int fmt, int64_t count, const int64_t* Ns,
+extern "C" int aq_qlinear_decode(const void* x, int64_t M, int64_t K, int fmt, int64_t count, const int64_t* Ns,
                                  const void* const* codes, const void* const* scales, const int64_t* Gs,
                                  const int32_t* const* row_ptrs, const int32_t* const* cols, const void* const* vals,
+                                 const int32_t* const* tile_ptrs, const uint32_t* const* tile_ents,
                                  const void* const* biases, void* const* ys, int prologue, const void* x2,
                                  const void* norm_weight, const void* norm_bias, float eps,
                                  const void* const* residuals, const int32_t* relu, void* stream) {
   const DecodeFuse fz{prologue, x2, norm_weight, norm_bias, eps, residuals, relu};
-  return qlinear_grouped_impl(x, 1, K, fmt, count, Ns, codes, scales, Gs, row_ptrs, cols, vals, nullptr, nullptr,
+  // no tile_max: the decode GEMVs never take the GEMM
+  return qlinear_grouped_impl(x, M, K, fmt, count, Ns, codes, scales, Gs, row_ptrs, cols, vals, tile_ptrs, tile_ents,
                               nullptr, biases, ys, nullptr, 0, stream, &fz);
 }
 

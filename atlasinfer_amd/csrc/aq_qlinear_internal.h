@@ -34,13 +34,15 @@ struct QLMat {
   int kg;      // K / G, scale blocks per row
   int gshift;  // log2(G) when G is a power of two, else -1
   int ldy;     // row stride of y: the whole matrix's N
-  // decode epilogue (M = 1 GEMV only; zero elsewhere): act 1 = ReLU of the
-  // fp16 output, then res (fp16 [N], this piece's rows) added in fp16
+  // decode epilogue (decode GEMVs only; zero elsewhere): act 1 = ReLU of the
+  // fp16 output, then res (fp16 [M][ldy], at this piece's first row) added
+  // in fp16
   const uint16_t* res;
   int act;
 };
 
-// Prologue of the M = 1 GEMV: what is staged in LDS in place of x.
+// Prologue of the decode GEMVs: what is staged in place of x (the norms on
+// the M = 1 GEMV only).
 enum : int { kProNone = 0, kProRms = 1, kProLayerNorm = 2, kProSwiGlu = 3 };
 
 struct QLArgs {
@@ -73,7 +75,6 @@ __device__ __forceinline__ QLMat pick(const QLArgs& a, int i) {
 __device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
 __device__ __forceinline__ uint32_t h2_bits(half2v h) { return __builtin_bit_cast(uint32_t, h); }
 
-// 8 codes (two dwords) -> 8 fp16 weights value(code) * s.
 // eight fp16 pairs (g, u) -> fp16(fp16(silu(g)) u)
 __device__ __forceinline__ u32x4 swiglu8(u32x4 g, u32x4 u) {
   const half8 gh = __builtin_bit_cast(half8, g), uh = __builtin_bit_cast(half8, u);
@@ -83,6 +84,7 @@ __device__ __forceinline__ u32x4 swiglu8(u32x4 g, u32x4 u) {
   return __builtin_bit_cast(u32x4, o);
 }
 
+// 8 codes (two dwords) -> 8 fp16 weights value(code) * s.
 template <int FMT>
 __device__ __forceinline__ half8 deq8(uint32_t w0, uint32_t w1, half2v s2) {
   uint32_t r[4];

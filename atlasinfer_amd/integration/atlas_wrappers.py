@@ -33,15 +33,18 @@ from ..quant.adaptive_quantizer import (QuantizedTensor, _format_id, _rows_cols,
 
 
 GEMV_MAX_M = 64  # aq_qlinear runs the dequant-GEMV up to this many rows of x
-# from this many rows of x on, calls pass the outlier block lists and the
-# workspace: the library then runs the GEMM for grids too short for the GEMV
-# (and always past GEMV_MAX_M)
-LISTS_MIN_M = 33
+# from this many rows of x on, calls pass the outlier block lists: the
+# shared-x GEMV (6 <= M <= 64) adds the outliers with MFMAs from them
+LISTS_MIN_M = 6
+# from this many rows on, calls pass the workspace too: given the lists the
+# library runs the GEMM for grids too short for the GEMV (and always past
+# GEMV_MAX_M)
+GEMM_MIN_M = 33
 
 
 def _workspace(M: int, Ns, K: int, dev: torch.device):
     """The GEMM's split-K workspace (None when the call needs none) and its size."""
-    if M < LISTS_MIN_M:
+    if M < GEMM_MIN_M:
         return None, 0
     # one query for the whole group: the library plans a grouped call over
     # all its output columns, and returns 0 when it runs the GEMV
@@ -103,13 +106,16 @@ PRO_NONE, PRO_RMS, PRO_LAYERNORM, PRO_SWIGLU = 0, 1, 2, 3
 
 
 def qlinear_decode(x: torch.Tensor, qts, biases, codes, prologue: int = PRO_NONE, x2=None, norm_weight=None,
-                   norm_bias=None, eps: float = 0.0, residuals=None, relu=None):
-    """One M = 1 launch of aq_qlinear_decode: [f(x) W_i^T + b_i] for up to 4
-    quantized W_i sharing in_features, where f is the prologue (none,
-    RMSNorm / LayerNorm with ``norm_weight`` / ``norm_bias`` and ``eps``, or
-    the SwiGLU product silu(x) * x2), each output optionally passed through
-    ReLU (``relu[i]``) and added to ``residuals[i]`` (fp16 [1, N_i]).
-    ``codes`` are the weights' tiled code arrays."""
+                   norm_bias=None, eps: float = 0.0, residuals=None, relu=None, tiles=None):
+    """One launch of aq_qlinear_decode: [f(x) W_i^T + b_i] for up to 4
+    quantized W_i sharing in_features, x of M rows (1, or 6..64), where f is
+    the prologue (none, RMSNorm / LayerNorm with ``norm_weight`` /
+    ``norm_bias`` and ``eps`` -- M = 1 only --, or the SwiGLU product
+    silu(x) * x2; every prologue needs M = 1), each output optionally passed
+    through ReLU (``relu[i]``) and added to ``residuals[i]`` (fp16 [M,
+    N_i]).  ``codes`` are the weights' tiled code arrays, ``tiles`` their
+    (tile_ptr, tile_ent, tile_max) outlier block lists (built when not
+    given, used from LISTS_MIN_M rows on)."""
     dev = x.device
     L = _lib.load()
     n = len(qts)
@@ -119,19 +125,25 @@ def qlinear_decode(x: torch.Tensor, qts, biases, codes, prologue: int = PRO_NONE
         if int(q.original_shape[-1]) != K or q.code_format != fmt or not fused_supported(q):
             raise ValueError("qlinear_decode: weights must share in_features and code format and tile")
     xs = [x.reshape(-1, K)] + ([x2.reshape(-1, K)] if x2 is not None else [])
+    M = xs[0].shape[0]
     for t in xs:
-        if t.shape[0] != 1 or not t.is_contiguous() or t.data_ptr() % 16 or t.dtype != torch.float16:
-            raise ValueError("qlinear_decode: x (and x2) must be one contiguous, 16-byte aligned fp16 row")
+        if t.shape[0] != M or not t.is_contiguous() or t.data_ptr() % 16 or t.dtype != torch.float16:
+            raise ValueError("qlinear_decode: x (and x2) must be contiguous, 16-byte aligned fp16 [M, K]")
     Ns = [_rows_cols(q.original_shape)[0] for q in qts]
-    ys = [torch.empty((1, N), dtype=torch.float16, device=dev) for N in Ns]
+    ys = [torch.empty((M, N), dtype=torch.float16, device=dev) for N in Ns]
     arr = _lib.ptr_array
     res = None if residuals is None else arr([_lib.ptr(r) for r in residuals])
     acts = None if relu is None else arr([int(bool(r)) for r in relu], ctypes.c_int32)
+    if M >= LISTS_MIN_M:
+        tiles = list(tiles) if tiles is not None else [outlier_tiles(q, dev) for q in qts]
+        tps, tes = arr([t[0].data_ptr() for t in tiles]), arr([t[1].data_ptr() for t in tiles])
+    else:
+        tps = tes = None
     _lib.check(L.aq_qlinear_decode(
-        xs[0].data_ptr(), K, _format_id(fmt), n, arr(Ns, ctypes.c_int64), arr([c.data_ptr() for c in codes]),
+        xs[0].data_ptr(), M, K, _format_id(fmt), n, arr(Ns, ctypes.c_int64), arr([c.data_ptr() for c in codes]),
         arr([q.scale_factors.data_ptr() for q in qts]), arr([q.block_size for q in qts], ctypes.c_int64),
         arr([q.outlier_row_ptr.data_ptr() for q in qts]), arr([_lib.ptr(q.outlier_cols) for q in qts]),
-        arr([_lib.ptr(q.fp16_outliers) for q in qts]), arr([_lib.ptr(b) for b in biases]),
+        arr([_lib.ptr(q.fp16_outliers) for q in qts]), tps, tes, arr([_lib.ptr(b) for b in biases]),
         arr([y.data_ptr() for y in ys]), int(prologue), None if x2 is None else xs[1].data_ptr(), _lib.ptr(norm_weight),
         _lib.ptr(norm_bias), ctypes.c_float(eps), res, acts, _lib.stream_of(dev)), "aq_qlinear_decode")
     return ys
@@ -194,12 +206,15 @@ class SiblingGroup:
         arr, n = _lib.ptr_array, len(qs)
         K = int(qs[0].original_shape[-1])
         Ns = [_rows_cols(q.original_shape)[0] for q in qs]
+        tiles = [m._ensure_tiles(q, dev) for m, q in zip(self.members, qs)]
+        # no tile_max: calls below GEMM_MIN_M rows always take a GEMV
         fixed = (_format_id(qs[0].code_format), n, arr(Ns, ctypes.c_int64), arr([c.data_ptr() for c in codes]),
                  arr([q.scale_factors.data_ptr() for q in qs]), arr([q.block_size for q in qs], ctypes.c_int64),
                  arr([q.outlier_row_ptr.data_ptr() for q in qs]), arr([_lib.ptr(q.outlier_cols) for q in qs]),
-                 arr([_lib.ptr(q.fp16_outliers) for q in qs]), None, None, None, arr([_lib.ptr(b) for b in biases]))
-        # the tuple keeps the weights, biases and codes its addresses point into
-        self._prep = p = (key, K, Ns, fixed, (qs, biases, codes))
+                 arr([_lib.ptr(q.fp16_outliers) for q in qs]), arr([t[0].data_ptr() for t in tiles]),
+                 arr([t[1].data_ptr() for t in tiles]), None, arr([_lib.ptr(b) for b in biases]))
+        # the tuple keeps the weights, biases, codes and block lists its addresses point into
+        self._prep = p = (key, K, Ns, fixed, (qs, biases, codes, tiles))
         return p
 
     def run(self, leader, x):
@@ -281,6 +296,13 @@ class QuantizedLinear(nn.Module):
         if self._codes is None or self._codes.device != dev:
             self._codes = kernel_codes(q, dev)
 
+    def _ensure_tiles(self, q: QuantizedTensor, dev: torch.device):
+        """The weight's outlier block lists on ``dev`` (stored ones, or built
+        once and kept); after _ensure_codes(q, dev)."""
+        if self._tiles is None or self._tiles[0].device != dev:
+            self._tiles = outlier_tiles(q, dev)
+        return self._tiles
+
     def _grouped_forward(self, x: torch.Tensor) -> Optional[torch.Tensor]:
         g = self._group
         y = g.take(self, x)
@@ -289,7 +311,7 @@ class QuantizedLinear(nn.Module):
         # an inference tensor has no version counter, so a kept output could
         # not be matched to an unmodified input: such inputs compute alone
         if (g.members[0] is self and not x.is_inference() and x.dtype == torch.float16 and x.device.type == "cuda"
-                and 0 < x.numel() < LISTS_MIN_M * x.shape[-1]
+                and 0 < x.numel() < GEMM_MIN_M * x.shape[-1]
                 and all(fused_supported(m.quantized_weights) for m in g.members)):
             return g.run(self, x)
         return None
@@ -305,7 +327,7 @@ class QuantizedLinear(nn.Module):
             y = self._grouped_forward(x)
             if y is not None:
                 return y
-        # decode fast path (M < LISTS_MIN_M rows of x): one library call with
+        # decode fast path (M < GEMM_MIN_M rows of x): one library call with
         # the weight's arguments prepared by an earlier forward on this device
         p = self._prep
         if (p is not None and x.dtype == torch.float16 and self.bias is p[1] and self.quantized_weights is p[2]
@@ -313,7 +335,7 @@ class QuantizedLinear(nn.Module):
             K, N = p[3], p[4]
             x2 = x.reshape(-1, K)
             M = x2.shape[0]
-            if 0 < M < LISTS_MIN_M:
+            if 0 < M < GEMM_MIN_M:
                 if not x2.is_contiguous() or x2.data_ptr() % 16:
                     x2 = x2.contiguous()
                 y = torch.empty((M, N), dtype=torch.float16, device=p[0])
@@ -346,15 +368,17 @@ class QuantizedLinear(nn.Module):
         if not fused_supported(q):
             return F.linear(x, dequantize_tensor(q, dev), self.bias)
         self._ensure_codes(q, dev)
-        if x.numel() >= LISTS_MIN_M * x.shape[-1] and (self._tiles is None or self._tiles[0].device != dev):
-            self._tiles = outlier_tiles(q, dev)
+        tp, te, _ = self._ensure_tiles(q, dev)
         if self._prep is None or self._prep[0] != dev or self._prep[1] is not self.bias or self._prep[2] is not q:
             N = q.original_shape.numel() // K
-            # the tuple holds the codes, weight and bias objects its addresses point into
+            # the tuple holds the codes, block lists, weight and bias objects
+            # its addresses point into (no tile_max: the fast path's calls
+            # always take a GEMV)
             self._prep = (dev, self.bias, q, K, N, _lib.load().aq_qlinear,
                           (self._codes.data_ptr(), q.scale_factors.data_ptr(), q.block_size,
                            _format_id(q.code_format), q.outlier_row_ptr.data_ptr(), _lib.ptr(q.outlier_cols),
-                           _lib.ptr(q.fp16_outliers), None, None, 0, _lib.ptr(self.bias)), self._codes)
+                           _lib.ptr(q.fp16_outliers), tp.data_ptr(), te.data_ptr(), 0, _lib.ptr(self.bias)),
+                          self._codes, self._tiles)
         return qlinear(x, q, self.bias, self._codes, self._tiles)
 
     def _apply(self, fn, recurse=True):

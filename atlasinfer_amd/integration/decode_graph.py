@@ -21,10 +21,12 @@ except the shapes: batch, cache length, model dimensions.  The host only
 guards that a replay never runs past the cache (``max_len``), so no index
 leaves its buffer.
 
-At batch 1 with quantized linears a layer is five launches (six with the
-attention's span merge): the norms, the SwiGLU product (OPT: ReLU) and the
-residual adds run inside the GEMV launches (``aq_qlinear_decode``).
-Otherwise, on the GPU with an fp16 model, a layer's step is about nine launches: one
+With quantized linears the decode GEMVs (``aq_qlinear_decode``) take the
+residual adds and the activation: at batch 1 also the norms and the SwiGLU
+product (OPT: the ReLU), so that a layer is five launches (six with the
+attention's span merge); for OPT at batch 6 to 64 the ReLU, each norm a
+launch of its own, seven (eight).  Otherwise, on the GPU with an fp16 model,
+a layer's step is about nine launches: one
 residual add + norm (``aq_decode_norm``) before the attention and one
 before the MLP, the q/k/v and gate/up projections as one grouped
 QuantizedLinear launch each, the attention (``aq_decode_attention``: query
@@ -121,9 +123,12 @@ class GraphDecoder:
             if nb < 0:
                 raise ValueError("aq_decode_attention_workspace refused these sizes")
             self.ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
-        # batch 1 with quantized linears: norms, SwiGLU / ReLU and residual
-        # adds folded into the GEMV launches (aq_qlinear_decode)
-        self.b1 = self._decode_ready()
+        # quantized linears at batch 1 (or OPT at 6..64): SwiGLU / ReLU and
+        # residual adds (batch 1: the norms too) folded into the GEMV launches
+        # (aq_qlinear_decode)
+        self.folded = self._decode_ready()
+        self.b1 = self.folded and B == 1
+        self.bm = self.folded and B > 1
 
     # ------------------------------------------------------------ one step
 
@@ -169,25 +174,31 @@ class GraphDecoder:
             return out
         return act(g) * u
 
-    # ---------------------------------------------- batch 1: five launches a layer
+    # ------------------------- batch 1 and 6..64: GEMVs with prologue and epilogue
 
     def _decode_ready(self) -> bool:
-        """Whether every layer can take the batch-1 form: all its linears
-        QuantizedLinear weights the fused GEMV takes (K <= 16384), the norms
-        HF's RMSNorm (Llama / Mistral, SiLU MLP) or LayerNorm with bias and
-        ReLU (OPT)."""
+        """Whether every layer can take the folded form (batch 1, or OPT at
+        6..64: the shared-x GEMV takes no prologue, so there Llama's SwiGLU
+        product stays a launch and folding the residual adds saves none):
+        all its linears QuantizedLinear weights the fused GEMVs take (at
+        batch 1 with K <= 16384), SiLU (Llama / Mistral) or ReLU (OPT)
+        between the MLP's linears and, at batch 1, whose norms fold into the
+        GEMV: HF's RMSNorm or LayerNorm with bias (OPT)."""
         from .atlas_wrappers import fused_supported
-        if not (self.fused and self.B == 1):
+        if not (self.fused and (self.B == 1 or (self.kind == "opt" and 6 <= self.B <= 64))):
             return False
+        b1 = self.B == 1
 
         def lin_ok(*mods):
             if not all(type(m).__name__ == "QuantizedLinear" for m in mods):
                 return False
             qs = [m.quantized_weights for m in mods]
             return (all(fused_supported(q) for q in qs) and len({int(q.original_shape[-1]) for q in qs}) == 1
-                    and len({q.code_format for q in qs}) == 1 and int(qs[0].original_shape[-1]) <= 16384)
+                    and len({q.code_format for q in qs}) == 1 and (not b1 or int(qs[0].original_shape[-1]) <= 16384))
 
         def norm_ok(mod):
+            if not b1:
+                return True  # a launch of its own (_addnorm)
             if self.kind == "opt":
                 return isinstance(mod, torch.nn.LayerNorm) and mod.weight is not None and mod.bias is not None
             return type(mod).__name__ in ("LlamaRMSNorm", "MistralRMSNorm")
@@ -215,6 +226,7 @@ class GraphDecoder:
         qs = [m._weights_on(self.dev) for m in mods]
         for m, q in zip(mods, qs):
             m._ensure_codes(q, self.dev)
+        tiles = [m._ensure_tiles(q, self.dev) for m, q in zip(mods, qs)] if self.B > 1 else None
         pro, nw, nb, eps = PRO_NONE, None, None, 0.0
         if norm is not None:
             if isinstance(norm, torch.nn.LayerNorm):
@@ -224,28 +236,36 @@ class GraphDecoder:
         elif u is not None:
             pro = PRO_SWIGLU
         return qlinear_decode(x, qs, [m.bias for m in mods], [m._codes for m in mods], pro, u, nw, nb, eps, res,
-                              relu)
+                              relu, tiles)
 
-    def _layer_b1(self, li, layer, x):
-        """One layer at batch 1 in five launches (OPT: five, plus none for
-        the ReLU): norm + q/k/v, attention (+ span merge), o_proj + residual,
-        norm + gate/up (OPT: norm + fc1 + ReLU), SwiGLU + down + residual
-        (OPT: fc2 + residual).  x [1, hidden] is the residual stream; returns
-        the next one."""
+    def _normed(self, mods, x, norm, relu=None):
+        """The linears ``mods`` on norm(x): the norm as the GEMV's prologue
+        at batch 1, a launch of its own (aq_decode_norm, no add) at batch
+        6..64."""
+        if self.B == 1:
+            return self._qdec(mods, x, norm=norm, relu=relu)
+        return self._qdec(mods, self._addnorm(x, None, norm), relu=relu)
+
+    def _layer_folded(self, li, layer, x):
+        """One layer in five launches at batch 1, seven for OPT at 6..64
+        (plus the attention's span merge where it splits): [norm,] norm +
+        q/k/v, attention, o_proj + residual, [norm,] norm + gate/up (OPT: fc1
+        + ReLU), SwiGLU + down + residual (OPT: fc2 + residual).  x [B,
+        hidden] is the residual stream; returns the next one."""
         B, H, Hkv, D = self.B, self.H, self.Hkv, self.D
         at = layer.self_attn
         if self.kind == "opt":
-            q, k, v = self._qdec([at.q_proj, at.k_proj, at.v_proj], x, norm=layer.self_attn_layer_norm)
+            q, k, v = self._normed([at.q_proj, at.k_proj, at.v_proj], x, layer.self_attn_layer_norm)
             o = self._attend_fused(li, q.view(B, H, D), k.view(B, Hkv, D), v.view(B, Hkv, D), 1.0, at.scaling,
                                    rope=False)
             x1 = self._qdec([at.out_proj], o, res=[x])[0]
-            f = self._qdec([layer.fc1], x1, norm=layer.final_layer_norm, relu=[1])[0]
+            f = self._normed([layer.fc1], x1, layer.final_layer_norm, relu=[1])[0]
             return self._qdec([layer.fc2], f, res=[x1])[0]
-        q, k, v = self._qdec([at.q_proj, at.k_proj, at.v_proj], x, norm=layer.input_layernorm)
+        q, k, v = self._normed([at.q_proj, at.k_proj, at.v_proj], x, layer.input_layernorm)
         o = self._attend_fused(li, q.view(B, H, D), k.view(B, Hkv, D), v.view(B, Hkv, D), at.scaling, 1.0,
                                rope=True)
         x1 = self._qdec([at.o_proj], o, res=[x])[0]
-        g, u = self._qdec([layer.mlp.gate_proj, layer.mlp.up_proj], x1, norm=layer.post_attention_layernorm)
+        g, u = self._normed([layer.mlp.gate_proj, layer.mlp.up_proj], x1, layer.post_attention_layernorm)
         return self._qdec([layer.mlp.down_proj], g, u=u, res=[x1])[0]
 
     def _layer_fused(self, li, layer, x, delta):
@@ -349,10 +369,10 @@ class GraphDecoder:
         else:
             x = m.model.embed_tokens(self.tok)
             final, layer_fn = m.model.norm, self._layer_llama
-        if self.b1:
+        if self.folded:
             x = x.contiguous()
             for li, layer in enumerate(self.layers):
-                x = self._layer_b1(li, layer, x)
+                x = self._layer_folded(li, layer, x)
             x = self._addnorm(x, None, final)
         elif self.fused:
             x = x.contiguous()

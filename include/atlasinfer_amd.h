@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define AQ_ABI_VERSION 5
+#define AQ_ABI_VERSION 6
 
 enum { AQ_FMT_INT8 = 0, AQ_FMT_E4M3 = 1 };
 enum { AQ_LAYOUT_FLAT = 0, AQ_LAYOUT_TILED = 1 };
@@ -166,7 +166,8 @@ int aq_zscore(const void* x, int64_t n, float eps, void* z, void* stats, void* s
  *   bias    fp16 [N] or NULL
  *   row_ptr, cols, vals   CSR outlier lists (aq_segment_offsets, aq_outlier_cols)
  *   tile_ptr, tile_ent    the same outliers per 16 x 64 block (aq_outlier_tiles);
- *                         required when M > 64, ignored (may be NULL) otherwise
+ *                         required when M > 64, used when given for
+ *                         6 <= M <= 64, ignored (may be NULL) for M <= 5
  *   tile_max              the largest entry count of any block (max of
  *                         tile_ptr[b+1] - tile_ptr[b]); above 64 the GEMM
  *                         takes a variant that reads the excess from memory
@@ -177,9 +178,12 @@ int aq_zscore(const void* x, int64_t n, float eps, void* z, void* stats, void* s
  *                 summed over a group) take the dequant-GEMM when tile_ptr
  *                 and tile_ent are given;
  *   M > 64        dequant-GEMM (tile_ptr, tile_ent required).
- * The GEMV adds the outliers from the CSR lists in fp32; the GEMM writes each
- * outlier's fp16 value over its decoded zero in the weight tile it
- * multiplies.  Either way the result is x times the dequantized weight
+ * The GEMVs add the outliers from the CSR lists in fp32, except the shared-x
+ * GEMV given the block lists (M <= 32, or groups under 768 tile rows), which
+ * multiplies each chunk's outliers with one more MFMA (x columns gathered
+ * against the outlier values); the GEMM
+ * writes each outlier's fp16 value over its decoded zero in the weight tile
+ * it multiplies.  Either way the result is x times the dequantized weight
  * accumulated in fp32, plus the bias, rounded once to fp16.
  * workspace: aq_qlinear_workspace_size(M, N, K) bytes, 16-byte aligned, or
  * NULL.  A nonzero size means the GEMM would split K (2, 4 or 8 ways, chosen
@@ -233,29 +237,34 @@ int aq_qlinear_noalloc(const void* x, int64_t M, int64_t K, int64_t N, const voi
                        void* y, void* stream);
 
 /*
- * One decode-step launch of up to 4 quantized linears sharing x (M = 1
- * row, K <= 16384), with the layer's neighbouring elementwise work folded
- * in: the M = 1 path of aq_qlinear_grouped (the reference's
- * QuantizedLinear.forward, integration/atlas_wrappers.py:56-67, at one
- * token) plus
+ * One decode-step launch of up to 4 quantized linears sharing x (M rows:
+ * 1 with K <= 16384, or 6 <= M <= 64), with the layer's neighbouring
+ * elementwise work folded in: the GEMV paths of aq_qlinear_grouped (the
+ * reference's QuantizedLinear.forward, integration/atlas_wrappers.py:56-67,
+ * at decode sizes) plus
  *   prologue  what the linears read instead of x:
  *             0  x as given
  *             1  RMSNorm(x): fp16(w fp16(x / sqrt(mean(x^2) + eps)))   (norm_weight)
  *             2  LayerNorm(x): fp16((x - mean) / sqrt(var + eps) w + b) (norm_weight, norm_bias)
  *             3  fp16(fp16(silu(x)) x2)  (x the gate, x2 the up projection)
- *             (the statistics in f32 over the row; the HF modules' order)
+ *             (the statistics in f32 over the row; the HF modules' order;
+ *             prologues need M = 1)
  *   epilogue  per member i: relu[i] = 1 applies ReLU to the fp16 output,
- *             then residuals[i] (fp16 [N_i], or NULL) is added in fp16.
+ *             then residuals[i] (fp16 [M, N_i], or NULL) is added in fp16.
+ * tile_ptrs, tile_ents: the members' outlier block lists (aq_outlier_tiles)
+ * or NULL; at 6 <= M <= 64 the GEMV adds the outliers with MFMAs from them
+ * (without them: from the CSR lists, slower).
  * relu and residuals may be NULL (none for every member).  The residual
  * must not be the output.  Replaces, at decode, the norm / activation /
  * residual operations of HF's decoder layers around the reference's
  * QuantizedLinear calls (no counterpart of its own in the reference).
  */
-int aq_qlinear_decode(const void* x, int64_t K, int fmt, int64_t count, const int64_t* Ns, const void* const* codes,
-                      const void* const* scales, const int64_t* Gs, const int32_t* const* row_ptrs,
-                      const int32_t* const* cols, const void* const* vals, const void* const* biases, void* const* ys,
-                      int prologue, const void* x2, const void* norm_weight, const void* norm_bias, float eps,
-                      const void* const* residuals, const int32_t* relu, void* stream);
+int aq_qlinear_decode(const void* x, int64_t M, int64_t K, int fmt, int64_t count, const int64_t* Ns,
+                      const void* const* codes, const void* const* scales, const int64_t* Gs,
+                      const int32_t* const* row_ptrs, const int32_t* const* cols, const void* const* vals,
+                      const int32_t* const* tile_ptrs, const uint32_t* const* tile_ents, const void* const* biases,
+                      void* const* ys, int prologue, const void* x2, const void* norm_weight, const void* norm_bias,
+                      float eps, const void* const* residuals, const int32_t* relu, void* stream);
 
 /*
  * Attention of one decode step over a static key/value cache, the position

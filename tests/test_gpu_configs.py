@@ -178,16 +178,21 @@ def raw_qlinear(q, x, with_lists):
 
 @pytest.mark.parametrize("K", [65536, 131072])
 def test_gemv_rows_of_64k_and_more(K):
-    """K >= 65536: the shared-x GEMV adds every outlier in its epilogue (the
-    column does not fit its 16-bit LDS entries); the direct GEMV reads x from
-    memory (no LDS copy past K = 16384)."""
+    """K >= 65536: without the block lists the shared-x GEMV adds every
+    outlier in its epilogue (the column does not fit its 16-bit LDS entries);
+    with them it adds each chunk's outliers by MFMA, its waves' chunk ranges
+    reloaded every 64 chunk groups (512 and 1024 chunks of 128 columns, 8
+    waves per tile row); the direct GEMV reads x from memory (no LDS copy
+    past K = 16384)."""
     N = 64
     G = min(K, 65536)  # aq_max_block_size: rows of 131072 take two blocks
     q, w, w_ref = quantized(("wide", K), lambda: R.make_weights(np.random.default_rng(K), (N, K), frac=0.01, t_dof=3),
                             G, "e4m3")
     for M in (1, 3, 6, 16, 33, 64):
         x = activations(M, K, K + M)
-        R.assert_close(raw_qlinear(q, x, with_lists=False), R.reference_linear(x, w_ref, None), x, w_ref)
+        yref = R.reference_linear(x, w_ref, None)
+        R.assert_close(raw_qlinear(q, x, with_lists=False), yref, x, w_ref)
+        R.assert_close(raw_qlinear(q, x, with_lists=True), yref, x, w_ref)
     check_layer(q, w_ref, activations(100, K, K + 100))
 
 

@@ -1,4 +1,4 @@
-"""aq_qlinear_decode (the M = 1 GEMV with a prologue and epilogue) against
+"""aq_qlinear_decode (the decode GEMVs with a prologue and epilogue) against
 the same work done by separate launches: the plain grouped GEMV, torch's
 fp16 ReLU / add, aq_silu_mul, and HF's RMSNorm / torch's LayerNorm modules.
 
@@ -38,15 +38,17 @@ def _close(a, b, what):
     assert rel <= 1e-3 and err <= 2e-3 * b.abs().max().item() + 1e-3, (what, err, rel)
 
 
+@pytest.mark.parametrize("M", [1, 8, 32])
 @pytest.mark.parametrize("Ns,K,bs", [([512, 128, 128], 2048, -1), ([2048], 8192, -1), ([4096, 4096], 1024, 128),
                                      ([1024], 4096, 256)])
-def test_epilogue_residual_and_relu_bit_exact(Ns, K, bs):
+def test_epilogue_residual_and_relu_bit_exact(Ns, K, bs, M):
+    """M = 1 takes the x-in-LDS GEMV, M = 8 and 32 the shared-x GEMV."""
     qts = _weights(Ns, K, 1, bs)
     codes = [kernel_codes(q, DEV) for q in qts]
     g = torch.Generator(device=DEV).manual_seed(2)
-    x = torch.randn(1, K, generator=g, device=DEV).half()
+    x = torch.randn(M, K, generator=g, device=DEV).half()
     biases = [torch.randn(N, generator=g, device=DEV).half() if i == 0 else None for i, N in enumerate(Ns)]
-    res = [torch.randn(1, N, generator=g, device=DEV).half() for N in Ns]
+    res = [torch.randn(M, N, generator=g, device=DEV).half() for N in Ns]
     ref = qlinear_grouped(x, qts, biases, codes)
     out = qlinear_decode(x, qts, biases, codes)
     for a, b in zip(out, ref):
@@ -61,16 +63,17 @@ def test_epilogue_residual_and_relu_bit_exact(Ns, K, bs):
 def test_swiglu_prologue_bit_exact(Ns, K, bs):
     """x holds the gate, x2 the up projection: identical to aq_silu_mul
     followed by the plain GEMV, bit for bit."""
+    M = 1
     qts = _weights(Ns, K, 3, bs)
     codes = [kernel_codes(q, DEV) for q in qts]
     g = torch.Generator(device=DEV).manual_seed(4)
-    gate = (torch.randn(1, K, generator=g, device=DEV) * 3).half()
-    up = torch.randn(1, K, generator=g, device=DEV).half()
+    gate = (torch.randn(M, K, generator=g, device=DEV) * 3).half()
+    up = torch.randn(M, K, generator=g, device=DEV).half()
     a = torch.empty_like(gate)
-    _lib.check(_lib.load().aq_silu_mul(gate.data_ptr(), up.data_ptr(), a.data_ptr(), K, _lib.stream_of(DEV)),
+    _lib.check(_lib.load().aq_silu_mul(gate.data_ptr(), up.data_ptr(), a.data_ptr(), M * K, _lib.stream_of(DEV)),
                "aq_silu_mul")
     ref = qlinear_grouped(a, qts, [None] * len(Ns), codes)
-    res = [torch.randn(1, N, generator=g, device=DEV).half() for N in Ns]
+    res = [torch.randn(M, N, generator=g, device=DEV).half() for N in Ns]
     out = qlinear_decode(gate, qts, [None] * len(Ns), codes, PRO_SWIGLU, x2=up, residuals=res)
     for o, b, r in zip(out, ref, res):
         assert torch.equal(o, b + r)
@@ -110,10 +113,32 @@ def test_norm_prologue_matches_modules(mode, Ns, K, bs):
         assert torch.equal(o, b)  # deterministic
 
 
+def test_swiglu_prologue_crowded_tile_rows():
+    """5 % outliers: a 16-row tile row holds thousands of entries: still bit
+    for bit the separate launches' result."""
+    M, N, K = 1, 256, 16384
+    g = torch.Generator(device=DEV).manual_seed(9)
+    w = torch.randn(N, K, generator=g, device=DEV) * 0.02
+    m = torch.rand(N, K, generator=g, device=DEV) < 0.05
+    w = torch.where(m, torch.sign(torch.randn(N, K, generator=g, device=DEV)) * 0.3, w).half()
+    q = quantize_tensor(w, block_size=-1, code_format="e4m3")
+    assert int(q.outlier_row_ptr[16].item()) > 2000  # the first tile row's entries
+    codes = [kernel_codes(q, DEV)]
+    gate = (torch.randn(M, K, generator=g, device=DEV) * 3).half()
+    up = torch.randn(M, K, generator=g, device=DEV).half()
+    a = torch.empty_like(gate)
+    _lib.check(_lib.load().aq_silu_mul(gate.data_ptr(), up.data_ptr(), a.data_ptr(), M * K, _lib.stream_of(DEV)),
+               "aq_silu_mul")
+    ref = qlinear_grouped(a, [q], [None], codes)[0]
+    assert torch.equal(qlinear_decode(a, [q], [None], codes)[0], ref)
+    out = qlinear_decode(gate, [q], [None], codes, PRO_SWIGLU, x2=up)[0]
+    assert torch.equal(out, ref)
+
+
 def test_decode_entry_checks():
-    """M = 1 only, K within the x-in-LDS limit, known prologues, the pieces
-    each prologue needs, the residual not the output: refused before any
-    launch."""
+    """M = 1 (K within the x-in-LDS limit) or 6..64 rows, prologues on one
+    row only, known prologues, the pieces each prologue needs, the
+    residual not the output: refused before any launch."""
     qts = _weights([256], 1024, 7)
     codes = [kernel_codes(q, DEV) for q in qts]
     x = torch.randn(1, 1024, device=DEV).half()
@@ -125,14 +150,22 @@ def test_decode_entry_checks():
         qlinear_decode(x, qts, [None], codes, PRO_LAYERNORM, norm_weight=torch.ones(1024, device=DEV).half())
     with pytest.raises(_lib.AQError, match="unknown prologue"):
         qlinear_decode(x, qts, [None], codes, 9)
+    x8 = torch.randn(8, 1024, device=DEV).half()
+    with pytest.raises(_lib.AQError, match="prologues take one row"):
+        qlinear_decode(x8, qts, [None], codes, PRO_RMS, norm_weight=torch.ones(1024, device=DEV).half())
+    with pytest.raises(_lib.AQError, match="prologues take one row"):
+        qlinear_decode(x8, qts, [None], codes, PRO_SWIGLU, x2=x8)
+    with pytest.raises(_lib.AQError, match="6 <= M <= 64"):
+        qlinear_decode(x8[:3].contiguous(), qts, [None], codes)
     L = _lib.load()
     arr = _lib.ptr_array
     q = qts[0]
     y = torch.empty(1, 256, dtype=torch.float16, device=DEV)
-    args = lambda res: (x.data_ptr(), 1024, 1, 1, arr([256], ctypes.c_int64), arr([codes[0].data_ptr()]),  # noqa: E731
+    args = lambda res: (x.data_ptr(), 1, 1024, 1, 1, arr([256], ctypes.c_int64), arr([codes[0].data_ptr()]),  # noqa: E731
                         arr([q.scale_factors.data_ptr()]), arr([q.block_size], ctypes.c_int64),
                         arr([q.outlier_row_ptr.data_ptr()]), arr([_lib.ptr(q.outlier_cols)]),
-                        arr([_lib.ptr(q.fp16_outliers)]), arr([None]), arr([y.data_ptr()]), PRO_NONE, None, None, None,
+                        arr([_lib.ptr(q.fp16_outliers)]), None, None, arr([None]), arr([y.data_ptr()]), PRO_NONE,
+                        None, None, None,
                         ctypes.c_float(0.0), res, None, _lib.stream_of(DEV))
     with pytest.raises(_lib.AQError, match="must not be the output"):
         _lib.check(L.aq_qlinear_decode(*args(arr([y.data_ptr()]))), "aq_qlinear_decode")

@@ -52,9 +52,9 @@ struct GemvIn {
   const uint16_t* x;
   int M, K;
 };
-__device__ __forceinline__ GemvIn gemv_in(const QLArgs& a) {
+__device__ __forceinline__ GemvIn gemv_in(const QLArgs& a, int off = 0) {
   GemvIn g;
-  g.w = a.mat[blockIdx.y];
+  g.w = a.mat[blockIdx.y + off];
   g.x = a.x;
   g.M = a.M;
   g.K = a.K;
@@ -138,6 +138,14 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W.bias ? W.bias + n0 : W.vals), (short)0, W.bias ? 32 : 0, kBufferDword3);
   const uint32_t bias_v = __builtin_amdgcn_raw_buffer_load_b16(br, (lane & 15) * 2, 0, 0);
+  // aq_qlinear_decode's residual of column n0 + lane % 16, read now for the
+  // same reason (at the end it would add a round trip to the launch)
+  uint32_t res_v = 0;
+  if (X1 == 2) {
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(W.res ? W.res + n0 : W.vals), (short)0, W.res ? 32 : 0, kBufferDword3);
+    res_v = __builtin_amdgcn_raw_buffer_load_b16(rr, (lane & 15) * 2, 0, 0);
+  }
   int p0 = 0, cnt = 0;
   uint32_t scol[kStageBatch], sval[kStageBatch], sx[MM][kStageBatch];
   auto stage_first_batch = [&]() {
@@ -477,7 +485,7 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       f16 o = rn_h(v);
       if (X1 == 2) {
         if (W.act == 1 && (float)o < 0.0f) o = (f16)0.0f;                   // ReLU
-        if (W.res) o = rn_h((float)bits_to_h(W.res[n0 + lane]) + (float)o);  // residual add
+        if (W.res) o = rn_h((float)bits_to_h((uint16_t)res_v) + (float)o);  // residual add
       }
       W.y[n0 + lane] = h_to_bits(o);
     }
@@ -538,18 +546,25 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   __shared__ __attribute__((aligned(16))) uint16_t xs[2][XR * XW];
   __shared__ uint32_t x_ent[TR][kXCsrCap];  // (value << 16) | column of the tile row's first outliers
 
-  const GemvIn in = gemv_in(a);
-  const QLMat& W = in.w;
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int tr = wave % TR, sp = wave / TR;
+  const int tr = wave % TR, sp = wave / TR;  // tr: the wave's tile-row slot
+  // SwiGLU pairs (a.pair > 0: a group of gate and up, a.pair pieces each,
+  // TR >= 2): slots TR / 2 and up take up's pieces (grid row blockIdx.y +
+  // a.pair), the same tile rows as the gate slots below them
+  const bool pair = a.pair > 0;
+  const int TRW = pair ? TR / 2 : TR;  // tile rows of a matrix per workgroup
+  const bool upper = pair && tr >= TRW;
+  const int trr = upper ? tr - TRW : tr;  // the wave's tile row in the workgroup
+  const GemvIn in = gemv_in(a, upper ? a.pair : 0);
+  const QLMat& W = in.w;
   const int M = in.M, K = in.K;
   const int nchunks = K >> 7;
   const int nrb = W.N / 16;
-  const int rb0 = blockIdx.x * TR;  // in the piece
-  if (rb0 >= nrb) return;  // the grid is as wide as the longest piece
-  const int rows_here = min(TR, nrb - rb0);  // tile rows of this workgroup inside the piece
+  const int rb0 = blockIdx.x * TRW;  // in the piece
+  if (rb0 >= nrb) return;  // the grid is as wide as the longest piece (uniform over the workgroup)
+  const int rows_here = min(TRW, nrb - rb0);  // tile rows of this workgroup inside the piece
   const int grp = lane >> 4, li = lane & 15;
   const int ngroups = (nchunks + S - 1) / S;
   const int nsteps = (ngroups + 1) & ~1;    // even: the loop body handles two groups
@@ -561,10 +576,10 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W.scales + (size_t)rb0 * 16 * W.kg), (short)0, rows_here * 16 * W.kg * 2, kBufferDword3);
   // tile rows past the piece: every code load of the wave is out of range (zero)
-  const uint32_t code_base = tr < rows_here ? (uint32_t)(tr * nchunks * 2048 + lane * 16) : kOutOfRange;
-  const uint32_t scale_row = (uint32_t)(tr * 16 + li) * W.kg;
+  const uint32_t code_base = trr < rows_here ? (uint32_t)(trr * nchunks * 2048 + lane * 16) : kOutOfRange;
+  const uint32_t scale_row = (uint32_t)(trr * 16 + li) * W.kg;
   uint16_t sb_row = 0;
-  if (PC) sb_row = tr < rows_here ? W.scales[(size_t)(rb0 + tr) * 16 + li] : (uint16_t)0;
+  if (PC) sb_row = trr < rows_here ? W.scales[(size_t)(rb0 + trr) * 16 + li] : (uint16_t)0;
 
   // OT: the block lists (tile_ptr offset to the piece's first tile row;
   // tile_ent holds 64 entries of read padding past the last)
@@ -579,7 +594,7 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   auto load_ranges = [&](int g0) {
     const int c = (g0 + lane) * S + sp;
     const uint32_t off =
-        tr < rows_here && c < nchunks ? (uint32_t)((rb0 + tr) * nb64 + 2 * c) * 4 : kOutOfRange;
+        trr < rows_here && c < nchunks ? (uint32_t)((rb0 + trr) * nb64 + 2 * c) * 4 : kOutOfRange;
     rg_s = __builtin_amdgcn_raw_buffer_load_b32(tpr, off, 0, 0);
     rg_m = __builtin_amdgcn_raw_buffer_load_b32(tpr, off + 4, 0, 0);
     rg_e = __builtin_amdgcn_raw_buffer_load_b32(tpr, off + 8, 0, 0);
@@ -706,8 +721,8 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   int op = 0, oend = 0;  // this lane's row: next staged entry and end of its staged entries
   int staged_row = 0;    // how many of the row's entries are staged
   auto stage_outliers = [&]() {
-    const bool fits = sp == 0 && tr < rows_here && K < 65536;
-    const int n0r = (rb0 + tr) * 16;
+    const bool fits = sp == 0 && trr < rows_here && K < 65536;
+    const int n0r = (rb0 + trr) * 16;
     int rpv = 0;
     if (fits && lane <= 16) rpv = W.row_ptr[n0r + lane];
     const int p0 = __shfl(rpv, 0, 64);
@@ -747,6 +762,21 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
     }
   };
 
+  // the epilogue's bias and residual (aq_qlinear_decode), read now so that
+  // their latency passes under the stream (at the end it would add a full
+  // round trip to the launch)
+  const bool active = sp == 0 && trr < rows_here;
+  const int n = (rb0 + trr) * 16 + li;  // the lane's output column (C layout below)
+  const float bv = active && W.bias ? (float)bits_to_h(W.bias[n]) : 0.0f;
+  uint16_t rv[MG][4];
+#pragma unroll
+  for (int gi = 0; gi < MG; gi++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int m = 16 * gi + 4 * grp + i;
+      rv[gi][i] = active && W.res && m < M ? W.res[(size_t)m * W.ldy + n] : (uint16_t)0;
+    }
+
   Slot sa, sb;
   if (OT) load_ranges(0);
   load(sa, 0);
@@ -778,15 +808,14 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
 #pragma unroll
           for (int i = 0; i < 4; i++) acc[gi][i] += red[(((s2 - 1) * TR + tr) * MG + gi) * 256 + i * 64 + lane];
   }
-  if (sp != 0 || tr >= rows_here) return;  // no barrier follows
+  if (!pair && !active) return;  // no barrier follows (pairs meet at one below)
 
   // C layout: lane l, element i -> row m = 16 gi + 4 (l / 16) + i, column n = n0 + l % 16.
   // Outliers of row n, eight entries at a time: their loads, then all the x
   // loads they need, then the FMAs.
-  const int n = (rb0 + tr) * 16 + li;
-  const int p_end = OT ? 0 : W.row_ptr[n + 1];
+  const int p_end = OT || !active ? 0 : W.row_ptr[n + 1];
   // the row's entries past the staged ones
-  for (int p = OT ? 0 : W.row_ptr[n] + staged_row; p < p_end; p += 8) {
+  for (int p = OT || !active ? 0 : W.row_ptr[n] + staged_row; p < p_end; p += 8) {
     int col[8];
     float wv[8];
 #pragma unroll
@@ -807,7 +836,27 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
         for (int b = 0; b < 8; b++) acc[gi][i] = __builtin_fmaf(xg[b], wv[b], acc[gi][i]);
       }
   }
-  const float bv = W.bias ? (float)bits_to_h(W.bias[n]) : 0.0f;
+  if (pair) {
+    // up's outputs (fp16, bias added) to LDS (x is no longer read, the
+    // partial sums sit in xs[0]); gate's waves write fp16(fp16(silu(g)) u)
+    uint16_t* pu = &xs[1][0];
+    if (active && upper)
+#pragma unroll
+      for (int gi = 0; gi < MG; gi++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) pu[((trr * MG + gi) * 4 + i) * 64 + lane] = h_to_bits(rn_h(acc[gi][i] + bv));
+    __syncthreads();
+    if (active && !upper)
+#pragma unroll
+      for (int gi = 0; gi < MG; gi++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int m = 16 * gi + 4 * grp + i;
+          const float u = (float)bits_to_h(pu[((trr * MG + gi) * 4 + i) * 64 + lane]);
+          if (m < M) W.y[(size_t)m * W.ldy + n] = h_to_bits(silu_mul_h((float)rn_h(acc[gi][i] + bv), u));
+        }
+    return;
+  }
 #pragma unroll
   for (int gi = 0; gi < MG; gi++)
 #pragma unroll
@@ -817,7 +866,7 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
         f16 o = rn_h(acc[gi][i] + bv);
         // aq_qlinear_decode's epilogue (zero / null for other calls)
         if (W.act == 1 && (float)o < 0.0f) o = (f16)0.0f;                                 // ReLU
-        if (W.res) o = rn_h((float)bits_to_h(W.res[(size_t)m * W.ldy + n]) + (float)o);  // residual add
+        if (W.res) o = rn_h((float)bits_to_h(rv[gi][i]) + (float)o);  // residual add
         W.y[(size_t)m * W.ldy + n] = h_to_bits(o);
       }
     }
@@ -1674,7 +1723,16 @@ hipError_t launch_gemv(const QLArgs& a, int fmt, bool per_channel, hipStream_t s
 template <int FMT, int MG, int S>
 hipError_t launch_gemv_x(const QLArgs& a, bool per_channel, hipStream_t s) {
   QLArgs p;
-  const dim3 g = gemv_pieces(a, kXWaves / S, &p);  // workgroups of 8 / S tile rows
+  // workgroups of 8 / S tile rows; a SwiGLU pair: 4 / S of each member, and
+  // the grid's rows over gate's pieces only (up's follow them in p.mat)
+  const bool pair = a.mat[0].act == 2;
+  dim3 g = gemv_pieces(a, pair ? kXWaves / S / 2 : kXWaves / S, &p);
+  p.pair = 0;
+  if (pair) {
+    p.pair = (int)g.y / 2;
+    g.y = (unsigned)p.pair;
+    for (int i = 0; i < p.count; i++) p.mat[i].act = 0;
+  }
   // Every member's block lists given: the MFMA outlier path, except with 3
   // or 4 row groups of x at S = 2, where the gathers (one per row group and
   // entry) cost more than the CSR walk of a wave shared by only two
@@ -1962,9 +2020,16 @@ static int qlinear_grouped_impl(const void* x, int64_t M, int64_t K, int fmt, in
     for (int i = 0; i < count; i++) {
       a.mat[i].res = fz->res ? (const uint16_t*)fz->res[i] : nullptr;
       a.mat[i].act = fz->act ? fz->act[i] : 0;
-      AQ_CHECK_ARG(a.mat[i].act == 0 || a.mat[i].act == 1, "aq_qlinear_decode: activation %d (0 none, 1 ReLU)",
-                   a.mat[i].act);
+      AQ_CHECK_ARG(a.mat[i].act == 0 || a.mat[i].act == 1 || (i == 0 && a.mat[i].act == 2),
+                   "aq_qlinear_decode: activation %d of member %d (0 none, 1 ReLU, 2 SwiGLU pair: member 0)",
+                   a.mat[i].act, i);
       AQ_CHECK_ARG(a.mat[i].res != ys[i], "aq_qlinear_decode: the residual must not be the output");
+    }
+    if (a.mat[0].act == 2) {
+      AQ_CHECK_ARG(count == 2 && Ns[0] == Ns[1] && M >= kGemvXMinM && a.pro == kProNone && a.mat[1].act == 0 &&
+                       !a.mat[0].res && !a.mat[1].res,
+                   "aq_qlinear_decode: a SwiGLU pair is two members of equal N (gate, up), 6 <= M <= 64, no "
+                   "prologue, activation or residual besides");
     }
   }
   if (M == 0) return AQ_OK;
@@ -1982,7 +2047,8 @@ static int qlinear_grouped_impl(const void* x, int64_t M, int64_t K, int fmt, in
     // leaves half the CUs idle).
     // Per decoder layer of those shapes it beats re-reading x per tile row
     // from M = 6 on (M = 6: 76 against 78 us, M = 16: 77 against 127 us)
-    const int S = blocks >= 768 ? 2 : (blocks >= 384 || M > 32) ? 4 : 8;
+    int S = blocks >= 768 ? 2 : (blocks >= 384 || M > 32) ? 4 : 8;
+    if (a.mat[0].act == 2) S = std::min(S, 4);  // a SwiGLU pair needs two tile-row slots per workgroup
     return aq::check_hip(launch_gemv_x(a, fmt, per_channel, S, s), "aq_qlinear: gemv launch");
   }
   if (gemv) {

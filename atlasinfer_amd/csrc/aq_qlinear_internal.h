@@ -24,7 +24,7 @@ struct QLMat {
   const int32_t* row_ptr;
   const int32_t* cols;
   const uint16_t* vals;
-  const int32_t* tptr;    // outliers per 16 x 64 block (GEMM only)
+  const int32_t* tptr;    // outliers per 16 x 64 block (GEMM, shared-x GEMV)
   const uint32_t* tent;
   const uint16_t* bias;
   uint16_t* y;
@@ -36,7 +36,7 @@ struct QLMat {
   int ldy;     // row stride of y: the whole matrix's N
   // decode epilogue (decode GEMVs only; zero elsewhere): act 1 = ReLU of the
   // fp16 output, then res (fp16 [M][ldy], at this piece's first row) added
-  // in fp16
+  // in fp16; act 2 (member 0 of two, shared-x GEMV): the SwiGLU pair
   const uint16_t* res;
   int act;
 };
@@ -57,6 +57,9 @@ struct QLArgs {
   // `per` run as two K halves, their fp32 partial sums in tpart (0: none)
   int tail, per;
   float* tpart;
+  // shared-x GEMV, aq_qlinear_decode: > 0 for a SwiGLU pair (gate, up), the
+  // number of pieces of each; the product goes to gate's output
+  int pair;
   int split;                 // GEMM: ways the K chunks are split (1: none)
   int first[kMaxGroup + 1];  // GEMM: first output tile of each matrix
   QLMat mat[kMaxPieces];     // GEMM: the group's matrices; GEMV: their pieces

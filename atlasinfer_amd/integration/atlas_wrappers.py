@@ -106,7 +106,7 @@ PRO_NONE, PRO_RMS, PRO_LAYERNORM, PRO_SWIGLU = 0, 1, 2, 3
 
 
 def qlinear_decode(x: torch.Tensor, qts, biases, codes, prologue: int = PRO_NONE, x2=None, norm_weight=None,
-                   norm_bias=None, eps: float = 0.0, residuals=None, relu=None, tiles=None):
+                   norm_bias=None, eps: float = 0.0, residuals=None, relu=None, tiles=None, swiglu_pair=False):
     """One launch of aq_qlinear_decode: [f(x) W_i^T + b_i] for up to 4
     quantized W_i sharing in_features, x of M rows (1, or 6..64), where f is
     the prologue (none, RMSNorm / LayerNorm with ``norm_weight`` /
@@ -115,7 +115,9 @@ def qlinear_decode(x: torch.Tensor, qts, biases, codes, prologue: int = PRO_NONE
     through ReLU (``relu[i]``) and added to ``residuals[i]`` (fp16 [M,
     N_i]).  ``codes`` are the weights' tiled code arrays, ``tiles`` their
     (tile_ptr, tile_ent, tile_max) outlier block lists (built when not
-    given, used from LISTS_MIN_M rows on)."""
+    given, used from LISTS_MIN_M rows on).  ``swiglu_pair``: qts are (gate,
+    up) and the result is [fp16(fp16(silu(x W_g^T)) (x W_u^T))], one
+    output (6 <= M <= 64)."""
     dev = x.device
     L = _lib.load()
     n = len(qts)
@@ -130,10 +132,17 @@ def qlinear_decode(x: torch.Tensor, qts, biases, codes, prologue: int = PRO_NONE
         if t.shape[0] != M or not t.is_contiguous() or t.data_ptr() % 16 or t.dtype != torch.float16:
             raise ValueError("qlinear_decode: x (and x2) must be contiguous, 16-byte aligned fp16 [M, K]")
     Ns = [_rows_cols(q.original_shape)[0] for q in qts]
-    ys = [torch.empty((M, N), dtype=torch.float16, device=dev) for N in Ns]
+    ys = [torch.empty((M, N), dtype=torch.float16, device=dev) for N in (Ns[:1] if swiglu_pair else Ns)]
     arr = _lib.ptr_array
     res = None if residuals is None else arr([_lib.ptr(r) for r in residuals])
-    acts = None if relu is None else arr([int(bool(r)) for r in relu], ctypes.c_int32)
+    yp = [y.data_ptr() for y in ys]
+    if swiglu_pair:
+        if n != 2 or Ns[0] != Ns[1]:
+            raise ValueError("qlinear_decode: a SwiGLU pair is two weights (gate, up) of equal out_features")
+        acts = arr([2, 0], ctypes.c_int32)
+        yp = [yp[0], yp[0]]  # the one output; up's is never written
+    else:
+        acts = None if relu is None else arr([int(bool(r)) for r in relu], ctypes.c_int32)
     if M >= LISTS_MIN_M:
         tiles = list(tiles) if tiles is not None else [outlier_tiles(q, dev) for q in qts]
         tps, tes = arr([t[0].data_ptr() for t in tiles]), arr([t[1].data_ptr() for t in tiles])
@@ -144,7 +153,7 @@ def qlinear_decode(x: torch.Tensor, qts, biases, codes, prologue: int = PRO_NONE
         arr([q.scale_factors.data_ptr() for q in qts]), arr([q.block_size for q in qts], ctypes.c_int64),
         arr([q.outlier_row_ptr.data_ptr() for q in qts]), arr([_lib.ptr(q.outlier_cols) for q in qts]),
         arr([_lib.ptr(q.fp16_outliers) for q in qts]), tps, tes, arr([_lib.ptr(b) for b in biases]),
-        arr([y.data_ptr() for y in ys]), int(prologue), None if x2 is None else xs[1].data_ptr(), _lib.ptr(norm_weight),
+        arr(yp), int(prologue), None if x2 is None else xs[1].data_ptr(), _lib.ptr(norm_weight),
         _lib.ptr(norm_bias), ctypes.c_float(eps), res, acts, _lib.stream_of(dev)), "aq_qlinear_decode")
     return ys
 

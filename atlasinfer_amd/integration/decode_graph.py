@@ -22,11 +22,12 @@ guards that a replay never runs past the cache (``max_len``), so no index
 leaves its buffer.
 
 With quantized linears the decode GEMVs (``aq_qlinear_decode``) take the
-residual adds and the activation: at batch 1 also the norms and the SwiGLU
-product (OPT: the ReLU), so that a layer is five launches (six with the
-attention's span merge); for OPT at batch 6 to 64 the ReLU, each norm a
-launch of its own, seven (eight).  Otherwise, on the GPU with an fp16 model,
-a layer's step is about nine launches: one
+residual adds and the activation: at batch 1 also the norms (the down
+projection stages the SwiGLU product as its input), so that a layer is five
+launches (six with the attention's span merge); at batch 6 to 64 each norm
+is a launch of its own and the gate/up launch writes the SwiGLU product (OPT:
+fc1 its ReLU), seven (eight).  Otherwise, on the GPU with an fp16 model, a
+layer's step is about nine launches: one
 residual add + norm (``aq_decode_norm``) before the attention and one
 before the MLP, the q/k/v and gate/up projections as one grouped
 QuantizedLinear launch each, the attention (``aq_decode_attention``: query
@@ -123,8 +124,8 @@ class GraphDecoder:
             if nb < 0:
                 raise ValueError("aq_decode_attention_workspace refused these sizes")
             self.ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
-        # quantized linears at batch 1 (or OPT at 6..64): SwiGLU / ReLU and
-        # residual adds (batch 1: the norms too) folded into the GEMV launches
+        # quantized linears at batch 1 or 6..64: SwiGLU / ReLU and residual
+        # adds (batch 1: the norms too) folded into the GEMV launches
         # (aq_qlinear_decode)
         self.folded = self._decode_ready()
         self.b1 = self.folded and B == 1
@@ -177,15 +178,13 @@ class GraphDecoder:
     # ------------------------- batch 1 and 6..64: GEMVs with prologue and epilogue
 
     def _decode_ready(self) -> bool:
-        """Whether every layer can take the folded form (batch 1, or OPT at
-        6..64: the shared-x GEMV takes no prologue, so there Llama's SwiGLU
-        product stays a launch and folding the residual adds saves none):
+        """Whether every layer can take the folded form (batch 1 or 6..64):
         all its linears QuantizedLinear weights the fused GEMVs take (at
         batch 1 with K <= 16384), SiLU (Llama / Mistral) or ReLU (OPT)
         between the MLP's linears and, at batch 1, whose norms fold into the
         GEMV: HF's RMSNorm or LayerNorm with bias (OPT)."""
         from .atlas_wrappers import fused_supported
-        if not (self.fused and (self.B == 1 or (self.kind == "opt" and 6 <= self.B <= 64))):
+        if not (self.fused and (self.B == 1 or 6 <= self.B <= 64)):
             return False
         b1 = self.B == 1
 
@@ -218,10 +217,11 @@ class GraphDecoder:
                 return False
         return True
 
-    def _qdec(self, mods, x, norm=None, u=None, res=None, relu=None):
+    def _qdec(self, mods, x, norm=None, u=None, res=None, relu=None, pair=False):
         """aq_qlinear_decode over ``mods`` (QuantizedLinear sharing x): the
         norm module or the SwiGLU product with u applied to x first, ReLU
-        and residual adds on the outputs."""
+        and residual adds on the outputs; ``pair``: mods are (gate, up) and
+        the one output is their SwiGLU product."""
         from .atlas_wrappers import PRO_LAYERNORM, PRO_NONE, PRO_RMS, PRO_SWIGLU, qlinear_decode
         qs = [m._weights_on(self.dev) for m in mods]
         for m, q in zip(mods, qs):
@@ -236,7 +236,7 @@ class GraphDecoder:
         elif u is not None:
             pro = PRO_SWIGLU
         return qlinear_decode(x, qs, [m.bias for m in mods], [m._codes for m in mods], pro, u, nw, nb, eps, res,
-                              relu, tiles)
+                              relu, tiles, swiglu_pair=pair)
 
     def _normed(self, mods, x, norm, relu=None):
         """The linears ``mods`` on norm(x): the norm as the GEMV's prologue
@@ -247,11 +247,12 @@ class GraphDecoder:
         return self._qdec(mods, self._addnorm(x, None, norm), relu=relu)
 
     def _layer_folded(self, li, layer, x):
-        """One layer in five launches at batch 1, seven for OPT at 6..64
-        (plus the attention's span merge where it splits): [norm,] norm +
-        q/k/v, attention, o_proj + residual, [norm,] norm + gate/up (OPT: fc1
-        + ReLU), SwiGLU + down + residual (OPT: fc2 + residual).  x [B,
-        hidden] is the residual stream; returns the next one."""
+        """One layer in five launches at batch 1, seven at 6..64 (plus the
+        attention's span merge where it splits): [norm,] norm + q/k/v,
+        attention, o_proj + residual, [norm,] norm + gate/up (batch 6..64:
+        + SwiGLU; OPT: fc1 + ReLU), [SwiGLU +] down + residual (OPT: fc2 +
+        residual).  x [B, hidden] is the residual stream; returns the next
+        one."""
         B, H, Hkv, D = self.B, self.H, self.Hkv, self.D
         at = layer.self_attn
         if self.kind == "opt":
@@ -265,8 +266,13 @@ class GraphDecoder:
         o = self._attend_fused(li, q.view(B, H, D), k.view(B, Hkv, D), v.view(B, Hkv, D), at.scaling, 1.0,
                                rope=True)
         x1 = self._qdec([at.o_proj], o, res=[x])[0]
-        g, u = self._normed([layer.mlp.gate_proj, layer.mlp.up_proj], x1, layer.post_attention_layernorm)
-        return self._qdec([layer.mlp.down_proj], g, u=u, res=[x1])[0]
+        mlp = layer.mlp
+        if self.B > 1:
+            h = self._addnorm(x1, None, layer.post_attention_layernorm)
+            a = self._qdec([mlp.gate_proj, mlp.up_proj], h, pair=True)[0]
+            return self._qdec([mlp.down_proj], a, res=[x1])[0]
+        g, u = self._normed([mlp.gate_proj, mlp.up_proj], x1, layer.post_attention_layernorm)
+        return self._qdec([mlp.down_proj], g, u=u, res=[x1])[0]
 
     def _layer_fused(self, li, layer, x, delta):
         """One layer on the GPU path: the residual stream x [B, hidden] is

@@ -250,7 +250,10 @@ int aq_qlinear_noalloc(const void* x, int64_t M, int64_t K, int64_t N, const voi
  *             (the statistics in f32 over the row; the HF modules' order;
  *             prologues need M = 1)
  *   epilogue  per member i: relu[i] = 1 applies ReLU to the fp16 output,
- *             then residuals[i] (fp16 [M, N_i], or NULL) is added in fp16.
+ *             then residuals[i] (fp16 [M, N_i], or NULL) is added in fp16;
+ *             relu[0] = 2 with two members of equal N (gate, up), 6 <= M <= 64
+ *             and nothing else folded: the SwiGLU pair, fp16(fp16(silu(g)) u)
+ *             written to ys[0] (ys[1] is not written).
  * tile_ptrs, tile_ents: the members' outlier block lists (aq_outlier_tiles)
  * or NULL; at 6 <= M <= 64 the GEMV adds the outliers with MFMAs from them
  * (without them: from the CSR lists, slower).

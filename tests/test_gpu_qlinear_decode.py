@@ -79,6 +79,32 @@ def test_swiglu_prologue_bit_exact(Ns, K, bs):
         assert torch.equal(o, b + r)
 
 
+@pytest.mark.parametrize("M", [8, 32, 64])
+@pytest.mark.parametrize("N,K,bs", [(14336, 4096, -1), (4096, 1024, 128), (2048, 2048, -1)])
+def test_swiglu_pair_epilogue(N, K, bs, M):
+    """gate and up in one launch writing fp16(fp16(silu(g)) u): bit for bit
+    the same GEMV's two outputs through aq_silu_mul where both take the same
+    waves per tile row (a pair takes at most 4: 2048 + 2048 rows at M <= 32
+    take 8 alone), else to the layer tolerance."""
+    qts = _weights([N, N], K, 11, bs)
+    codes = [kernel_codes(q, DEV) for q in qts]
+    g = torch.Generator(device=DEV).manual_seed(12)
+    x = torch.randn(M, K, generator=g, device=DEV).half()
+    biases = [torch.randn(N, generator=g, device=DEV).half() * 0.1 for _ in range(2)]
+    gate, up = qlinear_decode(x, qts, biases, codes)
+    ref = torch.empty_like(gate)
+    _lib.check(_lib.load().aq_silu_mul(gate.data_ptr(), up.data_ptr(), ref.data_ptr(), M * N, _lib.stream_of(DEV)),
+               "aq_silu_mul")
+    out = qlinear_decode(x, qts, biases, codes, swiglu_pair=True)
+    assert len(out) == 1 and out[0].shape == (M, N)
+    if N == 2048 and M <= 32:
+        _close(out[0], ref, "SwiGLU pair")
+    else:
+        assert torch.equal(out[0], ref)
+    again = qlinear_decode(x, qts, biases, codes, swiglu_pair=True)[0]
+    assert torch.equal(again, out[0])  # deterministic
+
+
 @pytest.mark.parametrize("mode,Ns,K,bs", [(PRO_RMS, [4096, 1024, 1024], 4096, -1), (PRO_RMS, [14336, 14336], 4096, -1),
                                           (PRO_LAYERNORM, [2048, 2048, 2048], 2048, -1),
                                           (PRO_LAYERNORM, [8192], 2048, 128), (PRO_RMS, [12288, 12288], 16384, -1)])
@@ -157,6 +183,14 @@ def test_decode_entry_checks():
         qlinear_decode(x8, qts, [None], codes, PRO_SWIGLU, x2=x8)
     with pytest.raises(_lib.AQError, match="6 <= M <= 64"):
         qlinear_decode(x8[:3].contiguous(), qts, [None], codes)
+    pq = _weights([256, 256], 1024, 8)
+    pc = [kernel_codes(q, DEV) for q in pq]
+    with pytest.raises(_lib.AQError, match="SwiGLU pair"):
+        qlinear_decode(x, pq, [None, None], pc, swiglu_pair=True)  # M = 1
+    with pytest.raises(_lib.AQError, match="SwiGLU pair"):
+        qlinear_decode(x8, pq, [None, None], pc, residuals=[x8[:, :256].contiguous(), None], swiglu_pair=True)
+    with pytest.raises(ValueError, match="SwiGLU pair"):
+        qlinear_decode(x8, qts, [None], codes, swiglu_pair=True)
     L = _lib.load()
     arr = _lib.ptr_array
     q = qts[0]

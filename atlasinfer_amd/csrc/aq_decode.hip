@@ -323,15 +323,24 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const int64_t* __re
   if (nact == 1) return;
   const float* pk = part + ((int64_t)b * Hkv + j) * ns * PF;
   __shared__ float f[G][kMaxSpans];
+  __shared__ float ls[G][kMaxSpans];
   __shared__ float den[G];
+  // every span's (m, l) read at once (a loop of dependent reads per head
+  // waited out one round trip per span)
+  for (int k = t; k < G * nact; k += 256) {
+    const int z = k / G, g = k - z * G;
+    f[g][z] = pk[z * PF + G * D + g];
+    ls[g][z] = pk[z * PF + G * D + G + g];
+  }
+  __syncthreads();
   if (t < G) {
     float mx = -INFINITY;
-    for (int z = 0; z < nact; z++) mx = fmaxf(mx, pk[z * PF + G * D + t]);
+    for (int z = 0; z < nact; z++) mx = fmaxf(mx, f[t][z]);
     float d = 0.0f;
     for (int z = 0; z < nact; z++) {
-      const float e = __expf(pk[z * PF + G * D + t] - mx);
+      const float e = __expf(f[t][z] - mx);
       f[t][z] = e;
-      d = fmaf(pk[z * PF + G * D + G + t], e, d);
+      d = fmaf(ls[t][z], e, d);
     }
     den[t] = d;
   }
@@ -340,7 +349,15 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const int64_t* __re
   for (int i = t; i < G * D; i += 256) {
     const int g = i / D;
     float num = 0.0f;
-    for (int z = 0; z < nact; z++) num = fmaf(pk[z * PF + i], f[g][z], num);
+    // eight spans' loads in flight, then their products in span order
+    for (int z0 = 0; z0 < nact; z0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[k] = z0 + k < nact ? pk[(z0 + k) * PF + i] : 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        if (z0 + k < nact) num = fmaf(v[k], f[g][z0 + k], num);
+    }
     o[i] = h_to_bits(rn_h(num / den[g]));
   }
 }

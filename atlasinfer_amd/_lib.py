@@ -38,6 +38,8 @@ SIGNATURES = {
     "aq_quantize_workspace_size": (_I64, [_I64, _I64]),
     "aq_quantize": (ctypes.c_int, [_P, _I64, _I64, ctypes.c_uint16, ctypes.c_int, _I64, ctypes.c_int, _P, _P, _I32P,
                                    _P, _I64, _P]),
+    "aq_quantize_grouped": (ctypes.c_int, [_I64, _P, _P, _I64, ctypes.c_uint16, ctypes.c_int, _I64, ctypes.c_int, _P,
+                                           _P, _P, _P, _P, _P]),
     "aq_quantize_finish": (ctypes.c_int, [_I64, _I64, _I64, _I32P, _I64, _P, _I64, _P, _P, _I32P, _P]),
     "aq_segment_offsets": (ctypes.c_int, [_P, _I64, _I64, _I64, _I32P, _P]),
     "aq_outlier_cols": (ctypes.c_int, [_P, _I64, _I64, _I32P, _P]),

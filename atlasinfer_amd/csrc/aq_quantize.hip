@@ -61,6 +61,16 @@ struct QuantArgs {
   uint16_t* stage_val;
 };
 
+// Up to kMaxQGroup weights of one block size quantized by one launch
+// (aq_quantize_grouped; aq_quantize is a group of one): workgroup b takes
+// unit b - first[i] of member i, first[i] <= b < first[i + 1].
+constexpr int kMaxQGroup = 8;
+struct QuantGroup {
+  QuantArgs m[kMaxQGroup];
+  int64_t first[kMaxQGroup + 1];
+  int count;
+};
+
 // E fp16 elements of one thread, two per 32-bit register (element 2i in
 // the low half); indices are compile-time constants after unrolling, so
 // reading an element costs at most a shift.
@@ -785,8 +795,14 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
 }
 
 template <int TAU, int E, int MODE>
-__global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantArgs a) {
+__global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantGroup q) {
   constexpr int NT = TAU > kWG ? TAU : kWG;
+  int mi = 0;  // the workgroup's member (uniform)
+#pragma unroll
+  for (int j = 1; j < kMaxQGroup; j++)
+    if (j < q.count && (int64_t)blockIdx.x >= q.first[j]) mi = j;
+  const QuantArgs& a = q.m[mi];
+  const int64_t bid = (int64_t)blockIdx.x - q.first[mi];
   constexpr int TEAMS = NT / TAU;
   constexpr int NWT = TAU > 64 ? TAU / 64 : 1;
   __shared__ double lds_d[TEAMS * NWT];
@@ -795,7 +811,7 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
 
   const int team = threadIdx.x / TAU;
   const int t = threadIdx.x % TAU;
-  const int64_t g = (int64_t)blockIdx.x * TEAMS + team;
+  const int64_t g = bid * TEAMS + team;
   const bool gvalid = g < a.nblocks;
   const int64_t G = a.G;
   const int64_t base = g * G;
@@ -814,9 +830,9 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantAr
   Elems<E> xs;
   bool staged = false;
   if constexpr (kStage) {
-    const int64_t wg_base = (int64_t)blockIdx.x * TEAMS * G;
+    const int64_t wg_base = bid * TEAMS * G;
     const int64_t wg_len = TEAMS * G;
-    if (a.vec && (int64_t)(blockIdx.x + 1) * TEAMS <= a.nblocks && wg_base + wg_len <= a.numel) {
+    if (a.vec && (bid + 1) * TEAMS <= a.nblocks && wg_base + wg_len <= a.numel) {
       staged = true;
       const int npieces = (int)(wg_len >> 3);
       const uint4* src = reinterpret_cast<const uint4*>(a.x + wg_base);
@@ -895,7 +911,14 @@ __global__ __launch_bounds__(256) void scan_apply_kernel(int32_t* off, int64_t n
 // instruction covers 1 KiB of contiguous memory (per-thread runs of 16 made
 // the single workgroup's loads touch 64 lines each).
 constexpr int kScanSmall = 1024 * 16;
-__global__ __launch_bounds__(1024) void scan_small_kernel(int32_t* off, int64_t n) {
+// One workgroup per member of a quantize group (n[i] <= kScanSmall counts in off[i]).
+struct ScanGroup {
+  int32_t* off[kMaxQGroup];
+  int64_t n[kMaxQGroup];
+};
+__global__ __launch_bounds__(1024) void scan_small_kernel(ScanGroup sg) {
+  int32_t* const off = sg.off[blockIdx.x];
+  const int64_t n = sg.n[blockIdx.x];
   __shared__ int lds[16];
   int carry = 0;
   for (int64_t r0 = 0; r0 < n; r0 += 4096) {
@@ -986,16 +1009,20 @@ int64_t next_pow2(int64_t g) {
 }
 
 template <int TAU, int E>
-hipError_t launch_quantize_t(const QuantArgs& a, hipStream_t stream) {
+hipError_t launch_quantize_t(QuantGroup q, hipStream_t stream) {
   constexpr int NT = TAU > kWG ? TAU : kWG;
   constexpr int TEAMS = NT / TAU;
-  const int64_t grid = aq::ceil_div(a.nblocks, TEAMS);
-  if (a.G == (int64_t)TAU * E)
-    hipLaunchKernelGGL((quantize_kernel<TAU, E, kFullBlocks>), dim3((unsigned)grid), dim3(NT), 0, stream, a);
-  else if (a.G % E == 0)
-    hipLaunchKernelGGL((quantize_kernel<TAU, E, kThreadAligned>), dim3((unsigned)grid), dim3(NT), 0, stream, a);
+  q.first[0] = 0;
+  for (int i = 0; i < q.count; i++) q.first[i + 1] = q.first[i] + aq::ceil_div(q.m[i].nblocks, TEAMS);
+  for (int i = q.count + 1; i <= kMaxQGroup; i++) q.first[i] = q.first[q.count];
+  const int64_t grid = q.first[q.count];
+  const int64_t G = q.m[0].G;  // one block size for the group
+  if (G == (int64_t)TAU * E)
+    hipLaunchKernelGGL((quantize_kernel<TAU, E, kFullBlocks>), dim3((unsigned)grid), dim3(NT), 0, stream, q);
+  else if (G % E == 0)
+    hipLaunchKernelGGL((quantize_kernel<TAU, E, kThreadAligned>), dim3((unsigned)grid), dim3(NT), 0, stream, q);
   else
-    hipLaunchKernelGGL((quantize_kernel<TAU, E, kAnyLen>), dim3((unsigned)grid), dim3(NT), 0, stream, a);
+    hipLaunchKernelGGL((quantize_kernel<TAU, E, kAnyLen>), dim3((unsigned)grid), dim3(NT), 0, stream, q);
   return hipGetLastError();
 }
 
@@ -1005,22 +1032,22 @@ hipError_t launch_quantize_t(const QuantArgs& a, hipStream_t stream) {
 // 4096 elements then needs no barrier at all), except 16384 (rows of 14336
 // such as down_proj's): 32 per thread on 8 waves ran 4 % faster than 64 on
 // 4, while 32 per thread at 4096 ran 15 % slower (measured).
-hipError_t launch_quantize(const QuantArgs& a, hipStream_t stream) {
-  const int64_t P = next_pow2(a.G);
+hipError_t launch_quantize(const QuantGroup& q, hipStream_t stream) {
+  const int64_t P = next_pow2(q.m[0].G);
   switch (P) {
-    case 1: case 2: case 4: case 8: case 16: return launch_quantize_t<1, 16>(a, stream);
-    case 32: return launch_quantize_t<2, 16>(a, stream);
-    case 64: return launch_quantize_t<4, 16>(a, stream);
-    case 128: return launch_quantize_t<8, 16>(a, stream);
-    case 256: return launch_quantize_t<16, 16>(a, stream);
-    case 512: return launch_quantize_t<32, 16>(a, stream);
-    case 1024: return launch_quantize_t<64, 16>(a, stream);
-    case 2048: return launch_quantize_t<64, 32>(a, stream);
-    case 4096: return launch_quantize_t<64, 64>(a, stream);
-    case 8192: return launch_quantize_t<128, 64>(a, stream);
-    case 16384: return launch_quantize_t<512, 32>(a, stream);
-    case 32768: return launch_quantize_t<512, 64>(a, stream);
-    default: return launch_quantize_t<1024, 64>(a, stream);
+    case 1: case 2: case 4: case 8: case 16: return launch_quantize_t<1, 16>(q, stream);
+    case 32: return launch_quantize_t<2, 16>(q, stream);
+    case 64: return launch_quantize_t<4, 16>(q, stream);
+    case 128: return launch_quantize_t<8, 16>(q, stream);
+    case 256: return launch_quantize_t<16, 16>(q, stream);
+    case 512: return launch_quantize_t<32, 16>(q, stream);
+    case 1024: return launch_quantize_t<64, 16>(q, stream);
+    case 2048: return launch_quantize_t<64, 32>(q, stream);
+    case 4096: return launch_quantize_t<64, 64>(q, stream);
+    case 8192: return launch_quantize_t<128, 64>(q, stream);
+    case 16384: return launch_quantize_t<512, 32>(q, stream);
+    case 32768: return launch_quantize_t<512, 64>(q, stream);
+    default: return launch_quantize_t<1024, 64>(q, stream);
   }
 }
 
@@ -1065,9 +1092,11 @@ extern "C" int64_t aq_quantize_workspace_size(int64_t numel, int64_t G) {
   return workspace_bytes(nblocks * G, nblocks);
 }
 
-extern "C" int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_thr_f16, int fmt, int64_t K,
-                           int layout, void* codes, void* scales, int32_t* block_off, void* workspace, int64_t ws_bytes,
-                           void* stream) {
+// Checks one weight's arguments and fills its QuantArgs (aq_quantize,
+// aq_quantize_grouped).
+static int quantize_args(const void* x, int64_t numel, int64_t G, uint16_t z_thr_f16, int fmt, int64_t K, int layout,
+                         void* codes, void* scales, int32_t* block_off, void* workspace, int64_t ws_bytes,
+                         QuantArgs* out, Workspace* wout) {
   AQ_CHECK_ARG(numel > 0, "aq_quantize: numel must be > 0 (got %lld)", (long long)numel);
   AQ_CHECK_ARG(G >= 1 && G <= kMaxG, "aq_quantize: block size %lld outside [1, %lld]", (long long)G,
                (long long)kMaxG);
@@ -1086,8 +1115,7 @@ extern "C" int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_t
   if (ws_bytes < workspace_bytes(padded, nblocks))
     return aq::set_error(AQ_EWORKSPACE, "aq_quantize: workspace of %lld bytes, %lld needed", (long long)ws_bytes,
                          (long long)workspace_bytes(padded, nblocks));
-  hipStream_t s = (hipStream_t)stream;
-  Workspace w = carve(workspace, padded, nblocks);
+  const Workspace w = carve(workspace, padded, nblocks);
   QuantArgs a;
   a.x = (const uint16_t*)x;
   a.numel = numel;
@@ -1107,10 +1135,29 @@ extern "C" int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_t
   a.block_cnt = block_off;
   a.stage_col = w.stage_col;
   a.stage_val = w.stage_val;
-  hipError_t e = launch_quantize(a, s);
+  *out = a;
+  *wout = w;
+  return AQ_OK;
+}
+
+extern "C" int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_thr_f16, int fmt, int64_t K,
+                           int layout, void* codes, void* scales, int32_t* block_off, void* workspace, int64_t ws_bytes,
+                           void* stream) {
+  QuantGroup q{};
+  Workspace w;
+  const int rc =
+      quantize_args(x, numel, G, z_thr_f16, fmt, K, layout, codes, scales, block_off, workspace, ws_bytes, &q.m[0], &w);
+  if (rc != AQ_OK) return rc;
+  q.count = 1;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t nblocks = q.m[0].nblocks;
+  hipError_t e = launch_quantize(q, s);
   if (e != hipSuccess) return aq::check_hip(e, "aq_quantize: quantize kernel launch");
   if (nblocks <= kScanSmall) {
-    hipLaunchKernelGGL(scan_small_kernel, dim3(1), dim3(1024), 0, s, block_off, nblocks);
+    ScanGroup sg{};
+    sg.off[0] = block_off;
+    sg.n[0] = nblocks;
+    hipLaunchKernelGGL(scan_small_kernel, dim3(1), dim3(1024), 0, s, sg);
     AQ_LAUNCH_CHECK("aq_quantize: scan launch");
     return AQ_OK;
   }
@@ -1119,6 +1166,36 @@ extern "C" int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_t
   AQ_LAUNCH_CHECK("aq_quantize: scan launch");
   hipLaunchKernelGGL(scan_apply_kernel, dim3((unsigned)nparts), dim3(256), 0, s, block_off, nblocks, w.partial);
   AQ_LAUNCH_CHECK("aq_quantize: scan launch");
+  return AQ_OK;
+}
+
+extern "C" int aq_quantize_grouped(int64_t count, const void* const* xs, const int64_t* numels, int64_t G,
+                                   uint16_t z_thr_f16, int fmt, int64_t K, int layout, void* const* codes,
+                                   void* const* scales, int32_t* const* block_offs, void* const* workspaces,
+                                   const int64_t* ws_bytes, void* stream) {
+  AQ_CHECK_ARG(count >= 1 && count <= kMaxQGroup, "aq_quantize_grouped: 1..%d weights, got %lld", kMaxQGroup,
+               (long long)count);
+  AQ_CHECK_ARG(xs && numels && codes && scales && block_offs && workspaces && ws_bytes,
+               "aq_quantize_grouped: null pointer argument");
+  QuantGroup q{};
+  ScanGroup sg{};
+  for (int i = 0; i < (int)count; i++) {
+    Workspace w;
+    const int rc = quantize_args(xs[i], numels[i], G, z_thr_f16, fmt, K, layout, codes[i], scales[i], block_offs[i],
+                                 workspaces[i], ws_bytes[i], &q.m[i], &w);
+    if (rc != AQ_OK) return rc;
+    AQ_CHECK_ARG(q.m[i].nblocks <= kScanSmall,
+                 "aq_quantize_grouped: weight %d has %lld blocks, more than %d (quantize it alone)", i,
+                 (long long)q.m[i].nblocks, kScanSmall);
+    sg.off[i] = block_offs[i];
+    sg.n[i] = q.m[i].nblocks;
+  }
+  q.count = (int)count;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = launch_quantize(q, s);
+  if (e != hipSuccess) return aq::check_hip(e, "aq_quantize_grouped: quantize kernel launch");
+  hipLaunchKernelGGL(scan_small_kernel, dim3((unsigned)count), dim3(1024), 0, s, sg);
+  AQ_LAUNCH_CHECK("aq_quantize_grouped: scan launch");
   return AQ_OK;
 }
 

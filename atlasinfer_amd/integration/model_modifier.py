@@ -18,7 +18,7 @@ import torch
 import torch.nn as nn
 
 from .. import _lib
-from ..quant.adaptive_quantizer import quantize_tensor
+from ..quant.adaptive_quantizer import quantize_tensor, quantize_tensors
 from .atlas_wrappers import QuantizedLinear
 
 MODEL_LAYER_PATTERNS = {
@@ -115,6 +115,32 @@ def apply_atlas_quantization_to_model(model: nn.Module, model_type: str, quantiz
         return
     print(f"Found {len(linear_modules)} linear layers to quantize...")
     replaced, failed = 0, 0
+    # Linears are quantized in runs of up to 8 (quantize_tensors: one launch
+    # for the members sharing a block size, the same results as one call
+    # each); a run that fails is retried member by member, so each failure
+    # is reported and skipped on its own as the reference's loop does
+    pending = []  # (parent, child name, name, fp16 weight, bias)
+
+    def flush():
+        nonlocal replaced, failed
+        if not pending:
+            return
+        try:
+            qts = quantize_tensors([p[3] for p in pending], **quantization_config)
+        except Exception:
+            qts = [None] * len(pending)
+        for (parent, child, name, w, b), qt in zip(pending, qts):
+            try:
+                if qt is None:
+                    qt = quantize_tensor(w, **quantization_config)
+                _replace_module(parent, child, QuantizedLinear(qt, b))
+                replaced += 1
+            except Exception as e:
+                print(f"!! FAILED quant layer {name}: {e}")
+                traceback.print_exc()
+                failed += 1
+        pending.clear()
+
     for name, module in list(linear_modules):
         parent_name, child_name = name.rsplit(".", 1) if "." in name else ("", name)
         parent = model.get_submodule(parent_name) if parent_name else model
@@ -127,14 +153,15 @@ def apply_atlas_quantization_to_model(model: nn.Module, model_type: str, quantiz
                 continue
             w = module.weight.data.to(dtype=torch.float16, device=dev)
             b = module.bias.data.to(dtype=torch.float16, device=dev).clone() if getattr(module, "bias", None) is not None else None
-            qt = quantize_tensor(w, **quantization_config)
-            _replace_module(parent, child_name, QuantizedLinear(qt, b))
-            replaced += 1
+            pending.append((parent, child_name, name, w, b))
             del w, module
         except Exception as e:
             print(f"!! FAILED quant layer {name}: {e}")
             traceback.print_exc()
             failed += 1
+        if len(pending) == 8:
+            flush()
+    flush()
     gc.collect()
     if fuse_siblings:
         print(f"Linked {link_sibling_linears(model)} sibling groups for grouped decode launches")

@@ -33,6 +33,7 @@ Code formats:
 """
 from __future__ import annotations
 
+import ctypes
 import threading
 from typing import NamedTuple, Optional
 
@@ -245,11 +246,23 @@ def quantize_tensor(
     if numel == 0:
         return _empty(original_shape, G, code_format, input_device)
 
+    p = _quantize_prepare(fp16_tensor, G, z_threshold, code_format, fmt)
+    L = _lib.load()
+    _lib.check(L.aq_quantize(*p["args"], p["stream"]), "aq_quantize")
+    nnz = int(p["block_off"][p["nblocks"]].item())  # the one host sync: sizes the outlier tensors
+    return _quantize_complete(p, nnz)
+
+
+def _quantize_prepare(fp16_tensor: torch.Tensor, G: int, z_threshold: float, code_format: str, fmt: int) -> dict:
+    """Outputs, workspace and aq_quantize arguments of one tensor (numel > 0,
+    fp16)."""
     L = _lib.load()
     if G > L.aq_max_block_size():
         raise ValueError(f"block_size {G} exceeds the supported maximum {L.aq_max_block_size()}")
+    input_device = fp16_tensor.device
+    original_shape = fp16_tensor.shape
+    numel = fp16_tensor.numel()
     dev = _lib.compute_device(input_device)
-    stream = _lib.stream_of(dev)
     x = fp16_tensor.to(dev).contiguous().view(-1)
     N, K = _rows_cols(original_shape)
     nblocks = (numel + G - 1) // G
@@ -257,16 +270,26 @@ def quantize_tensor(
     # e4m3 codes go straight into the layout the fused kernels read; int8
     # codes stay in element order for the reference's compacted stream
     layout = "tiled" if (fmt == _lib.FMT_E4M3 and tiled_eligible(original_shape, G)) else "flat"
-
     codes = torch.empty(padded, dtype=torch.uint8, device=dev)
     scales = torch.empty(nblocks, dtype=torch.float16, device=dev)
     block_off = torch.empty(nblocks + 1, dtype=torch.int32, device=dev)
     ws_bytes = int(L.aq_quantize_workspace_size(numel, G))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    _lib.check(L.aq_quantize(x.data_ptr(), numel, G, _threshold_bits(z_threshold), fmt, K, _lib.LAYOUTS[layout],
-                             codes.data_ptr(), scales.data_ptr(), block_off.data_ptr(), ws.data_ptr(), ws_bytes,
-                             stream), "aq_quantize")
-    nnz = int(block_off[nblocks].item())  # the one host sync: sizes the outlier tensors
+    args = (x.data_ptr(), numel, G, _threshold_bits(z_threshold), fmt, K, _lib.LAYOUTS[layout], codes.data_ptr(),
+            scales.data_ptr(), block_off.data_ptr(), ws.data_ptr(), ws_bytes)
+    return dict(x=x, input_device=input_device, original_shape=original_shape, numel=numel, G=G, N=N, K=K,
+                nblocks=nblocks, padded=padded, layout=layout, codes=codes, scales=scales, block_off=block_off,
+                ws=ws, ws_bytes=ws_bytes, args=args, fmt=fmt, code_format=code_format, dev=dev,
+                stream=_lib.stream_of(dev))
+
+
+def _quantize_complete(p: dict, nnz: int) -> QuantizedTensor:
+    """The outlier lists, CSR rows and block lists of a tensor whose
+    aq_quantize (or group) has run, given its outlier count."""
+    L = _lib.load()
+    dev, stream, G, K, N = p["dev"], p["stream"], p["G"], p["K"], p["N"]
+    numel, padded, fmt, layout = p["numel"], p["padded"], p["fmt"], p["layout"]
+    block_off, codes, ws, ws_bytes = p["block_off"], p["codes"], p["ws"], p["ws_bytes"]
     flat_idx = torch.empty(nnz, dtype=torch.int64, device=dev)
     vals = torch.empty(nnz, dtype=torch.float16, device=dev)
     cols = torch.empty(nnz, dtype=torch.int32, device=dev)
@@ -288,15 +311,15 @@ def quantize_tensor(
                                       stream), "aq_compact_codes")
     else:
         fp8_data = codes.view(torch.float8_e4m3fn)
-    del ws
+    p["ws"] = None
     qt = QuantizedTensor(
         fp8_data=fp8_data,
         fp16_outliers=vals,
         outlier_indices=flat_idx,
-        scale_factors=scales,
-        original_shape=original_shape,
+        scale_factors=p["scales"],
+        original_shape=p["original_shape"],
         block_size=G,
-        code_format=code_format,
+        code_format=p["code_format"],
         outlier_row_ptr=row_ptr,
         outlier_cols=cols,
         code_layout=layout,
@@ -304,7 +327,54 @@ def quantize_tensor(
     if layout == "tiled":
         tp, te, tmax = build_outlier_tiles(qt, dev, lazy_max=True)
         qt = qt._replace(outlier_tile_ptr=tp, outlier_tile_ent=te, outlier_tile_max=tmax)
-    return qt.to(input_device)
+    return qt.to(p["input_device"])
+
+
+# weights per aq_quantize_grouped launch, and most blocks a member may have
+_QUANT_GROUP_MAX, _QUANT_GROUP_MAX_BLOCKS = 8, 16384
+
+
+def quantize_tensors(tensors, block_size: int = 128, z_threshold: float = 3.0, *,
+                     code_format: str = DEFAULT_CODE_FORMAT):
+    """``[quantize_tensor(t, ...) for t in tensors]``, bit for bit, with
+    the tensors that share a device and a block size (and have at most
+    16384 blocks) quantized by one launch per 8 (aq_quantize_grouped): the
+    small weights of a layer then share the GPU instead of each filling one
+    round of it, and the whole list costs one host sync."""
+    fmt = _format_id(code_format)
+    out = [None] * len(tensors)
+    preps = {}
+    for i, t in enumerate(tensors):
+        if not isinstance(t, torch.Tensor) or t.dtype != torch.float16 or t.numel() == 0:
+            out[i] = quantize_tensor(t, block_size, z_threshold, code_format=code_format)
+            continue
+        G = _resolve_block(block_size, t.shape)
+        p = _quantize_prepare(t, G, z_threshold, code_format, fmt)
+        preps[i] = p
+    L = _lib.load()
+    groups = {}
+    for i, p in preps.items():
+        if p["nblocks"] <= _QUANT_GROUP_MAX_BLOCKS:
+            groups.setdefault((p["dev"], p["G"], p["K"], p["layout"]), []).append(i)
+        else:
+            _lib.check(L.aq_quantize(*p["args"], p["stream"]), "aq_quantize")
+    arr = _lib.ptr_array
+    for (dev, G, K, layout), idx in groups.items():
+        for c in range(0, len(idx), _QUANT_GROUP_MAX):
+            ps = [preps[i] for i in idx[c:c + _QUANT_GROUP_MAX]]
+            a0 = ps[0]["args"]
+            _lib.check(L.aq_quantize_grouped(
+                len(ps), arr([p["args"][0] for p in ps]), arr([p["numel"] for p in ps], ctypes.c_int64), G, a0[3],
+                fmt, K, a0[6], arr([p["args"][7] for p in ps]), arr([p["args"][8] for p in ps]),
+                arr([p["args"][9] for p in ps]), arr([p["args"][10] for p in ps]),
+                arr([p["ws_bytes"] for p in ps], ctypes.c_int64), ps[0]["stream"]), "aq_quantize_grouped")
+    if preps:
+        # the one host sync: every tensor's outlier count
+        counts = torch.stack([p["block_off"][p["nblocks"]].to(preps[next(iter(preps))]["dev"])
+                              for p in preps.values()]).tolist()
+        for (i, p), nnz in zip(preps.items(), counts):
+            out[i] = _quantize_complete(p, int(nnz))
+    return out
 
 
 def _stored_codes(q: QuantizedTensor, device: torch.device) -> torch.Tensor:

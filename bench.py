@@ -22,6 +22,7 @@ reference's CPU path timed on this host.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -191,13 +192,16 @@ def profiled_us_per_launch():
     return None
 
 
-def time_quantize_kernel(weights, reps=5):
+def time_quantize_kernel(weights, reps=5, grouped=False):
     """The quantize kernel alone (aq_quantize: statistics, codes, outlier
     staging and the scan of outlier counts), per-channel E4M3 into the tiled
     layout, timed with HIP events on the launch stream over ``reps`` replays
     of a graph holding one pass over every weight; returns (algorithmic
     bytes, seconds) of one pass.
-    Bytes: 2 N K read + N K codes + 2 N scales + 6 per outlier staged."""
+    Bytes: 2 N K read + N K codes + 2 N scales + 6 per outlier staged.
+    ``grouped``: the weights sharing K in aq_quantize_grouped launches of up
+    to 8 (as apply_atlas_quantization_to_model quantizes them), the rest
+    alone."""
     from atlasinfer_amd import _lib
     from atlasinfer_amd.quant import adaptive_quantizer as AQ
     L = _lib.load()
@@ -219,11 +223,27 @@ def time_quantize_kernel(weights, reps=5):
         nbytes += 3 * numel + 2 * N + 6 * nnz
     # one pass captured in a HIP graph (the launches issue no memset), so the
     # host's launch cost of the small weights is not timed
+    runs = [[c] for c in calls]
+    if grouped:
+        by_k = {}
+        for c in calls:
+            nblocks = -(-c[0][1] // c[0][2])
+            by_k.setdefault(c[0][5] if nblocks <= 16384 else id(c), []).append(c)
+        runs = [g[i:i + 8] for g in by_k.values() for i in range(0, len(g), 8)]
+    arr = _lib.ptr_array
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         cs = torch.cuda.current_stream().cuda_stream
-        for args, _keep in calls:
-            _lib.check(L.aq_quantize(*args, cs), "aq_quantize")
+        for run in runs:
+            if len(run) == 1:
+                _lib.check(L.aq_quantize(*run[0][0], cs), "aq_quantize")
+                continue
+            a0 = run[0][0]
+            _lib.check(L.aq_quantize_grouped(
+                len(run), arr([c[0][0] for c in run]), arr([c[0][1] for c in run], ctypes.c_int64), a0[2], a0[3],
+                a0[4], a0[5], a0[6], arr([c[0][7] for c in run]), arr([c[0][8] for c in run]),
+                arr([c[0][9] for c in run]), arr([c[0][10] for c in run]), arr([c[0][11] for c in run], ctypes.c_int64),
+                cs), "aq_quantize_grouped")
     graph.replay()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
@@ -608,7 +628,7 @@ def bench_config4(dev, gen, log, qlinear):
     shapes = [[(N, K) for _, N, K in LLAMA_LINEARS]] * 32 + [[(128256, 4096)], [(128256, 4096)]]
     for li, sh in enumerate(shapes):
         ws = [gen_weight_t3(N, K, gen, dev) for N, K in sh]
-        b, t = time_quantize_kernel(ws, reps=3)
+        b, t = time_quantize_kernel(ws, reps=3, grouped=True)
         q_bytes += b
         q_s += t
         params += sum(N * K for N, K in sh)
@@ -618,8 +638,9 @@ def bench_config4(dev, gen, log, qlinear):
     torch.cuda.empty_cache()
     part1 = {"params": params, "GBps": round(q_bytes / q_s / 1e9, 1),
              "frac_hbm_peak": round(q_bytes / q_s / 1e9 / HBM_PEAK_GBS, 4), "ms": round(1e3 * q_s, 2),
-             "note": "quantize kernel (aq_quantize, per-channel e4m3, tiled) over 32 Llama-3-8B layers + "
-                     "embedding + lm_head, Student-t(3)*0.02 weights with 1% U(8,20)*0.02 outliers"}
+             "note": "quantize kernel (per-channel e4m3, tiled; a layer's six K=4096 weights in one "
+                     "aq_quantize_grouped launch, the rest alone) over 32 Llama-3-8B layers + embedding + lm_head, "
+                     "Student-t(3)*0.02 weights with 1% U(8,20)*0.02 outliers"}
     log(f"config 4 part 1: {params / 1e9:.2f} B params quantized at {part1['GBps']} GB/s "
         f"({part1['ms']} ms of kernel time)")
     part2 = {}
@@ -728,20 +749,22 @@ def main():
     q_bytes, q_time = 0, 0.0
     keep_fp16 = {}
     for li in range(N_LAYERS):
+        # a layer's seven weights through quantize_tensors, as the model swap
+        # quantizes them (one launch for the six sharing K, one host sync)
+        ws = [gen_weight(N, K, gen, dev) for _, N, K in LLAMA_LINEARS]
+        AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")  # warm (allocations)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        qts = AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")
+        torch.cuda.synchronize()
+        q_time += time.perf_counter() - t0
         layer = {}
-        for name, N, K in LLAMA_LINEARS:
-            w = gen_weight(N, K, gen, dev)
-            AQ.quantize_tensor(w, block_size=-1, code_format="e4m3")  # warm (allocations)
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            qt = AQ.quantize_tensor(w, block_size=-1, code_format="e4m3")
-            torch.cuda.synchronize()
-            q_time += time.perf_counter() - t0
+        for (name, _, _), w, qt in zip(LLAMA_LINEARS, ws, qts):
             q_bytes += quantize_bytes(qt)
             layer[name] = qt
             if li == 0:
                 keep_fp16[name] = w
-            del w
+        del ws, w
         layers.append(layer)
         log(f"layer {li} quantized")
 
@@ -821,7 +844,8 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / 1e3 / iters
 
-    qk_bytes, qk_s = time_quantize_kernel([keep_fp16[name] for name, _, _ in LLAMA_LINEARS])
+    qk_bytes, qk_s = time_quantize_kernel([keep_fp16[name] for name, _, _ in LLAMA_LINEARS], grouped=True)
+    qk1_bytes, qk1_s = time_quantize_kernel([keep_fp16[name] for name, _, _ in LLAMA_LINEARS])
     log(f"quantize kernel: {qk_bytes / qk_s / 1e9:.1f} GB/s ({1e6 * qk_s:.1f} us per layer)")
 
     blas_m1_s = 0.0
@@ -929,9 +953,14 @@ def main():
             "gemv_m1_7launch_us_per_layer": round(1e6 * gpu7 / nsteps7, 2),
             "quantize_kernel_GBps": round(qk_bytes / qk_s / 1e9, 1),
             "quantize_kernel_frac_hbm_peak": round(qk_bytes / qk_s / 1e9 / HBM_PEAK_GBS, 4),
-            "quantize_kernel_note": "aq_quantize over the 7 layer-0 weights, per-channel e4m3, one graph per pass, events",
+            "quantize_kernel_note": "the 7 layer-0 weights, per-channel e4m3, one graph per pass, events: the six "
+                                    "K=4096 weights in one aq_quantize_grouped launch, down_proj alone (as the "
+                                    "model swap quantizes them); _single: one aq_quantize per weight",
+            "quantize_kernel_single_GBps": round(qk1_bytes / qk1_s / 1e9, 1),
+            "quantize_kernel_single_frac_hbm_peak": round(qk1_bytes / qk1_s / 1e9 / HBM_PEAK_GBS, 4),
             "quantize_GBps": round(q_bytes / q_time / 1e9, 1),
-            "quantize_note": "whole quantize_tensor call incl. host sync, outlier gather and block lists",
+            "quantize_note": "whole quantize_tensors call per layer (the 7 weights; one host sync) incl. outlier "
+                             "gather and block lists",
             "sweep": sweep or None,
             "cpu_reference": cpu_extra,
             "models": models,

@@ -82,6 +82,22 @@ int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_thr_f16, int
                 void* stream);
 
 /*
+ * aq_quantize for up to 8 weights of one block size G (and K, format,
+ * layout) in one launch of the quantize kernel and one of the scan: per
+ * member i the arguments of aq_quantize (xs[i], numels[i], codes[i],
+ * scales[i], block_offs[i], workspaces[i] of ws_bytes[i]), each with at
+ * most 16384 blocks.  Results are those of aq_quantize on each member, bit
+ * for bit.  No counterpart of its own in the reference (its quantize_tensor,
+ * adaptive_quantizer.py:51-148, takes one tensor; the model swap,
+ * model_modifier.py:95-143, calls it once per Linear): for callers that
+ * quantize a layer's weights together, whose small members alone fill the
+ * GPU for one round of waves at most.
+ */
+int aq_quantize_grouped(int64_t count, const void* const* xs, const int64_t* numels, int64_t G, uint16_t z_thr_f16,
+                        int fmt, int64_t K, int layout, void* const* codes, void* const* scales,
+                        int32_t* const* block_offs, void* const* workspaces, const int64_t* ws_bytes, void* stream);
+
+/*
  * Quantize, phase 2 of 2: write the outlier list in ascending flat order
  * (the reference's fp16_outliers / outlier_indices, adaptive_quantizer.py:
  * 109-117,137-138) plus the column of each outlier for row width K.

@@ -338,6 +338,17 @@ def quantize_only(args, dev, gen):
                       "copy_bytes": src.numel()}), flush=True)
 
 
+def quantize_layer_only(args, dev, gen):
+    """Trace workload of the grouped quantize: the seven Llama-3-8B weights
+    of one layer as the model swap quantizes them (the six K = 4096 weights
+    in one aq_quantize_grouped launch, down_proj alone), each pass one HIP
+    graph."""
+    ws = [gen_weight(N, K, gen, dev) for _, N, K in LLAMA_LINEARS]
+    nbytes, secs = time_quantize_kernel(ws, reps=max(args.steps // 4, 1), grouped=True)
+    print(json.dumps({"quantize_layer": True, "algorithmic_bytes_per_pass": nbytes,
+                      "us_per_pass": round(1e6 * secs, 3), "GBps": round(nbytes / secs / 1e9, 1)}), flush=True)
+
+
 def gemm_only(args, dev, gen, qlinear, qlinear_grouped, AQ):
     """Counter-run workload of the dequant-GEMM: the M = 2048 prefill launch
     pattern of one Llama-3-8B layer (q/k/v grouped, o, gate/up grouped,
@@ -711,6 +722,8 @@ def main():
     ap.add_argument("--quantize-only", action="store_true",
                     help="only the quantize kernel (4 rotated gate_proj weights) and a 512 MiB calibration copy, "
                          "for counter runs")
+    ap.add_argument("--quantize-layer", action="store_true",
+                    help="only the grouped quantize of one layer's seven weights, for traces")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the M=2048 prefill launches of one Llama-3-8B layer, for counter runs")
     ap.add_argument("--graph-decode", choices=["opt", "mistral"],
@@ -736,6 +749,9 @@ def main():
         return
     if args.quantize_only:
         quantize_only(args, dev, gen)
+        return
+    if args.quantize_layer:
+        quantize_layer_only(args, dev, gen)
         return
     if args.gemm_only:
         gemm_only(args, dev, gen, qlinear, qlinear_grouped, AQ)

@@ -198,9 +198,11 @@ class SiblingGroup:
         self.version = -1
         self.out = {}
 
-    def _prepare(self, dev):
+    def _prepare(self, dev, lists: bool):
         """The grouped call's fixed arguments for the members' current
-        weights and biases on ``dev`` (rebuilt when any of them changes)."""
+        weights and biases on ``dev`` (rebuilt when any of them changes);
+        ``lists``: with the outlier block lists (calls of LISTS_MIN_M rows or
+        more), else without them (none are built)."""
         qs, biases, codes = [], [], []
         for m in self.members:
             q = m._weights_on(dev)
@@ -208,27 +210,29 @@ class SiblingGroup:
             qs.append(q)
             biases.append(m.bias)
             codes.append(m._codes)
-        key = (dev, tuple(id(q) for q in qs), tuple(id(b) for b in biases))
+        key = (dev, tuple(id(q) for q in qs), tuple(id(b) for b in biases), lists)
         p = getattr(self, "_prep", None)
         if p is not None and p[0] == key:
             return p
         arr, n = _lib.ptr_array, len(qs)
         K = int(qs[0].original_shape[-1])
         Ns = [_rows_cols(q.original_shape)[0] for q in qs]
-        tiles = [m._ensure_tiles(q, dev) for m, q in zip(self.members, qs)]
+        tiles = ([m._ensure_tiles(q, dev) for m, q in zip(self.members, qs)] if lists
+                 else [(None, None, 0)] * n)
         # no tile_max: calls below GEMM_MIN_M rows always take a GEMV
         fixed = (_format_id(qs[0].code_format), n, arr(Ns, ctypes.c_int64), arr([c.data_ptr() for c in codes]),
                  arr([q.scale_factors.data_ptr() for q in qs]), arr([q.block_size for q in qs], ctypes.c_int64),
                  arr([q.outlier_row_ptr.data_ptr() for q in qs]), arr([_lib.ptr(q.outlier_cols) for q in qs]),
-                 arr([_lib.ptr(q.fp16_outliers) for q in qs]), arr([t[0].data_ptr() for t in tiles]),
-                 arr([t[1].data_ptr() for t in tiles]), None, arr([_lib.ptr(b) for b in biases]))
+                 arr([_lib.ptr(q.fp16_outliers) for q in qs]), arr([_lib.ptr(t[0]) for t in tiles]),
+                 arr([_lib.ptr(t[1]) for t in tiles]), None, arr([_lib.ptr(b) for b in biases]))
         # the tuple keeps the weights, biases, codes and block lists its addresses point into
         self._prep = p = (key, K, Ns, fixed, (qs, biases, codes, tiles))
         return p
 
     def run(self, leader, x):
         dev = x.device
-        _, K, Ns, fixed, _keep = self._prepare(dev)
+        K = int(x.shape[-1])
+        _, K, Ns, fixed, _keep = self._prepare(dev, x.numel() // K >= LISTS_MIN_M)
         x2 = x.reshape(-1, K)
         if not x2.is_contiguous() or x2.data_ptr() % 16:
             x2 = x2.contiguous()
@@ -344,7 +348,10 @@ class QuantizedLinear(nn.Module):
             K, N = p[3], p[4]
             x2 = x.reshape(-1, K)
             M = x2.shape[0]
-            if 0 < M < GEMM_MIN_M:
+            # from LISTS_MIN_M rows on the GEMV wants the outlier block lists:
+            # arguments prepared without them (an earlier call with fewer
+            # rows) go through _forward, which builds them once
+            if 0 < M < GEMM_MIN_M and (M < LISTS_MIN_M or p[8] is not None):
                 if not x2.is_contiguous() or x2.data_ptr() % 16:
                     x2 = x2.contiguous()
                 y = torch.empty((M, N), dtype=torch.float16, device=p[0])
@@ -377,18 +384,28 @@ class QuantizedLinear(nn.Module):
         if not fused_supported(q):
             return F.linear(x, dequantize_tensor(q, dev), self.bias)
         self._ensure_codes(q, dev)
-        tp, te, _ = self._ensure_tiles(q, dev)
-        if self._prep is None or self._prep[0] != dev or self._prep[1] is not self.bias or self._prep[2] is not q:
+        M = x.numel() // K if K else 0
+        if M >= LISTS_MIN_M:
+            self._ensure_tiles(q, dev)
+        elif self._tiles is not None and self._tiles[0].device != dev:
+            self._tiles = None
+        # block lists only once a call has enough rows to use them: fewer rows
+        # (decode at batch 1) never build them, which would cost a host sync
+        # per call for weights streamed in without stored lists
+        tiles = self._tiles
+        p = self._prep
+        if p is None or p[0] != dev or p[1] is not self.bias or p[2] is not q or (tiles is not None and p[8] is None):
             N = q.original_shape.numel() // K
+            tp, te = (None, None) if tiles is None else tiles[:2]
             # the tuple holds the codes, block lists, weight and bias objects
             # its addresses point into (no tile_max: the fast path's calls
             # always take a GEMV)
             self._prep = (dev, self.bias, q, K, N, _lib.load().aq_qlinear,
                           (self._codes.data_ptr(), q.scale_factors.data_ptr(), q.block_size,
                            _format_id(q.code_format), q.outlier_row_ptr.data_ptr(), _lib.ptr(q.outlier_cols),
-                           _lib.ptr(q.fp16_outliers), tp.data_ptr(), te.data_ptr(), 0, _lib.ptr(self.bias)),
-                          self._codes, self._tiles)
-        return qlinear(x, q, self.bias, self._codes, self._tiles)
+                           _lib.ptr(q.fp16_outliers), _lib.ptr(tp), _lib.ptr(te), 0, _lib.ptr(self.bias)),
+                          self._codes, tiles)
+        return qlinear(x, q, self.bias, self._codes, tiles)
 
     def _apply(self, fn, recurse=True):
         # module.to(device) / .cuda() also moves the quantized weight and the

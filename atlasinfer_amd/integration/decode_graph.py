@@ -151,10 +151,8 @@ class GraphDecoder:
         """x += delta in place (fp16 add; none when delta is None), then
         mod(x): one aq_decode_norm launch for HF's Llama/Mistral RMSNorm and
         for LayerNorm with weight and bias, else the torch add and module."""
-        name = type(mod).__name__
-        rms = name in ("LlamaRMSNorm", "MistralRMSNorm")
-        ln = isinstance(mod, torch.nn.LayerNorm) and mod.weight is not None and mod.bias is not None
-        if (rms or ln) and mod.weight.dtype == self.dtype and x.shape[-1] % 8 == 0 and x.shape[-1] <= 16384:
+        rms = type(mod).__name__ in ("LlamaRMSNorm", "MistralRMSNorm")
+        if self._norm_folds(mod) and x.shape[-1] % 8 == 0 and x.shape[-1] <= 16384:
             y = torch.empty_like(x)
             eps = mod.variance_epsilon if rms else mod.eps
             _lib.check(self._lib.aq_decode_norm(
@@ -177,6 +175,20 @@ class GraphDecoder:
 
     # ------------------------- batch 1 and 6..64: GEMVs with prologue and epilogue
 
+    def _norm_folds(self, mod) -> bool:
+        """Whether the norm ``mod`` can be the batch-1 GEMV's prologue: HF's
+        RMSNorm (Llama / Mistral) or LayerNorm with weight and bias (OPT),
+        whose parameters are fp16 [K], contiguous, on the decoder's device
+        and 16-byte aligned (the prologue reads them as fp16 pieces of 16
+        bytes).  Anything else keeps its own launch or torch module."""
+        def param_ok(t):
+            return (t is not None and t.dtype == torch.float16 and t.is_contiguous() and t.device == self.dev
+                    and t.data_ptr() % 16 == 0)
+
+        if self.kind == "opt":
+            return isinstance(mod, torch.nn.LayerNorm) and param_ok(mod.weight) and param_ok(mod.bias)
+        return type(mod).__name__ in ("LlamaRMSNorm", "MistralRMSNorm") and param_ok(mod.weight)
+
     def _decode_ready(self) -> bool:
         """Whether every layer can take the folded form (batch 1 or 6..64):
         all its linears QuantizedLinear weights the fused GEMVs take (at
@@ -196,11 +208,7 @@ class GraphDecoder:
                     and len({q.code_format for q in qs}) == 1 and (not b1 or int(qs[0].original_shape[-1]) <= 16384))
 
         def norm_ok(mod):
-            if not b1:
-                return True  # a launch of its own (_addnorm)
-            if self.kind == "opt":
-                return isinstance(mod, torch.nn.LayerNorm) and mod.weight is not None and mod.bias is not None
-            return type(mod).__name__ in ("LlamaRMSNorm", "MistralRMSNorm")
+            return not b1 or self._norm_folds(mod)  # batch 6..64: a launch of its own (_addnorm)
 
         for layer in self.layers:
             at = layer.self_attn

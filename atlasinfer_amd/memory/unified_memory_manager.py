@@ -226,9 +226,12 @@ class UnifiedMemoryManager:
 
     def _to_disk(self, layer: int, e: _Entry) -> bool:
         k, v = e.views()
-        ok = self.disk_interface.put(self._get_kv_key(layer, "K"), k) and \
-            self.disk_interface.put(self._get_kv_key(layer, "V"), v)
-        if not ok:
+        kkey = self._get_kv_key(layer, "K")
+        if not self.disk_interface.put(kkey, k):
+            return False
+        if not self.disk_interface.put(self._get_kv_key(layer, "V"), v):
+            # no entry will own the keys' file: take it back out with its bytes
+            self.disk_interface.delete(kkey)
             return False
         e.length = int(k.shape[2])
         e.k = e.v = None
@@ -488,10 +491,14 @@ class KVCacheLayer(_cache_layer_base()):
     def reset(self) -> None:
         self.manager.reset_layer(self.layer_idx)
 
-    def crop(self, tokens_to_remove: int) -> None:
+    def crop(self, max_length: int) -> None:
+        """Keep the first ``max_length`` positions (a negative value: drop
+        that many from the end), as HF's DynamicLayer.crop does; crop(0)
+        empties the layer."""
         n = self.get_seq_length()
-        keep = tokens_to_remove if tokens_to_remove > 0 else n - abs(tokens_to_remove)
-        self.manager.truncate(self.layer_idx, max(keep, 0))
+        keep = max_length if max_length >= 0 else n + max_length
+        if keep < n:
+            self.manager.truncate(self.layer_idx, max(keep, 0))
 
     def offload(self):
         pass  # the manager decides where the layer lives

@@ -48,10 +48,13 @@ PER_CHANNEL = -1
 
 class DeviceInt:
     """An int that still lives in a one-element device tensor: read (one host
-    sync) the first time it is used as a number, then kept.  Lets
+    sync) the first time it is used as a number -- converted, compared,
+    tested for truth, hashed or used in arithmetic -- then kept.  Lets
     quantize_tensor hand back the largest block-list count without waiting
     for it; the first consumer (the GEMM's kernel choice, serialization)
-    pays the wait."""
+    pays the wait.  That first use makes a device-to-host copy, which HIP
+    graph capture does not allow: a caller that captures should use the
+    value once before capturing (GraphDecoder's eager warm-up steps do)."""
     __slots__ = ("_t", "_v")
 
     def __init__(self, t: torch.Tensor):
@@ -83,8 +86,19 @@ class DeviceInt:
     def __ge__(self, o):
         return self._get() >= int(o)
 
+    def __ne__(self, o):
+        return self._get() != int(o)
+
+    def __bool__(self):
+        return self._get() != 0
+
     def __hash__(self):
         return hash(self._get())
+
+    def __mul__(self, o):
+        return self._get() * o
+
+    __rmul__ = __mul__
 
     def __add__(self, o):
         return self._get() + o
@@ -330,49 +344,63 @@ def _quantize_complete(p: dict, nnz: int) -> QuantizedTensor:
     return qt.to(p["input_device"])
 
 
-# weights per aq_quantize_grouped launch, and most blocks a member may have
-_QUANT_GROUP_MAX, _QUANT_GROUP_MAX_BLOCKS = 8, 16384
+# weights per aq_quantize_grouped launch, most blocks a member may have, and
+# most elements a launch may hold (each member's fp16 copy on the device,
+# codes and workspace are alive together until its completion)
+_QUANT_GROUP_MAX, _QUANT_GROUP_MAX_BLOCKS, _QUANT_GROUP_MAX_ELEMS = 8, 16384, 1 << 28
 
 
 def quantize_tensors(tensors, block_size: int = 128, z_threshold: float = 3.0, *,
                      code_format: str = DEFAULT_CODE_FORMAT):
     """``[quantize_tensor(t, ...) for t in tensors]``, bit for bit, with
-    the tensors that share a device and a block size (and have at most
-    16384 blocks) quantized by one launch per 8 (aq_quantize_grouped): the
-    small weights of a layer then share the GPU instead of each filling one
-    round of it, and the whole list costs one host sync."""
+    the tensors that share a device, a block size, a row length and a code
+    layout (and have at most 16384 blocks) quantized by one launch per run
+    of up to 8 (aq_quantize_grouped, at most 2^28 elements a run): the small
+    weights of a layer then share the GPU instead of each filling one round
+    of it, and each run costs one host sync.  Tensors with more blocks are
+    quantized one at a time, each completed before the next is prepared."""
     fmt = _format_id(code_format)
     out = [None] * len(tensors)
-    preps = {}
+    groups = {}
     for i, t in enumerate(tensors):
         if not isinstance(t, torch.Tensor) or t.dtype != torch.float16 or t.numel() == 0:
             out[i] = quantize_tensor(t, block_size, z_threshold, code_format=code_format)
             continue
         G = _resolve_block(block_size, t.shape)
-        p = _quantize_prepare(t, G, z_threshold, code_format, fmt)
-        preps[i] = p
+        if (t.numel() + G - 1) // G > _QUANT_GROUP_MAX_BLOCKS:
+            out[i] = quantize_tensor(t, block_size, z_threshold, code_format=code_format)
+            continue
+        layout = "tiled" if (fmt == _lib.FMT_E4M3 and tiled_eligible(t.shape, G)) else "flat"
+        key = (_lib.compute_device(t.device), G, _rows_cols(t.shape)[1], layout)
+        groups.setdefault(key, []).append(i)
+    runs = []
+    for idx in groups.values():
+        run, elems = [], 0
+        for i in idx:
+            n = tensors[i].numel()
+            if run and (len(run) == _QUANT_GROUP_MAX or elems + n > _QUANT_GROUP_MAX_ELEMS):
+                runs.append(run)
+                run, elems = [], 0
+            run.append(i)
+            elems += n
+        if run:
+            runs.append(run)
     L = _lib.load()
-    groups = {}
-    for i, p in preps.items():
-        if p["nblocks"] <= _QUANT_GROUP_MAX_BLOCKS:
-            groups.setdefault((p["dev"], p["G"], p["K"], p["layout"]), []).append(i)
-        else:
-            _lib.check(L.aq_quantize(*p["args"], p["stream"]), "aq_quantize")
     arr = _lib.ptr_array
-    for (dev, G, K, layout), idx in groups.items():
-        for c in range(0, len(idx), _QUANT_GROUP_MAX):
-            ps = [preps[i] for i in idx[c:c + _QUANT_GROUP_MAX]]
-            a0 = ps[0]["args"]
-            _lib.check(L.aq_quantize_grouped(
-                len(ps), arr([p["args"][0] for p in ps]), arr([p["numel"] for p in ps], ctypes.c_int64), G, a0[3],
-                fmt, K, a0[6], arr([p["args"][7] for p in ps]), arr([p["args"][8] for p in ps]),
-                arr([p["args"][9] for p in ps]), arr([p["args"][10] for p in ps]),
-                arr([p["ws_bytes"] for p in ps], ctypes.c_int64), ps[0]["stream"]), "aq_quantize_grouped")
-    if preps:
-        # the one host sync: every tensor's outlier count
-        counts = torch.stack([p["block_off"][p["nblocks"]].to(preps[next(iter(preps))]["dev"])
-                              for p in preps.values()]).tolist()
-        for (i, p), nnz in zip(preps.items(), counts):
+    for run in runs:
+        ps = []
+        for i in run:
+            t = tensors[i]
+            ps.append(_quantize_prepare(t, _resolve_block(block_size, t.shape), z_threshold, code_format, fmt))
+        a0 = ps[0]["args"]
+        _lib.check(L.aq_quantize_grouped(
+            len(ps), arr([p["args"][0] for p in ps]), arr([p["numel"] for p in ps], ctypes.c_int64), ps[0]["G"],
+            a0[3], fmt, ps[0]["K"], a0[6], arr([p["args"][7] for p in ps]), arr([p["args"][8] for p in ps]),
+            arr([p["args"][9] for p in ps]), arr([p["args"][10] for p in ps]),
+            arr([p["ws_bytes"] for p in ps], ctypes.c_int64), ps[0]["stream"]), "aq_quantize_grouped")
+        # the run's one host sync: every member's outlier count
+        counts = torch.stack([p["block_off"][p["nblocks"]] for p in ps]).tolist()
+        for i, p, nnz in zip(run, ps, counts):
             out[i] = _quantize_complete(p, int(nnz))
     return out
 

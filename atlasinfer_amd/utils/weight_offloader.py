@@ -46,27 +46,10 @@ from accelerate.hooks import AlignDevicesHook
 
 from ..quant import adaptive_quantizer as _aq
 from ..quant.adaptive_quantizer import QuantizedTensor
+from .helpers import map_structure  # noqa: F401  (re-exported, as the reference's module does)
 
 _QT_TENSOR_FIELDS = ("fp8_data", "fp16_outliers", "outlier_indices", "scale_factors", "outlier_row_ptr",
                      "outlier_cols", "outlier_tile_ptr", "outlier_tile_ent")
-
-
-def map_structure(func, obj: Any):
-    """``func`` applied to every tensor (and QuantizedTensor) in nested
-    dicts, lists and tuples; other objects are returned as they are
-    (reference helpers.py:9-51).  A QuantizedTensor is handed to ``func``
-    whole."""
-    if isinstance(obj, QuantizedTensor) or type(obj).__name__ == "QuantizedTensor":
-        return func(obj)
-    if isinstance(obj, dict):
-        return {k: map_structure(func, v) for k, v in obj.items()}
-    if isinstance(obj, (list, tuple)):
-        if hasattr(obj, "_fields"):
-            return type(obj)(*[map_structure(func, o) for o in obj])
-        return type(obj)(map_structure(func, o) for o in obj)
-    if isinstance(obj, torch.Tensor):
-        return func(obj)
-    return obj
 
 
 def _clear_specific_dequant_cache(obj_id: int) -> None:

@@ -60,3 +60,24 @@ def test_unsupported_model_type():
     cfg = transformers.GPT2Config(n_layer=1, n_embd=64, n_head=2, vocab_size=64)
     with pytest.raises(NotImplementedError):
         GraphDecoder(transformers.GPT2LMHeadModel(cfg).eval(), batch=1, max_len=8)
+
+
+def test_norm_folds_only_fp16_norms():
+    """The batch-1 GEMV prologue reads the norm's weight (and LayerNorm's
+    bias) as fp16: a norm kept in fp32 or bf16 inside an fp16 model must not
+    be folded (nor take aq_decode_norm), whatever its class."""
+    for kind in ("opt", "llama"):
+        m = _model(kind).half()
+        gd = GraphDecoder(m, batch=1, max_len=16, graph=False)
+        layer = gd.layers[0]
+        norm = layer.self_attn_layer_norm if kind == "opt" else layer.input_layernorm
+        assert gd._norm_folds(norm)
+        for dt in (torch.float32, torch.bfloat16):
+            norm.to(dt)
+            assert not gd._norm_folds(norm), (kind, dt)
+        norm.half()
+        if kind == "opt":
+            norm.bias.data = norm.bias.data.float()  # weight fp16, bias not
+            assert not gd._norm_folds(norm)
+            norm.bias = None
+            assert not gd._norm_folds(norm)

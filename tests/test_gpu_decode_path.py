@@ -97,3 +97,37 @@ def test_inputs_needing_gradients_take_the_reference_path():
     assert bg.grad is not None and torch.all(bg.grad == 4)
     with torch.no_grad():
         assert not ql(x).requires_grad
+
+
+def test_block_lists_built_only_for_calls_that_use_them():
+    """A weight without stored block lists (int8, flat layout) gets them
+    only when a call has LISTS_MIN_M rows or more: calls with fewer rows
+    (decode at batch 1) build nothing, and so make no host sync; the
+    arguments prepared before the lists existed are replaced once they do,
+    and every call keeps the stateless call's bits.  The same holds for a
+    sibling group's launch."""
+    N, K = 256, 1024
+    q = _q(7, N, K, "int8", 128)
+    assert q.outlier_tile_ptr is None
+    ql = AW.QuantizedLinear(q, None)
+    x1 = torch.randn(1, K, device=DEV).half()
+    x8 = torch.randn(8, K, device=DEV).half()
+    for _ in range(3):
+        assert torch.equal(ql(x1), AW.qlinear(x1, q, None))
+    assert ql._tiles is None and ql._prep is not None and ql._prep[8] is None
+    y8 = ql(x8)
+    assert ql._tiles is not None and ql._prep[8] is not None
+    assert torch.equal(y8, AW.qlinear(x8, q, None))
+    assert torch.equal(ql(x8), y8)  # fast path with the lists
+    assert torch.equal(ql(x1), AW.qlinear(x1, q, None))
+
+    qa, qb = _q(8, N, K, "int8", 128), _q(9, N, K, "int8", 128)
+    la, lb = AW.QuantizedLinear(qa, None), AW.QuantizedLinear(qb, None)
+    g = AW.SiblingGroup([la, lb])
+    la._group = lb._group = g
+    ya = la(x1)
+    assert la._tiles is None and lb._tiles is None
+    assert torch.equal(ya, AW.qlinear(x1, qa, None)) and torch.equal(lb(x1), AW.qlinear(x1, qb, None))
+    ya8 = la(x8)
+    assert la._tiles is not None and lb._tiles is not None
+    assert torch.equal(ya8, AW.qlinear(x8, qa, None)) and torch.equal(lb(x8), AW.qlinear(x8, qb, None))

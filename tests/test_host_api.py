@@ -104,3 +104,40 @@ def test_device_int_reads_once_and_acts_as_int():
     assert (ctypes.c_int64 * 1)(DeviceInt(torch.tensor(9)))[0] == 9
     assert int(copy.deepcopy(DeviceInt(torch.tensor(5)))) == 5
     assert int(pickle.loads(pickle.dumps(DeviceInt(torch.tensor(6))))) == 6
+    # a stored count of 0 is falsy, like the int (a tensor object is always truthy)
+    assert not DeviceInt(torch.tensor(0)) and bool(DeviceInt(torch.tensor(2)))
+    assert DeviceInt(torch.tensor(3)) != 4 and not DeviceInt(torch.tensor(3)) != 3
+    assert DeviceInt(torch.tensor(3)) * 2 == 6 and 2 * DeviceInt(torch.tensor(3)) == 6
+
+
+def test_dequant_cache_never_serves_another_objects_weights():
+    """The dequant cache is keyed by id(QuantizedTensor), as in the
+    reference (adaptive_quantizer.py:153-171,248-249), but an id is only a
+    hit for the very object it was stored for: (a) each entry keeps its
+    QuantizedTensor alive, so while it exists the id cannot be handed to a
+    new object; (b) an entry found under an object's id but stored for
+    another object is recomputed, not returned."""
+    import gc
+
+    def empty_qt(cols):
+        return AQ.quantize_tensor(torch.empty(0, cols, dtype=torch.float16))
+
+    AQ.clear_dequantized_cache()
+    q = empty_qt(4)
+    w = AQ.dequantize_tensor(q, torch.device("cpu"))
+    assert AQ.dequantize_tensor(q, torch.device("cpu")) is w  # memoised by identity
+    qid = id(q)
+    del q
+    gc.collect()
+    # still alive in its cache entry, so id(q) stays taken
+    assert id(AQ._dequantized_weights_cache[qid][0]) == qid
+    AQ.clear_dequantized_cache(qid)
+    assert qid not in AQ._dequantized_weights_cache
+    # a stale entry under a live object's id (what id reuse would produce)
+    q2 = empty_qt(8)
+    impostor = torch.full((0, 4), 1.0, dtype=torch.float16)
+    AQ._dequantized_weights_cache[id(q2)] = (empty_qt(4), impostor)
+    out = AQ.dequantize_tensor(q2, torch.device("cpu"))
+    assert out is not impostor and out.shape == (0, 8)
+    assert AQ._dequantized_weights_cache[id(q2)][0] is q2
+    AQ.clear_dequantized_cache()

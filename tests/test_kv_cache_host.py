@@ -88,6 +88,39 @@ def test_append_grows_and_equals_concatenation():
     assert m.seq_length(0) == 100 and torch.equal(m.get_kv(0)[0], torch.cat(ks, 2)[:, :, :100])
 
 
+def test_crop_follows_hf_dynamic_layer():
+    """KVCacheLayer.crop(n) keeps the first n positions and crop(-n) drops n
+    from the end, as HF's DynamicLayer.crop; crop(0) empties the layer and a
+    length at or past the history changes nothing."""
+    m = _mgr(ram_kib=4096)
+    k, v = _kv(3, 20)
+    layer = UMM.KVCacheLayer(m, 0)
+    layer.update(k, v)
+    layer.crop(50)
+    assert layer.get_seq_length() == 20
+    layer.crop(-5)
+    assert layer.get_seq_length() == 15 and torch.equal(m.get_kv(0)[0], k[:, :, :15])
+    layer.crop(12)
+    assert layer.get_seq_length() == 12 and torch.equal(m.get_kv(0)[1], v[:, :, :12])
+    layer.crop(0)
+    assert layer.get_seq_length() == 0
+
+
+def test_failed_value_write_leaves_no_key_file(tmp_path):
+    """A layer demoted to disk whose keys fit the disk limit but whose
+    values do not: the keys' file and its bytes are taken back out, so the
+    store holds nothing that no entry owns."""
+    # a layer's keys and values are 1 x 2 x 16 x 8 x 2 B = 512 B each: the
+    # host tier holds one layer, the disk limit (768 B) its keys only
+    m = _mgr(ram_kib=1, disk=str(tmp_path / "kv"), disk_kib=0.75)
+    for i in range(2):
+        m.put_kv(i, *_kv(i, 16))
+    st = m.disk_interface
+    assert st.used == 0 and not st.sizes and not list((tmp_path / "kv").iterdir())
+    assert 0 not in m.disk_entries
+    m.close()
+
+
 def _tiny(kind, seed):
     transformers = pytest.importorskip("transformers")
     torch.manual_seed(seed)

@@ -17,7 +17,13 @@ throughput, the quantize-kernel throughput, hipBLASLt fp16 F.linear on the
 dequantized weights for comparison, the roofline of the GEMV and the
 reference's CPU path timed on this host.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--sweep]
+The default run also carries config 2's sweep over M (layer and per launch),
+configs 1 and 3 (OPT-1.3b and Mistral-7B with their Linears swapped: graph
+decode tok/s, prefill TFLOP/s, beside fp16) and config 4 (quantize of an 8 B
+Llama-3-shaped weight set, Gemma-2B shapes at M = 1 and 2048).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-sweep] [--models opt,mistral|none]
+                    [--no-config4] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -563,14 +569,31 @@ def graph_decode_only(args, dev, log):
                       "tok_s": round(tps * args.batch, 1)}))
 
 
-def bench_models(dev, which, log):
+def prefill_s(model, ids, reps=3):
+    """Seconds of one forward over the prompt ``ids`` (best of ``reps``,
+    after a warm-up call)."""
+    with torch.no_grad():
+        model(ids)
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            model(ids)
+            torch.cuda.synchronize()
+            best = min(best, time.perf_counter() - t0)
+    return best
+
+
+def bench_models(dev, which, log, eager_generate=False):
     """BASELINE configs 1 (OPT-1.3b, every Linear quantized, 32-token prompt,
     128 greedy tokens, batch 1) and 3 (Mistral-7B, 512-token prompts, 256
     greedy tokens, batch 1/8/32; prefill TFLOP/s of the linears): random-init
     weights with planted outliers, fp16 model against the same model with its
     Linears swapped by apply_atlas_quantization_to_model (per-channel E4M3).
-    HF generate runs eagerly: tok/s there includes the framework's per-token
-    Python work, identical in both columns."""
+    Decode through GraphDecoder (one HIP graph per token); OPT also through
+    HF's eager generate, and Mistral with ``eager_generate``: tok/s there
+    includes the framework's per-token Python work, identical in both
+    columns."""
     from atlasinfer_amd.integration.model_modifier import apply_atlas_quantization_to_model
     out = {}
     gen = torch.Generator(device=dev).manual_seed(7)
@@ -600,6 +623,7 @@ def bench_models(dev, which, log):
     if "mistral" in which:
         model, cfg = config_model("mistral", dev, gen)
         res = {}
+        ids_b = {B: torch.randint(0, cfg.vocab_size, (B, 512), generator=gen, device=dev) for B in (1, 8, 32)}
         for phase in ("fp16", "quantized"):
             if phase == "quantized":
                 t0 = time.perf_counter()
@@ -608,20 +632,103 @@ def bench_models(dev, which, log):
                 res["quantize_s"] = round(time.perf_counter() - t0, 2)
                 res["linears_quantized"] = rep
                 res["failed"] = fail
-            for B in (1, 8, 32):
-                ids = torch.randint(0, cfg.vocab_size, (B, 512), generator=gen, device=dev)
-                tps, t_pre = generate_tokps(model, ids, 256)
+            for B, ids in ids_b.items():
+                t_pre = prefill_s(model, ids)
                 flops = linear_flops(model, B * 512) if phase == "fp16" else res[f"fp16_b{B}_prefill_flops"]
-                res[f"{phase}_b{B}_decode_tok_s"] = round(tps * B, 1)
-                g_tps, _ = graph_decode_tokps(model, ids, 256)
-                res[f"{phase}_b{B}_graph_decode_tok_s"] = round(g_tps * B, 1)
-                res[f"{phase}_b{B}_prefill_tflops"] = round(flops / t_pre / 1e12, 1)
                 if phase == "fp16":
                     res[f"fp16_b{B}_prefill_flops"] = flops
-                log(f"Mistral-7B {phase} batch {B}: {tps * B:.1f} tok/s decode, prefill {flops / t_pre / 1e12:.1f} TFLOP/s")
+                res[f"{phase}_b{B}_prefill_tflops"] = round(flops / t_pre / 1e12, 1)
+                res[f"{phase}_b{B}_prefill_ms"] = round(1e3 * t_pre, 2)
+                g_tps, _ = graph_decode_tokps(model, ids, 256)
+                res[f"{phase}_b{B}_graph_decode_tok_s"] = round(g_tps * B, 1)
+                if eager_generate:
+                    tps, _ = generate_tokps(model, ids, 256)
+                    res[f"{phase}_b{B}_decode_tok_s"] = round(tps * B, 1)
+                log(f"Mistral-7B {phase} batch {B}: graph decode {g_tps * B:.1f} tok/s, prefill "
+                    f"{flops / t_pre / 1e12:.1f} TFLOP/s ({1e3 * t_pre:.1f} ms)")
         out["mistral7b"] = {k: v for k, v in res.items() if "prefill_flops" not in k}
+        out["mistral7b"]["note"] = ("512-token random prompts, 256 new tokens (GraphDecoder: one HIP graph replay "
+                                    "per token, greedy); prefill = one forward of the prompt through HF (all "
+                                    "linears incl. the fp16 lm_head counted), best of 3")
         del model
         torch.cuda.empty_cache()
+    return out
+
+
+def bench_sweep(layers, gen, dev, log, qlinear, qlinear_grouped, Ms=(1, 4, 8, 16, 64, 512, 2048)):
+    """BASELINE config 2's sweep over M: per M, a Llama-3-8B layer in the
+    decode/prefill launch pattern (q/k/v grouped, o, gate/up grouped, down)
+    and each of those launches alone.  M <= 64 (the GEMV regime): every
+    rotated layer (past the MALL) in one HIP graph, HIP events around the
+    replays, GB/s of the algorithmic bytes; M >= 512 (the GEMM): eager calls
+    on layer 1, HIP events, TFLOP/s."""
+    out = {}
+    Ks = {K for _, _, K in LLAMA_LINEARS}
+    pattern = [("qkv", ["q_proj", "k_proj", "v_proj"]), ("o", ["o_proj"]), ("gate_up", ["gate_proj", "up_proj"]),
+               ("down", ["down_proj"])]
+    kof = {name: K for name, _, K in LLAMA_LINEARS}
+
+    def launch(layer, names, xm):
+        qs = [layer[n] for n in names]
+        x = xm[kof[names[0]]]
+        return qlinear_grouped(x, qs) if len(qs) > 1 else qlinear(x, qs[0], None)
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / reps
+
+    def graph_of(fn):
+        fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        return g
+
+    for M in Ms:
+        xm = {K: gen_x(M, K, gen, dev) for K in Ks}
+        res = {}
+        if M <= 64:
+            def all_layers():
+                for layer in layers:
+                    for _, names in pattern:
+                        launch(layer, names, xm)
+            g = graph_of(all_layers)
+            t_layer = timed(g.replay, 20) / len(layers)
+            nb = sum(gemv_bytes(layers[i][n], M) for i in range(len(layers)) for n, _, _ in LLAMA_LINEARS)
+            nb //= len(layers)
+            res["layer"] = {"us": round(1e6 * t_layer, 2), "GBps": round(nb / t_layer / 1e9, 1),
+                            "frac_hbm_peak": round(nb / t_layer / 1e9 / HBM_PEAK_GBS, 4)}
+            for key, names in pattern:
+                g = graph_of(lambda names=names: [launch(layer, names, xm) for layer in layers])
+                t = timed(g.replay, 20) / len(layers)
+                b = sum(gemv_bytes(layers[i][n], M) for i in range(len(layers)) for n in names) // len(layers)
+                res[key] = {"us": round(1e6 * t, 2), "GBps": round(b / t / 1e9, 1),
+                            "frac_hbm_peak": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
+            del g
+        else:
+            layer = layers[1]
+            tot = 0.0
+            for key, names in pattern:
+                t = timed(lambda names=names: launch(layer, names, xm), 10)
+                f = sum(2 * M * layer[n].original_shape[0] * kof[n] for n in names)
+                tot += t
+                res[key] = {"us": round(1e6 * t, 1), "TFLOPs": round(f / t / 1e12, 1),
+                            "frac_fp16_peak": round(f / t / 1e12 / FP16_PEAK_TFLOPS, 4)}
+            f = sum(2 * M * N * K for _, N, K in LLAMA_LINEARS)
+            res["layer"] = {"us": round(1e6 * tot, 1), "TFLOPs": round(f / tot / 1e12, 1),
+                            "frac_fp16_peak": round(f / tot / 1e12 / FP16_PEAK_TFLOPS, 4)}
+        out[str(M)] = res
+        log(f"sweep M={M}: {res}")
+        del xm
     return out
 
 
@@ -701,21 +808,100 @@ def bench_config4(dev, gen, log, qlinear):
     return {"quantize_8b": part1, "gemma2b": part2}
 
 
+OPT_LAYER = [("q_proj", 2048, 2048), ("k_proj", 2048, 2048), ("v_proj", 2048, 2048), ("out_proj", 2048, 2048),
+             ("fc1", 8192, 2048), ("fc2", 2048, 8192)]  # (name, N = out, K = in)
+
+
+def config0_cpu(args, dev, log):
+    """BASELINE config 0 on this host's cores, in full: the six linears of
+    one OPT-1.3b layer (W ~ N(0, 0.02) fp16, round(0.001 N K) positions from
+    randperm replaced by +-U(8, 20) * 0.02; bias N(0, 0.02); x ~ N(0, 1) at
+    M = 1 and 128), through the reference's CPU path restated op for op
+    (oracle/ref_loop.py): the per-block quantize loop (adaptive_quantizer.py:
+    102-133, block 128, the reference's default) and dequantize loop
+    (:188-239) over every block, a cold forward (the dequantize loop, then
+    F.linear, atlas_wrappers.py:56,67) and a warm one (F.linear on the cached
+    weight).  Each linear's loop outputs are checked bit for bit against
+    this build's HIP quantizer (int8 format, the reference's layout) and its
+    dequantize, and its warm outputs against the HIP quantized linear."""
+    from oracle import ref_loop
+    from atlasinfer_amd.quant import adaptive_quantizer as AQ
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(0)
+    res, tot = {}, {"quantize_s": 0.0, "dequantize_s": 0.0, "blocks": 0, "params": 0}
+    for name, N, K in OPT_LAYER:
+        w = torch.randn(N * K, generator=g) * 0.02
+        k = int(round(0.001 * N * K))
+        pos = torch.randperm(N * K, generator=g)[:k]
+        sign = torch.where(torch.rand(k, generator=g) < 0.5, -1.0, 1.0)
+        w[pos] = sign * (torch.rand(k, generator=g) * 12 + 8) * 0.02
+        w = w.view(N, K).half()
+        b = (torch.randn(N, generator=g) * 0.02).half()
+        t0 = time.perf_counter()
+        codes, outs, idx, scales, nb = ref_loop.quantize_loop(w, 128, 3.0)
+        tq = time.perf_counter() - t0
+        log(f"config 0 {name} [{N}, {K}]: quantize loop {tq:.1f} s over {nb} blocks")
+        t0 = time.perf_counter()
+        deq, _ = ref_loop.dequantize_loop(codes, outs, idx, scales, N * K, 128)
+        td = time.perf_counter() - t0
+        w_deq = deq[:N * K].view(N, K)
+        log(f"config 0 {name}: dequantize loop {td:.1f} s ({idx.numel()} outliers)")
+        q = AQ.quantize_tensor(w.to(dev), block_size=128, code_format="int8")
+        same = (torch.equal(q.fp8_data.cpu(), codes) and torch.equal(q.outlier_indices.cpu(), idx)
+                and torch.equal(q.fp16_outliers.cpu().view(torch.int16), outs.view(torch.int16))
+                and torch.equal(q.scale_factors.cpu().view(torch.int16), scales.view(torch.int16))
+                and torch.equal(AQ.dequantize_tensor(q, dev).cpu().view(torch.int16), w_deq.view(torch.int16)))
+        AQ.clear_dequantized_cache()
+        if not same:
+            raise SystemExit(f"config 0 {name}: the reference loop and the HIP quantizer disagree")
+        row = {"N": N, "K": K, "blocks": nb, "nnz": int(idx.numel()), "quantize_loop_s": round(tq, 2),
+               "dequantize_loop_s": round(td, 2), "hip_int8_bit_exact": same}
+        for M in (1, 128):
+            x = torch.randn(M, K, generator=g).half()
+            ref_loop.forward_warm(x, w_deq, b)
+            reps = 0
+            t0 = time.perf_counter()
+            while reps < 3 or time.perf_counter() - t0 < 0.5:
+                y = ref_loop.forward_warm(x, w_deq, b)
+                reps += 1
+            tw = (time.perf_counter() - t0) / reps
+            yg = torch.nn.functional.linear(x.to(dev), AQ.dequantize_tensor(q, dev), b.to(dev)).cpu()
+            AQ.clear_dequantized_cache()
+            row[f"m{M}_warm_ms"] = round(1e3 * tw, 3)
+            row[f"m{M}_cold_ms"] = round(1e3 * (td + tw), 1)
+            row[f"m{M}_max_abs_vs_gpu_flinear"] = float((y.float() - yg.float()).abs().max())
+        res[name] = row
+        tot["quantize_s"] += tq
+        tot["dequantize_s"] += td
+        tot["blocks"] += nb
+        tot["params"] += N * K
+    tot = {k: round(v, 2) if isinstance(v, float) else v for k, v in tot.items()}
+    print(json.dumps({"config0_cpu": True, "cores": torch.get_num_threads(), "layer": tot, "linears": res,
+                      "note": "reference CPU path restated op for op (oracle/ref_loop.py), block 128, every block "
+                              "timed (no extrapolation); cold forward = dequantize loop + F.linear"}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--sweep", action="store_true", help="also time M in {4,16,32,64,512} per shape")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip config 2's sweep over M in {1,4,8,16,64,512,2048} (layer and per launch)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
-    ap.add_argument("--models", default="opt", help="comma list of opt,mistral (or none): BASELINE configs 1 / 3 "
-                                                     "(HF generate on random-init models; opt takes about half a "
-                                                     "minute, mistral a few minutes)")
-    ap.add_argument("--config4", action="store_true",
-                    help="also run BASELINE config 4: quantize kernel over a full 8B Llama-3-shaped weight set "
-                         "(Student-t(3), 1%% outliers) and the Gemma-2B lm_head / FFN at M = 1 and 2048 "
-                         "(a minute or two)")
+    ap.add_argument("--models", default="opt,mistral",
+                    help="comma list of opt,mistral (or none): BASELINE configs 1 / 3 on random-init models "
+                         "(opt: HF generate and graph decode, about half a minute; mistral: graph decode at "
+                         "batch 1/8/32 and prefill, fp16 and quantized, about a minute)")
+    ap.add_argument("--eager-generate", action="store_true",
+                    help="config 3 also through HF's eager generate (256 tokens at batch 1/8/32; minutes)")
+    ap.add_argument("--no-config4", action="store_true",
+                    help="skip BASELINE config 4: quantize kernel over a full 8B Llama-3-shaped weight set "
+                         "(Student-t(3), 1%% outliers) and the Gemma-2B lm_head / FFN at M = 1 and 2048")
+    ap.add_argument("--config0-cpu", action="store_true",
+                    help="only BASELINE config 0 on the host: the reference's per-block quantize and dequantize "
+                         "loops over a whole OPT-1.3b layer, cold and warm forward at M = 1 and 128 (minutes)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant kernel (gate+up grouped GEMV, 4 rotated layers) and a 512 MiB "
                          "calibration copy, for counter runs")
@@ -758,6 +944,9 @@ def main():
         return
     if args.graph_decode:
         graph_decode_only(args, dev, log)
+        return
+    if args.config0_cpu:
+        config0_cpu(args, dev, log)
         return
 
     # ---- weights: 4 layers x 7 linears, quantized on the GPU (also timed)
@@ -892,25 +1081,15 @@ def main():
     log(f"M=2048 GEMM: {gemm_tflops:.1f} TFLOP/s in 7 launches, {grouped_tflops:.1f} in 4 grouped launches "
         f"(hipBLASLt fp16, 7 launches: {blas_tflops:.1f})")
 
-    sweep = {}
-    if args.sweep:
-        for Ms in (4, 16, 32, 64, 512):
-            xm = {K: gen_x(Ms, K, gen, dev) for K in {K for _, _, K in LLAMA_LINEARS}}
-            per = {}
-            for name, N, K in LLAMA_LINEARS:
-                qt = layers[2][name]
-                s = time_eager(lambda: qlinear(xm[K], qt, None), 20)
-                per[name] = {"us": round(s * 1e6, 2), "GB/s": round(gemv_bytes(qt, Ms) / s / 1e9, 1),
-                             "TFLOP/s": round(2 * Ms * N * K / s / 1e12, 1)}
-            sweep[str(Ms)] = per
+    sweep = None if args.no_sweep else bench_sweep(layers, gen, dev, log, qlinear, qlinear_grouped)
 
-    config4 = bench_config4(dev, gen, log, qlinear) if args.config4 else None
+    config4 = None if args.no_config4 else bench_config4(dev, gen, log, qlinear)
 
     models = None
     if args.models and args.models != "none":
         import contextlib
         with contextlib.redirect_stdout(sys.stderr):  # stdout carries only the result line
-            models = bench_models(dev, args.models.split(","), log)
+            models = bench_models(dev, args.models.split(","), log, args.eager_generate)
             models["kv_cache_update"] = bench_kv_cache(dev, log)
 
     # ---- the reference's CPU path on this host (warm F.linear, M=1)

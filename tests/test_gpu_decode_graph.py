@@ -1,9 +1,10 @@
 """GraphDecoder on the GPU with quantized models: every replay of the
 captured decode step gives bit-identical logits and tokens to the same step
-run eagerly (the eager decoder's work runs between the replays), and the
-generated tokens follow HF's own generate on the same quantized model up to
-the first near-tie of the top logits (the attention arithmetic differs: f32
-scores and softmax here, HF's SDPA there)."""
+run eagerly (the eager decoder's work runs between the replays), and,
+teacher-forced with HF's tokens, each step's logits stay within a stated
+bound of HF's own generate on the same quantized model at every step (the
+attention arithmetic differs: f32 scores and softmax here, HF's SDPA
+there)."""
 import copy
 
 import pytest
@@ -59,27 +60,46 @@ def test_graph_generate_follows_hf_generate(kind, batch):
     """Batch 1 takes the five-launch layers (norms, activation and residual
     adds inside the GEMV launches), batch 2 the nine-launch ones, batch 8
     the seven-launch ones (SwiGLU / ReLU and residual adds inside the GEMV
-    launches, the norms apart)."""
+    launches, the norms apart).
+
+    Teacher-forced against HF's generate on the same quantized model: each
+    step is fed HF's token, and its logits must lie within a bound of HF's
+    at every one of the n steps (no step is skipped after a near-tie).  The
+    bound covers the attention arithmetic, which differs (f32 scores and
+    softmax weights here, HF's SDPA in fp16 there): max |d logits| <=
+    2e-2 * max |HF logits| per row and step.  Free-running, the decoder's own
+    greedy tokens then match HF's wherever HF's two best logits are not
+    within that bound of each other."""
     m = _model(kind, 2)
-    ids = torch.randint(0, 512, (batch, 12), device=DEV)
-    n = 16
+    S, n = 12, 16
+    ids = torch.randint(0, 512, (batch, S), device=DEV)
     with torch.no_grad():
         ref = m.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=n, do_sample=False,
                          return_dict_in_generate=True, output_logits=True)
     g = GraphDecoder(m, batch=batch, max_len=64)
     assert g.b1 == (batch == 1) and g.bm == (batch == 8)
+    first = g.prefill(ids)
+    assert torch.equal(first, ref.sequences[:, S])  # prefill is HF's own forward
+    worst = 0.0
+    for t in range(1, n):
+        g.tok.copy_(ref.sequences[:, S + t - 1])  # HF's token goes in
+        lg = g.step().float()
+        hf = ref.logits[t].float()
+        err = ((lg - hf).abs().amax(-1) / hf.abs().amax(-1)).max().item()
+        worst = max(worst, err)
+        assert err <= 2e-2, (t, err)
+    print(f"{kind} batch {batch}: largest per-step logit difference {worst:.2e} of max |logit|")
     out = g.generate(ids, n)
     assert out.shape == ref.sequences.shape
     for t in range(n):
-        a, b = out[:, 12 + t], ref.sequences[:, 12 + t]
-        lg = ref.logits[t].float()
-        top2 = lg.topk(2, dim=-1).values
-        for row in range(batch):
-            if a[row] != b[row]:
-                # only a near-tie of HF's two best logits may flip the choice
-                gap = (top2[row, 0] - top2[row, 1]).item()
-                assert gap < 2e-2 * top2[row, 0].abs().item() + 1e-2, (t, row, gap)
-                return
+        hf = ref.logits[t].float()
+        top2 = hf.topk(2, dim=-1).values
+        same_prefix = torch.all(out[:, S:S + t] == ref.sequences[:, S:S + t], dim=1)
+        clear = (top2[:, 0] - top2[:, 1]) > 4e-2 * hf.abs().amax(-1)
+        # a row whose earlier tokens all agree and whose best logit is clear
+        # of the second must pick HF's token
+        must = same_prefix & clear
+        assert torch.equal(out[must, S + t], ref.sequences[must, S + t]), t
 
 
 def _attention_call(lib, q, kn, vn, K, V, pos, ws, scale, q_scale=1.0, cos=None, sin=None):

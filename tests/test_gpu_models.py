@@ -1,4 +1,4 @@
-"""BASELINE configurations 1 and 3 end to end on the GPU: full-size
+"""BASELINE configurations 1 and 3 (and a Gemma model) end to end on the GPU:
 random-init HF models with every Linear swapped by
 apply_atlas_quantization_to_model (integration/model_modifier.py:95-143),
 checked against the oracle.
@@ -19,7 +19,10 @@ Mistral-7B (32 layers, hidden 4096, 32 / 8 heads, FFN 14336, vocab 32000,
 RoPE 1e6), 512-token prompts at batch 1, 8 and 32; weights checked against
 the oracle on row slices (one whole tile row of 16 plus 3 single rows per
 weight; the full-weight checks of these shapes are in test_gpu_configs.py),
-reference weights from the torch restatement of dequantize_tensor.
+reference weights from the torch restatement of dequantize_tensor; greedy
+generate runs the config's 256 new tokens at batch 1 and 8 at batch 8 and
+32.  Gemma: Gemma-2B's shapes at two layers (the reference's Gemma pattern
+set), every Linear swapped and checked against the oracle in full.
 Weights: the HF init (N(0, 0.02)) with 0.1 % of each Linear's entries
 replaced by +-U(8, 20) * 0.02, as in BASELINE config 0.
 """
@@ -208,5 +211,50 @@ def test_config3_mistral_7b(mistral, B):
         assert checks.n == 2 * rep
         assert_logits_close(out.logits, model, w_refs, f"Mistral-7B batch {B}", input_ids=ids)
         del out
-        gen = model.generate(ids, max_new_tokens=8, min_new_tokens=8, do_sample=False, pad_token_id=0)
-    assert gen.shape == (B, 520)
+        # the config's whole 256 new tokens at batch 1; 8 at the larger batches
+        n = 256 if B == 1 else 8
+        gen = model.generate(ids, max_new_tokens=n, min_new_tokens=n, do_sample=False, pad_token_id=0)
+    assert gen.shape == (B, 512 + n)
+    assert torch.equal(gen[:, :512], ids)
+
+
+def test_gemma_2b_architecture_swap_generate():
+    """A Gemma model (the reference's fourth pattern set,
+    model_modifier.py:43-48): Gemma-2B's layer shapes (hidden 2048, 8 query
+    heads, one key/value head, head_dim 256, GELU-tanh MLP of 16384, vocab
+    256000, lm_head tied to the embedding) at two layers.  Every Linear is
+    swapped, the tied lm_head [256000, 2048] included; each weight is
+    checked against the oracle in full, each layer's output on the prefill
+    and on a decode step by the hooks, the prompt's logits against the
+    reference's forward, and greedy generate runs.  The swapped model's
+    weight bytes (estimate_quantized_model_vram, reference helpers.py:54-82)
+    are the QuantizedTensors' components plus the embedding and the norms."""
+    transformers = pytest.importorskip("transformers")
+    from atlasinfer_core.utils.helpers import estimate_quantized_model_vram
+    cfg = transformers.GemmaConfig(num_hidden_layers=2, hidden_size=2048, num_attention_heads=8,
+                                   num_key_value_heads=1, head_dim=256, intermediate_size=16384, vocab_size=256000,
+                                   hidden_activation="gelu_pytorch_tanh", max_position_embeddings=2048)
+    torch.manual_seed(0)
+    with torch.device(DEV):
+        model = transformers.GemmaForCausalLM(cfg).half().eval()
+    assert model.lm_head.weight is model.model.embed_tokens.weight
+    plant_outliers(model, 4)
+    rep, w_refs = swap(model, "gemma", [], full_oracle=True)
+    assert rep == 2 * 7 + 1
+    assert type(model.lm_head).__name__ == "QuantizedLinear"
+    qbytes = sum(m.quantized_weights.memory_footprint(include_overhead=False)
+                 for m in model.modules() if type(m).__name__ == "QuantizedLinear")
+    plain = sum(p.numel() * 2 for n, p in model.named_parameters())  # embedding + norms, fp16
+    assert estimate_quantized_model_vram(model) == qbytes + plain
+    g = torch.Generator(device=DEV).manual_seed(5)
+    ids = torch.randint(0, cfg.vocab_size, (2, 48), generator=g, device=DEV)
+    with torch.no_grad():
+        checks = LayerChecks(model, w_refs)
+        out = model(input_ids=ids, use_cache=True)  # prefill: M = 96
+        nxt = out.logits[:, -1:].argmax(-1)
+        model(input_ids=nxt, past_key_values=out.past_key_values, use_cache=True)  # decode step: M = 2
+        checks.remove()
+        assert checks.n == 2 * rep
+        assert_logits_close(out.logits, model, w_refs, "Gemma-2B shapes, 2 layers", input_ids=ids)
+        gen = model.generate(ids, max_new_tokens=32, min_new_tokens=32, do_sample=False, pad_token_id=0)
+    assert gen.shape == (2, 80) and torch.equal(gen[:, :48], ids)

@@ -168,21 +168,134 @@ __device__ __forceinline__ int lower_bound_i32(const int32_t* a, int lo, int hi,
 // Position of row r (0..15), column k (0..63) in a block's entry: r << 6 | k.
 __device__ __forceinline__ uint32_t block_position(int r, int k) { return ((uint32_t)r << 6) | (uint32_t)k; }
 
-// One thread per block of 16 rows x 64 columns (tile row rb, chunk c).
-// Entries are ordered by block, then row, then column, so a block starts
-// after every outlier of the rows above it plus, in each of its own rows,
-// the outliers left of column 64c.
+// One workgroup per tile row (16 rows): a stable counting sort of the tile
+// row's CSR entries (already in row, column order) by 64-column chunk, which
+// is the block lists' order (block, then row, then column).  Per (row,
+// chunk) counts in LDS (atomic adds), turned into each chunk's block total
+// and per-row offsets within the block; an exclusive scan of the block
+// totals gives the block starts; an entry's place is its block's start, the
+// entries of its chunk in the rows above, and its rank among its own row's
+// entries of that chunk (a binary search of the row's sorted columns).  The
+// workgroup also raises *tile_max to its largest block.  Workgroup nrb
+// writes the list's end and the 64 padding entries.  LDS: 17 * nch ints.
+constexpr int kTileRowsMaxChunks = 1024;  // K <= 65536 (wider rows: outlier_tiles_kernel)
+
+__global__ __launch_bounds__(256) void outlier_tile_rows_kernel(const int32_t* row_ptr, const int32_t* cols,
+                                                                const uint16_t* vals, int nrb, int nch,
+                                                                int32_t* tile_ptr, uint32_t* tile_ent,
+                                                                int32_t* tile_max) {
+  extern __shared__ int sm[];
+  int* cnt = sm;               // [16][nch]: counts, then offsets within the block
+  int* bstart = sm + 16 * nch;  // [nch]: block totals, then block starts
+  __shared__ int part[256];
+  const int rb = blockIdx.x, t = threadIdx.x;
+  if (rb == nrb) {
+    const int end = row_ptr[nrb * 16];
+    if (t == 0) tile_ptr[(int64_t)nrb * nch] = end;
+    if (t < 64) tile_ent[end + t] = 0u;
+    return;
+  }
+  int rs[17];
+#pragma unroll
+  for (int r = 0; r <= 16; r++) rs[r] = row_ptr[rb * 16 + r];
+  const int p0 = rs[0], p1 = rs[16];
+  for (int i = t; i < 16 * nch; i += 256) cnt[i] = 0;
+  __syncthreads();
+  auto row_of = [&](int i) {
+    int r = 0;
+#pragma unroll
+    for (int k = 1; k < 16; k++) r += i >= rs[k];
+    return r;
+  };
+  for (int i = p0 + t; i < p1; i += 256) atomicAdd(&cnt[row_of(i) * nch + (cols[i] >> 6)], 1);
+  __syncthreads();
+  // per chunk: offsets of the rows within the block, and the block's total
+  int mx = 0;
+  for (int c = t; c < nch; c += 256) {
+    int run = 0;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int n = cnt[r * nch + c];
+      cnt[r * nch + c] = run;
+      run += n;
+    }
+    bstart[c] = run;
+    mx = max(mx, run);
+  }
+  // exclusive scan of the block totals: thread t takes chunks 4t..4t+3 of
+  // each run of 1024, its sum scanned across the workgroup in LDS
+  int carry = 0;
+  for (int c0 = 0; c0 < nch; c0 += 1024) {
+    __syncthreads();
+    int v[4], sum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int c = c0 + 4 * t + k;
+      v[k] = c < nch ? bstart[c] : 0;
+      sum += v[k];
+    }
+    part[t] = sum;
+    __syncthreads();
+    for (int d = 1; d < 256; d <<= 1) {
+      const int add = t >= d ? part[t - d] : 0;
+      __syncthreads();
+      part[t] += add;
+      __syncthreads();
+    }
+    int run = carry + part[t] - sum;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int c = c0 + 4 * t + k;
+      if (c < nch) {
+        bstart[c] = run;
+        tile_ptr[(int64_t)rb * nch + c] = p0 + run;
+      }
+      run += v[k];
+    }
+    carry += part[255];
+  }
+  __syncthreads();
+  for (int i = p0 + t; i < p1; i += 256) {
+    const int r = row_of(i), col = cols[i], c = col >> 6;
+    const int rank = i - lower_bound_i32(cols, rs[r], i, c * 64);
+    tile_ent[p0 + bstart[c] + cnt[r * nch + c] + rank] = ((uint32_t)vals[i] << 16) | block_position(r, col - c * 64);
+  }
+  // the largest block of the tile row
+  for (int d = 32; d >= 1; d >>= 1) mx = max(mx, __shfl_xor(mx, d));
+  if ((t & 63) == 0 && tile_max && mx > 0) atomicMax(tile_max, mx);
+}
+
+// One thread per block of 16 rows x 64 columns (tile row rb, chunk c), for
+// rows wider than outlier_tile_rows_kernel takes.  Entries are ordered by
+// block, then row, then column, so a block starts after every outlier of
+// the rows above it plus, in each of its own rows, the outliers left of
+// column 64c.
 __global__ __launch_bounds__(256) void outlier_tiles_kernel(const int32_t* row_ptr, const int32_t* cols,
                                                             const uint16_t* vals, int nrb, int nch,
-                                                            int32_t* tile_ptr, uint32_t* tile_ent) {
+                                                            int32_t* tile_ptr, uint32_t* tile_ent,
+                                                            int32_t* tile_max) {
   const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t nblk = (int64_t)nrb * nch;
   if (b > nblk) return;
   if (b == nblk) {
-    tile_ptr[b] = row_ptr[nrb * 16];
+    const int end = row_ptr[nrb * 16];
+    tile_ptr[b] = end;
+    for (int k = 0; k < 64; k++) tile_ent[end + k] = 0u;
     return;
   }
   const int rb = (int)(b / nch), c = (int)(b % nch);
+  if (c == 0 && tile_max) {
+    int mx = 0;
+    for (int cc = 0; cc < nch; cc++) {
+      int n = 0;
+      for (int r = 0; r < 16; r++) {
+        const int p0 = row_ptr[rb * 16 + r], p1 = row_ptr[rb * 16 + r + 1];
+        n += lower_bound_i32(cols, p0, p1, cc * 64 + 64) - lower_bound_i32(cols, p0, p1, cc * 64);
+      }
+      mx = max(mx, n);
+    }
+    if (mx > 0) atomicMax(tile_max, mx);
+  }
   int lo[16], hi[16];
   int pos = row_ptr[rb * 16];
 #pragma unroll
@@ -306,16 +419,21 @@ extern "C" int aq_dequantize(const void* codes, const void* scales, int64_t nume
 }
 
 extern "C" int aq_outlier_tiles(const int32_t* row_ptr, const int32_t* cols, const void* vals, int64_t N, int64_t K,
-                                int32_t* tile_ptr, uint32_t* tile_ent, void* stream) {
+                                int32_t* tile_ptr, uint32_t* tile_ent, int32_t* tile_max, void* stream) {
   AQ_CHECK_ARG(N >= 16 && N % 16 == 0 && K >= 64 && K % 64 == 0 && N < (1 << 30) && K < (1 << 30) &&
                    (N / 16) * (K / 64) < ((int64_t)1 << 31),
                "aq_outlier_tiles: N must be a multiple of 16 and K of 64 (N=%lld K=%lld)", (long long)N,
                (long long)K);
   AQ_CHECK_ARG(row_ptr && tile_ptr, "aq_outlier_tiles: null pointer argument");
   const int64_t nblk = (N / 16) * (K / 64);
-  hipLaunchKernelGGL(outlier_tiles_kernel, dim3((unsigned)aq::ceil_div(nblk + 1, 256)), dim3(256), 0,
-                     (hipStream_t)stream, row_ptr, cols, (const uint16_t*)vals, (int)(N / 16), (int)(K / 64),
-                     tile_ptr, tile_ent);
+  if (K / 64 <= kTileRowsMaxChunks)
+    hipLaunchKernelGGL(outlier_tile_rows_kernel, dim3((unsigned)(N / 16 + 1)), dim3(256),
+                       (size_t)17 * (K / 64) * sizeof(int), (hipStream_t)stream, row_ptr, cols,
+                       (const uint16_t*)vals, (int)(N / 16), (int)(K / 64), tile_ptr, tile_ent, tile_max);
+  else
+    hipLaunchKernelGGL(outlier_tiles_kernel, dim3((unsigned)aq::ceil_div(nblk + 1, 256)), dim3(256), 0,
+                       (hipStream_t)stream, row_ptr, cols, (const uint16_t*)vals, (int)(N / 16), (int)(K / 64),
+                       tile_ptr, tile_ent, tile_max);
   AQ_LAUNCH_CHECK("aq_outlier_tiles: launch");
   return AQ_OK;
 }

@@ -472,14 +472,15 @@ def build_outlier_tiles(qt: QuantizedTensor, device: torch.device, lazy_max: boo
     N, K = _rows_cols(q.original_shape)
     nnz = q.fp16_outliers.numel()
     tile_ptr = torch.empty((N // 16) * (K // 64) + 1, dtype=torch.int32, device=device)
-    tile_ent = torch.zeros(nnz + 64, dtype=torch.int32, device=device)  # 64 entries of read padding
+    tile_ent = torch.empty(nnz + 64, dtype=torch.int32, device=device)  # + 64 entries of read padding (zeroed)
+    tmax = torch.zeros(1, dtype=torch.int32, device=device)  # raised to the largest block's count
     _lib.check(L.aq_outlier_tiles(q.outlier_row_ptr.data_ptr(), _lib.ptr(q.outlier_cols), _lib.ptr(q.fp16_outliers),
-                                  N, K, tile_ptr.data_ptr(), tile_ent.data_ptr(), _lib.stream_of(device)),
+                                  N, K, tile_ptr.data_ptr(), tile_ent.data_ptr(), tmax.data_ptr(),
+                                  _lib.stream_of(device)),
                "aq_outlier_tiles")
     if not nnz:
         return tile_ptr, tile_ent, 0
-    tmax = (tile_ptr[1:] - tile_ptr[:-1]).max()
-    return tile_ptr, tile_ent, DeviceInt(tmax) if lazy_max else int(tmax.item())
+    return tile_ptr, tile_ent, DeviceInt(tmax[0]) if lazy_max else int(tmax.item())
 
 
 def outlier_tiles(qt: QuantizedTensor, device: torch.device):

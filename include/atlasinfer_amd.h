@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define AQ_ABI_VERSION 6
+#define AQ_ABI_VERSION 7
 
 enum { AQ_FMT_INT8 = 0, AQ_FMT_E4M3 = 1 };
 enum { AQ_LAYOUT_FLAT = 0, AQ_LAYOUT_TILED = 1 };
@@ -135,10 +135,14 @@ int aq_outlier_cols(const int64_t* flat_idx, int64_t nnz, int64_t K, int32_t* co
  *                                           ordered by block, row, column; the
  *                                           last 64 slots are padding the
  *                                           kernels may read but never use
+ *                                           (written as 0)
+ *   tile_max int32  [1] or NULL             raised (atomic max) to the largest
+ *                                           block's count; the caller sets it
+ *                                           to 0 first
  * from the CSR lists (row_ptr, cols, vals) of the same outliers.
  */
 int aq_outlier_tiles(const int32_t* row_ptr, const int32_t* cols, const void* vals, int64_t N, int64_t K,
-                     int32_t* tile_ptr, uint32_t* tile_ent, void* stream);
+                     int32_t* tile_ptr, uint32_t* tile_ent, int32_t* tile_max, void* stream);
 
 /*
  * Reference layout <-> dense flat codes.  The reference stores only the codes

@@ -71,8 +71,8 @@ def test_bad_arguments_return_einval_with_message(lib):
     # the dequant-GEMM (M > 64) needs the outlier block lists
     assert lib.aq_qlinear(p, 100, 4096, 16, p, p, 4096, 1, p, p, p, None, None, 0, None, p, p, 0, None) == AQ_EINVAL
     assert b"aq_outlier_tiles" in lib.aq_last_error()
-    assert lib.aq_outlier_tiles(p, p, p, 20, 128, p, p, None) == AQ_EINVAL
-    assert lib.aq_outlier_tiles(p, p, p, 32, 100, p, p, None) == AQ_EINVAL
+    assert lib.aq_outlier_tiles(p, p, p, 20, 128, p, p, None, None) == AQ_EINVAL
+    assert lib.aq_outlier_tiles(p, p, p, 32, 100, p, p, None, None) == AQ_EINVAL
     assert lib.aq_dequantize(p, p, 10, 0, 0, 10, 0, None, None, 0, p, None) == AQ_EINVAL
     assert lib.aq_zscore(p, 0, 1e-6, p, None, None) == AQ_EINVAL
     assert lib.aq_tile_codes(p, 20, 128, p, None) == AQ_EINVAL

@@ -274,20 +274,32 @@ def expected_tiles(q, N, K):
     return ptr.astype(np.int32), ent[order]
 
 
-@pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128)])
-def test_outlier_tiles_match_flat_indices(fmt, G):
-    rng = np.random.default_rng(5 + abs(G))
-    N, K = 96, 512
+@pytest.mark.parametrize("fmt,G,N,K", [("e4m3", -1, 96, 512), ("int8", 128, 96, 512), ("e4m3", -1, 48, 14336),
+                                       ("e4m3", 4096, 32, 65536), ("int8", 1024, 16, 131072)])
+def test_outlier_tiles_match_flat_indices(fmt, G, N, K):
+    """aq_outlier_tiles against the block lists rebuilt from the flat
+    indices: one workgroup per 16-row tile row up to 1024 chunks of 64
+    columns (K = 65536), one thread per block beyond (K = 131072); the
+    largest block count, the 64 zeroed padding entries; both on heavy-tailed
+    weights (many outliers per block) and on a weight with none."""
+    rng = np.random.default_rng(5 + abs(G) + K)
     w = make_weights(rng, (N, K), frac=0.02, t_dof=3)
-    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=G, code_format=fmt)
-    tp, te, tmax = AQ.outlier_tiles(q, torch.device(DEV))
-    ptr, ent = expected_tiles(q, N, K)
-    assert tmax == np.diff(ptr).max()
-    nnz = q.outlier_indices.numel()
-    assert nnz > 100
-    assert np.array_equal(tp.cpu().numpy(), ptr)
-    assert te.numel() == nnz + 64
-    assert np.array_equal(te[:nnz].cpu().numpy().view(np.uint32), ent)
+    for ww in (w, np.zeros_like(w)):
+        q = AQ.quantize_tensor(torch.from_numpy(ww).to(DEV), block_size=G, code_format=fmt)
+        tp, te, tmax = AQ.build_outlier_tiles(q, torch.device(DEV))
+        ptr, ent = expected_tiles(q, N, K)
+        nnz = q.outlier_indices.numel()
+        assert tmax == (np.diff(ptr).max() if nnz else 0)
+        if ww is w:
+            assert nnz > 100
+        assert np.array_equal(tp.cpu().numpy(), ptr)
+        assert te.numel() == nnz + 64
+        assert np.array_equal(te[:nnz].cpu().numpy().view(np.uint32), ent)
+        assert not te[nnz:].any()
+        # the lists quantize_tensor stores (largest count read lazily) are the same
+        if q.outlier_tile_ptr is not None:
+            assert torch.equal(q.outlier_tile_ptr, tp) and torch.equal(q.outlier_tile_ent, te)
+            assert int(q.outlier_tile_max) == tmax
 
 
 @pytest.mark.parametrize("M", [17, 65, 200])

@@ -171,22 +171,27 @@ __device__ __forceinline__ uint32_t block_position(int r, int k) { return ((uint
 // One workgroup per tile row (16 rows): a stable counting sort of the tile
 // row's CSR entries (already in row, column order) by 64-column chunk, which
 // is the block lists' order (block, then row, then column).  Per (row,
-// chunk) counts in LDS (atomic adds), turned into each chunk's block total
-// and per-row offsets within the block; an exclusive scan of the block
-// totals gives the block starts; an entry's place is its block's start, the
-// entries of its chunk in the rows above, and its rank among its own row's
-// entries of that chunk (a binary search of the row's sorted columns).  The
-// workgroup also raises *tile_max to its largest block.  Workgroup nrb
-// writes the list's end and the 64 padding entries.  LDS: 17 * nch ints.
-constexpr int kTileRowsMaxChunks = 1024;  // K <= 65536 (wider rows: outlier_tiles_kernel)
+// chunk) counts and first entries in LDS (atomic add, atomic min), turned
+// into each chunk's block total and per-row offsets within the block; an
+// exclusive scan of the block totals gives the block starts; an entry's
+// place is its block's start, the entries of its chunk in the rows above,
+// and its rank in its (row, chunk) run, which is contiguous in the row's
+// sorted columns: its index minus the run's first.  A thread's first
+// kTileRowsRegs entries (and their values) stay in registers between the
+// two passes.  The workgroup also raises *tile_max to its largest block.
+// Workgroup nrb writes the list's end and the 64 padding entries.
+// LDS: 33 * nch ints.
+constexpr int kTileRowsMaxChunks = 480;  // K <= 30720, LDS <= 63360 bytes (wider rows: outlier_tiles_kernel)
+constexpr int kTileRowsRegs = 4;
 
 __global__ __launch_bounds__(256) void outlier_tile_rows_kernel(const int32_t* row_ptr, const int32_t* cols,
                                                                 const uint16_t* vals, int nrb, int nch,
                                                                 int32_t* tile_ptr, uint32_t* tile_ent,
                                                                 int32_t* tile_max) {
   extern __shared__ int sm[];
-  int* cnt = sm;               // [16][nch]: counts, then offsets within the block
-  int* bstart = sm + 16 * nch;  // [nch]: block totals, then block starts
+  int* cnt = sm;                  // [16][nch]: counts, then offsets within the block
+  int* first = sm + 16 * nch;     // [16][nch]: index of the (row, chunk) run's first entry
+  int* bstart = sm + 32 * nch;    // [nch]: block totals, then block starts
   __shared__ int part[256];
   const int rb = blockIdx.x, t = threadIdx.x;
   if (rb == nrb) {
@@ -199,7 +204,20 @@ __global__ __launch_bounds__(256) void outlier_tile_rows_kernel(const int32_t* r
 #pragma unroll
   for (int r = 0; r <= 16; r++) rs[r] = row_ptr[rb * 16 + r];
   const int p0 = rs[0], p1 = rs[16];
-  for (int i = t; i < 16 * nch; i += 256) cnt[i] = 0;
+  // this thread's first entries: column and value loads go out before the
+  // LDS is cleared
+  int ccol[kTileRowsRegs];
+  uint32_t cval[kTileRowsRegs];
+#pragma unroll
+  for (int k = 0; k < kTileRowsRegs; k++) {
+    const int i = p0 + t + 256 * k;
+    ccol[k] = i < p1 ? cols[i] : 0;
+    cval[k] = i < p1 ? vals[i] : 0u;
+  }
+  for (int i = t; i < 16 * nch; i += 256) {
+    cnt[i] = 0;
+    first[i] = 0x7FFFFFFF;
+  }
   __syncthreads();
   auto row_of = [&](int i) {
     int r = 0;
@@ -207,7 +225,20 @@ __global__ __launch_bounds__(256) void outlier_tile_rows_kernel(const int32_t* r
     for (int k = 1; k < 16; k++) r += i >= rs[k];
     return r;
   };
-  for (int i = p0 + t; i < p1; i += 256) atomicAdd(&cnt[row_of(i) * nch + (cols[i] >> 6)], 1);
+#pragma unroll
+  for (int k = 0; k < kTileRowsRegs; k++) {
+    const int i = p0 + t + 256 * k;
+    if (i < p1) {
+      const int b = row_of(i) * nch + (ccol[k] >> 6);
+      atomicAdd(&cnt[b], 1);
+      atomicMin(&first[b], i);
+    }
+  }
+  for (int i = p0 + t + 256 * kTileRowsRegs; i < p1; i += 256) {
+    const int b = row_of(i) * nch + (cols[i] >> 6);
+    atomicAdd(&cnt[b], 1);
+    atomicMin(&first[b], i);
+  }
   __syncthreads();
   // per chunk: offsets of the rows within the block, and the block's total
   int mx = 0;
@@ -255,11 +286,16 @@ __global__ __launch_bounds__(256) void outlier_tile_rows_kernel(const int32_t* r
     carry += part[255];
   }
   __syncthreads();
-  for (int i = p0 + t; i < p1; i += 256) {
-    const int r = row_of(i), col = cols[i], c = col >> 6;
-    const int rank = i - lower_bound_i32(cols, rs[r], i, c * 64);
-    tile_ent[p0 + bstart[c] + cnt[r * nch + c] + rank] = ((uint32_t)vals[i] << 16) | block_position(r, col - c * 64);
+  auto place = [&](int i, int col, uint32_t val) {
+    const int r = row_of(i), c = col >> 6, b = r * nch + c;
+    tile_ent[p0 + bstart[c] + cnt[b] + (i - first[b])] = (val << 16) | block_position(r, col - c * 64);
+  };
+#pragma unroll
+  for (int k = 0; k < kTileRowsRegs; k++) {
+    const int i = p0 + t + 256 * k;
+    if (i < p1) place(i, ccol[k], cval[k]);
   }
+  for (int i = p0 + t + 256 * kTileRowsRegs; i < p1; i += 256) place(i, cols[i], vals[i]);
   // the largest block of the tile row
   for (int d = 32; d >= 1; d >>= 1) mx = max(mx, __shfl_xor(mx, d));
   if ((t & 63) == 0 && tile_max && mx > 0) atomicMax(tile_max, mx);
@@ -428,7 +464,7 @@ extern "C" int aq_outlier_tiles(const int32_t* row_ptr, const int32_t* cols, con
   const int64_t nblk = (N / 16) * (K / 64);
   if (K / 64 <= kTileRowsMaxChunks)
     hipLaunchKernelGGL(outlier_tile_rows_kernel, dim3((unsigned)(N / 16 + 1)), dim3(256),
-                       (size_t)17 * (K / 64) * sizeof(int), (hipStream_t)stream, row_ptr, cols,
+                       (size_t)33 * (K / 64) * sizeof(int), (hipStream_t)stream, row_ptr, cols,
                        (const uint16_t*)vals, (int)(N / 16), (int)(K / 64), tile_ptr, tile_ent, tile_max);
   else
     hipLaunchKernelGGL(outlier_tiles_kernel, dim3((unsigned)aq::ceil_div(nblk + 1, 256)), dim3(256), 0,

@@ -357,7 +357,8 @@ def quantize_tensors(tensors, block_size: int = 128, z_threshold: float = 3.0, *
     layout (and have at most 16384 blocks) quantized by one launch per run
     of up to 8 (aq_quantize_grouped, at most 2^28 elements a run): the small
     weights of a layer then share the GPU instead of each filling one round
-    of it, and each run costs one host sync.  Tensors with more blocks are
+    of it, and each run costs one host sync, taken once the next run is
+    queued (two runs are in flight at a time).  Tensors with more blocks are
     quantized one at a time, each completed before the next is prepared."""
     fmt = _format_id(code_format)
     out = [None] * len(tensors)
@@ -387,6 +388,15 @@ def quantize_tensors(tensors, block_size: int = 128, z_threshold: float = 3.0, *
             runs.append(run)
     L = _lib.load()
     arr = _lib.ptr_array
+
+    def complete(entry):
+        # the run's one host sync: every member's outlier count
+        run_i, ps_i, counts, done = entry
+        done.synchronize()
+        for i, p, nnz in zip(run_i, ps_i, counts.tolist()):
+            out[i] = _quantize_complete(p, int(nnz))
+
+    inflight = None  # the run launched last, completed once the next one is queued
     for run in runs:
         ps = []
         for i in run:
@@ -398,10 +408,18 @@ def quantize_tensors(tensors, block_size: int = 128, z_threshold: float = 3.0, *
             a0[3], fmt, ps[0]["K"], a0[6], arr([p["args"][7] for p in ps]), arr([p["args"][8] for p in ps]),
             arr([p["args"][9] for p in ps]), arr([p["args"][10] for p in ps]),
             arr([p["ws_bytes"] for p in ps], ctypes.c_int64), ps[0]["stream"]), "aq_quantize_grouped")
-        # the run's one host sync: every member's outlier count
-        counts = torch.stack([p["block_off"][p["nblocks"]] for p in ps]).tolist()
-        for i, p, nnz in zip(run, ps, counts):
-            out[i] = _quantize_complete(p, int(nnz))
+        # the outlier counts go to pinned host memory behind the launch; the
+        # host waits for them after queueing the next run, so that run's
+        # kernel runs while this one's outputs are allocated and finished
+        counts = torch.empty(len(ps), dtype=torch.int32, pin_memory=True)
+        counts.copy_(torch.stack([p["block_off"][p["nblocks"]] for p in ps]), non_blocking=True)
+        done = torch.cuda.Event()
+        done.record(torch.cuda.current_stream(ps[0]["dev"]))
+        if inflight is not None:
+            complete(inflight)
+        inflight = (run, ps, counts, done)
+    if inflight is not None:
+        complete(inflight)
     return out
 
 

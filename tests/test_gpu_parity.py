@@ -275,13 +275,15 @@ def expected_tiles(q, N, K):
 
 
 @pytest.mark.parametrize("fmt,G,N,K", [("e4m3", -1, 96, 512), ("int8", 128, 96, 512), ("e4m3", -1, 48, 14336),
-                                       ("e4m3", 4096, 32, 65536), ("int8", 1024, 16, 131072)])
+                                       ("e4m3", -1, 16, 30720), ("e4m3", 4096, 32, 65536),
+                                       ("int8", 1024, 16, 131072)])
 def test_outlier_tiles_match_flat_indices(fmt, G, N, K):
     """aq_outlier_tiles against the block lists rebuilt from the flat
-    indices: one workgroup per 16-row tile row up to 1024 chunks of 64
-    columns (K = 65536), one thread per block beyond (K = 131072); the
-    largest block count, the 64 zeroed padding entries; both on heavy-tailed
-    weights (many outliers per block) and on a weight with none."""
+    indices: one workgroup per 16-row tile row up to 480 chunks of 64
+    columns (K = 30720), one thread per block beyond (K = 65536, 131072);
+    the largest block count, the 64 zeroed padding entries; both on
+    heavy-tailed weights (many outliers per block: more than the 1024 a
+    workgroup keeps in registers at K = 30720) and on a weight with none."""
     rng = np.random.default_rng(5 + abs(G) + K)
     w = make_weights(rng, (N, K), frac=0.02, t_dof=3)
     for ww in (w, np.zeros_like(w)):

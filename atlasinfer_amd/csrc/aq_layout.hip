@@ -11,6 +11,7 @@
 // of the ascending index list with two binary searches, stages it in LDS, and
 // every thread walks its 16 elements against it.
 #include "aq_common.h"
+#include "aq_tiles.h"
 
 namespace {
 
@@ -154,151 +155,30 @@ __global__ __launch_bounds__(256) void scatter_outliers_kernel(const int64_t* id
   if (j >= 0 && j < numel) out[j] = vals[p];
 }
 
-__device__ __forceinline__ int lower_bound_i32(const int32_t* a, int lo, int hi, int key) {
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (a[mid] < key)
-      lo = mid + 1;
-    else
-      hi = mid;
-  }
-  return lo;
-}
+using aq::block_position;
+using aq::lower_bound_i32;
 
-// Position of row r (0..15), column k (0..63) in a block's entry: r << 6 | k.
-__device__ __forceinline__ uint32_t block_position(int r, int k) { return ((uint32_t)r << 6) | (uint32_t)k; }
-
-// One workgroup per tile row (16 rows): a stable counting sort of the tile
-// row's CSR entries (already in row, column order) by 64-column chunk, which
-// is the block lists' order (block, then row, then column).  Per (row,
-// chunk) counts and first entries in LDS (atomic add, atomic min), turned
-// into each chunk's block total and per-row offsets within the block; an
-// exclusive scan of the block totals gives the block starts; an entry's
-// place is its block's start, the entries of its chunk in the rows above,
-// and its rank in its (row, chunk) run, which is contiguous in the row's
-// sorted columns: its index minus the run's first.  A thread's first
-// kTileRowsRegs entries (and their values) stay in registers between the
-// two passes.  The workgroup also raises *tile_max to its largest block.
-// Workgroup nrb writes the list's end and the 64 padding entries.
-// LDS: 33 * nch ints.
-constexpr int kTileRowsMaxChunks = 480;  // K <= 30720, LDS <= 63360 bytes (wider rows: outlier_tiles_kernel)
-constexpr int kTileRowsRegs = 4;
-
-__global__ __launch_bounds__(256) void outlier_tile_rows_kernel(const int32_t* row_ptr, const int32_t* cols,
-                                                                const uint16_t* vals, int nrb, int nch,
-                                                                int32_t* tile_ptr, uint32_t* tile_ent,
+// One workgroup per tile row (aq_tiles.h); workgroup nrb writes the list's
+// end and the 64 padding entries.  LDS: 33 * nch ints.
+__global__ __launch_bounds__(256) void outlier_tile_rows_kernel(const int32_t* row_ptr, int64_t rstride,
+                                                                const int32_t* cols, const uint16_t* vals, int nrb,
+                                                                int nch, int32_t* tile_ptr, uint32_t* tile_ent,
                                                                 int32_t* tile_max) {
   extern __shared__ int sm[];
-  int* cnt = sm;                  // [16][nch]: counts, then offsets within the block
-  int* first = sm + 16 * nch;     // [16][nch]: index of the (row, chunk) run's first entry
-  int* bstart = sm + 32 * nch;    // [nch]: block totals, then block starts
   __shared__ int part[256];
   const int rb = blockIdx.x, t = threadIdx.x;
   if (rb == nrb) {
-    const int end = row_ptr[nrb * 16];
+    const int end = row_ptr[(int64_t)nrb * 16 * rstride];
     if (t == 0) tile_ptr[(int64_t)nrb * nch] = end;
     if (t < 64) tile_ent[end + t] = 0u;
     return;
   }
-  int rs[17];
+  aq::CsrTileSrc src;
 #pragma unroll
-  for (int r = 0; r <= 16; r++) rs[r] = row_ptr[rb * 16 + r];
-  const int p0 = rs[0], p1 = rs[16];
-  // this thread's first entries: column and value loads go out before the
-  // LDS is cleared
-  int ccol[kTileRowsRegs];
-  uint32_t cval[kTileRowsRegs];
-#pragma unroll
-  for (int k = 0; k < kTileRowsRegs; k++) {
-    const int i = p0 + t + 256 * k;
-    ccol[k] = i < p1 ? cols[i] : 0;
-    cval[k] = i < p1 ? vals[i] : 0u;
-  }
-  for (int i = t; i < 16 * nch; i += 256) {
-    cnt[i] = 0;
-    first[i] = 0x7FFFFFFF;
-  }
-  __syncthreads();
-  auto row_of = [&](int i) {
-    int r = 0;
-#pragma unroll
-    for (int k = 1; k < 16; k++) r += i >= rs[k];
-    return r;
-  };
-#pragma unroll
-  for (int k = 0; k < kTileRowsRegs; k++) {
-    const int i = p0 + t + 256 * k;
-    if (i < p1) {
-      const int b = row_of(i) * nch + (ccol[k] >> 6);
-      atomicAdd(&cnt[b], 1);
-      atomicMin(&first[b], i);
-    }
-  }
-  for (int i = p0 + t + 256 * kTileRowsRegs; i < p1; i += 256) {
-    const int b = row_of(i) * nch + (cols[i] >> 6);
-    atomicAdd(&cnt[b], 1);
-    atomicMin(&first[b], i);
-  }
-  __syncthreads();
-  // per chunk: offsets of the rows within the block, and the block's total
-  int mx = 0;
-  for (int c = t; c < nch; c += 256) {
-    int run = 0;
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int n = cnt[r * nch + c];
-      cnt[r * nch + c] = run;
-      run += n;
-    }
-    bstart[c] = run;
-    mx = max(mx, run);
-  }
-  // exclusive scan of the block totals: thread t takes chunks 4t..4t+3 of
-  // each run of 1024, its sum scanned across the workgroup in LDS
-  int carry = 0;
-  for (int c0 = 0; c0 < nch; c0 += 1024) {
-    __syncthreads();
-    int v[4], sum = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const int c = c0 + 4 * t + k;
-      v[k] = c < nch ? bstart[c] : 0;
-      sum += v[k];
-    }
-    part[t] = sum;
-    __syncthreads();
-    for (int d = 1; d < 256; d <<= 1) {
-      const int add = t >= d ? part[t - d] : 0;
-      __syncthreads();
-      part[t] += add;
-      __syncthreads();
-    }
-    int run = carry + part[t] - sum;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const int c = c0 + 4 * t + k;
-      if (c < nch) {
-        bstart[c] = run;
-        tile_ptr[(int64_t)rb * nch + c] = p0 + run;
-      }
-      run += v[k];
-    }
-    carry += part[255];
-  }
-  __syncthreads();
-  auto place = [&](int i, int col, uint32_t val) {
-    const int r = row_of(i), c = col >> 6, b = r * nch + c;
-    tile_ent[p0 + bstart[c] + cnt[b] + (i - first[b])] = (val << 16) | block_position(r, col - c * 64);
-  };
-#pragma unroll
-  for (int k = 0; k < kTileRowsRegs; k++) {
-    const int i = p0 + t + 256 * k;
-    if (i < p1) place(i, ccol[k], cval[k]);
-  }
-  for (int i = p0 + t + 256 * kTileRowsRegs; i < p1; i += 256) place(i, cols[i], vals[i]);
-  // the largest block of the tile row
-  for (int d = 32; d >= 1; d >>= 1) mx = max(mx, __shfl_xor(mx, d));
-  if ((t & 63) == 0 && tile_max && mx > 0) atomicMax(tile_max, mx);
+  for (int r = 0; r <= 16; r++) src.rs[r] = row_ptr[(int64_t)(rb * 16 + r) * rstride];
+  src.cols = cols;
+  src.vals = vals;
+  aq::tile_row_sort(src, rb, nch, src.rs[0], src.rs[16], sm, part, tile_ptr, tile_ent, tile_max);
 }
 
 // One thread per block of 16 rows x 64 columns (tile row rb, chunk c), for
@@ -306,15 +186,15 @@ __global__ __launch_bounds__(256) void outlier_tile_rows_kernel(const int32_t* r
 // block, then row, then column, so a block starts after every outlier of
 // the rows above it plus, in each of its own rows, the outliers left of
 // column 64c.
-__global__ __launch_bounds__(256) void outlier_tiles_kernel(const int32_t* row_ptr, const int32_t* cols,
-                                                            const uint16_t* vals, int nrb, int nch,
-                                                            int32_t* tile_ptr, uint32_t* tile_ent,
+__global__ __launch_bounds__(256) void outlier_tiles_kernel(const int32_t* row_ptr, int64_t rstride,
+                                                            const int32_t* cols, const uint16_t* vals, int nrb,
+                                                            int nch, int32_t* tile_ptr, uint32_t* tile_ent,
                                                             int32_t* tile_max) {
   const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t nblk = (int64_t)nrb * nch;
   if (b > nblk) return;
   if (b == nblk) {
-    const int end = row_ptr[nrb * 16];
+    const int end = row_ptr[(int64_t)nrb * 16 * rstride];
     tile_ptr[b] = end;
     for (int k = 0; k < 64; k++) tile_ent[end + k] = 0u;
     return;
@@ -325,7 +205,7 @@ __global__ __launch_bounds__(256) void outlier_tiles_kernel(const int32_t* row_p
     for (int cc = 0; cc < nch; cc++) {
       int n = 0;
       for (int r = 0; r < 16; r++) {
-        const int p0 = row_ptr[rb * 16 + r], p1 = row_ptr[rb * 16 + r + 1];
+        const int p0 = row_ptr[(int64_t)(rb * 16 + r) * rstride], p1 = row_ptr[(int64_t)(rb * 16 + r + 1) * rstride];
         n += lower_bound_i32(cols, p0, p1, cc * 64 + 64) - lower_bound_i32(cols, p0, p1, cc * 64);
       }
       mx = max(mx, n);
@@ -333,10 +213,10 @@ __global__ __launch_bounds__(256) void outlier_tiles_kernel(const int32_t* row_p
     if (mx > 0) atomicMax(tile_max, mx);
   }
   int lo[16], hi[16];
-  int pos = row_ptr[rb * 16];
+  int pos = row_ptr[(int64_t)rb * 16 * rstride];
 #pragma unroll
   for (int r = 0; r < 16; r++) {
-    const int p0 = row_ptr[rb * 16 + r], p1 = row_ptr[rb * 16 + r + 1];
+    const int p0 = row_ptr[(int64_t)(rb * 16 + r) * rstride], p1 = row_ptr[(int64_t)(rb * 16 + r + 1) * rstride];
     lo[r] = lower_bound_i32(cols, p0, p1, c * 64);
     hi[r] = lower_bound_i32(cols, lo[r], p1, c * 64 + 64);
     pos += lo[r] - p0;
@@ -454,6 +334,20 @@ extern "C" int aq_dequantize(const void* codes, const void* scales, int64_t nume
   return AQ_OK;
 }
 
+hipError_t aq::launch_outlier_tiles(const int32_t* row_ptr, int64_t rstride, const int32_t* cols, const uint16_t* vals,
+                                   int64_t N, int64_t K, int32_t* tile_ptr, uint32_t* tile_ent, int32_t* tile_max,
+                                   hipStream_t stream) {
+  const int64_t nblk = (N / 16) * (K / 64);
+  if (K / 64 <= aq::kTileRowsMaxChunks)
+    hipLaunchKernelGGL(outlier_tile_rows_kernel, dim3((unsigned)(N / 16 + 1)), dim3(256),
+                       (size_t)33 * (K / 64) * sizeof(int), stream, row_ptr, rstride, cols, vals, (int)(N / 16),
+                       (int)(K / 64), tile_ptr, tile_ent, tile_max);
+  else
+    hipLaunchKernelGGL(outlier_tiles_kernel, dim3((unsigned)aq::ceil_div(nblk + 1, 256)), dim3(256), 0, stream,
+                       row_ptr, rstride, cols, vals, (int)(N / 16), (int)(K / 64), tile_ptr, tile_ent, tile_max);
+  return hipGetLastError();
+}
+
 extern "C" int aq_outlier_tiles(const int32_t* row_ptr, const int32_t* cols, const void* vals, int64_t N, int64_t K,
                                 int32_t* tile_ptr, uint32_t* tile_ent, int32_t* tile_max, void* stream) {
   AQ_CHECK_ARG(N >= 16 && N % 16 == 0 && K >= 64 && K % 64 == 0 && N < (1 << 30) && K < (1 << 30) &&
@@ -461,15 +355,8 @@ extern "C" int aq_outlier_tiles(const int32_t* row_ptr, const int32_t* cols, con
                "aq_outlier_tiles: N must be a multiple of 16 and K of 64 (N=%lld K=%lld)", (long long)N,
                (long long)K);
   AQ_CHECK_ARG(row_ptr && tile_ptr, "aq_outlier_tiles: null pointer argument");
-  const int64_t nblk = (N / 16) * (K / 64);
-  if (K / 64 <= kTileRowsMaxChunks)
-    hipLaunchKernelGGL(outlier_tile_rows_kernel, dim3((unsigned)(N / 16 + 1)), dim3(256),
-                       (size_t)33 * (K / 64) * sizeof(int), (hipStream_t)stream, row_ptr, cols,
-                       (const uint16_t*)vals, (int)(N / 16), (int)(K / 64), tile_ptr, tile_ent, tile_max);
-  else
-    hipLaunchKernelGGL(outlier_tiles_kernel, dim3((unsigned)aq::ceil_div(nblk + 1, 256)), dim3(256), 0,
-                       (hipStream_t)stream, row_ptr, cols, (const uint16_t*)vals, (int)(N / 16), (int)(K / 64),
-                       tile_ptr, tile_ent, tile_max);
-  AQ_LAUNCH_CHECK("aq_outlier_tiles: launch");
+  const hipError_t e = aq::launch_outlier_tiles(row_ptr, 1, cols, (const uint16_t*)vals, N, K, tile_ptr, tile_ent,
+                                                tile_max, (hipStream_t)stream);
+  if (e != hipSuccess) return aq::check_hip(e, "aq_outlier_tiles: launch");
   return AQ_OK;
 }

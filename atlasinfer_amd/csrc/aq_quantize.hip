@@ -29,6 +29,7 @@
 #include <math.h>
 
 #include "aq_common.h"
+#include "aq_tiles.h"
 
 namespace {
 
@@ -976,6 +977,98 @@ __global__ __launch_bounds__(256) void gather_kernel(const int32_t* off, int64_t
   }
 }
 
+// ---- the flat list and the 16 x 64 block lists in one pass
+
+// Entries of one tile row straight from the quantize workspace: block g's
+// outliers are staged at stage_col / stage_val[g G .. g G + n_g - 1]
+// (columns within the block, ascending), and its first entry's index is
+// off[g].  In the counting pass each entry also goes to the flat list, as
+// gather_kernel writes it.
+struct WsTileSrc {
+  int rs[17];            // the tile row's row starts, off[(16 rb + r) bpr]
+  const int32_t* off;    // block offsets
+  const int* loff;       // the tile row's 16 bpr + 1 block offsets in LDS, or null (read off)
+  int64_t g0;            // the tile row's first block
+  int bpr;               // blocks per row, K / G
+  int64_t G;
+  const int32_t* stage_col;
+  const uint16_t* stage_val;
+  int64_t* flat_idx;
+  uint16_t* vals;
+  int32_t* cols;
+  __device__ __forceinline__ int block_start(int b) const { return loff ? loff[b] : off[g0 + b]; }
+  __device__ __forceinline__ aq::TileEnt operator()(int i, bool first) const {
+    int b, r;
+    if (bpr == 1) {
+      r = aq::tile_row_of(rs, i);
+      b = r;
+    } else {
+      // the last block of the tile row starting at or before entry i (blocks
+      // may be empty): block_start(0) <= i < block_start(16 bpr)
+      int lo = 1, hi = 16 * bpr;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (block_start(mid) <= i)
+          lo = mid + 1;
+        else
+          hi = mid;
+      }
+      b = lo - 1;
+      r = b / bpr;
+    }
+    const int64_t g = g0 + b;
+    const int64_t at = g * G + (i - (bpr == 1 ? rs[r] : block_start(b)));
+    const int sc = stage_col[at];
+    const uint32_t v = stage_val[at];
+    const int col = (b - r * bpr) * (int)G + sc;
+    if (first) {
+      flat_idx[i] = g * G + sc;
+      vals[i] = (uint16_t)v;
+      cols[i] = col;
+    }
+    return aq::TileEnt{r, col, v};
+  }
+};
+
+// One workgroup per tile row; workgroup nrb writes the block lists' end and
+// their 64 padding entries.  LDS: 33 * nch ints, and with loff_lds the tile
+// row's block offsets after them.
+__global__ __launch_bounds__(256) void finish_tiles_kernel(const int32_t* off, int64_t G, int bpr, int nrb, int nch,
+                                                           int loff_lds, const int32_t* stage_col,
+                                                           const uint16_t* stage_val, int64_t* flat_idx,
+                                                           uint16_t* vals, int32_t* cols, int32_t* tile_ptr,
+                                                           uint32_t* tile_ent, int32_t* tile_max) {
+  extern __shared__ int sm[];
+  __shared__ int part[256];
+  const int rb = blockIdx.x, t = threadIdx.x;
+  if (rb == nrb) {
+    const int end = off[(int64_t)nrb * 16 * bpr];
+    if (t == 0) tile_ptr[(int64_t)nrb * nch] = end;
+    if (t < 64) tile_ent[end + t] = 0u;
+    return;
+  }
+  WsTileSrc src;
+#pragma unroll
+  for (int r = 0; r <= 16; r++) src.rs[r] = off[(int64_t)(rb * 16 + r) * bpr];
+  src.off = off;
+  src.loff = nullptr;
+  src.g0 = (int64_t)rb * 16 * bpr;
+  src.bpr = bpr;
+  src.G = G;
+  src.stage_col = stage_col;
+  src.stage_val = stage_val;
+  src.flat_idx = flat_idx;
+  src.vals = vals;
+  src.cols = cols;
+  if (loff_lds) {
+    int* l = sm + 33 * nch;
+    for (int k = t; k <= 16 * bpr; k += 256) l[k] = off[src.g0 + k];
+    __syncthreads();
+    src.loff = l;
+  }
+  aq::tile_row_sort(src, rb, nch, src.rs[0], src.rs[16], sm, part, tile_ptr, tile_ent, tile_max);
+}
+
 // ---- calculate_zscore_manual of one block of n elements
 
 template <int TAU, int E>
@@ -1222,6 +1315,46 @@ extern "C" int aq_quantize_finish(int64_t numel, int64_t G, int64_t K, const int
                        w.stage_col, w.stage_val, flat_idx, (uint16_t*)vals, cols);
   }
   AQ_LAUNCH_CHECK("aq_quantize_finish: gather launch");
+  return AQ_OK;
+}
+
+extern "C" int aq_quantize_finish_tiles(int64_t numel, int64_t G, int64_t K, const int32_t* block_off, int64_t nnz,
+                                        const void* workspace, int64_t ws_bytes, int64_t* flat_idx, void* vals,
+                                        int32_t* cols, int32_t* tile_ptr, uint32_t* tile_ent, int32_t* tile_max,
+                                        void* stream) {
+  AQ_CHECK_ARG(numel > 0 && G >= 1 && G <= kMaxG, "aq_quantize_finish_tiles: bad numel/G");
+  AQ_CHECK_ARG(K >= 64 && K % 64 == 0 && K % G == 0 && numel % (16 * K) == 0 && K < (1 << 30) &&
+                   (numel / K / 16) * (K / 64) < ((int64_t)1 << 31),
+               "aq_quantize_finish_tiles: needs K %% 64 == 0, a block dividing K and rows %% 16 == 0 "
+               "(numel=%lld K=%lld G=%lld)",
+               (long long)numel, (long long)K, (long long)G);
+  const int64_t nblocks = numel / G;
+  if (ws_bytes < workspace_bytes(numel, nblocks))
+    return aq::set_error(AQ_EWORKSPACE, "aq_quantize_finish_tiles: workspace too small");
+  AQ_CHECK_ARG(block_off && workspace && tile_ptr && tile_ent && (nnz == 0 || (flat_idx && vals && cols)),
+               "aq_quantize_finish_tiles: null pointer argument");
+  const int64_t N = numel / K, nch = K / 64, bpr = K / G;
+  hipStream_t s = (hipStream_t)stream;
+  if (nch > aq::kTileRowsMaxChunks) {
+    // rows too wide for one workgroup's LDS: the flat list, then the block
+    // lists from it (one thread per block), the block offsets serving as
+    // the CSR row pointer at a stride of K / G
+    const int rc = aq_quantize_finish(numel, G, K, block_off, nnz, workspace, ws_bytes, flat_idx, vals, cols, stream);
+    if (rc != AQ_OK) return rc;
+    const hipError_t e = aq::launch_outlier_tiles(block_off, bpr, cols, (const uint16_t*)vals, N, K, tile_ptr,
+                                                  tile_ent, tile_max, s);
+    if (e != hipSuccess) return aq::check_hip(e, "aq_quantize_finish_tiles: block list launch");
+    return AQ_OK;
+  }
+  Workspace w = carve((void*)workspace, numel, nblocks);
+  // the tile row's block offsets go to LDS when the sort leaves room (64 KiB in all)
+  const int64_t sort_ints = 33 * nch;
+  const int loff_lds = bpr > 1 && sort_ints + 16 * bpr + 1 <= 16384;
+  const size_t lds = (size_t)(sort_ints + (loff_lds ? 16 * bpr + 1 : 0)) * sizeof(int);
+  hipLaunchKernelGGL(finish_tiles_kernel, dim3((unsigned)(N / 16 + 1)), dim3(256), lds, s, block_off, G, (int)bpr,
+                     (int)(N / 16), (int)nch, loff_lds, w.stage_col, w.stage_val, flat_idx, (uint16_t*)vals, cols,
+                     tile_ptr, tile_ent, tile_max);
+  AQ_LAUNCH_CHECK("aq_quantize_finish_tiles: launch");
   return AQ_OK;
 }
 

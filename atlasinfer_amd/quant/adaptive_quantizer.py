@@ -297,9 +297,11 @@ def _quantize_prepare(fp16_tensor: torch.Tensor, G: int, z_threshold: float, cod
                 stream=_lib.stream_of(dev))
 
 
-def _quantize_complete(p: dict, nnz: int) -> QuantizedTensor:
+def _quantize_complete(p: dict, nnz: int, tmax: Optional[torch.Tensor] = None) -> QuantizedTensor:
     """The outlier lists, CSR rows and block lists of a tensor whose
-    aq_quantize (or group) has run, given its outlier count."""
+    aq_quantize (or group) has run, given its outlier count.  ``tmax``: a
+    zeroed one-element int32 device tensor to receive the largest block
+    count (allocated here if not given)."""
     L = _lib.load()
     dev, stream, G, K, N = p["dev"], p["stream"], p["G"], p["K"], p["N"]
     numel, padded, fmt, layout = p["numel"], p["padded"], p["fmt"], p["layout"]
@@ -307,9 +309,23 @@ def _quantize_complete(p: dict, nnz: int) -> QuantizedTensor:
     flat_idx = torch.empty(nnz, dtype=torch.int64, device=dev)
     vals = torch.empty(nnz, dtype=torch.float16, device=dev)
     cols = torch.empty(nnz, dtype=torch.int32, device=dev)
-    _lib.check(L.aq_quantize_finish(numel, G, K, block_off.data_ptr(), nnz, ws.data_ptr(), ws_bytes,
-                                    _lib.ptr(flat_idx), _lib.ptr(vals), _lib.ptr(cols), stream),
-               "aq_quantize_finish")
+    tiles = None
+    if layout == "tiled":
+        # the flat list and the 16 x 64 block lists in one launch; the
+        # largest block count is read when first used
+        tile_ptr = torch.empty((N // 16) * (K // 64) + 1, dtype=torch.int32, device=dev)
+        tile_ent = torch.empty(nnz + 64, dtype=torch.int32, device=dev)
+        if tmax is None:
+            tmax = torch.zeros(1, dtype=torch.int32, device=dev)
+        _lib.check(L.aq_quantize_finish_tiles(numel, G, K, block_off.data_ptr(), nnz, ws.data_ptr(), ws_bytes,
+                                              _lib.ptr(flat_idx), _lib.ptr(vals), _lib.ptr(cols),
+                                              tile_ptr.data_ptr(), tile_ent.data_ptr(), tmax.data_ptr(), stream),
+                   "aq_quantize_finish_tiles")
+        tiles = (tile_ptr, tile_ent, DeviceInt(tmax[0]) if nnz else 0)
+    else:
+        _lib.check(L.aq_quantize_finish(numel, G, K, block_off.data_ptr(), nnz, ws.data_ptr(), ws_bytes,
+                                        _lib.ptr(flat_idx), _lib.ptr(vals), _lib.ptr(cols), stream),
+                   "aq_quantize_finish")
     if K % G == 0:
         # blocks tile the rows, so a row's first outlier is its first block's:
         # the CSR row pointers are every (K / G)-th block offset (per output
@@ -338,9 +354,8 @@ def _quantize_complete(p: dict, nnz: int) -> QuantizedTensor:
         outlier_cols=cols,
         code_layout=layout,
     )
-    if layout == "tiled":
-        tp, te, tmax = build_outlier_tiles(qt, dev, lazy_max=True)
-        qt = qt._replace(outlier_tile_ptr=tp, outlier_tile_ent=te, outlier_tile_max=tmax)
+    if tiles is not None:
+        qt = qt._replace(outlier_tile_ptr=tiles[0], outlier_tile_ent=tiles[1], outlier_tile_max=tiles[2])
     return qt.to(p["input_device"])
 
 
@@ -391,10 +406,10 @@ def quantize_tensors(tensors, block_size: int = 128, z_threshold: float = 3.0, *
 
     def complete(entry):
         # the run's one host sync: every member's outlier count
-        run_i, ps_i, counts, done = entry
+        run_i, ps_i, counts, done, tmaxs = entry
         done.synchronize()
-        for i, p, nnz in zip(run_i, ps_i, counts.tolist()):
-            out[i] = _quantize_complete(p, int(nnz))
+        for k, (i, p, nnz) in enumerate(zip(run_i, ps_i, counts.tolist())):
+            out[i] = _quantize_complete(p, int(nnz), tmaxs[k:k + 1])
 
     inflight = None  # the run launched last, completed once the next one is queued
     for run in runs:
@@ -415,9 +430,11 @@ def quantize_tensors(tensors, block_size: int = 128, z_threshold: float = 3.0, *
         counts.copy_(torch.stack([p["block_off"][p["nblocks"]] for p in ps]), non_blocking=True)
         done = torch.cuda.Event()
         done.record(torch.cuda.current_stream(ps[0]["dev"]))
+        # the members' largest block counts, zeroed by one fill
+        tmaxs = torch.zeros(len(ps), dtype=torch.int32, device=ps[0]["dev"])
         if inflight is not None:
             complete(inflight)
-        inflight = (run, ps, counts, done)
+        inflight = (run, ps, counts, done, tmaxs)
     if inflight is not None:
         complete(inflight)
     return out

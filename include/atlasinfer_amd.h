@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define AQ_ABI_VERSION 7
+#define AQ_ABI_VERSION 8
 
 enum { AQ_FMT_INT8 = 0, AQ_FMT_E4M3 = 1 };
 enum { AQ_LAYOUT_FLAT = 0, AQ_LAYOUT_TILED = 1 };
@@ -143,6 +143,23 @@ int aq_outlier_cols(const int64_t* flat_idx, int64_t nnz, int64_t K, int32_t* co
  */
 int aq_outlier_tiles(const int32_t* row_ptr, const int32_t* cols, const void* vals, int64_t N, int64_t K,
                      int32_t* tile_ptr, uint32_t* tile_ent, int32_t* tile_max, void* stream);
+
+/*
+ * aq_quantize_finish (with cols) and aq_outlier_tiles of the same weight in
+ * one launch, read straight from the quantize workspace: the flat list and
+ * the block lists, bit for bit those of the two calls.  For weights
+ * quantized with blocks that tile the rows (K % G == 0) and whose [N, K]
+ * view has N % 16 == 0 and K % 64 == 0 (every weight quantized into the
+ * tiled layout); rows wider than 30720 take two launches inside.  Same
+ * arguments as the two calls; cols is required (non-NULL when nnz > 0),
+ * tile_ptr and tile_ent always, tile_max may be NULL (else the caller sets
+ * it to 0 first).  Serves the reference's quantize_tensor
+ * (adaptive_quantizer.py:109-117,137-138) for callers that also want the
+ * block lists the dequant-GEMM reads.
+ */
+int aq_quantize_finish_tiles(int64_t numel, int64_t G, int64_t K, const int32_t* block_off, int64_t nnz,
+                             const void* workspace, int64_t workspace_bytes, int64_t* flat_idx, void* vals,
+                             int32_t* cols, int32_t* tile_ptr, uint32_t* tile_ent, int32_t* tile_max, void* stream);
 
 /*
  * Reference layout <-> dense flat codes.  The reference stores only the codes

@@ -29,7 +29,7 @@ def test_header_declares_the_expected_api():
     names = declared_functions()
     for must in ["aq_abi_version", "aq_last_error", "aq_quantize", "aq_quantize_finish", "aq_dequantize",
                  "aq_qlinear", "aq_zscore", "aq_compact_codes", "aq_expand_codes", "aq_segment_offsets",
-                 "aq_outlier_tiles"]:
+                 "aq_outlier_tiles", "aq_quantize_finish_tiles"]:
         assert must in names
 
 
@@ -73,6 +73,14 @@ def test_bad_arguments_return_einval_with_message(lib):
     assert b"aq_outlier_tiles" in lib.aq_last_error()
     assert lib.aq_outlier_tiles(p, p, p, 20, 128, p, p, None, None) == AQ_EINVAL
     assert lib.aq_outlier_tiles(p, p, p, 32, 100, p, p, None, None) == AQ_EINVAL
+    # the fused finish needs rows of a multiple of 64, blocks tiling them, 16-row tiles
+    ws = 1 << 30
+    assert lib.aq_quantize_finish_tiles(16 * 100, 100, 100, p, 0, p, ws, p, p, p, p, p, None, None) == AQ_EINVAL
+    assert b"aq_quantize_finish_tiles" in lib.aq_last_error()
+    assert lib.aq_quantize_finish_tiles(16 * 128, 96, 128, p, 0, p, ws, p, p, p, p, p, None, None) == AQ_EINVAL
+    assert lib.aq_quantize_finish_tiles(20 * 128, 128, 128, p, 0, p, ws, p, p, p, p, p, None, None) == AQ_EINVAL
+    assert lib.aq_quantize_finish_tiles(16 * 128, 128, 128, p, 5, p, ws, p, p, None, p, p, None, None) == AQ_EINVAL
+    assert b"null pointer" in lib.aq_last_error()
     assert lib.aq_dequantize(p, p, 10, 0, 0, 10, 0, None, None, 0, p, None) == AQ_EINVAL
     assert lib.aq_zscore(p, 0, 1e-6, p, None, None) == AQ_EINVAL
     assert lib.aq_tile_codes(p, 20, 128, p, None) == AQ_EINVAL

@@ -275,15 +275,20 @@ def expected_tiles(q, N, K):
 
 
 @pytest.mark.parametrize("fmt,G,N,K", [("e4m3", -1, 96, 512), ("int8", 128, 96, 512), ("e4m3", -1, 48, 14336),
-                                       ("e4m3", -1, 16, 30720), ("e4m3", 4096, 32, 65536),
-                                       ("int8", 1024, 16, 131072)])
+                                       ("e4m3", -1, 16, 30720), ("e4m3", 128, 32, 4096), ("e4m3", 32, 16, 30720),
+                                       ("e4m3", 4096, 32, 65536), ("int8", 1024, 16, 131072)])
 def test_outlier_tiles_match_flat_indices(fmt, G, N, K):
     """aq_outlier_tiles against the block lists rebuilt from the flat
     indices: one workgroup per 16-row tile row up to 480 chunks of 64
     columns (K = 30720), one thread per block beyond (K = 65536, 131072);
     the largest block count, the 64 zeroed padding entries; both on
     heavy-tailed weights (many outliers per block: more than the 1024 a
-    workgroup keeps in registers at K = 30720) and on a weight with none."""
+    workgroup keeps in registers at K = 30720) and on a weight with none.
+    E4M3 weights store the lists aq_quantize_finish_tiles builds in the
+    same launch as the flat list (per row, several blocks per row with the
+    tile row's block offsets in LDS (G = 128) or searched in memory
+    (G = 32, K = 30720), and in two launches past 480 chunks): those, and
+    that flat list, are checked too."""
     rng = np.random.default_rng(5 + abs(G) + K)
     w = make_weights(rng, (N, K), frac=0.02, t_dof=3)
     for ww in (w, np.zeros_like(w)):
@@ -299,9 +304,16 @@ def test_outlier_tiles_match_flat_indices(fmt, G, N, K):
         assert np.array_equal(te[:nnz].cpu().numpy().view(np.uint32), ent)
         assert not te[nnz:].any()
         # the lists quantize_tensor stores (largest count read lazily) are the same
+        assert (q.outlier_tile_ptr is not None) == (fmt == "e4m3")
         if q.outlier_tile_ptr is not None:
             assert torch.equal(q.outlier_tile_ptr, tp) and torch.equal(q.outlier_tile_ent, te)
             assert int(q.outlier_tile_max) == tmax
+        # the flat list: ascending, the weight's own values, columns and rows
+        idx = q.outlier_indices.cpu().numpy()
+        assert np.all(np.diff(idx) > 0)
+        assert np.array_equal(bits(q.fp16_outliers), ww.reshape(-1).view(np.uint16)[idx])
+        assert np.array_equal(q.outlier_cols.cpu().numpy(), idx % K)
+        assert np.array_equal(q.outlier_row_ptr.cpu().numpy(), np.searchsorted(idx, np.arange(N + 1) * K))
 
 
 @pytest.mark.parametrize("M", [17, 65, 200])

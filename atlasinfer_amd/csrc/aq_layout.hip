@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) void outlier_tile_rows_kernel(const int32_t* r
                                                                 int nch, int32_t* tile_ptr, uint32_t* tile_ent,
                                                                 int32_t* tile_max) {
   extern __shared__ int sm[];
-  __shared__ int part[256];
+  __shared__ int part[4];
   const int rb = blockIdx.x, t = threadIdx.x;
   if (rb == nrb) {
     const int end = row_ptr[(int64_t)nrb * 16 * rstride];

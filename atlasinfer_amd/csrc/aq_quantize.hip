@@ -1039,7 +1039,7 @@ __global__ __launch_bounds__(256) void finish_tiles_kernel(const int32_t* off, i
                                                            uint16_t* vals, int32_t* cols, int32_t* tile_ptr,
                                                            uint32_t* tile_ent, int32_t* tile_max) {
   extern __shared__ int sm[];
-  __shared__ int part[256];
+  __shared__ int part[4];
   const int rb = blockIdx.x, t = threadIdx.x;
   if (rb == nrb) {
     const int end = off[(int64_t)nrb * 16 * bpr];

@@ -63,7 +63,7 @@ struct CsrTileSrc {
 
 // The counting sort of tile row rb's entries p0 .. p1 - 1 (Src(i, first)
 // gives entry i; first is true in the counting pass, false when an entry
-// is read again for its placement).  sm: 33 * nch ints of LDS; part: 256.
+// is read again for its placement).  sm: 33 * nch ints of LDS; part: 4.
 // Writes tile_ptr[rb * nch + c] for every chunk and the entries, and raises
 // *tile_max (if not null) to the largest block.  Every thread of the
 // workgroup calls it.
@@ -116,7 +116,8 @@ __device__ __forceinline__ void tile_row_sort(const Src& src, int rb, int nch, i
     mx = max(mx, run);
   }
   // exclusive scan of the block totals: thread t takes chunks 4t..4t+3 of
-  // each run of 1024, its sum scanned across the workgroup in LDS
+  // each run of 1024, its sum scanned across the workgroup (wave scans, the
+  // wave totals through LDS)
   int carry = 0;
   for (int c0 = 0; c0 < nch; c0 += 1024) {
     __syncthreads();
@@ -127,15 +128,8 @@ __device__ __forceinline__ void tile_row_sort(const Src& src, int rb, int nch, i
       v[k] = c < nch ? bstart[c] : 0;
       sum += v[k];
     }
-    part[t] = sum;
-    __syncthreads();
-    for (int d = 1; d < 256; d <<= 1) {
-      const int add = t >= d ? part[t - d] : 0;
-      __syncthreads();
-      part[t] += add;
-      __syncthreads();
-    }
-    int run = carry + part[t] - sum;
+    int total;
+    int run = carry + team_excl_scan_i32<256>(sum, part, &total);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const int c = c0 + 4 * t + k;
@@ -145,7 +139,7 @@ __device__ __forceinline__ void tile_row_sort(const Src& src, int rb, int nch, i
       }
       run += v[k];
     }
-    carry += part[255];
+    carry += total;
   }
   __syncthreads();
 #pragma unroll

@@ -998,9 +998,18 @@ struct WsTileSrc {
   int32_t* cols;
   __device__ __forceinline__ int block_start(int b) const { return loff ? loff[b] : off[g0 + b]; }
   __device__ __forceinline__ aq::TileEnt operator()(int i, bool first) const {
-    int b, r;
+    int b, r, o;
     if (bpr == 1) {
-      r = aq::tile_row_of(rs, i);
+      // the row and its start by a select chain (an index into rs would move
+      // the array to scratch memory)
+      r = 0;
+      o = rs[0];
+#pragma unroll
+      for (int k = 1; k < 16; k++)
+        if (i >= rs[k]) {
+          r = k;
+          o = rs[k];
+        }
       b = r;
     } else {
       // the last block of the tile row starting at or before entry i (blocks
@@ -1015,9 +1024,10 @@ struct WsTileSrc {
       }
       b = lo - 1;
       r = b / bpr;
+      o = block_start(b);
     }
     const int64_t g = g0 + b;
-    const int64_t at = g * G + (i - (bpr == 1 ? rs[r] : block_start(b)));
+    const int64_t at = g * G + (i - o);
     const int sc = stage_col[at];
     const uint32_t v = stage_val[at];
     const int col = (b - r * bpr) * (int)G + sc;

@@ -842,7 +842,9 @@ def config0_cpu(args, dev, log):
         tq = time.perf_counter() - t0
         log(f"config 0 {name} [{N}, {K}]: quantize loop {tq:.1f} s over {nb} blocks")
         t0 = time.perf_counter()
-        deq, _ = ref_loop.dequantize_loop(codes, outs, idx, scales, N * K, 128)
+        deq, _ = ref_loop.dequantize_loop(codes, outs, idx, scales, N * K, 128,
+                                          progress=lambda i, n: log(f"config 0 {name}: dequantize loop "
+                                                                    f"{i}/{n} blocks"))
         td = time.perf_counter() - t0
         w_deq = deq[:N * K].view(N, K)
         log(f"config 0 {name}: dequantize loop {td:.1f} s ({idx.numel()} outliers)")

@@ -56,10 +56,13 @@ def quantize_loop(fp16_tensor: torch.Tensor, block_size: int = 128, z_threshold:
 
 
 def dequantize_loop(fp8_data: torch.Tensor, fp16_outliers: torch.Tensor, outlier_indices: torch.Tensor,
-                    scale_factors: torch.Tensor, numel: int, block_size: int, max_blocks: int | None = None):
+                    scale_factors: torch.Tensor, numel: int, block_size: int, max_blocks: int | None = None,
+                    progress=None, every: int = 16384):
     """Per-block loop of dequantize_tensor on CPU (the reference's int8
     layout: compacted codes of the non-outliers); stops after ``max_blocks``
-    blocks.  Returns (flat fp16 tensor of the padded length, blocks_done)."""
+    blocks.  ``progress(blocks_done, blocks)`` is called every ``every``
+    blocks (long runs report as they go).  Returns (flat fp16 tensor of the
+    padded length, blocks_done)."""
     padded = (numel + block_size - 1) // block_size * block_size
     nb = padded // block_size if max_blocks is None else min(max_blocks, padded // block_size)
     out = torch.zeros(padded, dtype=torch.float16)
@@ -83,6 +86,8 @@ def dequantize_loop(fp8_data: torch.Tensor, fp16_outliers: torch.Tensor, outlier
         n_keep = keep.sum().item()  # :234, the host sync of every block
         blk[keep] = deq[:n_keep]
         out[b0:b1] = blk
+        if progress is not None and (i + 1) % every == 0:
+            progress(i + 1, nb)
     return out, nb
 
 

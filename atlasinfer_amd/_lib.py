@@ -17,7 +17,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libatlasinfer_amd.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 FMT_INT8 = 0
 FMT_E4M3 = 1
@@ -46,6 +46,8 @@ SIGNATURES = {
     "aq_outlier_tiles": (ctypes.c_int, [_I32P, _I32P, _P, _I64, _I64, _I32P, _P, _I32P, _P]),
     "aq_quantize_finish_tiles": (ctypes.c_int, [_I64, _I64, _I64, _I32P, _I64, _P, _I64, _P, _P, _I32P, _I32P, _P,
                                                 _I32P, _P]),
+    "aq_quantize_finish_tiles_grouped": (ctypes.c_int, [_I64, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                                        _I32P, _P]),
     "aq_compact_codes": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P]),
     "aq_expand_codes": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P]),
     "aq_tile_codes": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),

@@ -1040,43 +1040,67 @@ struct WsTileSrc {
   }
 };
 
-// One workgroup per tile row; workgroup nrb writes the block lists' end and
-// their 64 padding entries.  LDS: 33 * nch ints, and with loff_lds the tile
-// row's block offsets after them.
-__global__ __launch_bounds__(256) void finish_tiles_kernel(const int32_t* off, int64_t G, int bpr, int nrb, int nch,
-                                                           int loff_lds, const int32_t* stage_col,
-                                                           const uint16_t* stage_val, int64_t* flat_idx,
-                                                           uint16_t* vals, int32_t* cols, int32_t* tile_ptr,
-                                                           uint32_t* tile_ent, int32_t* tile_max) {
+// The weights of one aq_quantize_finish_tiles(_grouped) launch: they share
+// the block size and the row length.  Member i takes workgroups first[i] ..
+// first[i + 1] - 1: one per tile row, and a last one that writes the block
+// lists' end and their 64 padding entries.
+struct FinishMember {
+  const int32_t* off;
+  const int32_t* stage_col;
+  const uint16_t* stage_val;
+  int64_t* flat_idx;
+  uint16_t* vals;
+  int32_t* cols;
+  int32_t* tile_ptr;
+  uint32_t* tile_ent;
+  int32_t* tile_max;
+  int nrb;
+};
+struct FinishGroup {
+  FinishMember m[kMaxQGroup];
+  int first[kMaxQGroup + 1];
+  int count;
+  int bpr, nch, loff_lds;
+  int64_t G;
+};
+
+// LDS: 33 * nch ints, and with loff_lds the tile row's block offsets after them.
+__global__ __launch_bounds__(256) void finish_tiles_kernel(FinishGroup fg) {
   extern __shared__ int sm[];
   __shared__ int part[4];
-  const int rb = blockIdx.x, t = threadIdx.x;
-  if (rb == nrb) {
-    const int end = off[(int64_t)nrb * 16 * bpr];
-    if (t == 0) tile_ptr[(int64_t)nrb * nch] = end;
-    if (t < 64) tile_ent[end + t] = 0u;
+  int mi = 0;  // the workgroup's member (uniform)
+#pragma unroll
+  for (int j = 1; j < kMaxQGroup; j++)
+    if (j < fg.count && (int)blockIdx.x >= fg.first[j]) mi = j;
+  const FinishMember& m = fg.m[mi];
+  const int bpr = fg.bpr, nch = fg.nch;
+  const int rb = (int)blockIdx.x - fg.first[mi], t = threadIdx.x;
+  if (rb == m.nrb) {
+    const int end = m.off[(int64_t)m.nrb * 16 * bpr];
+    if (t == 0) m.tile_ptr[(int64_t)m.nrb * nch] = end;
+    if (t < 64) m.tile_ent[end + t] = 0u;
     return;
   }
   WsTileSrc src;
 #pragma unroll
-  for (int r = 0; r <= 16; r++) src.rs[r] = off[(int64_t)(rb * 16 + r) * bpr];
-  src.off = off;
+  for (int r = 0; r <= 16; r++) src.rs[r] = m.off[(int64_t)(rb * 16 + r) * bpr];
+  src.off = m.off;
   src.loff = nullptr;
   src.g0 = (int64_t)rb * 16 * bpr;
   src.bpr = bpr;
-  src.G = G;
-  src.stage_col = stage_col;
-  src.stage_val = stage_val;
-  src.flat_idx = flat_idx;
-  src.vals = vals;
-  src.cols = cols;
-  if (loff_lds) {
+  src.G = fg.G;
+  src.stage_col = m.stage_col;
+  src.stage_val = m.stage_val;
+  src.flat_idx = m.flat_idx;
+  src.vals = m.vals;
+  src.cols = m.cols;
+  if (fg.loff_lds) {
     int* l = sm + 33 * nch;
-    for (int k = t; k <= 16 * bpr; k += 256) l[k] = off[src.g0 + k];
+    for (int k = t; k <= 16 * bpr; k += 256) l[k] = m.off[src.g0 + k];
     __syncthreads();
     src.loff = l;
   }
-  aq::tile_row_sort(src, rb, nch, src.rs[0], src.rs[16], sm, part, tile_ptr, tile_ent, tile_max);
+  aq::tile_row_sort(src, rb, nch, src.rs[0], src.rs[16], sm, part, m.tile_ptr, m.tile_ent, m.tile_max);
 }
 
 // ---- calculate_zscore_manual of one block of n elements
@@ -1328,44 +1352,118 @@ extern "C" int aq_quantize_finish(int64_t numel, int64_t G, int64_t K, const int
   return AQ_OK;
 }
 
+// Checks one member of aq_quantize_finish_tiles(_grouped) and fills its
+// FinishMember (fg->G, bpr, nch set by the caller).
+static int finish_tiles_member(const char* fn, int64_t numel, int64_t G, int64_t K, const int32_t* block_off,
+                               int64_t nnz, const void* workspace, int64_t ws_bytes, int64_t* flat_idx, void* vals,
+                               int32_t* cols, int32_t* tile_ptr, uint32_t* tile_ent, int32_t* tile_max,
+                               FinishMember* out) {
+  AQ_CHECK_ARG(numel > 0 && G >= 1 && G <= kMaxG, "%s: bad numel/G", fn);
+  AQ_CHECK_ARG(K >= 64 && K % 64 == 0 && K % G == 0 && numel % (16 * K) == 0 && K < (1 << 30) &&
+                   (numel / K / 16) * (K / 64) < ((int64_t)1 << 31),
+               "%s: needs K %% 64 == 0, a block dividing K and rows %% 16 == 0 (numel=%lld K=%lld G=%lld)", fn,
+               (long long)numel, (long long)K, (long long)G);
+  const int64_t nblocks = numel / G;
+  if (ws_bytes < workspace_bytes(numel, nblocks))
+    return aq::set_error(AQ_EWORKSPACE, "%s: workspace too small", fn);
+  AQ_CHECK_ARG(block_off && workspace && tile_ptr && tile_ent && (nnz == 0 || (flat_idx && vals && cols)),
+               "%s: null pointer argument", fn);
+  const Workspace w = carve((void*)workspace, numel, nblocks);
+  FinishMember m;
+  m.off = block_off;
+  m.stage_col = w.stage_col;
+  m.stage_val = w.stage_val;
+  m.flat_idx = flat_idx;
+  m.vals = (uint16_t*)vals;
+  m.cols = cols;
+  m.tile_ptr = tile_ptr;
+  m.tile_ent = tile_ent;
+  m.tile_max = tile_max;
+  m.nrb = (int)(numel / K / 16);
+  *out = m;
+  return AQ_OK;
+}
+
+// One launch for the group's members (all of one block size G and row length K).
+static int launch_finish_tiles(FinishGroup& fg, int64_t G, int64_t K, const char* fn, hipStream_t s) {
+  const int64_t nch = K / 64, bpr = K / G;
+  fg.G = G;
+  fg.bpr = (int)bpr;
+  fg.nch = (int)nch;
+  fg.first[0] = 0;
+  for (int i = 0; i < fg.count; i++) fg.first[i + 1] = fg.first[i] + fg.m[i].nrb + 1;
+  for (int i = fg.count + 1; i <= kMaxQGroup; i++) fg.first[i] = fg.first[fg.count];
+  // the tile row's block offsets go to LDS when the sort leaves room (64 KiB in all)
+  const int64_t sort_ints = 33 * nch;
+  fg.loff_lds = bpr > 1 && sort_ints + 16 * bpr + 1 <= 16384;
+  const size_t lds = (size_t)(sort_ints + (fg.loff_lds ? 16 * bpr + 1 : 0)) * sizeof(int);
+  hipLaunchKernelGGL(finish_tiles_kernel, dim3((unsigned)fg.first[fg.count]), dim3(256), lds, s, fg);
+  AQ_LAUNCH_CHECK(fn);
+  return AQ_OK;
+}
+
+// Rows too wide for one workgroup's LDS: the flat list, then the block lists
+// from it (one thread per block), the block offsets serving as the CSR row
+// pointer at a stride of K / G.
+static int finish_tiles_wide(int64_t numel, int64_t G, int64_t K, const int32_t* block_off, int64_t nnz,
+                             const void* workspace, int64_t ws_bytes, int64_t* flat_idx, void* vals, int32_t* cols,
+                             int32_t* tile_ptr, uint32_t* tile_ent, int32_t* tile_max, const char* fn,
+                             hipStream_t s) {
+  const int rc = aq_quantize_finish(numel, G, K, block_off, nnz, workspace, ws_bytes, flat_idx, vals, cols, s);
+  if (rc != AQ_OK) return rc;
+  const hipError_t e = aq::launch_outlier_tiles(block_off, K / G, cols, (const uint16_t*)vals, numel / K, K,
+                                                tile_ptr, tile_ent, tile_max, s);
+  if (e != hipSuccess) return aq::check_hip(e, fn);
+  return AQ_OK;
+}
+
 extern "C" int aq_quantize_finish_tiles(int64_t numel, int64_t G, int64_t K, const int32_t* block_off, int64_t nnz,
                                         const void* workspace, int64_t ws_bytes, int64_t* flat_idx, void* vals,
                                         int32_t* cols, int32_t* tile_ptr, uint32_t* tile_ent, int32_t* tile_max,
                                         void* stream) {
-  AQ_CHECK_ARG(numel > 0 && G >= 1 && G <= kMaxG, "aq_quantize_finish_tiles: bad numel/G");
-  AQ_CHECK_ARG(K >= 64 && K % 64 == 0 && K % G == 0 && numel % (16 * K) == 0 && K < (1 << 30) &&
-                   (numel / K / 16) * (K / 64) < ((int64_t)1 << 31),
-               "aq_quantize_finish_tiles: needs K %% 64 == 0, a block dividing K and rows %% 16 == 0 "
-               "(numel=%lld K=%lld G=%lld)",
-               (long long)numel, (long long)K, (long long)G);
-  const int64_t nblocks = numel / G;
-  if (ws_bytes < workspace_bytes(numel, nblocks))
-    return aq::set_error(AQ_EWORKSPACE, "aq_quantize_finish_tiles: workspace too small");
-  AQ_CHECK_ARG(block_off && workspace && tile_ptr && tile_ent && (nnz == 0 || (flat_idx && vals && cols)),
-               "aq_quantize_finish_tiles: null pointer argument");
-  const int64_t N = numel / K, nch = K / 64, bpr = K / G;
+  static const char* fn = "aq_quantize_finish_tiles";
+  FinishGroup fg{};
+  int rc = finish_tiles_member(fn, numel, G, K, block_off, nnz, workspace, ws_bytes, flat_idx, vals, cols, tile_ptr,
+                               tile_ent, tile_max, &fg.m[0]);
+  if (rc != AQ_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
-  if (nch > aq::kTileRowsMaxChunks) {
-    // rows too wide for one workgroup's LDS: the flat list, then the block
-    // lists from it (one thread per block), the block offsets serving as
-    // the CSR row pointer at a stride of K / G
-    const int rc = aq_quantize_finish(numel, G, K, block_off, nnz, workspace, ws_bytes, flat_idx, vals, cols, stream);
+  if (K / 64 > aq::kTileRowsMaxChunks)
+    return finish_tiles_wide(numel, G, K, block_off, nnz, workspace, ws_bytes, flat_idx, vals, cols, tile_ptr,
+                             tile_ent, tile_max, fn, s);
+  fg.count = 1;
+  return launch_finish_tiles(fg, G, K, fn, s);
+}
+
+extern "C" int aq_quantize_finish_tiles_grouped(int64_t count, const int64_t* numels, int64_t G, int64_t K,
+                                                const int32_t* const* block_offs, const int64_t* nnzs,
+                                                const void* const* workspaces, const int64_t* ws_bytes,
+                                                int64_t* const* flat_idx, void* const* vals, int32_t* const* cols,
+                                                int32_t* const* tile_ptrs, uint32_t* const* tile_ents,
+                                                int32_t* tile_max, void* stream) {
+  static const char* fn = "aq_quantize_finish_tiles_grouped";
+  AQ_CHECK_ARG(count >= 1 && count <= kMaxQGroup, "%s: 1..%d weights, got %lld", fn, kMaxQGroup, (long long)count);
+  AQ_CHECK_ARG(numels && block_offs && nnzs && workspaces && ws_bytes && flat_idx && vals && cols && tile_ptrs &&
+                   tile_ents,
+               "%s: null pointer argument", fn);
+  FinishGroup fg{};
+  for (int i = 0; i < (int)count; i++) {
+    const int rc = finish_tiles_member(fn, numels[i], G, K, block_offs[i], nnzs[i], workspaces[i], ws_bytes[i],
+                                       flat_idx[i], vals[i], cols[i], tile_ptrs[i], tile_ents[i],
+                                       tile_max ? tile_max + i : nullptr, &fg.m[i]);
     if (rc != AQ_OK) return rc;
-    const hipError_t e = aq::launch_outlier_tiles(block_off, bpr, cols, (const uint16_t*)vals, N, K, tile_ptr,
-                                                  tile_ent, tile_max, s);
-    if (e != hipSuccess) return aq::check_hip(e, "aq_quantize_finish_tiles: block list launch");
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (K / 64 > aq::kTileRowsMaxChunks) {
+    for (int i = 0; i < (int)count; i++) {
+      const int rc = finish_tiles_wide(numels[i], G, K, block_offs[i], nnzs[i], workspaces[i], ws_bytes[i],
+                                       flat_idx[i], vals[i], cols[i], tile_ptrs[i], tile_ents[i],
+                                       tile_max ? tile_max + i : nullptr, fn, s);
+      if (rc != AQ_OK) return rc;
+    }
     return AQ_OK;
   }
-  Workspace w = carve((void*)workspace, numel, nblocks);
-  // the tile row's block offsets go to LDS when the sort leaves room (64 KiB in all)
-  const int64_t sort_ints = 33 * nch;
-  const int loff_lds = bpr > 1 && sort_ints + 16 * bpr + 1 <= 16384;
-  const size_t lds = (size_t)(sort_ints + (loff_lds ? 16 * bpr + 1 : 0)) * sizeof(int);
-  hipLaunchKernelGGL(finish_tiles_kernel, dim3((unsigned)(N / 16 + 1)), dim3(256), lds, s, block_off, G, (int)bpr,
-                     (int)(N / 16), (int)nch, loff_lds, w.stage_col, w.stage_val, flat_idx, (uint16_t*)vals, cols,
-                     tile_ptr, tile_ent, tile_max);
-  AQ_LAUNCH_CHECK("aq_quantize_finish_tiles: launch");
-  return AQ_OK;
+  fg.count = (int)count;
+  return launch_finish_tiles(fg, G, K, fn, s);
 }
 
 extern "C" int aq_zscore(const void* x, int64_t n, float eps, void* z, void* stats, void* stream) {

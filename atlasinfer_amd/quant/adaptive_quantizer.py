@@ -297,35 +297,28 @@ def _quantize_prepare(fp16_tensor: torch.Tensor, G: int, z_threshold: float, cod
                 stream=_lib.stream_of(dev))
 
 
-def _quantize_complete(p: dict, nnz: int, tmax: Optional[torch.Tensor] = None) -> QuantizedTensor:
-    """The outlier lists, CSR rows and block lists of a tensor whose
-    aq_quantize (or group) has run, given its outlier count.  ``tmax``: a
-    zeroed one-element int32 device tensor to receive the largest block
-    count (allocated here if not given)."""
-    L = _lib.load()
-    dev, stream, G, K, N = p["dev"], p["stream"], p["G"], p["K"], p["N"]
-    numel, padded, fmt, layout = p["numel"], p["padded"], p["fmt"], p["layout"]
-    block_off, codes, ws, ws_bytes = p["block_off"], p["codes"], p["ws"], p["ws_bytes"]
+def _finish_outputs(p: dict, nnz: int):
+    """The outlier list tensors of a tensor with ``nnz`` outliers (flat
+    indices, values, columns) and, for the tiled layout, its block lists
+    (tile_ptr, tile_ent with 64 entries of read padding); None otherwise."""
+    dev, N, K = p["dev"], p["N"], p["K"]
     flat_idx = torch.empty(nnz, dtype=torch.int64, device=dev)
     vals = torch.empty(nnz, dtype=torch.float16, device=dev)
     cols = torch.empty(nnz, dtype=torch.int32, device=dev)
     tiles = None
-    if layout == "tiled":
-        # the flat list and the 16 x 64 block lists in one launch; the
-        # largest block count is read when first used
-        tile_ptr = torch.empty((N // 16) * (K // 64) + 1, dtype=torch.int32, device=dev)
-        tile_ent = torch.empty(nnz + 64, dtype=torch.int32, device=dev)
-        if tmax is None:
-            tmax = torch.zeros(1, dtype=torch.int32, device=dev)
-        _lib.check(L.aq_quantize_finish_tiles(numel, G, K, block_off.data_ptr(), nnz, ws.data_ptr(), ws_bytes,
-                                              _lib.ptr(flat_idx), _lib.ptr(vals), _lib.ptr(cols),
-                                              tile_ptr.data_ptr(), tile_ent.data_ptr(), tmax.data_ptr(), stream),
-                   "aq_quantize_finish_tiles")
-        tiles = (tile_ptr, tile_ent, DeviceInt(tmax[0]) if nnz else 0)
-    else:
-        _lib.check(L.aq_quantize_finish(numel, G, K, block_off.data_ptr(), nnz, ws.data_ptr(), ws_bytes,
-                                        _lib.ptr(flat_idx), _lib.ptr(vals), _lib.ptr(cols), stream),
-                   "aq_quantize_finish")
+    if p["layout"] == "tiled":
+        tiles = (torch.empty((N // 16) * (K // 64) + 1, dtype=torch.int32, device=dev),
+                 torch.empty(nnz + 64, dtype=torch.int32, device=dev))
+    return flat_idx, vals, cols, tiles
+
+
+def _finished_tensor(p: dict, nnz: int, flat_idx, vals, cols, tiles, tmax) -> QuantizedTensor:
+    """The QuantizedTensor of a tensor whose outlier lists are written (and,
+    for int8, its compacted codes, built here); ``tmax`` holds the largest
+    block count of the tiled layout's lists (read when first used)."""
+    L = _lib.load()
+    dev, stream, G, K, N = p["dev"], p["stream"], p["G"], p["K"], p["N"]
+    block_off, codes, padded = p["block_off"], p["codes"], p["padded"]
     if K % G == 0:
         # blocks tile the rows, so a row's first outlier is its first block's:
         # the CSR row pointers are every (K / G)-th block offset (per output
@@ -335,13 +328,17 @@ def _quantize_complete(p: dict, nnz: int, tmax: Optional[torch.Tensor] = None) -
         row_ptr = torch.empty(N + 1, dtype=torch.int32, device=dev)
         _lib.check(L.aq_segment_offsets(_lib.ptr(flat_idx), nnz, N, K, row_ptr.data_ptr(), stream),
                    "aq_segment_offsets")
-    if fmt == _lib.FMT_INT8:
+    if p["fmt"] == _lib.FMT_INT8:
         fp8_data = torch.empty(padded - nnz, dtype=torch.int8, device=dev)
         _lib.check(L.aq_compact_codes(codes.data_ptr(), padded, _lib.ptr(flat_idx), nnz, _lib.ptr(fp8_data),
                                       stream), "aq_compact_codes")
     else:
         fp8_data = codes.view(torch.float8_e4m3fn)
     p["ws"] = None
+    extra = {}
+    if tiles is not None:
+        extra = dict(outlier_tile_ptr=tiles[0], outlier_tile_ent=tiles[1],
+                     outlier_tile_max=DeviceInt(tmax[0]) if nnz else 0)
     qt = QuantizedTensor(
         fp8_data=fp8_data,
         fp16_outliers=vals,
@@ -352,11 +349,49 @@ def _quantize_complete(p: dict, nnz: int, tmax: Optional[torch.Tensor] = None) -
         code_format=p["code_format"],
         outlier_row_ptr=row_ptr,
         outlier_cols=cols,
-        code_layout=layout,
+        code_layout=p["layout"],
+        **extra,
     )
-    if tiles is not None:
-        qt = qt._replace(outlier_tile_ptr=tiles[0], outlier_tile_ent=tiles[1], outlier_tile_max=tiles[2])
     return qt.to(p["input_device"])
+
+
+def _quantize_complete(p: dict, nnz: int) -> QuantizedTensor:
+    """The outlier lists, CSR rows and block lists of a tensor whose
+    aq_quantize has run, given its outlier count: the tiled layout's flat
+    list and 16 x 64 block lists in one launch (aq_quantize_finish_tiles),
+    the flat list alone otherwise (aq_quantize_finish)."""
+    L = _lib.load()
+    flat_idx, vals, cols, tiles = _finish_outputs(p, nnz)
+    args = (p["numel"], p["G"], p["K"], p["block_off"].data_ptr(), nnz, p["ws"].data_ptr(), p["ws_bytes"],
+            _lib.ptr(flat_idx), _lib.ptr(vals), _lib.ptr(cols))
+    tmax = None
+    if tiles is not None:
+        tmax = torch.zeros(1, dtype=torch.int32, device=p["dev"])
+        _lib.check(L.aq_quantize_finish_tiles(*args, tiles[0].data_ptr(), tiles[1].data_ptr(), tmax.data_ptr(),
+                                              p["stream"]), "aq_quantize_finish_tiles")
+    else:
+        _lib.check(L.aq_quantize_finish(*args, p["stream"]), "aq_quantize_finish")
+    return _finished_tensor(p, nnz, flat_idx, vals, cols, tiles, tmax)
+
+
+def _quantize_complete_group(ps: list, nnzs: list) -> list:
+    """_quantize_complete for the members of one aq_quantize_grouped launch
+    (one block size, row length and layout): for the tiled layout one
+    aq_quantize_finish_tiles_grouped launch and one zero fill serve them all."""
+    if ps[0]["layout"] != "tiled":
+        return [_quantize_complete(p, nnz) for p, nnz in zip(ps, nnzs)]
+    L = _lib.load()
+    arr = _lib.ptr_array
+    outs = [_finish_outputs(p, nnz) for p, nnz in zip(ps, nnzs)]
+    tmaxs = torch.zeros(len(ps), dtype=torch.int32, device=ps[0]["dev"])
+    _lib.check(L.aq_quantize_finish_tiles_grouped(
+        len(ps), arr([p["numel"] for p in ps], ctypes.c_int64), ps[0]["G"], ps[0]["K"],
+        arr([p["block_off"].data_ptr() for p in ps]), arr(nnzs, ctypes.c_int64), arr([p["ws"].data_ptr() for p in ps]),
+        arr([p["ws_bytes"] for p in ps], ctypes.c_int64), arr([_lib.ptr(o[0]) for o in outs]),
+        arr([_lib.ptr(o[1]) for o in outs]), arr([_lib.ptr(o[2]) for o in outs]),
+        arr([o[3][0].data_ptr() for o in outs]), arr([o[3][1].data_ptr() for o in outs]), tmaxs.data_ptr(),
+        ps[0]["stream"]), "aq_quantize_finish_tiles_grouped")
+    return [_finished_tensor(p, nnz, *o, tmaxs[k:k + 1]) for k, (p, nnz, o) in enumerate(zip(ps, nnzs, outs))]
 
 
 # weights per aq_quantize_grouped launch, most blocks a member may have, and
@@ -406,10 +441,10 @@ def quantize_tensors(tensors, block_size: int = 128, z_threshold: float = 3.0, *
 
     def complete(entry):
         # the run's one host sync: every member's outlier count
-        run_i, ps_i, counts, done, tmaxs = entry
+        run_i, ps_i, counts, done = entry
         done.synchronize()
-        for k, (i, p, nnz) in enumerate(zip(run_i, ps_i, counts.tolist())):
-            out[i] = _quantize_complete(p, int(nnz), tmaxs[k:k + 1])
+        for i, qt in zip(run_i, _quantize_complete_group(ps_i, [int(n) for n in counts.tolist()])):
+            out[i] = qt
 
     inflight = None  # the run launched last, completed once the next one is queued
     for run in runs:
@@ -430,11 +465,9 @@ def quantize_tensors(tensors, block_size: int = 128, z_threshold: float = 3.0, *
         counts.copy_(torch.stack([p["block_off"][p["nblocks"]] for p in ps]), non_blocking=True)
         done = torch.cuda.Event()
         done.record(torch.cuda.current_stream(ps[0]["dev"]))
-        # the members' largest block counts, zeroed by one fill
-        tmaxs = torch.zeros(len(ps), dtype=torch.int32, device=ps[0]["dev"])
         if inflight is not None:
             complete(inflight)
-        inflight = (run, ps, counts, done, tmaxs)
+        inflight = (run, ps, counts, done)
     if inflight is not None:
         complete(inflight)
     return out

@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define AQ_ABI_VERSION 8
+#define AQ_ABI_VERSION 9
 
 enum { AQ_FMT_INT8 = 0, AQ_FMT_E4M3 = 1 };
 enum { AQ_LAYOUT_FLAT = 0, AQ_LAYOUT_TILED = 1 };
@@ -160,6 +160,25 @@ int aq_outlier_tiles(const int32_t* row_ptr, const int32_t* cols, const void* va
 int aq_quantize_finish_tiles(int64_t numel, int64_t G, int64_t K, const int32_t* block_off, int64_t nnz,
                              const void* workspace, int64_t workspace_bytes, int64_t* flat_idx, void* vals,
                              int32_t* cols, int32_t* tile_ptr, uint32_t* tile_ent, int32_t* tile_max, void* stream);
+
+/*
+ * aq_quantize_finish_tiles for up to 8 weights of one block size G and row
+ * length K in one launch (the members of an aq_quantize_grouped call): per
+ * member i the arguments of aq_quantize_finish_tiles (numels[i],
+ * block_offs[i], nnzs[i], workspaces[i] of ws_bytes[i], flat_idx[i],
+ * vals[i], cols[i], tile_ptrs[i], tile_ents[i]); tile_max, if not NULL,
+ * points to count zeroed counts, member i's at tile_max[i].  Results are
+ * those of aq_quantize_finish_tiles on each member, bit for bit.  No
+ * counterpart of its own in the reference (quantize_tensor,
+ * adaptive_quantizer.py:109-117,137-138, finishes one tensor): for callers
+ * that quantize a layer's weights together.
+ */
+int aq_quantize_finish_tiles_grouped(int64_t count, const int64_t* numels, int64_t G, int64_t K,
+                                     const int32_t* const* block_offs, const int64_t* nnzs,
+                                     const void* const* workspaces, const int64_t* ws_bytes,
+                                     int64_t* const* flat_idx, void* const* vals, int32_t* const* cols,
+                                     int32_t* const* tile_ptrs, uint32_t* const* tile_ents, int32_t* tile_max,
+                                     void* stream);
 
 /*
  * Reference layout <-> dense flat codes.  The reference stores only the codes

@@ -29,7 +29,7 @@ def test_header_declares_the_expected_api():
     names = declared_functions()
     for must in ["aq_abi_version", "aq_last_error", "aq_quantize", "aq_quantize_finish", "aq_dequantize",
                  "aq_qlinear", "aq_zscore", "aq_compact_codes", "aq_expand_codes", "aq_segment_offsets",
-                 "aq_outlier_tiles", "aq_quantize_finish_tiles"]:
+                 "aq_outlier_tiles", "aq_quantize_finish_tiles", "aq_quantize_finish_tiles_grouped"]:
         assert must in names
 
 
@@ -81,6 +81,15 @@ def test_bad_arguments_return_einval_with_message(lib):
     assert lib.aq_quantize_finish_tiles(20 * 128, 128, 128, p, 0, p, ws, p, p, p, p, p, None, None) == AQ_EINVAL
     assert lib.aq_quantize_finish_tiles(16 * 128, 128, 128, p, 5, p, ws, p, p, None, p, p, None, None) == AQ_EINVAL
     assert b"null pointer" in lib.aq_last_error()
+    arr = lambda *v: (ctypes.c_int64 * len(v))(*v)  # noqa: E731
+    ptrs = (ctypes.c_void_p * 1)(16)
+    assert lib.aq_quantize_finish_tiles_grouped(0, arr(2048), 128, 128, ptrs, arr(0), ptrs, arr(ws), ptrs, ptrs,
+                                                ptrs, ptrs, ptrs, None, None) == AQ_EINVAL
+    assert b"aq_quantize_finish_tiles_grouped" in lib.aq_last_error()
+    assert lib.aq_quantize_finish_tiles_grouped(9, arr(2048), 128, 128, ptrs, arr(0), ptrs, arr(ws), ptrs, ptrs,
+                                                ptrs, ptrs, ptrs, None, None) == AQ_EINVAL
+    assert lib.aq_quantize_finish_tiles_grouped(1, arr(20 * 128), 128, 128, ptrs, arr(0), ptrs, arr(ws), ptrs, ptrs,
+                                                ptrs, ptrs, ptrs, None, None) == AQ_EINVAL
     assert lib.aq_dequantize(p, p, 10, 0, 0, 10, 0, None, None, 0, p, None) == AQ_EINVAL
     assert lib.aq_zscore(p, 0, 1e-6, p, None, None) == AQ_EINVAL
     assert lib.aq_tile_codes(p, 20, 128, p, None) == AQ_EINVAL

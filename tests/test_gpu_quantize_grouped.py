@@ -47,3 +47,13 @@ def test_more_members_than_one_launch_takes():
     ws = [_w((256, 4096), 40 + i) for i in range(11)]
     for w, q in zip(ws, AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")):
         _same(q, AQ.quantize_tensor(w, block_size=-1, code_format="e4m3"))
+
+
+def test_grouped_wide_rows():
+    """Rows wider than one workgroup's block-list sort (K = 32768: 512
+    chunks of 64): the grouped finish takes each member's two-launch path;
+    results as quantize_tensor gives them."""
+    ws = [_w((32, 32768), 60 + i) for i in range(3)]
+    for w, q in zip(ws, AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")):
+        assert q.outlier_tile_ptr is not None
+        _same(q, AQ.quantize_tensor(w, block_size=-1, code_format="e4m3"))

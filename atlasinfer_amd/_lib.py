@@ -17,7 +17,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libatlasinfer_amd.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 FMT_INT8 = 0
 FMT_E4M3 = 1
@@ -39,7 +39,7 @@ SIGNATURES = {
     "aq_quantize": (ctypes.c_int, [_P, _I64, _I64, ctypes.c_uint16, ctypes.c_int, _I64, ctypes.c_int, _P, _P, _I32P,
                                    _P, _I64, _P]),
     "aq_quantize_grouped": (ctypes.c_int, [_I64, _P, _P, _I64, ctypes.c_uint16, ctypes.c_int, _I64, ctypes.c_int, _P,
-                                           _P, _P, _P, _P, _P]),
+                                           _P, _P, _P, _P, _I32P, _P]),
     "aq_quantize_finish": (ctypes.c_int, [_I64, _I64, _I64, _I32P, _I64, _P, _I64, _P, _P, _I32P, _P]),
     "aq_segment_offsets": (ctypes.c_int, [_P, _I64, _I64, _I64, _I32P, _P]),
     "aq_outlier_cols": (ctypes.c_int, [_P, _I64, _I64, _I32P, _P]),

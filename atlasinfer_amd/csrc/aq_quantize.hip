@@ -916,6 +916,7 @@ constexpr int kScanSmall = 1024 * 16;
 struct ScanGroup {
   int32_t* off[kMaxQGroup];
   int64_t n[kMaxQGroup];
+  int32_t* totals;  // [count] or null: member i's total also goes to totals[i]
 };
 __global__ __launch_bounds__(1024) void scan_small_kernel(ScanGroup sg) {
   int32_t* const off = sg.off[blockIdx.x];
@@ -953,7 +954,10 @@ __global__ __launch_bounds__(1024) void scan_small_kernel(ScanGroup sg) {
     }
     carry += total;
   }
-  if (threadIdx.x == 0) off[n] = carry;
+  if (threadIdx.x == 0) {
+    off[n] = carry;
+    if (sg.totals) sg.totals[blockIdx.x] = carry;
+  }
 }
 
 // ---- gather the staged outliers into the ascending list
@@ -1299,7 +1303,7 @@ extern "C" int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_t
 extern "C" int aq_quantize_grouped(int64_t count, const void* const* xs, const int64_t* numels, int64_t G,
                                    uint16_t z_thr_f16, int fmt, int64_t K, int layout, void* const* codes,
                                    void* const* scales, int32_t* const* block_offs, void* const* workspaces,
-                                   const int64_t* ws_bytes, void* stream) {
+                                   const int64_t* ws_bytes, int32_t* totals, void* stream) {
   AQ_CHECK_ARG(count >= 1 && count <= kMaxQGroup, "aq_quantize_grouped: 1..%d weights, got %lld", kMaxQGroup,
                (long long)count);
   AQ_CHECK_ARG(xs && numels && codes && scales && block_offs && workspaces && ws_bytes,
@@ -1318,6 +1322,7 @@ extern "C" int aq_quantize_grouped(int64_t count, const void* const* xs, const i
     sg.n[i] = q.m[i].nblocks;
   }
   q.count = (int)count;
+  sg.totals = totals;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = launch_quantize(q, s);
   if (e != hipSuccess) return aq::check_hip(e, "aq_quantize_grouped: quantize kernel launch");

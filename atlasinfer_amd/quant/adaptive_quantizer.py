@@ -55,14 +55,15 @@ class DeviceInt:
     pays the wait.  That first use makes a device-to-host copy, which HIP
     graph capture does not allow: a caller that captures should use the
     value once before capturing (GraphDecoder's eager warm-up steps do)."""
-    __slots__ = ("_t", "_v")
+    __slots__ = ("_t", "_i", "_v")
 
-    def __init__(self, t: torch.Tensor):
-        self._t, self._v = t, None
+    def __init__(self, t: torch.Tensor, index: Optional[int] = None):
+        # the value is t[index] (t itself when index is None)
+        self._t, self._i, self._v = t, index, None
 
     def _get(self) -> int:
         if self._v is None:
-            self._v = int(self._t.item())
+            self._v = int((self._t if self._i is None else self._t[self._i]).item())
             self._t = None
         return self._v
 
@@ -267,57 +268,72 @@ def quantize_tensor(
     return _quantize_complete(p, nnz)
 
 
+def _member_prepare(fp16_tensor: torch.Tensor, G: int, fmt: int, code_format: str, layout: str,
+                    dev: torch.device) -> dict:
+    """The outputs of one tensor's quantize (numel > 0, fp16) that do not
+    depend on its outlier count: codes (E4M3 codes allocated as
+    float8_e4m3fn, the dtype they are handed out in; int8 codes as bytes in
+    element order, compacted later), scales, block offsets and, for the
+    tiled layout, the block lists' pointer array."""
+    original_shape = fp16_tensor.shape
+    numel = fp16_tensor.numel()
+    x = fp16_tensor if fp16_tensor.device == dev and fp16_tensor.is_contiguous() else \
+        fp16_tensor.to(dev).contiguous()
+    N, K = _rows_cols(original_shape)
+    nblocks = (numel + G - 1) // G
+    padded = nblocks * G
+    codes = torch.empty(padded, dtype=torch.float8_e4m3fn if fmt == _lib.FMT_E4M3 else torch.uint8, device=dev)
+    scales = torch.empty(nblocks, dtype=torch.float16, device=dev)
+    block_off = torch.empty(nblocks + 1, dtype=torch.int32, device=dev)
+    tile_ptr = None
+    if layout == "tiled":
+        tile_ptr = torch.empty((N // 16) * (K // 64) + 1, dtype=torch.int32, device=dev)
+    return dict(x=x, input_device=fp16_tensor.device, original_shape=original_shape, numel=numel, G=G, N=N, K=K,
+                nblocks=nblocks, padded=padded, layout=layout, codes=codes, scales=scales, block_off=block_off,
+                tile_ptr=tile_ptr, fmt=fmt, code_format=code_format, dev=dev)
+
+
+def _layout_of(fmt: int, shape, G: int) -> str:
+    # e4m3 codes go straight into the layout the fused kernels read; int8
+    # codes stay in element order for the reference's compacted stream
+    return "tiled" if (fmt == _lib.FMT_E4M3 and tiled_eligible(shape, G)) else "flat"
+
+
 def _quantize_prepare(fp16_tensor: torch.Tensor, G: int, z_threshold: float, code_format: str, fmt: int) -> dict:
     """Outputs, workspace and aq_quantize arguments of one tensor (numel > 0,
     fp16)."""
     L = _lib.load()
     if G > L.aq_max_block_size():
         raise ValueError(f"block_size {G} exceeds the supported maximum {L.aq_max_block_size()}")
-    input_device = fp16_tensor.device
-    original_shape = fp16_tensor.shape
-    numel = fp16_tensor.numel()
-    dev = _lib.compute_device(input_device)
-    x = fp16_tensor.to(dev).contiguous().view(-1)
-    N, K = _rows_cols(original_shape)
-    nblocks = (numel + G - 1) // G
-    padded = nblocks * G
-    # e4m3 codes go straight into the layout the fused kernels read; int8
-    # codes stay in element order for the reference's compacted stream
-    layout = "tiled" if (fmt == _lib.FMT_E4M3 and tiled_eligible(original_shape, G)) else "flat"
-    codes = torch.empty(padded, dtype=torch.uint8, device=dev)
-    scales = torch.empty(nblocks, dtype=torch.float16, device=dev)
-    block_off = torch.empty(nblocks + 1, dtype=torch.int32, device=dev)
-    ws_bytes = int(L.aq_quantize_workspace_size(numel, G))
+    dev = _lib.compute_device(fp16_tensor.device)
+    p = _member_prepare(fp16_tensor, G, fmt, code_format, _layout_of(fmt, fp16_tensor.shape, G), dev)
+    ws_bytes = int(L.aq_quantize_workspace_size(p["numel"], G))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    args = (x.data_ptr(), numel, G, _threshold_bits(z_threshold), fmt, K, _lib.LAYOUTS[layout], codes.data_ptr(),
-            scales.data_ptr(), block_off.data_ptr(), ws.data_ptr(), ws_bytes)
-    return dict(x=x, input_device=input_device, original_shape=original_shape, numel=numel, G=G, N=N, K=K,
-                nblocks=nblocks, padded=padded, layout=layout, codes=codes, scales=scales, block_off=block_off,
-                ws=ws, ws_bytes=ws_bytes, args=args, fmt=fmt, code_format=code_format, dev=dev,
-                stream=_lib.stream_of(dev))
+    p.update(ws=ws, ws_ptr=ws.data_ptr(), ws_bytes=ws_bytes, stream=_lib.stream_of(dev))
+    p["args"] = (p["x"].data_ptr(), p["numel"], G, _threshold_bits(z_threshold), fmt, p["K"],
+                 _lib.LAYOUTS[p["layout"]], p["codes"].data_ptr(), p["scales"].data_ptr(), p["block_off"].data_ptr(),
+                 ws.data_ptr(), ws_bytes)
+    return p
 
 
 def _finish_outputs(p: dict, nnz: int):
     """The outlier list tensors of a tensor with ``nnz`` outliers (flat
-    indices, values, columns) and, for the tiled layout, its block lists
-    (tile_ptr, tile_ent with 64 entries of read padding); None otherwise."""
-    dev, N, K = p["dev"], p["N"], p["K"]
+    indices, values, columns) and, for the tiled layout, its block-list
+    entries (64 entries of read padding after the last); None otherwise."""
+    dev = p["dev"]
     flat_idx = torch.empty(nnz, dtype=torch.int64, device=dev)
     vals = torch.empty(nnz, dtype=torch.float16, device=dev)
     cols = torch.empty(nnz, dtype=torch.int32, device=dev)
-    tiles = None
-    if p["layout"] == "tiled":
-        tiles = (torch.empty((N // 16) * (K // 64) + 1, dtype=torch.int32, device=dev),
-                 torch.empty(nnz + 64, dtype=torch.int32, device=dev))
-    return flat_idx, vals, cols, tiles
+    tile_ent = torch.empty(nnz + 64, dtype=torch.int32, device=dev) if p["layout"] == "tiled" else None
+    return flat_idx, vals, cols, tile_ent
 
 
-def _finished_tensor(p: dict, nnz: int, flat_idx, vals, cols, tiles, tmax) -> QuantizedTensor:
+def _finished_tensor(p: dict, nnz: int, flat_idx, vals, cols, tile_ent, tmax: Optional[DeviceInt]) -> QuantizedTensor:
     """The QuantizedTensor of a tensor whose outlier lists are written (and,
     for int8, its compacted codes, built here); ``tmax`` holds the largest
     block count of the tiled layout's lists (read when first used)."""
     L = _lib.load()
-    dev, stream, G, K, N = p["dev"], p["stream"], p["G"], p["K"], p["N"]
+    dev, G, K, N = p["dev"], p["G"], p["K"], p["N"]
     block_off, codes, padded = p["block_off"], p["codes"], p["padded"]
     if K % G == 0:
         # blocks tile the rows, so a row's first outlier is its first block's:
@@ -326,19 +342,19 @@ def _finished_tensor(p: dict, nnz: int, flat_idx, vals, cols, tiles, tmax) -> Qu
         row_ptr = block_off if G == K else block_off[::K // G].contiguous()
     else:
         row_ptr = torch.empty(N + 1, dtype=torch.int32, device=dev)
-        _lib.check(L.aq_segment_offsets(_lib.ptr(flat_idx), nnz, N, K, row_ptr.data_ptr(), stream),
+        _lib.check(L.aq_segment_offsets(_lib.ptr(flat_idx), nnz, N, K, row_ptr.data_ptr(), p["stream"]),
                    "aq_segment_offsets")
     if p["fmt"] == _lib.FMT_INT8:
         fp8_data = torch.empty(padded - nnz, dtype=torch.int8, device=dev)
         _lib.check(L.aq_compact_codes(codes.data_ptr(), padded, _lib.ptr(flat_idx), nnz, _lib.ptr(fp8_data),
-                                      stream), "aq_compact_codes")
+                                      p["stream"]), "aq_compact_codes")
     else:
-        fp8_data = codes.view(torch.float8_e4m3fn)
-    p["ws"] = None
+        fp8_data = codes
+    p.pop("ws", None)
     extra = {}
-    if tiles is not None:
-        extra = dict(outlier_tile_ptr=tiles[0], outlier_tile_ent=tiles[1],
-                     outlier_tile_max=DeviceInt(tmax[0]) if nnz else 0)
+    if tile_ent is not None:
+        extra = dict(outlier_tile_ptr=p["tile_ptr"], outlier_tile_ent=tile_ent,
+                     outlier_tile_max=tmax if nnz else 0)
     qt = QuantizedTensor(
         fp8_data=fp8_data,
         fp16_outliers=vals,
@@ -361,43 +377,86 @@ def _quantize_complete(p: dict, nnz: int) -> QuantizedTensor:
     list and 16 x 64 block lists in one launch (aq_quantize_finish_tiles),
     the flat list alone otherwise (aq_quantize_finish)."""
     L = _lib.load()
-    flat_idx, vals, cols, tiles = _finish_outputs(p, nnz)
-    args = (p["numel"], p["G"], p["K"], p["block_off"].data_ptr(), nnz, p["ws"].data_ptr(), p["ws_bytes"],
+    flat_idx, vals, cols, tile_ent = _finish_outputs(p, nnz)
+    args = (p["numel"], p["G"], p["K"], p["block_off"].data_ptr(), nnz, p["ws_ptr"], p["ws_bytes"],
             _lib.ptr(flat_idx), _lib.ptr(vals), _lib.ptr(cols))
     tmax = None
-    if tiles is not None:
-        tmax = torch.zeros(1, dtype=torch.int32, device=p["dev"])
-        _lib.check(L.aq_quantize_finish_tiles(*args, tiles[0].data_ptr(), tiles[1].data_ptr(), tmax.data_ptr(),
+    if tile_ent is not None:
+        t = torch.zeros(1, dtype=torch.int32, device=p["dev"])
+        _lib.check(L.aq_quantize_finish_tiles(*args, p["tile_ptr"].data_ptr(), tile_ent.data_ptr(), t.data_ptr(),
                                               p["stream"]), "aq_quantize_finish_tiles")
+        tmax = DeviceInt(t, 0)
     else:
         _lib.check(L.aq_quantize_finish(*args, p["stream"]), "aq_quantize_finish")
-    return _finished_tensor(p, nnz, flat_idx, vals, cols, tiles, tmax)
-
-
-def _quantize_complete_group(ps: list, nnzs: list) -> list:
-    """_quantize_complete for the members of one aq_quantize_grouped launch
-    (one block size, row length and layout): for the tiled layout one
-    aq_quantize_finish_tiles_grouped launch and one zero fill serve them all."""
-    if ps[0]["layout"] != "tiled":
-        return [_quantize_complete(p, nnz) for p, nnz in zip(ps, nnzs)]
-    L = _lib.load()
-    arr = _lib.ptr_array
-    outs = [_finish_outputs(p, nnz) for p, nnz in zip(ps, nnzs)]
-    tmaxs = torch.zeros(len(ps), dtype=torch.int32, device=ps[0]["dev"])
-    _lib.check(L.aq_quantize_finish_tiles_grouped(
-        len(ps), arr([p["numel"] for p in ps], ctypes.c_int64), ps[0]["G"], ps[0]["K"],
-        arr([p["block_off"].data_ptr() for p in ps]), arr(nnzs, ctypes.c_int64), arr([p["ws"].data_ptr() for p in ps]),
-        arr([p["ws_bytes"] for p in ps], ctypes.c_int64), arr([_lib.ptr(o[0]) for o in outs]),
-        arr([_lib.ptr(o[1]) for o in outs]), arr([_lib.ptr(o[2]) for o in outs]),
-        arr([o[3][0].data_ptr() for o in outs]), arr([o[3][1].data_ptr() for o in outs]), tmaxs.data_ptr(),
-        ps[0]["stream"]), "aq_quantize_finish_tiles_grouped")
-    return [_finished_tensor(p, nnz, *o, tmaxs[k:k + 1]) for k, (p, nnz, o) in enumerate(zip(ps, nnzs, outs))]
+    return _finished_tensor(p, nnz, flat_idx, vals, cols, tile_ent, tmax)
 
 
 # weights per aq_quantize_grouped launch, most blocks a member may have, and
 # most elements a launch may hold (each member's fp16 copy on the device,
 # codes and workspace are alive together until its completion)
 _QUANT_GROUP_MAX, _QUANT_GROUP_MAX_BLOCKS, _QUANT_GROUP_MAX_ELEMS = 8, 16384, 1 << 28
+
+
+def _run_launch(tensors, key, z_bits: int, fmt: int, code_format: str) -> dict:
+    """Prepare and launch one run of quantize_tensors (members sharing the
+    key's device, block size, row length and layout): one workspace for the
+    run, one aq_quantize_grouped launch, whose outlier counts (``totals``)
+    go to pinned host memory behind it, with an event to wait for them."""
+    L = _lib.load()
+    arr = _lib.ptr_array
+    dev, G, K, layout = key
+    ps = [_member_prepare(t, G, fmt, code_format, layout, dev) for t in tensors]
+    n = len(ps)
+    ws_bytes = [(int(L.aq_quantize_workspace_size(p["numel"], G)) + 255) // 256 * 256 for p in ps]
+    ws = torch.empty(sum(ws_bytes), dtype=torch.uint8, device=dev)
+    ws_ptrs, at = [], ws.data_ptr()
+    for b in ws_bytes:
+        ws_ptrs.append(at)
+        at += b
+    # [0, n): the outlier counts; [n, 2n): the block lists' largest counts,
+    # raised from 0 by the finish
+    aux = torch.zeros(2 * n, dtype=torch.int32, device=dev) if layout == "tiled" else \
+        torch.empty(n, dtype=torch.int32, device=dev)
+    stream = _lib.stream_of(dev)
+    numels = arr([p["numel"] for p in ps], ctypes.c_int64)
+    offs = arr([p["block_off"].data_ptr() for p in ps])
+    ws_ptrs, ws_bytes = arr(ws_ptrs), arr(ws_bytes, ctypes.c_int64)
+    _lib.check(L.aq_quantize_grouped(
+        n, arr([p["x"].data_ptr() for p in ps]), numels, G, z_bits, fmt, K, _lib.LAYOUTS[layout],
+        arr([p["codes"].data_ptr() for p in ps]), arr([p["scales"].data_ptr() for p in ps]), offs, ws_ptrs, ws_bytes,
+        aux.data_ptr(), stream), "aq_quantize_grouped")
+    counts = torch.empty(aux.numel(), dtype=torch.int32, pin_memory=True)
+    counts.copy_(aux, non_blocking=True)
+    done = torch.cuda.Event()
+    done.record(torch.cuda.current_stream(dev))
+    for p, w, b in zip(ps, ws_ptrs, ws_bytes):
+        p["ws_ptr"], p["ws_bytes"], p["stream"] = w, b, stream
+    return dict(ps=ps, ws=ws, aux=aux, counts=counts, done=done, stream=stream, G=G, K=K, numels=numels, offs=offs,
+                ws_ptrs=ws_ptrs, ws_bytes=ws_bytes)
+
+
+def _run_complete(r: dict) -> list:
+    """The QuantizedTensors of a launched run, once its outlier counts are
+    on the host: for the tiled layout every member's flat list and block
+    lists in one aq_quantize_finish_tiles_grouped launch; one finish per
+    member otherwise."""
+    ps = r["ps"]
+    n = len(ps)
+    r["done"].synchronize()
+    nnzs = r["counts"].tolist()[:n]
+    if ps[0]["layout"] != "tiled":
+        return [_quantize_complete(p, nnz) for p, nnz in zip(ps, nnzs)]
+    L = _lib.load()
+    arr = _lib.ptr_array
+    outs = [_finish_outputs(p, nnz) for p, nnz in zip(ps, nnzs)]
+    aux = r["aux"]
+    _lib.check(L.aq_quantize_finish_tiles_grouped(
+        n, r["numels"], r["G"], r["K"], r["offs"], arr(nnzs, ctypes.c_int64), r["ws_ptrs"], r["ws_bytes"],
+        arr([_lib.ptr(o[0]) for o in outs]), arr([_lib.ptr(o[1]) for o in outs]), arr([_lib.ptr(o[2]) for o in outs]),
+        arr([p["tile_ptr"].data_ptr() for p in ps]), arr([o[3].data_ptr() for o in outs]), aux.data_ptr() + 4 * n,
+        r["stream"]), "aq_quantize_finish_tiles_grouped")
+    r["ws"] = None  # the finish is queued: the workspace may go back to the allocator
+    return [_finished_tensor(p, nnz, *o, DeviceInt(aux, n + k)) for k, (p, nnz, o) in enumerate(zip(ps, nnzs, outs))]
 
 
 def quantize_tensors(tensors, block_size: int = 128, z_threshold: float = 3.0, *,
@@ -413,6 +472,7 @@ def quantize_tensors(tensors, block_size: int = 128, z_threshold: float = 3.0, *
     fmt = _format_id(code_format)
     out = [None] * len(tensors)
     groups = {}
+    L = None
     for i, t in enumerate(tensors):
         if not isinstance(t, torch.Tensor) or t.dtype != torch.float16 or t.numel() == 0:
             out[i] = quantize_tensor(t, block_size, z_threshold, code_format=code_format)
@@ -421,55 +481,38 @@ def quantize_tensors(tensors, block_size: int = 128, z_threshold: float = 3.0, *
         if (t.numel() + G - 1) // G > _QUANT_GROUP_MAX_BLOCKS:
             out[i] = quantize_tensor(t, block_size, z_threshold, code_format=code_format)
             continue
-        layout = "tiled" if (fmt == _lib.FMT_E4M3 and tiled_eligible(t.shape, G)) else "flat"
-        key = (_lib.compute_device(t.device), G, _rows_cols(t.shape)[1], layout)
+        if L is None:
+            L = _lib.load()
+        if G > L.aq_max_block_size():
+            raise ValueError(f"block_size {G} exceeds the supported maximum {L.aq_max_block_size()}")
+        key = (_lib.compute_device(t.device), G, _rows_cols(t.shape)[1], _layout_of(fmt, t.shape, G))
         groups.setdefault(key, []).append(i)
     runs = []
-    for idx in groups.values():
+    for key, idx in groups.items():
         run, elems = [], 0
         for i in idx:
             n = tensors[i].numel()
             if run and (len(run) == _QUANT_GROUP_MAX or elems + n > _QUANT_GROUP_MAX_ELEMS):
-                runs.append(run)
+                runs.append((key, run))
                 run, elems = [], 0
             run.append(i)
             elems += n
         if run:
-            runs.append(run)
-    L = _lib.load()
-    arr = _lib.ptr_array
-
-    def complete(entry):
-        # the run's one host sync: every member's outlier count
-        run_i, ps_i, counts, done = entry
-        done.synchronize()
-        for i, qt in zip(run_i, _quantize_complete_group(ps_i, [int(n) for n in counts.tolist()])):
-            out[i] = qt
-
+            runs.append((key, run))
+    z_bits = _threshold_bits(z_threshold)
     inflight = None  # the run launched last, completed once the next one is queued
-    for run in runs:
-        ps = []
-        for i in run:
-            t = tensors[i]
-            ps.append(_quantize_prepare(t, _resolve_block(block_size, t.shape), z_threshold, code_format, fmt))
-        a0 = ps[0]["args"]
-        _lib.check(L.aq_quantize_grouped(
-            len(ps), arr([p["args"][0] for p in ps]), arr([p["numel"] for p in ps], ctypes.c_int64), ps[0]["G"],
-            a0[3], fmt, ps[0]["K"], a0[6], arr([p["args"][7] for p in ps]), arr([p["args"][8] for p in ps]),
-            arr([p["args"][9] for p in ps]), arr([p["args"][10] for p in ps]),
-            arr([p["ws_bytes"] for p in ps], ctypes.c_int64), ps[0]["stream"]), "aq_quantize_grouped")
-        # the outlier counts go to pinned host memory behind the launch; the
-        # host waits for them after queueing the next run, so that run's
-        # kernel runs while this one's outputs are allocated and finished
-        counts = torch.empty(len(ps), dtype=torch.int32, pin_memory=True)
-        counts.copy_(torch.stack([p["block_off"][p["nblocks"]] for p in ps]), non_blocking=True)
-        done = torch.cuda.Event()
-        done.record(torch.cuda.current_stream(ps[0]["dev"]))
+    for key, run in runs:
+        r = _run_launch([tensors[i] for i in run], key, z_bits, fmt, code_format)
+        r["run"] = run
+        # the host waits for a run's outlier counts only after queueing the
+        # next run, so that run's kernel runs while this one is finished
         if inflight is not None:
-            complete(inflight)
-        inflight = (run, ps, counts, done)
+            for i, qt in zip(inflight["run"], _run_complete(inflight)):
+                out[i] = qt
+        inflight = r
     if inflight is not None:
-        complete(inflight)
+        for i, qt in zip(inflight["run"], _run_complete(inflight)):
+            out[i] = qt
     return out
 
 

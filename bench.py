@@ -249,7 +249,7 @@ def time_quantize_kernel(weights, reps=5, grouped=False):
                 len(run), arr([c[0][0] for c in run]), arr([c[0][1] for c in run], ctypes.c_int64), a0[2], a0[3],
                 a0[4], a0[5], a0[6], arr([c[0][7] for c in run]), arr([c[0][8] for c in run]),
                 arr([c[0][9] for c in run]), arr([c[0][10] for c in run]), arr([c[0][11] for c in run], ctypes.c_int64),
-                cs), "aq_quantize_grouped")
+                None, cs), "aq_quantize_grouped")
     graph.replay()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()

@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define AQ_ABI_VERSION 9
+#define AQ_ABI_VERSION 10
 
 enum { AQ_FMT_INT8 = 0, AQ_FMT_E4M3 = 1 };
 enum { AQ_LAYOUT_FLAT = 0, AQ_LAYOUT_TILED = 1 };
@@ -87,7 +87,10 @@ int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_thr_f16, int
  * member i the arguments of aq_quantize (xs[i], numels[i], codes[i],
  * scales[i], block_offs[i], workspaces[i] of ws_bytes[i]), each with at
  * most 16384 blocks.  Results are those of aq_quantize on each member, bit
- * for bit.  No counterpart of its own in the reference (its quantize_tensor,
+ * for bit.  totals (device int32[count], or NULL) receives each member's
+ * outlier count (block_offs[i][nblocks_i]) as well, so that a caller sizing
+ * the outlier lists reads them all with one copy.  No counterpart of its
+ * own in the reference (its quantize_tensor,
  * adaptive_quantizer.py:51-148, takes one tensor; the model swap,
  * model_modifier.py:95-143, calls it once per Linear): for callers that
  * quantize a layer's weights together, whose small members alone fill the
@@ -95,7 +98,8 @@ int aq_quantize(const void* x, int64_t numel, int64_t G, uint16_t z_thr_f16, int
  */
 int aq_quantize_grouped(int64_t count, const void* const* xs, const int64_t* numels, int64_t G, uint16_t z_thr_f16,
                         int fmt, int64_t K, int layout, void* const* codes, void* const* scales,
-                        int32_t* const* block_offs, void* const* workspaces, const int64_t* ws_bytes, void* stream);
+                        int32_t* const* block_offs, void* const* workspaces, const int64_t* ws_bytes,
+                        int32_t* totals, void* stream);
 
 /*
  * Quantize, phase 2 of 2: write the outlier list in ascending flat order

@@ -57,3 +57,46 @@ def test_grouped_wide_rows():
     for w, q in zip(ws, AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")):
         assert q.outlier_tile_ptr is not None
         _same(q, AQ.quantize_tensor(w, block_size=-1, code_format="e4m3"))
+
+
+def test_caller_stream_order():
+    """quantize_tensors on a caller's stream, its inputs written on that
+    stream just before the call (behind a long matmul) and its outputs read
+    on it just after, with no synchronisation in between: the call's kernels
+    follow the caller's earlier work and precede its later work."""
+    shapes = [(4096, 4096), (1024, 14336), (2048, 4096), (512, 14336)]
+    base = [_w(s, 70 + i) for i, s in enumerate(shapes)]
+    ref = [AQ.quantize_tensor(w, block_size=-1, code_format="e4m3") for w in base]
+    ws = [torch.zeros_like(w) for w in base]
+    a = torch.randn(8192, 8192, device=DEV, dtype=torch.float16)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream(device=DEV)
+    with torch.cuda.stream(s):
+        for _ in range(4):
+            a = torch.matmul(a, a) * 1e-3
+        for w, b in zip(ws, base):
+            w.copy_(b)
+        qs = AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")
+        got = [[None if getattr(q, f) is None else getattr(q, f).clone() for f in FIELDS] for q in qs]
+    torch.cuda.synchronize()
+    for q, r, g in zip(qs, ref, got):
+        for f, t in zip(FIELDS, g):
+            x = getattr(r, f)
+            if x is None:
+                assert t is None, f
+            else:
+                assert torch.equal(t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t,
+                                   x.view(torch.uint8) if x.dtype == torch.float8_e4m3fn else x), f
+        assert int(q.outlier_tile_max) == int(r.outlier_tile_max)
+
+
+def test_copied_inputs_on_second_stream():
+    """Inputs that need a copy first (transposed views, a host tensor) in
+    grouped runs: results as quantize_tensor gives them, on the inputs'
+    devices."""
+    ws = [_w((4096, 4096), 80), _w((14336, 1024), 81).t(), _w((4096, 1024), 82), _w((14336, 512), 83).t()]
+    ws[2] = ws[2].cpu()
+    got = AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")
+    for w, q in zip(ws, got):
+        r = AQ.quantize_tensor(w, block_size=-1, code_format="e4m3")
+        _same(q.to(DEV), r.to(DEV))

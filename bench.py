@@ -953,27 +953,36 @@ def main():
 
     # ---- weights: 4 layers x 7 linears, quantized on the GPU (also timed)
     layers = []
-    q_bytes, q_time = 0, 0.0
+    q_rates, q_calls = [], []
     keep_fp16 = {}
     for li in range(N_LAYERS):
         # a layer's seven weights through quantize_tensors, as the model swap
-        # quantizes them (one launch for the six sharing K, one host sync)
+        # quantizes them (one launch for the six sharing K, one host sync):
+        # one warm call (allocations), then 3 calls each timed alone (GPU
+        # idle before and after), the layer's figure their median
         ws = [gen_weight(N, K, gen, dev) for _, N, K in LLAMA_LINEARS]
-        AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")  # warm (allocations)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        qts = AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")
-        torch.cuda.synchronize()
-        q_time += time.perf_counter() - t0
+        AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")
+        times = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            qts = AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
         layer = {}
+        nb = 0
         for (name, _, _), w, qt in zip(LLAMA_LINEARS, ws, qts):
-            q_bytes += quantize_bytes(qt)
+            nb += quantize_bytes(qt)
             layer[name] = qt
             if li == 0:
                 keep_fp16[name] = w
         del ws, w
         layers.append(layer)
-        log(f"layer {li} quantized")
+        t_med = sorted(times)[1]
+        q_rates.append(nb / t_med)
+        q_calls.append(round(1e6 * t_med, 1))
+        log(f"layer {li} quantized: whole quantize_tensors call {1e6 * t_med:.1f} us (calls: "
+            f"{', '.join(f'{1e6 * t:.1f}' for t in times)})")
 
     # ---- M=1 dequant-GEMV, one HIP graph per layer.  The decode-time launch
     # pattern: q/k/v share x (one grouped launch), o, gate/up share x (one
@@ -1155,9 +1164,12 @@ def main():
                                     "model swap quantizes them); _single: one aq_quantize per weight",
             "quantize_kernel_single_GBps": round(qk1_bytes / qk1_s / 1e9, 1),
             "quantize_kernel_single_frac_hbm_peak": round(qk1_bytes / qk1_s / 1e9 / HBM_PEAK_GBS, 4),
-            "quantize_GBps": round(q_bytes / q_time / 1e9, 1),
-            "quantize_note": "whole quantize_tensors call per layer (the 7 weights; one host sync) incl. outlier "
-                             "gather and block lists",
+            "quantize_GBps": round(sum(q_rates) / len(q_rates) / 1e9, 1),
+            "quantize_call_us": q_calls,
+            "quantize_note": "whole quantize_tensors call per layer (the 7 weights; one host sync per run) incl. "
+                             "outlier lists and block lists, each call timed alone (synchronized before and after); "
+                             "per layer the median of 3 calls after a warm one, averaged over the 4 layers "
+                             "(quantize_call_us: the medians)",
             "sweep": sweep or None,
             "cpu_reference": cpu_extra,
             "models": models,

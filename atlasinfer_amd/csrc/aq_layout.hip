@@ -178,7 +178,7 @@ __global__ __launch_bounds__(256) void outlier_tile_rows_kernel(const int32_t* r
   for (int r = 0; r <= 16; r++) src.rs[r] = row_ptr[(int64_t)(rb * 16 + r) * rstride];
   src.cols = cols;
   src.vals = vals;
-  aq::tile_row_sort(src, rb, nch, src.rs[0], src.rs[16], sm, part, tile_ptr, tile_ent, tile_max);
+  aq::tile_row_sort<256>(src, rb, nch, src.rs[0], src.rs[16], sm, part, tile_ptr, tile_ent, tile_max);
 }
 
 // One thread per block of 16 rows x 64 columns (tile row rb, chunk c), for

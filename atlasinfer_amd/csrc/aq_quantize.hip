@@ -1068,10 +1068,14 @@ struct FinishGroup {
   int64_t G;
 };
 
-// LDS: 33 * nch ints, and with loff_lds the tile row's block offsets after them.
-__global__ __launch_bounds__(256) void finish_tiles_kernel(FinishGroup fg) {
+// LDS: 33 * nch ints, and with loff_lds the tile row's block offsets after
+// them.  NT threads per tile row: 128 for rows up to 128 chunks (a tile row of
+// such weights holds a few hundred entries, and the small workgroups let a
+// layer's tile rows all be resident at once), 256 for wider ones.
+template <int NT>
+__global__ __launch_bounds__(NT) void finish_tiles_kernel(FinishGroup fg) {
   extern __shared__ int sm[];
-  __shared__ int part[4];
+  __shared__ int part[NT / 64];
   int mi = 0;  // the workgroup's member (uniform)
 #pragma unroll
   for (int j = 1; j < kMaxQGroup; j++)
@@ -1100,11 +1104,11 @@ __global__ __launch_bounds__(256) void finish_tiles_kernel(FinishGroup fg) {
   src.cols = m.cols;
   if (fg.loff_lds) {
     int* l = sm + 33 * nch;
-    for (int k = t; k <= 16 * bpr; k += 256) l[k] = m.off[src.g0 + k];
+    for (int k = t; k <= 16 * bpr; k += NT) l[k] = m.off[src.g0 + k];
     __syncthreads();
     src.loff = l;
   }
-  aq::tile_row_sort(src, rb, nch, src.rs[0], src.rs[16], sm, part, m.tile_ptr, m.tile_ent, m.tile_max);
+  aq::tile_row_sort<NT>(src, rb, nch, src.rs[0], src.rs[16], sm, part, m.tile_ptr, m.tile_ent, m.tile_max);
 }
 
 // ---- calculate_zscore_manual of one block of n elements
@@ -1402,7 +1406,10 @@ static int launch_finish_tiles(FinishGroup& fg, int64_t G, int64_t K, const char
   const int64_t sort_ints = 33 * nch;
   fg.loff_lds = bpr > 1 && sort_ints + 16 * bpr + 1 <= 16384;
   const size_t lds = (size_t)(sort_ints + (fg.loff_lds ? 16 * bpr + 1 : 0)) * sizeof(int);
-  hipLaunchKernelGGL(finish_tiles_kernel, dim3((unsigned)fg.first[fg.count]), dim3(256), lds, s, fg);
+  if (nch <= 128)
+    hipLaunchKernelGGL(finish_tiles_kernel<128>, dim3((unsigned)fg.first[fg.count]), dim3(128), lds, s, fg);
+  else
+    hipLaunchKernelGGL(finish_tiles_kernel<256>, dim3((unsigned)fg.first[fg.count]), dim3(256), lds, s, fg);
   AQ_LAUNCH_CHECK(fn);
   return AQ_OK;
 }

@@ -5,7 +5,7 @@
 // same launch that writes the flat outlier list).
 //
 // A tile row is 16 rows; its entries come in row, column order (a CSR
-// slice).  One workgroup of 256 threads sorts them stably by 64-column
+// slice).  One workgroup (128 or 256 threads) sorts them stably by 64-column
 // chunk: per (row, chunk) counts and first entries in LDS (atomic add,
 // atomic min), turned into each chunk's block total and per-row offsets
 // within the block; an exclusive scan of the block totals gives the block
@@ -63,13 +63,15 @@ struct CsrTileSrc {
 
 // The counting sort of tile row rb's entries p0 .. p1 - 1 (Src(i, first)
 // gives entry i; first is true in the counting pass, false when an entry
-// is read again for its placement).  sm: 33 * nch ints of LDS; part: 4.
-// Writes tile_ptr[rb * nch + c] for every chunk and the entries, and raises
+// is read again for its placement) by a workgroup of NT threads (128 or
+// 256).  sm: 33 * nch ints of LDS; part: NT / 64.  Writes
+// tile_ptr[rb * nch + c] for every chunk and the entries, and raises
 // *tile_max (if not null) to the largest block.  Every thread of the
 // workgroup calls it.
-template <typename Src>
+template <int NT, typename Src>
 __device__ __forceinline__ void tile_row_sort(const Src& src, int rb, int nch, int p0, int p1, int* sm, int* part,
                                               int32_t* tile_ptr, uint32_t* tile_ent, int32_t* tile_max) {
+  static_assert(NT == 128 || NT == 256, "workgroup size");
   int* cnt = sm;                // [16][nch]: counts, then offsets within the block
   int* first = sm + 16 * nch;   // [16][nch]: index of the (row, chunk) run's first entry
   int* bstart = sm + 32 * nch;  // [nch]: block totals, then block starts
@@ -78,24 +80,24 @@ __device__ __forceinline__ void tile_row_sort(const Src& src, int rb, int nch, i
   TileEnt ce[kTileRowsRegs];
 #pragma unroll
   for (int k = 0; k < kTileRowsRegs; k++) {
-    const int i = p0 + t + 256 * k;
+    const int i = p0 + t + NT * k;
     ce[k] = i < p1 ? src(i, true) : TileEnt{0, 0, 0u};
   }
-  for (int i = t; i < 16 * nch; i += 256) {
+  for (int i = t; i < 16 * nch; i += NT) {
     cnt[i] = 0;
     first[i] = 0x7FFFFFFF;
   }
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < kTileRowsRegs; k++) {
-    const int i = p0 + t + 256 * k;
+    const int i = p0 + t + NT * k;
     if (i < p1) {
       const int b = ce[k].r * nch + (ce[k].col >> 6);
       atomicAdd(&cnt[b], 1);
       atomicMin(&first[b], i);
     }
   }
-  for (int i = p0 + t + 256 * kTileRowsRegs; i < p1; i += 256) {
+  for (int i = p0 + t + NT * kTileRowsRegs; i < p1; i += NT) {
     const TileEnt e = src(i, true);
     const int b = e.r * nch + (e.col >> 6);
     atomicAdd(&cnt[b], 1);
@@ -104,7 +106,7 @@ __device__ __forceinline__ void tile_row_sort(const Src& src, int rb, int nch, i
   __syncthreads();
   // per chunk: offsets of the rows within the block, and the block's total
   int mx = 0;
-  for (int c = t; c < nch; c += 256) {
+  for (int c = t; c < nch; c += NT) {
     int run = 0;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
@@ -116,10 +118,10 @@ __device__ __forceinline__ void tile_row_sort(const Src& src, int rb, int nch, i
     mx = max(mx, run);
   }
   // exclusive scan of the block totals: thread t takes chunks 4t..4t+3 of
-  // each run of 1024, its sum scanned across the workgroup (wave scans, the
+  // each run of 4 NT, its sum scanned across the workgroup (wave scans, the
   // wave totals through LDS)
   int carry = 0;
-  for (int c0 = 0; c0 < nch; c0 += 1024) {
+  for (int c0 = 0; c0 < nch; c0 += 4 * NT) {
     __syncthreads();
     int v[4], sum = 0;
 #pragma unroll
@@ -129,7 +131,7 @@ __device__ __forceinline__ void tile_row_sort(const Src& src, int rb, int nch, i
       sum += v[k];
     }
     int total;
-    int run = carry + team_excl_scan_i32<256>(sum, part, &total);
+    int run = carry + team_excl_scan_i32<NT>(sum, part, &total);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const int c = c0 + 4 * t + k;
@@ -144,13 +146,13 @@ __device__ __forceinline__ void tile_row_sort(const Src& src, int rb, int nch, i
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < kTileRowsRegs; k++) {
-    const int i = p0 + t + 256 * k;
+    const int i = p0 + t + NT * k;
     if (i < p1) {
       const int c = ce[k].col >> 6, b = ce[k].r * nch + c;
       tile_ent[p0 + bstart[c] + cnt[b] + (i - first[b])] = (ce[k].val << 16) | block_position(ce[k].r, ce[k].col - c * 64);
     }
   }
-  for (int i = p0 + t + 256 * kTileRowsRegs; i < p1; i += 256) {
+  for (int i = p0 + t + NT * kTileRowsRegs; i < p1; i += NT) {
     const TileEnt e = src(i, false);
     const int c = e.col >> 6, b = e.r * nch + c;
     tile_ent[p0 + bstart[c] + cnt[b] + (i - first[b])] = (e.val << 16) | block_position(e.r, e.col - c * 64);

@@ -157,6 +157,7 @@ __global__ __launch_bounds__(256) void scatter_outliers_kernel(const int64_t* id
 
 using aq::block_position;
 using aq::lower_bound_i32;
+using aq::raise_to;
 
 // One workgroup per tile row (aq_tiles.h); workgroup nrb writes the list's
 // end and the 64 padding entries.  LDS: 33 * nch ints.
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(256) void outlier_tiles_kernel(const int32_t* row_p
       }
       mx = max(mx, n);
     }
-    if (mx > 0) atomicMax(tile_max, mx);
+    if (mx > 0) raise_to(tile_max, mx);
   }
   int lo[16], hi[16];
   int pos = row_ptr[(int64_t)rb * 16 * rstride];

@@ -36,6 +36,15 @@ __device__ __forceinline__ int lower_bound_i32(const int32_t* a, int lo, int hi,
   return lo;
 }
 
+// Raise *p to at least v.  Many workgroups raise one word: a relaxed read
+// first skips the atomic when the word is already that large (it only
+// grows, so skipping keeps the maximum), since atomics on one address are
+// serialized at the L2 (one per wave over a layer's tile rows took three
+// quarters of the tile-row sort's launch).
+__device__ __forceinline__ void raise_to(int32_t* p, int v) {
+  if (v > __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) atomicMax(p, v);
+}
+
 // Row (0..15) of entry i of a tile row whose 17 row starts are rs.
 __device__ __forceinline__ int tile_row_of(const int (&rs)[17], int i) {
   int r = 0;
@@ -157,9 +166,19 @@ __device__ __forceinline__ void tile_row_sort(const Src& src, int rb, int nch, i
     const int c = e.col >> 6, b = e.r * nch + c;
     tile_ent[p0 + bstart[c] + cnt[b] + (i - first[b])] = (e.val << 16) | block_position(e.r, e.col - c * 64);
   }
-  // the largest block of the tile row
+  // the largest block of the tile row: wave maxima through LDS (part is
+  // free again after the barrier), one raise per workgroup
   for (int d = 32; d >= 1; d >>= 1) mx = max(mx, __shfl_xor(mx, d));
-  if ((t & 63) == 0 && tile_max && mx > 0) atomicMax(tile_max, mx);
+  if (tile_max) {
+    __syncthreads();
+    if ((t & 63) == 0) part[t >> 6] = mx;
+    __syncthreads();
+    if (t == 0) {
+#pragma unroll
+      for (int w = 1; w < NT / 64; w++) mx = max(mx, part[w]);
+      if (mx > 0) raise_to(tile_max, mx);
+    }
+  }
 }
 
 // The block lists from CSR lists whose row r starts at row_ptr[r * rstride]

@@ -536,13 +536,18 @@ constexpr int kXWaves = 8;
 constexpr int kXPad = 8;  // halves of padding per LDS row of x
 constexpr int kXCsrCap = 512;  // outlier entries of a tile row staged in LDS (the rest: epilogue)
 
-template <int FMT, int PC, int MG, int S, int OT>
+// XH: rows of x staged, 16 MG, or 8 for M <= 8 with one row group (the MFMA
+// rows 8..15 then read rows 0..7 again; their outputs are never stored)
+template <int FMT, int PC, int MG, int S, int OT, int XH>
 __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) {
   constexpr int TR = kXWaves / S;
-  constexpr int XR = 16 * MG;              // staged rows of x
+  constexpr int XR = XH;                   // staged rows of x
+  static_assert(XH == 16 * MG || (XH == 8 && MG == 1), "staged rows");
   constexpr int XW = S * 128 + kXPad;      // LDS row pitch (halves)
   constexpr int XP = XR * S * 16 / (64 * kXWaves);  // 16-byte x pieces per thread and group
-  static_assert(XP >= 1, "x pieces");
+  static_assert(XP >= 1 && XR * S * 16 % (64 * kXWaves) == 0, "x pieces");
+  // the staged row an MFMA row (16 gi + r) reads
+  auto xrow = [](int r) { return XR == 8 ? (r & 7) : r; };
   __shared__ __attribute__((aligned(16))) uint16_t xs[2][XR * XW];
   __shared__ uint32_t x_ent[TR][kXCsrCap];  // (value << 16) | column of the tile row's first outliers
 
@@ -667,7 +672,7 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
         bv[b] = valid && (int)((ent >> 6) & 15u) == li ? bits_to_h((uint16_t)(ent >> 16)) : (f16)0.0f;
 #pragma unroll
         for (int gi = 0; gi < MG; gi++) {
-          const f16 xv = bits_to_h(xb[(16 * gi + li) * XW + sp * 128 + k]);
+          const f16 xv = bits_to_h(xb[xrow(16 * gi + li) * XW + sp * 128 + k]);
           av[gi][b] = valid ? xv : (f16)0.0f;
         }
       }
@@ -701,7 +706,7 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
 #pragma unroll
     for (int gi = 0; gi < MG; gi++) {
       // A operand: x row 16 gi + li at columns 16 grp + {0, 8, 64, 72} of this wave's chunk
-      const uint16_t* xp = xw + (16 * gi + li) * XW;
+      const uint16_t* xp = xw + xrow(16 * gi + li) * XW;
       acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(xp), w0, acc[gi], 0, 0, 0);
       acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(xp + 8), w1, acc[gi], 0, 0, 0);
       acc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8*>(xp + 64), w2, acc[gi], 0, 0, 0);
@@ -752,12 +757,12 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
       const int col = (int)(ent & 0xFFFFu);
       if (col >= gend) break;
       const float wv = (float)bits_to_h((uint16_t)(ent >> 16));
-      const uint16_t* xc = xb + (col - gstart) + 4 * grp * XW;
+      const uint16_t* xc = xb + (col - gstart);
 #pragma unroll
       for (int gi = 0; gi < MG; gi++)
 #pragma unroll
         for (int i = 0; i < 4; i++)
-          acc[gi][i] = __builtin_fmaf((float)bits_to_h(xc[(16 * gi + i) * XW]), wv, acc[gi][i]);
+          acc[gi][i] = __builtin_fmaf((float)bits_to_h(xc[xrow(16 * gi + 4 * grp + i) * XW]), wv, acc[gi][i]);
       op++;
     }
   };
@@ -1720,7 +1725,7 @@ hipError_t launch_gemv(const QLArgs& a, int fmt, bool per_channel, hipStream_t s
                             : launch_gemv<NS, AQ_FMT_INT8>(a, per_channel, s);
 }
 
-template <int FMT, int MG, int S>
+template <int FMT, int MG, int S, int XH>
 hipError_t launch_gemv_x(const QLArgs& a, bool per_channel, hipStream_t s) {
   QLArgs p;
   // workgroups of 8 / S tile rows; a SwiGLU pair: 4 / S of each member, and
@@ -1743,28 +1748,32 @@ hipError_t launch_gemv_x(const QLArgs& a, bool per_channel, hipStream_t s) {
     for (int i = 0; i < a.count; i++) lists = lists && a.mat[i].tptr && a.mat[i].tent;
     if (lists) {
       if (per_channel)
-        hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 1, MG, S, 1>), g, dim3(64 * kXWaves), 0, s, p);
+        hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 1, MG, S, 1, XH>), g, dim3(64 * kXWaves), 0, s, p);
       else
-        hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 0, MG, S, 1>), g, dim3(64 * kXWaves), 0, s, p);
+        hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 0, MG, S, 1, XH>), g, dim3(64 * kXWaves), 0, s, p);
       return hipGetLastError();
     }
   }
   if (per_channel)
-    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 1, MG, S, 0>), g, dim3(64 * kXWaves), 0, s, p);
+    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 1, MG, S, 0, XH>), g, dim3(64 * kXWaves), 0, s, p);
   else
-    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 0, MG, S, 0>), g, dim3(64 * kXWaves), 0, s, p);
+    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 0, MG, S, 0, XH>), g, dim3(64 * kXWaves), 0, s, p);
   return hipGetLastError();
 }
 
-template <int MG, int S>
+template <int MG, int S, int XH = 16 * MG>
 hipError_t launch_gemv_x(const QLArgs& a, int fmt, bool per_channel, hipStream_t s) {
-  return fmt == AQ_FMT_E4M3 ? launch_gemv_x<AQ_FMT_E4M3, MG, S>(a, per_channel, s)
-                            : launch_gemv_x<AQ_FMT_INT8, MG, S>(a, per_channel, s);
+  return fmt == AQ_FMT_E4M3 ? launch_gemv_x<AQ_FMT_E4M3, MG, S, XH>(a, per_channel, s)
+                            : launch_gemv_x<AQ_FMT_INT8, MG, S, XH>(a, per_channel, s);
 }
 
 // 6 <= M <= 64: x row groups of 16 per MFMA (MG = 1, 2, 3 or 4 for M up to 16, 32, 48, 64),
 // S = 2 or 4 waves per tile row
 hipError_t launch_gemv_x(const QLArgs& a, int fmt, bool per_channel, int S, hipStream_t s) {
+  // up to 8 rows with 4 or 8 waves per tile row: 8 staged rows of x, half
+  // the x loads and LDS stores of a 16-row group
+  if (a.M <= 8 && S >= 4)
+    return S == 4 ? launch_gemv_x<1, 4, 8>(a, fmt, per_channel, s) : launch_gemv_x<1, 8, 8>(a, fmt, per_channel, s);
   if (a.M <= 16)
     return S == 2 ? launch_gemv_x<1, 2>(a, fmt, per_channel, s)
            : S == 4 ? launch_gemv_x<1, 4>(a, fmt, per_channel, s) : launch_gemv_x<1, 8>(a, fmt, per_channel, s);

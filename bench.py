@@ -959,11 +959,14 @@ def main():
         # a layer's seven weights through quantize_tensors, as the model swap
         # quantizes them (one launch for the six sharing K, one host sync):
         # one warm call (allocations), then 3 calls each timed alone (GPU
-        # idle before and after), the layer's figure their median
+        # idle before and after, the previous call's outputs freed first, so
+        # that each call meets the same warm allocator), the layer's figure
+        # their median
         ws = [gen_weight(N, K, gen, dev) for _, N, K in LLAMA_LINEARS]
-        AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")
+        qts = AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")
         times = []
         for _ in range(3):
+            del qts
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             qts = AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3")
@@ -1167,9 +1170,9 @@ def main():
             "quantize_GBps": round(sum(q_rates) / len(q_rates) / 1e9, 1),
             "quantize_call_us": q_calls,
             "quantize_note": "whole quantize_tensors call per layer (the 7 weights; one host sync per run) incl. "
-                             "outlier lists and block lists, each call timed alone (synchronized before and after); "
-                             "per layer the median of 3 calls after a warm one, averaged over the 4 layers "
-                             "(quantize_call_us: the medians)",
+                             "outlier lists and block lists, each call timed alone (synchronized before and after, "
+                             "the previous call's outputs freed first); per layer the median of 3 calls after a warm "
+                             "one, averaged over the 4 layers (quantize_call_us: the medians)",
             "sweep": sweep or None,
             "cpu_reference": cpu_extra,
             "models": models,

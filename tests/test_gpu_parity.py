@@ -259,6 +259,24 @@ def test_qlinear_heavy_outliers_and_3d_input():
     assert_close(y, yref, x, w_deq)
 
 
+@pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128)])
+def test_gemv_m1_crowded_tile_rows(fmt, G):
+    """M = 1 with tile rows of more outliers than the GEMV stages (512 a
+    tile row: Student-t(3) weights with 5 % heavy outliers give thousands):
+    the staged entries summed in the stream, the rest from memory after it."""
+    rng = np.random.default_rng(91)
+    w = make_weights(rng, (256, 4096), frac=0.05, t_dof=3)
+    q = AQ.quantize_tensor(torch.from_numpy(w).to(DEV), block_size=G, code_format=fmt)
+    rp = q.outlier_row_ptr.cpu().numpy()
+    assert (rp[16::16] - rp[:-16:16]).max() > 512  # some tile row overflows the staged entries
+    w_deq = oref(q, w)
+    b = torch.from_numpy(rng.standard_normal(256).astype(np.float16)).to(DEV)
+    for m in (1, 2, 5):
+        x = torch.from_numpy(rng.standard_normal((m, 4096)).astype(np.float16)).to(DEV)
+        y = AW.QuantizedLinear(q, b)(x)
+        assert_close(y, reference_linear(x, w_deq, b), x, w_deq)
+
+
 def expected_tiles(q, N, K):
     """The 16 x 64 block outlier lists restated with numpy from the flat
     indices: entry (fp16 bits << 16) | r << 6 | k with r = row % 16 and

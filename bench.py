@@ -955,6 +955,7 @@ def main():
     layers = []
     q_rates, q_calls = [], []
     keep_fp16 = {}
+    all_ws = []  # every layer's fp16 weights, for the back-to-back timing below
     for li in range(N_LAYERS):
         # a layer's seven weights through quantize_tensors, as the model swap
         # quantizes them (one launch for the six sharing K, one host sync):
@@ -979,13 +980,30 @@ def main():
             layer[name] = qt
             if li == 0:
                 keep_fp16[name] = w
-        del ws, w
+        all_ws.append(ws)
+        del w
         layers.append(layer)
         t_med = sorted(times)[1]
         q_rates.append(nb / t_med)
         q_calls.append(round(1e6 * t_med, 1))
         log(f"layer {li} quantized: whole quantize_tensors call {1e6 * t_med:.1f} us (calls: "
             f"{', '.join(f'{1e6 * t:.1f}' for t in times)})")
+    # the same calls back to back, as the model swap issues them: the 4
+    # layers' quantize_tensors calls in a row, synchronized only before and
+    # after the 4 (each call still waits for its own outlier counts); the
+    # outputs of a pass freed before the next pass; median of 3 passes
+    q_b2b = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        outs = [AQ.quantize_tensors(ws, block_size=-1, code_format="e4m3") for ws in all_ws]
+        torch.cuda.synchronize()
+        q_b2b.append(time.perf_counter() - t0)
+        del outs
+    q_b2b_bytes = sum(quantize_bytes(qt) for layer in layers for qt in layer.values())
+    q_b2b_s = sorted(q_b2b)[1]
+    log(f"quantize_tensors back to back: {1e6 * q_b2b_s / N_LAYERS:.1f} us per layer call")
+    del all_ws, ws
 
     # ---- M=1 dequant-GEMV, one HIP graph per layer.  The decode-time launch
     # pattern: q/k/v share x (one grouped launch), o, gate/up share x (one
@@ -1169,6 +1187,10 @@ def main():
             "quantize_kernel_single_frac_hbm_peak": round(qk1_bytes / qk1_s / 1e9 / HBM_PEAK_GBS, 4),
             "quantize_GBps": round(sum(q_rates) / len(q_rates) / 1e9, 1),
             "quantize_call_us": q_calls,
+            "quantize_b2b_GBps": round(q_b2b_bytes / q_b2b_s / 1e9, 1),
+            "quantize_b2b_note": "the 4 layers' quantize_tensors calls back to back (the model swap's pattern: each "
+                                 "call waits only for its own outlier counts), synchronized before and after the "
+                                 "4; median of 3 passes",
             "quantize_note": "whole quantize_tensors call per layer (the 7 weights; one host sync per run) incl. "
                              "outlier lists and block lists, each call timed alone (synchronized before and after, "
                              "the previous call's outputs freed first); per layer the median of 3 calls after a warm "

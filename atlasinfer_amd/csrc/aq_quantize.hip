@@ -585,6 +585,12 @@ __device__ __forceinline__ uint32_t quot2(uint32_t xp, float r) {
   return q;
 }
 
+// Code exchange of a workgroup of four 4096-element rows (per-channel
+// blocks): 16-byte piece (column piece c, row r) at slot 4 c + r, the low
+// four bits XORed with bits 4-7 so that both the writes (lanes 16 slots
+// apart) and the reads (consecutive slots) spread over the LDS banks.
+__device__ __forceinline__ int xchg_slot(int i) { return i ^ ((i >> 4) & 15); }
+
 // The rest of a block after its elements are loaded, when a thread's E
 // elements are all inside the block or all padding (E divides G).  Works on
 // element pairs with packed arithmetic: d = x - mean in fp16, then, since
@@ -598,7 +604,8 @@ __device__ __forceinline__ uint32_t quot2(uint32_t xp, float r) {
 template <int TAU, int E, int MODE>
 __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& xs, int64_t g, bool gvalid,
                                                   int64_t base, int i0, int t, double* lds_d, float* lds_f,
-                                                  int* lds_i, const uint16_t* staged, int unit_e0) {
+                                                  int* lds_i, const uint16_t* staged, int unit_e0,
+                                                  uint4* xchg) {
   constexpr int NP = E / 2;              // pairs per thread
   constexpr int PW = NP < 16 ? NP : 16;  // pairs per flag word
   constexpr int NWD = NP / PW;
@@ -736,7 +743,11 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
   const int vstep = a.tiled ? 256 : 16;
   auto store16 = [&](int v, const uint32_t (&w)[4]) {
     if (!(gvalid && tvalid)) return;
-    if (a.vec) {
+    if (xchg) {
+      // the row's column piece i0 / 16 + v, beside the same piece of the
+      // workgroup's other three rows
+      xchg[xchg_slot((((i0 >> 4) + v) << 2) | (int)(g & 3))] = make_uint4(w[0], w[1], w[2], w[3]);
+    } else if (a.vec) {
       *reinterpret_cast<uint4*>(dst + v * vstep) = make_uint4(w[0], w[1], w[2], w[3]);
     } else {
       const int64_t j = base + i0 + 16 * v;
@@ -746,6 +757,8 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
             (uint8_t)(w[b / 4] >> (8 * (b % 4)));
     }
   };
+  // every wave of the workgroup is past its reads of the staged copy
+  if (xchg) __syncthreads();
   // codes, 16 elements (8 pairs, four words) at a time; one loop per format
   if (a.fmt == AQ_FMT_INT8) {
 #pragma unroll
@@ -787,6 +800,20 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
     }
   }
 
+  if (xchg) {
+    // the workgroup's four rows' codes out of LDS: lanes 4j .. 4j + 3 store
+    // the four rows' 16-byte pieces of one column piece, 64 contiguous bytes
+    // of the tiled layout
+    __syncthreads();
+    const int64_t row0 = g & ~(int64_t)3;
+    const int rr = threadIdx.x & 3;
+#pragma unroll
+    for (int i = 0; i < E / 16; i++) {
+      const int c = (threadIdx.x >> 2) + i * 64;
+      *reinterpret_cast<uint4*>(a.codes + tiled_offset(row0 + rr, (int64_t)c << 4, a.nchunks)) =
+          xchg[xchg_slot((c << 2) | rr)];
+    }
+  }
   // the block's scale and count (the same values in every lane of the team:
   // all lanes store them, no branch around the stores)
   if (gvalid) {
@@ -860,10 +887,18 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantGr
   if constexpr (MODE == kAnyLen)
     finish_block_any<TAU, E, MODE>(a, xs, g, gvalid, base, i0, t, lds_d + team * NWT, lds_f + team * NWT,
                                    lds_i + team * NWT);
-  else
+  else {
+    // four one-row blocks of 4096 elements staged together, tiled codes:
+    // the codes go out through the stage in 64-byte runs (a store
+    // instruction of 16-byte pieces, one per lane, would otherwise touch 64
+    // cache lines)
+    uint4* xchg = nullptr;
+    if constexpr (kStage && TAU == 64 && E == 64 && NT == 256)
+      if (staged && a.tiled && a.bpr == 1) xchg = stage;
     finish_block_fast<TAU, E, MODE>(a, xs, g, gvalid, base, i0, t, lds_d + team * NWT, lds_f + team * NWT,
                                     lds_i + team * NWT, staged ? reinterpret_cast<const uint16_t*>(stage) : nullptr,
-                                    (int)(team * G + i0));
+                                    (int)(team * G + i0), xchg);
+  }
 }
 
 // ---- exclusive scan of the per-block counts (in place, two passes)

@@ -251,6 +251,8 @@ __device__ __forceinline__ float wave_group_max_f32(float v) {
   return v;
 }
 
+constexpr int pow2_ceil(int n) { return n <= 1 ? 1 : 2 * pow2_ceil((n + 1) / 2); }
+
 template <int TAU>
 __device__ __forceinline__ double team_sum_f64(double v, double* lds_team) {
   constexpr int WL = TAU < 64 ? TAU : 64;
@@ -262,11 +264,14 @@ __device__ __forceinline__ double team_sum_f64(double v, double* lds_team) {
     __syncthreads();
     if (lane == 0) lds_team[w] = v;
     __syncthreads();
-    double t[NW];
+    // a team of NW waves sums as one of the next power of two whose last
+    // waves hold +0 (the balanced tree over next_pow2(TAU) leaves)
+    constexpr int NP = pow2_ceil(NW);
+    double t[NP];
 #pragma unroll
-    for (int i = 0; i < NW; i++) t[i] = lds_team[i];
+    for (int i = 0; i < NP; i++) t[i] = i < NW ? lds_team[i] : 0.0;
 #pragma unroll
-    for (int s = NW; s > 1; s >>= 1)
+    for (int s = NP; s > 1; s >>= 1)
 #pragma unroll
       for (int i = 0; i < s / 2; i++) t[i] = t[2 * i] + t[2 * i + 1];
     v = t[0];
@@ -287,11 +292,12 @@ __device__ __forceinline__ float team_sum_f32(float v, float* lds_team) {
     __syncthreads();
     if (lane == 0) lds_team[w] = v;
     __syncthreads();
-    float t[NW];
+    constexpr int NP = pow2_ceil(NW);
+    float t[NP];
 #pragma unroll
-    for (int i = 0; i < NW; i++) t[i] = lds_team[i];
+    for (int i = 0; i < NP; i++) t[i] = i < NW ? lds_team[i] : 0.0f;
 #pragma unroll
-    for (int s = NW; s > 1; s >>= 1)
+    for (int s = NP; s > 1; s >>= 1)
 #pragma unroll
       for (int i = 0; i < s / 2; i++) t[i] = t[2 * i] + t[2 * i + 1];
     v = t[0];

@@ -1199,10 +1199,16 @@ hipError_t launch_quantize_t(QuantGroup q, hipStream_t stream) {
 // Team shape per padded block size P: up to 1024 elements, 16 per thread
 // (teams of at most one wave, several per workgroup); 2048, 32 per thread on
 // one wave; from 4096 on, 64 per thread (one wave for 4096, a block of
-// 4096 elements then needs no barrier at all), except 16384 (rows of 14336
-// such as down_proj's): 32 per thread on 8 waves ran 4 % faster than 64 on
-// 4, while 32 per thread at 4096 ran 15 % slower (measured).
+// 4096 elements then needs no barrier at all), except 16384: 32 per thread
+// on 8 waves ran 4 % faster than 64 on 4 for rows of 14336 such as
+// down_proj's (which now take 7 waves, below), while 32 per thread at 4096
+// ran 15 % slower (measured).
 hipError_t launch_quantize(const QuantGroup& q, hipStream_t stream) {
+  // Rows of exactly 14336 (Llama-3 / Mistral down_proj): a team of 448
+  // threads (7 waves) instead of 512, whose eighth wave would hold only
+  // padding; the team sums pad the eighth wave's partial with +0, the same
+  // tree.  Four such workgroups fit a CU against three of 8 waves.
+  if (q.m[0].G == 448 * 32) return launch_quantize_t<448, 32>(q, stream);
   const int64_t P = next_pow2(q.m[0].G);
   switch (P) {
     case 1: case 2: case 4: case 8: case 16: return launch_quantize_t<1, 16>(q, stream);

@@ -523,18 +523,23 @@ def test_signed_zeros_survive(oracle):
     assert np.array_equal(bits(z), bits(zr))
 
 
-@pytest.mark.parametrize("G", [128, 4096])
-def test_quantize_block_means_near_fp16_ties(oracle, G):
+@pytest.mark.parametrize("G,rows,K", [(128, 64, 4096), (4096, 64, 4096), (14336, 32, 14336)])
+def test_quantize_block_means_near_fp16_ties(oracle, G, rows, K):
     """Blocks whose exact mean sits within a few 2^-24 / G of the midpoint of
     two fp16 neighbours h1 < h2 ~ 2^-13 (mean = h1 + 2^-24 + d 2^-24 / G,
     d in -3..3), the rest of each block cancelling pairs +-B with B up to
     6e4, so fp32 partial sums of the block lose the small terms: every
-    block's mean16, and so its codes and outliers, must be the oracle's."""
+    block's mean16, and so its codes and outliers, must be the oracle's.
+    Rows of 14336 run on a team of 7 waves whose sums pad an eighth with +0."""
     rng = np.random.default_rng(G)
-    rows, K = 64, 4096
     nb = rows * K // G
     w = np.zeros((nb, G), np.float16)
-    h1 = np.float16(2.0 ** -13) + np.float16(2.0 ** -23) * rng.integers(0, 1023, nb).astype(np.float16)
+    # h1 * G must be an fp16 value: any h1 for a power-of-two G; at
+    # G = 14336 = 7 * 2^11 (products near 1.75, ulp 2^-10) h1's offset a
+    # multiple of 4 * 2^-23
+    steps = rng.integers(0, 1023, nb) if G & (G - 1) == 0 else 4 * rng.integers(0, 36, nb)
+    h1 = np.float16(2.0 ** -13) + np.float16(2.0 ** -23) * steps.astype(np.float16)
+    assert np.all(np.float16(h1 * np.float16(G)).astype(np.float64) == h1.astype(np.float64) * G)
     d = rng.integers(-3, 4, nb)
     npair = (G - 4) // 2
     big = (rng.uniform(1.0, 6e4, (nb, npair)) * rng.choice([1e-4, 1.0], (nb, 1))).astype(np.float16)

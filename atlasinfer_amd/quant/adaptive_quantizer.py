@@ -293,6 +293,45 @@ def _member_prepare(fp16_tensor: torch.Tensor, G: int, fmt: int, code_format: st
                 tile_ptr=tile_ptr, fmt=fmt, code_format=code_format, dev=dev)
 
 
+def _a256(n: int) -> int:
+    return (n + 255) // 256 * 256
+
+
+def _run_plan(tensors, G: int, fmt: int, code_format: str, dev: torch.device):
+    """The members of a tiled run before anything is allocated for them, and
+    the byte offsets of their codes, scales, block offsets and block-list
+    pointers in one buffer for the run (each 256-byte aligned)."""
+    ps, at = [], 0
+    for t in tensors:
+        numel = t.numel()
+        x = t if t.device == dev and t.is_contiguous() else t.to(dev).contiguous()
+        N, K = _rows_cols(t.shape)
+        nblocks = (numel + G - 1) // G
+        ntile = (N // 16) * (K // 64) + 1
+        p = dict(x=x, input_device=t.device, original_shape=t.shape, numel=numel, G=G, N=N, K=K, nblocks=nblocks,
+                 padded=nblocks * G, ntile=ntile, layout="tiled", fmt=fmt, code_format=code_format, dev=dev)
+        offs = []
+        for nb in (nblocks * G, 2 * nblocks, 4 * (nblocks + 1), 4 * ntile):  # codes, scales, offsets, pointers
+            offs.append(at)
+            at += _a256(nb)
+        p["at"] = tuple(offs)
+        ps.append(p)
+    return ps, at
+
+
+def _run_views(ps, buf: torch.Tensor):
+    """Each member's codes, scales, block offsets and block-list pointers as
+    views of the run's buffer (taken after the launch that fills them: the
+    host builds them while the kernel runs)."""
+    f8, f16, i32 = buf.view(torch.float8_e4m3fn), buf.view(torch.float16), buf.view(torch.int32)
+    for p in ps:
+        c, s, o, t = p["at"]
+        p["codes"] = f8[c:c + p["padded"]]
+        p["scales"] = f16[s // 2:s // 2 + p["nblocks"]]
+        p["block_off"] = i32[o // 4:o // 4 + p["nblocks"] + 1]
+        p["tile_ptr"] = i32[t // 4:t // 4 + p["ntile"]]
+
+
 def _layout_of(fmt: int, shape, G: int) -> str:
     # e4m3 codes go straight into the layout the fused kernels read; int8
     # codes stay in element order for the reference's compacted stream
@@ -405,7 +444,19 @@ def _run_launch(tensors, key, z_bits: int, fmt: int, code_format: str) -> dict:
     L = _lib.load()
     arr = _lib.ptr_array
     dev, G, K, layout = key
-    ps = [_member_prepare(t, G, fmt, code_format, layout, dev) for t in tensors]
+    # tiled runs (E4M3 codes, the final outputs): every member's
+    # count-independent outputs in one allocation, addressed by offset for
+    # the launch and viewed after it; flat runs keep their own tensors (int8
+    # codes are compacted into new ones)
+    buf = None
+    if layout == "tiled":
+        ps, nbytes = _run_plan(tensors, G, fmt, code_format, dev)
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        b0 = buf.data_ptr()
+        addr = [tuple(b0 + a for a in p["at"]) for p in ps]
+    else:
+        ps = [_member_prepare(t, G, fmt, code_format, layout, dev) for t in tensors]
+        addr = [(p["codes"].data_ptr(), p["scales"].data_ptr(), p["block_off"].data_ptr(), None) for p in ps]
     n = len(ps)
     ws_bytes = [(int(L.aq_quantize_workspace_size(p["numel"], G)) + 255) // 256 * 256 for p in ps]
     ws = torch.empty(sum(ws_bytes), dtype=torch.uint8, device=dev)
@@ -419,16 +470,18 @@ def _run_launch(tensors, key, z_bits: int, fmt: int, code_format: str) -> dict:
         torch.empty(n, dtype=torch.int32, device=dev)
     stream = _lib.stream_of(dev)
     numels = arr([p["numel"] for p in ps], ctypes.c_int64)
-    offs = arr([p["block_off"].data_ptr() for p in ps])
+    offs = arr([a[2] for a in addr])
     ws_ptrs, ws_bytes = arr(ws_ptrs), arr(ws_bytes, ctypes.c_int64)
     _lib.check(L.aq_quantize_grouped(
         n, arr([p["x"].data_ptr() for p in ps]), numels, G, z_bits, fmt, K, _lib.LAYOUTS[layout],
-        arr([p["codes"].data_ptr() for p in ps]), arr([p["scales"].data_ptr() for p in ps]), offs, ws_ptrs, ws_bytes,
-        aux.data_ptr(), stream), "aq_quantize_grouped")
+        arr([a[0] for a in addr]), arr([a[1] for a in addr]), offs, ws_ptrs, ws_bytes, aux.data_ptr(), stream),
+        "aq_quantize_grouped")
     counts = torch.empty(aux.numel(), dtype=torch.int32, pin_memory=True)
     counts.copy_(aux, non_blocking=True)
     done = torch.cuda.Event()
     done.record(torch.cuda.current_stream(dev))
+    if buf is not None:
+        _run_views(ps, buf)
     for p, w, b in zip(ps, ws_ptrs, ws_bytes):
         p["ws_ptr"], p["ws_bytes"], p["stream"] = w, b, stream
     return dict(ps=ps, ws=ws, aux=aux, counts=counts, done=done, stream=stream, G=G, K=K, numels=numels, offs=offs,
@@ -448,14 +501,29 @@ def _run_complete(r: dict) -> list:
         return [_quantize_complete(p, nnz) for p, nnz in zip(ps, nnzs)]
     L = _lib.load()
     arr = _lib.ptr_array
-    outs = [_finish_outputs(p, nnz) for p, nnz in zip(ps, nnzs)]
+    # every member's outlier lists in one allocation: flat indices (int64),
+    # values (fp16), columns (int32) and block-list entries (int32, 64 of
+    # read padding), addressed by offset for the finish and viewed after it
+    at, spans = 0, []
+    for nnz in nnzs:
+        sp = []
+        for nb in (8 * nnz, 2 * nnz, 4 * nnz, 4 * (nnz + 64)):  # indices, values, columns, block-list entries
+            sp.append(at)
+            at += _a256(nb)
+        spans.append(sp)
+    lists = torch.empty(at, dtype=torch.uint8, device=r["ps"][0]["dev"])
+    b0 = lists.data_ptr()
+    nz = lambda a, k: b0 + a if k else None  # noqa: E731  (no address for an empty list)
     aux = r["aux"]
     _lib.check(L.aq_quantize_finish_tiles_grouped(
         n, r["numels"], r["G"], r["K"], r["offs"], arr(nnzs, ctypes.c_int64), r["ws_ptrs"], r["ws_bytes"],
-        arr([_lib.ptr(o[0]) for o in outs]), arr([_lib.ptr(o[1]) for o in outs]), arr([_lib.ptr(o[2]) for o in outs]),
-        arr([p["tile_ptr"].data_ptr() for p in ps]), arr([o[3].data_ptr() for o in outs]), aux.data_ptr() + 4 * n,
-        r["stream"]), "aq_quantize_finish_tiles_grouped")
+        arr([nz(sp[0], k) for sp, k in zip(spans, nnzs)]), arr([nz(sp[1], k) for sp, k in zip(spans, nnzs)]),
+        arr([nz(sp[2], k) for sp, k in zip(spans, nnzs)]), arr([p["tile_ptr"].data_ptr() for p in ps]),
+        arr([b0 + sp[3] for sp in spans]), aux.data_ptr() + 4 * n, r["stream"]), "aq_quantize_finish_tiles_grouped")
     r["ws"] = None  # the finish is queued: the workspace may go back to the allocator
+    i64, f16, i32 = lists.view(torch.int64), lists.view(torch.float16), lists.view(torch.int32)
+    outs = [(i64[sp[0] // 8:sp[0] // 8 + k], f16[sp[1] // 2:sp[1] // 2 + k], i32[sp[2] // 4:sp[2] // 4 + k],
+             i32[sp[3] // 4:sp[3] // 4 + k + 64]) for sp, k in zip(spans, nnzs)]
     return [_finished_tensor(p, nnz, *o, DeviceInt(aux, n + k)) for k, (p, nnz, o) in enumerate(zip(ps, nnzs, outs))]
 
 

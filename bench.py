@@ -329,9 +329,11 @@ def kernel_only(args, dev, gen, qlinear_grouped, AQ):
 def quantize_only(args, dev, gen):
     """Counter-run workload of the quantize kernel: aq_quantize (per-channel
     E4M3, tiled) over 4 rotated gate_proj weights [14336, 4096] (470 MB of
-    fp16, past the 256 MB MALL), each pass one HIP graph, plus the same
-    512 MiB calibration copy as --kernel-only."""
-    ws = [gen_weight(14336, 4096, gen, dev) for _ in range(4)]
+    fp16, past the 256 MB MALL; ``--quantize-down``: down_proj's [4096,
+    14336]), each pass one HIP graph, plus the same 512 MiB calibration copy
+    as --kernel-only."""
+    N, K = (4096, 14336) if args.quantize_down else (14336, 4096)
+    ws = [gen_weight(N, K, gen, dev) for _ in range(4)]
     nbytes, secs = time_quantize_kernel(ws, reps=max(args.steps // 4, 1))
     src = torch.empty(512 << 20, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
@@ -910,6 +912,8 @@ def main():
     ap.add_argument("--quantize-only", action="store_true",
                     help="only the quantize kernel (4 rotated gate_proj weights) and a 512 MiB calibration copy, "
                          "for counter runs")
+    ap.add_argument("--quantize-down", action="store_true",
+                    help="with --quantize-only: down_proj's shape [4096, 14336] instead of gate_proj's")
     ap.add_argument("--quantize-layer", action="store_true",
                     help="only the grouped quantize of one layer's seven weights, for traces")
     ap.add_argument("--gemm-only", action="store_true",

@@ -323,11 +323,9 @@ __device__ __forceinline__ float team_max_f32(float v, float* lds_team) {
   return v;
 }
 
-// Exclusive prefix sum of v over the team (in thread order); *total gets the
-// team sum.
-template <int TAU>
-__device__ __forceinline__ int team_excl_scan_i32(int v, int* lds_team, int* total) {
-  constexpr int WL = TAU < 64 ? TAU : 64;
+// Inclusive prefix sum of v over groups of WL lanes (in lane order).
+template <int WL>
+__device__ __forceinline__ int wave_incl_scan_i32(int v) {
   const int lane_in = threadIdx.x & (WL - 1);
   // inclusive scan: DPP row shifts within rows of 16 lanes (zero from
   // outside the row), then the gfx9 row broadcasts of lane 15 into rows 1
@@ -351,6 +349,15 @@ __device__ __forceinline__ int team_excl_scan_i32(int v, int* lds_team, int* tot
   }
   if constexpr (WL > 16) inc += __builtin_amdgcn_update_dpp(0, inc, 0x142, 0xA, 0xF, false);  // row_bcast:15
   if constexpr (WL > 32) inc += __builtin_amdgcn_update_dpp(0, inc, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return inc;
+}
+
+// Exclusive prefix sum of v over the team (in thread order); *total gets the
+// team sum.
+template <int TAU>
+__device__ __forceinline__ int team_excl_scan_i32(int v, int* lds_team, int* total) {
+  constexpr int WL = TAU < 64 ? TAU : 64;
+  const int inc = wave_incl_scan_i32<WL>(v);
   int wave_total = __shfl(inc, WL - 1, WL);
   int excl = inc - v;
   if constexpr (TAU > 64) {
@@ -372,5 +379,77 @@ __device__ __forceinline__ int team_excl_scan_i32(int v, int* lds_team, int* tot
   } else {
     *total = wave_total;
   }
+  return excl;
+}
+
+// Two independent team reductions through one cross-wave exchange (one pair
+// of barriers instead of two), with the same trees as the single ones:
+// team_sum_f64(a) and team_sum_f32(b), in every lane of the team.
+template <int TAU>
+__device__ __forceinline__ void team_sum_f64_f32(double& a, float& b, double* lds_d, float* lds_f) {
+  constexpr int WL = TAU < 64 ? TAU : 64;
+  a = wave_group_sum_f64<WL>(a);
+  b = wave_group_sum_f32<WL>(b);
+  if constexpr (TAU > 64) {
+    constexpr int NW = TAU / 64;
+    constexpr int NP = pow2_ceil(NW);
+    const int w = (threadIdx.x % TAU) >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+      lds_d[w] = a;
+      lds_f[w] = b;
+    }
+    __syncthreads();
+    double t[NP];
+    float u[NP];
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+      t[i] = i < NW ? lds_d[i] : 0.0;
+      u[i] = i < NW ? lds_f[i] : 0.0f;
+    }
+#pragma unroll
+    for (int s = NP; s > 1; s >>= 1)
+#pragma unroll
+      for (int i = 0; i < s / 2; i++) {
+        t[i] = t[2 * i] + t[2 * i + 1];
+        u[i] = u[2 * i] + u[2 * i + 1];
+      }
+    a = t[0];
+    b = u[0];
+  }
+}
+
+// team_excl_scan_i32(v, .., total) and team_max_f32(m) through one
+// cross-wave exchange; returns the exclusive prefix, *m becomes the maximum.
+template <int TAU>
+__device__ __forceinline__ int team_scan_max(int v, float* m, int* lds_i, float* lds_f, int* total) {
+  constexpr int WL = TAU < 64 ? TAU : 64;
+  const int inc = wave_incl_scan_i32<WL>(v);
+  const int wave_total = __shfl(inc, WL - 1, WL);
+  int excl = inc - v;
+  float mx = wave_group_max_f32<WL>(*m);
+  if constexpr (TAU > 64) {
+    constexpr int NW = TAU / 64;
+    const int lane = threadIdx.x & 63;
+    const int w = (threadIdx.x % TAU) >> 6;
+    __syncthreads();
+    if (lane == 63) lds_i[w] = wave_total;
+    if (lane == 0) lds_f[w] = mx;
+    __syncthreads();
+    int before = 0, all = 0;
+    mx = lds_f[0];
+#pragma unroll
+    for (int i = 0; i < NW; i++) {
+      const int c = lds_i[i];
+      before += (i < w) ? c : 0;
+      all += c;
+      if (i > 0) mx = fmaxf(mx, lds_f[i]);
+    }
+    excl += before;
+    *total = all;
+  } else {
+    *total = wave_total;
+  }
+  *m = mx;
   return excl;
 }

@@ -484,8 +484,9 @@ __device__ __forceinline__ BlockStats block_stats_fast(Elems<E>& xs, int i0, con
     q[(2 * i) & 3] = sq_acc_lo(xs.p[i], q[(2 * i) & 3]);
     q[(2 * i + 1) & 3] = sq_acc_hi(xs.p[i], q[(2 * i + 1) & 3]);
   }
-  const double Sf = team_sum_f64<TAU>((double)sp[0], lds_d);
-  const float Qf = team_sum_f32<TAU>((q[0] + q[1]) + (q[2] + q[3]), lds_f);
+  double Sf = (double)sp[0];
+  float Qf = (q[0] + q[1]) + (q[2] + q[3]);
+  team_sum_f64_f32<TAU>(Sf, Qf, lds_d, lds_f);
   const double Q = (double)Qf;
   // sqrt(G Q) from above: (1 + 2^-14) covers Q's 2^-19 and the two f32
   // products' roundings, (1 + 2^-20) the square root's one ulp and the last
@@ -688,11 +689,19 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
     if (!tvalid) obits[w] = 0;  // padding threads hold zeros that may pass the test
     nout += __builtin_popcount(obits[w]);
   }
+  // the absmax over non-outliers (NaN and, past a finite cut, infinities are
+  // outliers, so the extremes are ordered values); -1 when the thread has
+  // none; its team maximum travels with the outlier counts' prefix sum
+  float amax = -1.0f;
+  if (tvalid && nout < E) {
+    const half2v hx = as_h2(mx), hn = as_h2(mn);
+    amax = fmaxf(fmaxf((float)hx.x, (float)hx.y), -fminf((float)hn.x, (float)hn.y));
+  }
   // outlier compaction: team prefix sum, then the block's staging slot in
   // element order (flag word w: pair PW w + j low / high at bit PW - 1 - j /
   // 16 + PW - 1 - j, so after a bit reversal L and H below hold them at bit j)
   int total;
-  const int pre = team_excl_scan_i32<TAU>(nout, lds_i, &total);
+  const int pre = team_scan_max<TAU>(nout, &amax, lds_i, lds_f, &total);
   if (gvalid) {
     int k = pre;
 #pragma unroll
@@ -723,14 +732,6 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
   // the outlier stores go out before the code stores (see the end)
   asm volatile("" ::: "memory");
 
-  // the absmax over non-outliers (NaN and, past a finite cut, infinities are
-  // outliers, so the extremes are ordered values); -1 when the thread has none
-  float amax = -1.0f;
-  if (tvalid && nout < E) {
-    const half2v hx = as_h2(mx), hn = as_h2(mn);
-    amax = fmaxf(fmaxf((float)hx.x, (float)hx.y), -fminf((float)hn.x, (float)hn.y));
-  }
-  amax = team_max_f32<TAU>(amax, lds_f);
   xs.fence();
 
   const float qmax = a.fmt == AQ_FMT_INT8 ? 127.0f : 448.0f;

@@ -384,8 +384,10 @@ __device__ __forceinline__ int team_excl_scan_i32(int v, int* lds_team, int* tot
 
 // Two independent team reductions through one cross-wave exchange (one pair
 // of barriers instead of two), with the same trees as the single ones:
-// team_sum_f64(a) and team_sum_f32(b), in every lane of the team.
-template <int TAU>
+// team_sum_f64(a) and team_sum_f32(b), in every lane of the team.  FRESH:
+// no wave has read lds_d / lds_f since the last barrier every wave passed,
+// so the barrier before the writes is left out.
+template <int TAU, bool FRESH = false>
 __device__ __forceinline__ void team_sum_f64_f32(double& a, float& b, double* lds_d, float* lds_f) {
   constexpr int WL = TAU < 64 ? TAU : 64;
   a = wave_group_sum_f64<WL>(a);
@@ -394,7 +396,7 @@ __device__ __forceinline__ void team_sum_f64_f32(double& a, float& b, double* ld
     constexpr int NW = TAU / 64;
     constexpr int NP = pow2_ceil(NW);
     const int w = (threadIdx.x % TAU) >> 6;
-    __syncthreads();
+    if constexpr (!FRESH) __syncthreads();
     if ((threadIdx.x & 63) == 0) {
       lds_d[w] = a;
       lds_f[w] = b;
@@ -421,7 +423,8 @@ __device__ __forceinline__ void team_sum_f64_f32(double& a, float& b, double* ld
 
 // team_excl_scan_i32(v, .., total) and team_max_f32(m) through one
 // cross-wave exchange; returns the exclusive prefix, *m becomes the maximum.
-template <int TAU>
+// FRESH as for team_sum_f64_f32 (for lds_i / lds_f).
+template <int TAU, bool FRESH = false>
 __device__ __forceinline__ int team_scan_max(int v, float* m, int* lds_i, float* lds_f, int* total) {
   constexpr int WL = TAU < 64 ? TAU : 64;
   const int inc = wave_incl_scan_i32<WL>(v);
@@ -432,7 +435,7 @@ __device__ __forceinline__ int team_scan_max(int v, float* m, int* lds_i, float*
     constexpr int NW = TAU / 64;
     const int lane = threadIdx.x & 63;
     const int w = (threadIdx.x % TAU) >> 6;
-    __syncthreads();
+    if constexpr (!FRESH) __syncthreads();
     if (lane == 63) lds_i[w] = wave_total;
     if (lane == 0) lds_f[w] = mx;
     __syncthreads();

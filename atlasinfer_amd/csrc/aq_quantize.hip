@@ -486,7 +486,8 @@ __device__ __forceinline__ BlockStats block_stats_fast(Elems<E>& xs, int i0, con
   }
   double Sf = (double)sp[0];
   float Qf = (q[0] + q[1]) + (q[2] + q[3]);
-  team_sum_f64_f32<TAU>(Sf, Qf, lds_d, lds_f);
+  // the block's first use of lds_d / lds_f (one block per team and workgroup)
+  team_sum_f64_f32<TAU, true>(Sf, Qf, lds_d, lds_f);
   const double Q = (double)Qf;
   // sqrt(G Q) from above: (1 + 2^-14) covers Q's 2^-19 and the two f32
   // products' roundings, (1 + 2^-20) the square root's one ulp and the last
@@ -701,7 +702,10 @@ __device__ __forceinline__ void finish_block_fast(const QuantArgs& a, Elems<E>& 
   // element order (flag word w: pair PW w + j low / high at bit PW - 1 - j /
   // 16 + PW - 1 - j, so after a bit reversal L and H below hold them at bit j)
   int total;
-  const int pre = team_scan_max<TAU>(nout, &amax, lds_i, lds_f, &total);
+  // the block's first use of lds_i, its counts in the first NWT words, the
+  // absmax in the next NWT
+  constexpr int NWT = TAU > 64 ? TAU / 64 : 1;
+  const int pre = team_scan_max<TAU, true>(nout, &amax, lds_i, reinterpret_cast<float*>(lds_i + NWT), &total);
   if (gvalid) {
     int k = pre;
 #pragma unroll
@@ -850,7 +854,7 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantGr
   constexpr int NWT = TAU > 64 ? TAU / 64 : 1;
   __shared__ double lds_d[TEAMS * NWT];
   __shared__ float lds_f[TEAMS * NWT];
-  __shared__ int lds_i[TEAMS * NWT];
+  __shared__ int lds_i[2 * TEAMS * NWT];  // per team: NWT counts, NWT maxima (finish_block_fast)
 
   const int team = threadIdx.x / TAU;
   const int t = threadIdx.x % TAU;
@@ -901,7 +905,7 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantGr
 
   if constexpr (MODE == kAnyLen)
     finish_block_any<TAU, E, MODE>(a, xs, g, gvalid, base, i0, t, lds_d + team * NWT, lds_f + team * NWT,
-                                   lds_i + team * NWT);
+                                   lds_i + 2 * team * NWT);
   else {
     // four one-row blocks of 4096 elements staged together, tiled codes:
     // the codes go out through the stage in 64-byte runs (a store
@@ -911,7 +915,7 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantGr
     if constexpr (kStage && TAU == 64 && E == 64 && NT == 256)
       if (staged && a.tiled && a.bpr == 1) xchg = stage;
     finish_block_fast<TAU, E, MODE>(a, xs, g, gvalid, base, i0, t, lds_d + team * NWT, lds_f + team * NWT,
-                                    lds_i + team * NWT, staged ? reinterpret_cast<const uint16_t*>(stage) : nullptr,
+                                    lds_i + 2 * team * NWT, staged ? reinterpret_cast<const uint16_t*>(stage) : nullptr,
                                     (int)(team * G + i0), xchg);
   }
 }

@@ -76,6 +76,7 @@ SHAPES = [
     (8, 14336, -1, 3.0, "int8", None, 0.001),     # per-row block of 14336 (team of 448 x 32), flat codes
     (48, 14336, -1, 3.0, "e4m3", 3, 0.01),        # the same into tiled codes, rows in XCD-contiguous order
     (32, 4096, 128, 3.0, "e4m3", 3, 0.01),        # 32 blocks of 128 (one row) per workgroup, tiled, XCD order
+    (32, 8192, -1, 3.0, "e4m3", 3, 0.01),         # two 2-wave teams per workgroup (block-wide votes, paired exchanges)
     (4, 40000, -1, 3.0, "e4m3", None, 0.001),     # block > 16384: 64 elements per thread
     (128, 96, 32, 1.0, "int8", None, 0.05),       # many outliers per block
     (7, 13, 8, 2.0, "e4m3", None, 0.05),          # G < 16, unaligned rows

@@ -536,7 +536,11 @@ def quantize_tensors(tensors, block_size: int = 128, z_threshold: float = 3.0, *
     weights of a layer then share the GPU instead of each filling one round
     of it, and each run costs one host sync, taken once the next run is
     queued (two runs are in flight at a time).  Tensors with more blocks are
-    quantized one at a time, each completed before the next is prepared."""
+    quantized one at a time, each completed before the next is prepared.
+    The members of a tiled run share two allocations (their codes, scales,
+    offsets and block-list pointers; their outlier lists), so a run's device
+    memory goes back to the allocator when the last of its QuantizedTensors
+    does."""
     fmt = _format_id(code_format)
     out = [None] * len(tensors)
     groups = {}

@@ -124,7 +124,7 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   const uint32_t code_lane = lane * 16;
   const uint32_t x_lane = (uint32_t)(li * K + 16 * grp) * 2;  // x row li, columns 16 grp + ...
   const uint32_t scale_row = (uint32_t)li * W.kg;
-  const uint16_t sb_row = PC ? W.scales[n] : (uint16_t)0;
+  const uint16_t sb_row = PC == 1 ? W.scales[n] : (uint16_t)0;
 
   // Wave 0 also handles the rows' outliers.  Its row_ptr load goes out
   // first; the (col, val) loads of up to 64 * kStageBatch entries go out
@@ -239,7 +239,11 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       const uint32_t co = in ? code_lane + (uint32_t)c * 2048 : kOutOfRange;
       B.q[u][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co, 0, kCodePolicy));
       B.q[u][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co + 1024, 0, kCodePolicy));
-      if (!PC) {
+      if (PC == 2) {
+        // blocks of 128 or more, a power of two: one scale per row and chunk
+        const uint32_t k = (uint32_t)(in ? c : 0) * 128;
+        B.s[u][0] = __builtin_amdgcn_raw_buffer_load_b16(sr, (scale_row + (k >> W.gshift)) * 2, 0, 0);
+      } else if (PC == 0) {
         const uint32_t k = (uint32_t)(in ? c : 0) * 128 + 16 * grp;
         const uint32_t k0 = W.gshift >= 0 ? k >> W.gshift : k / W.G;
         const uint32_t k1 = W.gshift >= 0 ? (k + 64) >> W.gshift : (k + 64) / W.G;
@@ -277,8 +281,8 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   auto compute = [&](const Batch& B) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const half2v s0 = scale2(PC ? sb_row : (uint16_t)B.s[u][0]);
-      const half2v s1 = scale2(PC ? sb_row : (uint16_t)B.s[u][1]);
+      const half2v s0 = scale2(PC == 1 ? sb_row : (uint16_t)B.s[u][0]);
+      const half2v s1 = PC == 0 ? scale2((uint16_t)B.s[u][1]) : s0;
       const half8 w0 = deq8<FMT>(B.q[u][0].x, B.q[u][0].y, s0);
       const half8 w1 = deq8<FMT>(B.q[u][0].z, B.q[u][0].w, s0);
       const half8 w2 = deq8<FMT>(B.q[u][1].x, B.q[u][1].y, s1);
@@ -362,10 +366,13 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       load_q(B1, wave + step);
       __builtin_amdgcn_sched_barrier(0);
       // x arrived, the codes may not have: the loads after x are 2 U code
-      // pieces per batch, + 2 U scales with block-wise scales (the
-      // compiler's own count gives up on the conditional loads above)
-      if (PC)
+      // pieces per batch, + 2 U scales with block-wise scales (U with one
+      // scale per chunk) (the compiler's own count gives up on the
+      // conditional loads above)
+      if (PC == 1)
         __builtin_amdgcn_s_waitcnt(kVmcnt<4 * U>);
+      else if (PC == 2)
+        __builtin_amdgcn_s_waitcnt(kVmcnt<6 * U>);
       else
         __builtin_amdgcn_s_waitcnt(kVmcnt<8 * U>);
       x_store(threadIdx.x);
@@ -584,7 +591,7 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   const uint32_t code_base = trr < rows_here ? (uint32_t)(trr * nchunks * 2048 + lane * 16) : kOutOfRange;
   const uint32_t scale_row = (uint32_t)(trr * 16 + li) * W.kg;
   uint16_t sb_row = 0;
-  if (PC) sb_row = trr < rows_here ? W.scales[(size_t)(rb0 + trr) * 16 + li] : (uint16_t)0;
+  if (PC == 1) sb_row = trr < rows_here ? W.scales[(size_t)(rb0 + trr) * 16 + li] : (uint16_t)0;
 
   // OT: the block lists (tile_ptr offset to the piece's first tile row;
   // tile_ent holds 64 entries of read padding past the last)
@@ -617,7 +624,11 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
     // codes are read once per call: non-temporal
     sl.q0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co, 0, 2));
     sl.q1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co + 1024, 0, 2));
-    if (!PC) {
+    if (PC == 2) {
+      // blocks of 128 or more, a power of two: one scale per row and chunk
+      const uint32_t k = (uint32_t)(c < nchunks ? c : 0) * 128;
+      sl.s0 = __builtin_amdgcn_raw_buffer_load_b16(sr, (scale_row + (k >> W.gshift)) * 2, 0, 0);
+    } else if (PC == 0) {
       const uint32_t k = (uint32_t)(c < nchunks ? c : 0) * 128 + 16 * grp;
       const uint32_t k0 = W.gshift >= 0 ? k >> W.gshift : k / W.G;
       const uint32_t k1 = W.gshift >= 0 ? (k + 64) >> W.gshift : (k + 64) / W.G;
@@ -682,8 +693,8 @@ __global__ __launch_bounds__(64 * kXWaves) void qlinear_gemv_x_kernel(QLArgs a) 
   };
 
   auto step = [&](Slot& sl, int j, uint16_t* xb) {
-    const half2v s0 = scale2(PC ? sb_row : (uint16_t)sl.s0);
-    const half2v s1 = scale2(PC ? sb_row : (uint16_t)sl.s1);
+    const half2v s0 = scale2(PC == 1 ? sb_row : (uint16_t)sl.s0);
+    const half2v s1 = PC == 0 ? scale2((uint16_t)sl.s1) : s0;
     const half8 w0 = deq8<FMT>(sl.q0.x, sl.q0.y, s0);
     const half8 w1 = deq8<FMT>(sl.q0.z, sl.q0.w, s0);
     const half8 w2 = deq8<FMT>(sl.q1.x, sl.q1.y, s1);
@@ -1678,6 +1689,15 @@ dim3 gemv_pieces(const QLArgs& a, int unit, QLArgs* g) {
   return dim3((unsigned)aq::ceil_div(P, unit), (unsigned)n);
 }
 
+// Block-wise scales with blocks of a power of two of at least 128: a
+// 128-column chunk lies inside one block, so the GEMVs load one scale per
+// row and chunk (scale mode 2) instead of one per 64 columns.
+bool chunk_scales(const QLArgs& a) {
+  for (int i = 0; i < a.count; i++)
+    if (a.mat[i].kg == 1 || a.mat[i].gshift < 7) return false;
+  return true;
+}
+
 template <int NS, int FMT>
 hipError_t launch_gemv(const QLArgs& a, bool per_channel, hipStream_t s) {
   // decode (M = 1) with x small enough: x in LDS (dynamic size), read by
@@ -1708,6 +1728,13 @@ hipError_t launch_gemv(const QLArgs& a, bool per_channel, hipStream_t s) {
       hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 0, 1>), g, b, 0, s, p);
     else
       hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 1, 0, R>), g, b, 0, s, p);
+  } else if (chunk_scales(a)) {
+    if (x1)
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 2, 1, 1>), g, b, lds, s, p);
+    else if (a.M == 1)
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 2, 0, 1>), g, b, 0, s, p);
+    else
+      hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 2, 0, R>), g, b, 0, s, p);
   } else {
     if (x1)
       hipLaunchKernelGGL((qlinear_gemv_kernel<NS, FMT, 0, 1, 1>), g, b, lds, s, p);
@@ -1749,6 +1776,8 @@ hipError_t launch_gemv_x(const QLArgs& a, bool per_channel, hipStream_t s) {
     if (lists) {
       if (per_channel)
         hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 1, MG, S, 1, XH>), g, dim3(64 * kXWaves), 0, s, p);
+      else if (chunk_scales(a))
+        hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 2, MG, S, 1, XH>), g, dim3(64 * kXWaves), 0, s, p);
       else
         hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 0, MG, S, 1, XH>), g, dim3(64 * kXWaves), 0, s, p);
       return hipGetLastError();
@@ -1756,6 +1785,8 @@ hipError_t launch_gemv_x(const QLArgs& a, bool per_channel, hipStream_t s) {
   }
   if (per_channel)
     hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 1, MG, S, 0, XH>), g, dim3(64 * kXWaves), 0, s, p);
+  else if (chunk_scales(a))
+    hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 2, MG, S, 0, XH>), g, dim3(64 * kXWaves), 0, s, p);
   else
     hipLaunchKernelGGL((qlinear_gemv_x_kernel<FMT, 0, MG, S, 0, XH>), g, dim3(64 * kXWaves), 0, s, p);
   return hipGetLastError();

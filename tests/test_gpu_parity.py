@@ -153,8 +153,10 @@ def test_compact_expand_round_trip():
 
 
 @pytest.mark.parametrize("M", [1, 2, 4, 5, 6, 8, 12, 16, 17, 33, 64, 65, 300])
-@pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128), ("e4m3", 64)])
+@pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128), ("e4m3", 64), ("e4m3", 128), ("e4m3", 256)])
 def test_qlinear_matches_reference_linear(M, fmt, G):
+    """Per-channel scales, blocks of 64 (two scales per 128-column chunk) and
+    blocks of 128 / 256 (one scale per chunk: the GEMVs' third scale mode)."""
     rng = np.random.default_rng(M + 31 * abs(G))
     N, K = 1024, 2048
     w = make_weights(rng, (N, K))
@@ -173,7 +175,7 @@ def test_qlinear_matches_reference_linear(M, fmt, G):
 
 @pytest.mark.parametrize("N,K", [(1040, 640), (6160, 384), (12304, 384)])
 @pytest.mark.parametrize("M", [9, 17, 48, 64])
-@pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128)])
+@pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128), ("e4m3", 128)])
 def test_gemv_shared_x_ragged_shapes(N, K, M, fmt, G):
     """6 <= M <= 64: tile-row counts that leave the last workgroup partly
     empty, chunk counts that leave the last chunk group partly past K, and

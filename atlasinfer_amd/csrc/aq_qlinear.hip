@@ -240,9 +240,15 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       B.q[u][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co, 0, kCodePolicy));
       B.q[u][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, co + 1024, 0, kCodePolicy));
       if (PC == 2) {
-        // blocks of 128 or more, a power of two: one scale per row and chunk
-        const uint32_t k = (uint32_t)(in ? c : 0) * 128;
-        B.s[u][0] = __builtin_amdgcn_raw_buffer_load_b16(sr, (scale_row + (k >> W.gshift)) * 2, 0, 0);
+        // blocks of 128 or more, a power of two: one scale per row and
+        // chunk; the lanes of row group g load the scale of the batch's
+        // chunk g (min(g, U - 1)), handed to the others in compute
+        static_assert(U <= 4, "one row group per chunk of the batch");
+        if (u == 0) {
+          const int cg = c0 + (grp < U ? grp : U - 1) * NS;
+          const uint32_t k = (uint32_t)(cg < nchunks ? cg : 0) * 128;
+          B.s[0][0] = __builtin_amdgcn_raw_buffer_load_b16(sr, (scale_row + (k >> W.gshift)) * 2, 0, 0);
+        }
       } else if (PC == 0) {
         const uint32_t k = (uint32_t)(in ? c : 0) * 128 + 16 * grp;
         const uint32_t k0 = W.gshift >= 0 ? k >> W.gshift : k / W.G;
@@ -281,7 +287,9 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
   auto compute = [&](const Batch& B) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const half2v s0 = scale2(PC == 1 ? sb_row : (uint16_t)B.s[u][0]);
+      const half2v s0 = scale2(PC == 1   ? sb_row
+                               : PC == 2 ? (uint16_t)__shfl((int)B.s[0][0], 16 * u + li)
+                                         : (uint16_t)B.s[u][0]);
       const half2v s1 = PC == 0 ? scale2((uint16_t)B.s[u][1]) : s0;
       const half8 w0 = deq8<FMT>(B.q[u][0].x, B.q[u][0].y, s0);
       const half8 w1 = deq8<FMT>(B.q[u][0].z, B.q[u][0].w, s0);
@@ -366,13 +374,13 @@ __global__ __launch_bounds__(64 * NS) void qlinear_gemv_kernel(QLArgs a) {
       load_q(B1, wave + step);
       __builtin_amdgcn_sched_barrier(0);
       // x arrived, the codes may not have: the loads after x are 2 U code
-      // pieces per batch, + 2 U scales with block-wise scales (U with one
+      // pieces per batch, + 2 U scales with block-wise scales (one with one
       // scale per chunk) (the compiler's own count gives up on the
       // conditional loads above)
       if (PC == 1)
         __builtin_amdgcn_s_waitcnt(kVmcnt<4 * U>);
       else if (PC == 2)
-        __builtin_amdgcn_s_waitcnt(kVmcnt<6 * U>);
+        __builtin_amdgcn_s_waitcnt(kVmcnt<4 * U + 2>);
       else
         __builtin_amdgcn_s_waitcnt(kVmcnt<8 * U>);
       x_store(threadIdx.x);

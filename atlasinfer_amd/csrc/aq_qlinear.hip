@@ -2087,7 +2087,11 @@ static int qlinear_grouped_impl(const void* x, int64_t M, int64_t K, int fmt, in
   bool have_lists = tile_ptrs && tile_ents && tile_maxes;
   for (int i = 0; i < count && have_lists; i++) have_lists = tile_ptrs[i] && tile_ents[i];
   const bool gemv = M <= kGemvShortMaxM || (M <= kGemvMaxM && (blocks >= kGemvShortRows || !have_lists));
-  if (gemv && M >= kGemvXMinM) {
+  // From M = 2 the shared-x GEMV also takes tall groups with block-wise
+  // scales (block-128 gate+up at M = 4: 29.9 against 26.7 us; shorter grids
+  // and per-channel scales stay faster re-reading x per tile row below)
+  const bool x_tall = !per_channel && M >= 2 && blocks >= 768;
+  if (gemv && (M >= kGemvXMinM || x_tall)) {
     // S = 2 waves per tile row for tall groups, 4 for short ones and 8 for
     // fewer than 384 tile rows up to M = 32 (one tile row per workgroup; at
     // M = 64 its x stages do not fit LDS) (measured on the Llama-3-8B

@@ -174,13 +174,14 @@ def test_qlinear_matches_reference_linear(M, fmt, G):
 
 
 @pytest.mark.parametrize("N,K", [(1040, 640), (6160, 384), (12304, 384)])
-@pytest.mark.parametrize("M", [9, 17, 48, 64])
+@pytest.mark.parametrize("M", [2, 5, 9, 17, 48, 64])
 @pytest.mark.parametrize("fmt,G", [("e4m3", -1), ("int8", 128), ("e4m3", 128)])
 def test_gemv_shared_x_ragged_shapes(N, K, M, fmt, G):
-    """6 <= M <= 64: tile-row counts that leave the last workgroup partly
-    empty, chunk counts that leave the last chunk group partly past K, and
-    every split width (12304 rows take 2 waves per tile row, 6160 take 4,
-    1040 take 8 up to M = 32 and 4 above)."""
+    """6 <= M <= 64 (and from M = 2 tall groups with block-wise scales):
+    tile-row counts that leave the last workgroup partly empty, chunk counts
+    that leave the last chunk group partly past K, and every split width
+    (12304 rows take 2 waves per tile row, 6160 take 4, 1040 take 8 up to
+    M = 32 and 4 above)."""
     rng = np.random.default_rng(N + K + M + abs(G))
     w = make_weights(rng, (N, K), frac=0.004)
     x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV)

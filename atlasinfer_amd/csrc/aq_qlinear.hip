@@ -21,9 +21,10 @@
 //    one launch, cut into pieces of equal tile-row count, one grid row
 //    (blockIdx.y) per piece, so that a wave finds its matrix without
 //    loading anything first.
-//  * 6 <= M <= 64: the same streaming, but 8 waves per workgroup share each
-//    chunk of x through LDS (details at its kernel below), since x is then
-//    comparable to or larger than the codes it multiplies.  (M = 1..5 re-read
+//  * 6 <= M <= 64 (and from M = 2 tall groups with block-wise scales): the
+//    same streaming, but 8 waves per workgroup share each chunk of x through
+//    LDS (details at its kernel below), since x is then comparable to or
+//    larger than the codes it multiplies.  (M = 1..5 re-read
 //    x per tile row above; decode stages it in LDS once per workgroup.)
 //  * M > 64: dequant-GEMM (details at its kernel below): 128 or 256 rows of
 //    x by 128 output columns per workgroup, x and decoded weights staged in

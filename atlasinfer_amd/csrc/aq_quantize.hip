@@ -1220,11 +1220,11 @@ hipError_t launch_quantize_t(QuantGroup q, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Team shape per padded block size P: up to 1024 elements, 16 per thread
-// (teams of at most one wave, several per workgroup; 128, the reference's
-// default block, 32 per thread: a lane's fixed work per block over twice
-// the elements); 2048, 32 per thread on
-// one wave; from 4096 on, 64 per thread (one wave for 4096, a block of
+// Team shape per padded block size P: up to 32 elements, 16 per thread;
+// 64 to 2048, 32 per thread (teams of at most one wave, several per
+// workgroup: a lane's fixed work per block over twice the elements of 16
+// per thread, measured 11 to 25 % faster for 64 to 1024 on a 4096 x 14336
+// weight); 2048 on one wave; from 4096 on, 64 per thread (one wave for 4096, a block of
 // 4096 elements then needs no barrier at all), except 16384: 32 per thread
 // on 8 waves ran 4 % faster than 64 on 4 for rows of 14336 such as
 // down_proj's (which now take 7 waves, below), while 32 per thread at 4096
@@ -1239,11 +1239,11 @@ hipError_t launch_quantize(const QuantGroup& q, hipStream_t stream) {
   switch (P) {
     case 1: case 2: case 4: case 8: case 16: return launch_quantize_t<1, 16>(q, stream);
     case 32: return launch_quantize_t<2, 16>(q, stream);
-    case 64: return launch_quantize_t<4, 16>(q, stream);
-    case 128: return launch_quantize_t<4, 32>(q, stream);  // 8 x 16 measured 11 % slower
-    case 256: return launch_quantize_t<16, 16>(q, stream);
-    case 512: return launch_quantize_t<32, 16>(q, stream);
-    case 1024: return launch_quantize_t<64, 16>(q, stream);
+    case 64: return launch_quantize_t<2, 32>(q, stream);
+    case 128: return launch_quantize_t<4, 32>(q, stream);
+    case 256: return launch_quantize_t<8, 32>(q, stream);
+    case 512: return launch_quantize_t<16, 32>(q, stream);
+    case 1024: return launch_quantize_t<32, 32>(q, stream);
     case 2048: return launch_quantize_t<64, 32>(q, stream);
     case 4096: return launch_quantize_t<64, 64>(q, stream);
     case 8192: return launch_quantize_t<128, 64>(q, stream);

@@ -79,6 +79,16 @@ SHAPES = [
     (32, 8192, -1, 3.0, "e4m3", 3, 0.01),         # two 2-wave teams per workgroup (block-wide votes, paired exchanges)
     (4, 40000, -1, 3.0, "e4m3", None, 0.001),     # block > 16384: 64 elements per thread
     (128, 96, 32, 1.0, "int8", None, 0.05),       # many outliers per block
+    # blocks of 33..1024 on teams of 32 elements per thread: full blocks,
+    # thread-aligned (G a multiple of 32) and ragged lengths
+    (40, 640, 64, 3.0, "e4m3", 3, 0.01),
+    (24, 500, 50, 2.0, "int8", None, 0.02),
+    (16, 960, 96, 3.0, "e4m3", 3, 0.01),
+    (16, 2048, 256, 3.0, "e4m3", 3, 0.01),
+    (20, 3000, 300, 2.5, "e4m3", None, 0.01),
+    (12, 3072, 1024, 3.0, "e4m3", 3, 0.01),
+    (10, 2400, 800, 2.0, "int8", None, 0.01),
+    (10, 2100, 700, 3.0, "e4m3", 3, 0.01),
     (7, 13, 8, 2.0, "e4m3", None, 0.05),          # G < 16, unaligned rows
     (1, 10, 64, 3.0, "int8", None, 0.0),          # smaller than one block
     (256, 512, 1, 3.0, "int8", None, 0.0),        # G = 1: std is NaN, no outliers

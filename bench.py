@@ -198,13 +198,13 @@ def profiled_us_per_launch():
     return None
 
 
-def time_quantize_kernel(weights, reps=5, grouped=False):
+def time_quantize_kernel(weights, reps=5, grouped=False, G=None):
     """The quantize kernel alone (aq_quantize: statistics, codes, outlier
-    staging and the scan of outlier counts), per-channel E4M3 into the tiled
-    layout, timed with HIP events on the launch stream over ``reps`` replays
-    of a graph holding one pass over every weight; returns (algorithmic
-    bytes, seconds) of one pass.
-    Bytes: 2 N K read + N K codes + 2 N scales + 6 per outlier staged.
+    staging and the scan of outlier counts), E4M3 into the tiled layout,
+    per-channel (``G`` None) or in blocks of ``G``, timed with HIP events on
+    the launch stream over ``reps`` replays of a graph holding one pass over
+    every weight; returns (algorithmic bytes, seconds) of one pass.
+    Bytes: 2 N K read + N K codes + 2 per scale + 6 per outlier staged.
     ``grouped``: the weights sharing K in aq_quantize_grouped launches of up
     to 8 (as apply_atlas_quantization_to_model quantizes them), the rest
     alone."""
@@ -215,18 +215,21 @@ def time_quantize_kernel(weights, reps=5, grouped=False):
     for w in weights:
         N, K = w.shape
         numel = N * K
+        Gw = K if G is None else G
+        assert K % Gw == 0
+        nb = numel // Gw
         codes = torch.empty(numel, dtype=torch.uint8, device=w.device)
-        scales = torch.empty(N, dtype=torch.float16, device=w.device)
-        off = torch.empty(N + 1, dtype=torch.int32, device=w.device)
-        wsb = int(L.aq_quantize_workspace_size(numel, K))
+        scales = torch.empty(nb, dtype=torch.float16, device=w.device)
+        off = torch.empty(nb + 1, dtype=torch.int32, device=w.device)
+        wsb = int(L.aq_quantize_workspace_size(numel, Gw))
         ws = torch.empty(wsb, dtype=torch.uint8, device=w.device)
-        args = (w.data_ptr(), numel, K, AQ._threshold_bits(3.0), _lib.FMT_E4M3, K, _lib.LAYOUT_TILED,
+        args = (w.data_ptr(), numel, Gw, AQ._threshold_bits(3.0), _lib.FMT_E4M3, K, _lib.LAYOUT_TILED,
                 codes.data_ptr(), scales.data_ptr(), off.data_ptr(), ws.data_ptr(), wsb)
         calls.append((args, (codes, scales, off, ws)))
         _lib.check(L.aq_quantize(*args, _lib.stream_of(w.device)), "aq_quantize")
         torch.cuda.synchronize()
-        nnz = int(off[N].item())
-        nbytes += 3 * numel + 2 * N + 6 * nnz
+        nnz = int(off[nb].item())
+        nbytes += 3 * numel + 2 * nb + 6 * nnz
     # one pass captured in a HIP graph (the launches issue no memset), so the
     # host's launch cost of the small weights is not timed
     runs = [[c] for c in calls]
@@ -330,11 +333,12 @@ def quantize_only(args, dev, gen):
     """Counter-run workload of the quantize kernel: aq_quantize (per-channel
     E4M3, tiled) over 4 rotated gate_proj weights [14336, 4096] (470 MB of
     fp16, past the 256 MB MALL; ``--quantize-down``: down_proj's [4096,
-    14336]), each pass one HIP graph, plus the same 512 MiB calibration copy
-    as --kernel-only."""
+    14336]; ``--quantize-block G``: blocks of G instead of one per row),
+    each pass one HIP graph, plus the same 512 MiB calibration copy as
+    --kernel-only."""
     N, K = (4096, 14336) if args.quantize_down else (14336, 4096)
     ws = [gen_weight(N, K, gen, dev) for _ in range(4)]
-    nbytes, secs = time_quantize_kernel(ws, reps=max(args.steps // 4, 1))
+    nbytes, secs = time_quantize_kernel(ws, reps=max(args.steps // 4, 1), G=args.quantize_block)
     src = torch.empty(512 << 20, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
@@ -920,6 +924,8 @@ def main():
                          "for counter runs")
     ap.add_argument("--quantize-down", action="store_true",
                     help="with --quantize-only: down_proj's shape [4096, 14336] instead of gate_proj's")
+    ap.add_argument("--quantize-block", type=int, default=None,
+                    help="with --quantize-only: blocks of this size (dividing the row) instead of per-channel")
     ap.add_argument("--quantize-layer", action="store_true",
                     help="only the grouped quantize of one layer's seven weights, for traces")
     ap.add_argument("--gemm-only", action="store_true",
@@ -1093,6 +1099,7 @@ def main():
 
     qk_bytes, qk_s = time_quantize_kernel([keep_fp16[name] for name, _, _ in LLAMA_LINEARS], grouped=True)
     qk1_bytes, qk1_s = time_quantize_kernel([keep_fp16[name] for name, _, _ in LLAMA_LINEARS])
+    qkb_bytes, qkb_s = time_quantize_kernel([keep_fp16[name] for name, _, _ in LLAMA_LINEARS], G=128)
     log(f"quantize kernel: {qk_bytes / qk_s / 1e9:.1f} GB/s ({1e6 * qk_s:.1f} us per layer)")
 
     blas_m1_s = 0.0
@@ -1195,6 +1202,10 @@ def main():
                                     "model swap quantizes them); _single: one aq_quantize per weight",
             "quantize_kernel_single_GBps": round(qk1_bytes / qk1_s / 1e9, 1),
             "quantize_kernel_single_frac_hbm_peak": round(qk1_bytes / qk1_s / 1e9 / HBM_PEAK_GBS, 4),
+            "quantize_kernel_g128_GBps": round(qkb_bytes / qkb_s / 1e9, 1),
+            "quantize_kernel_g128_frac_hbm_peak": round(qkb_bytes / qkb_s / 1e9 / HBM_PEAK_GBS, 4),
+            "quantize_kernel_g128_note": "the same 7 weights in blocks of 128 (the reference example's default, "
+                                         "run_atlas_inference.py:42), one aq_quantize per weight",
             "quantize_GBps": round(sum(q_rates) / len(q_rates) / 1e9, 1),
             "quantize_call_us": q_calls,
             "quantize_b2b_GBps": round(q_b2b_bytes / q_b2b_s / 1e9, 1),

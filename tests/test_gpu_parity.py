@@ -89,6 +89,10 @@ SHAPES = [
     (12, 3072, 1024, 3.0, "e4m3", 3, 0.01),
     (10, 2400, 800, 2.0, "int8", None, 0.01),
     (10, 2100, 700, 3.0, "e4m3", 3, 0.01),
+    # count scans over many workgroups: 131 072 blocks (runs of 4 counts per
+    # thread) and 2 099 200 blocks (runs of 16), both with outliers in most blocks
+    (1024, 4096, 32, 1.0, "e4m3", None, 0.0),
+    (8200, 4096, 16, 1.0, "int8", None, 0.0),
     (7, 13, 8, 2.0, "e4m3", None, 0.05),          # G < 16, unaligned rows
     (1, 10, 64, 3.0, "int8", None, 0.0),          # smaller than one block
     (256, 512, 1, 3.0, "int8", None, 0.0),        # G = 1: std is NaN, no outliers

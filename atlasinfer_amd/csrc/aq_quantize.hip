@@ -922,11 +922,12 @@ __global__ __launch_bounds__(TAU > kWG ? TAU : kWG) void quantize_kernel(QuantGr
 
 // ---- exclusive scan of the per-block counts (in place, two passes)
 
-// PT consecutive counts per thread, 256 * PT per workgroup: runs of 4 keep
-// a load instruction's lanes within 1 KiB and give the 458 752 blocks of a
-// Llama-3-8B weight in blocks of 128 448 workgroups (runs of 16: 112, and
-// 4.7 + 6.5 us for the two passes); runs of 16 from 2048 chunks of 1024 on,
-// where each apply workgroup's sum over the partials before it would grow.
+// PT consecutive counts per thread, 256 * PT per workgroup.  Runs of 4 keep
+// a load instruction's lanes within 1 KiB; a Llama-3-8B weight quantized in
+// blocks of 128 has 458 752 counts, which then take 448 workgroups (runs of
+// 16: 112 workgroups, and 4.7 + 6.5 us for the two passes against 4.7 +
+// 4.6).  Beyond 2048 chunks of 1024, runs of 16, so that each apply
+// workgroup's sum over the partials before it stays short.
 template <int PT>
 __global__ __launch_bounds__(256) void scan_partials_kernel(const int32_t* cnt, int64_t n, int32_t* partial) {
   __shared__ int lds[4];
